@@ -1,0 +1,405 @@
+#!/usr/bin/env python3
+"""Benchmark of the fused MaxSim forward on one MI355X.
+
+Default workload (the north-star metric): fp16
+candidate scoring, Q (128, 32, 256), gallery (128, 180, 100_000), idxs
+(1000, 256) uniform in 1..100_000 with 1% of slots invalid (-> neg), masks
+all true (as true_mask allocates them).  One step = one
+launch_candidates_scan over the whole batch (scores + argmax tape), inputs
+resident in HBM, outputs preallocated.  Prints ONE JSON line.
+
+Other workloads (--workload c3 | c4 | c4d1024 | c5) measure the in-batch,
+packed and INT8 scans the same way; they are reported in DESIGN.md.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "flashmaxsim.jl_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0      # MI355X HBM3E, published
+FP16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16/bf16 MFMA, published
+INT8_PEAK_TOPS = 5000.0
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="c2", choices=["c2", "c3", "c4", "c4d1024", "c5"])
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="target duration of the bounded CPU baseline sample")
+    ap.add_argument("--check", type=int, default=256,
+                    help="pairs re-scored by the CPU oracle as a full-size parity spot check")
+    return ap.parse_args()
+
+
+# ---- synthetic data ---------------------------------------------------------------------
+
+def normalized_randn(torch, shape, gen, dtype, device, chunk_rows=4096):
+    """randn tokens, L2-normalised per token (x / sqrt(sum x^2 + eps)), cast to dtype.
+    Generated on the device in chunks along the leading axis."""
+    out = torch.empty(shape, dtype=dtype, device=device)
+    eps = torch.finfo(torch.float32).eps
+    n = shape[0]
+    for a in range(0, n, chunk_rows):
+        b = min(n, a + chunk_rows)
+        x = torch.randn((b - a,) + tuple(shape[1:]), generator=gen, device=device,
+                        dtype=torch.float32)
+        x = x / torch.sqrt((x * x).sum(-1, keepdim=True) + eps)
+        out[a:b] = x.to(dtype)
+        del x
+    return out
+
+
+def timed_steps(torch, fn, steps, warmup):
+    """W untimed steps, then exactly K steps bracketed by synchronize; per-launch HIP
+    events on the current stream (the stream every scan is enqueued on)."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(steps)]
+    t0 = time.perf_counter()
+    for e0, e1 in ev:
+        e0.record(st)
+        fn()
+        e1.record(st)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    launch_ms = [e0.elapsed_time(e1) for e0, e1 in ev]
+    return wall, launch_ms
+
+
+def cpu_threads():
+    n = os.cpu_count() or 1
+    return max(1, min(n, 16))  # the GPU box grants 16 host cores per GPU
+
+
+# ---- workloads --------------------------------------------------------------------------
+
+def run_c2(args, torch, fm, boundary, dev):
+    dim, Lq, Ld, C, B, N = 128, 32, 180, 1000, 256, 100_000
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(2)
+    log("c2: generating gallery (100000 x 180 x 128 fp16) ...")
+    G = normalized_randn(torch, (N, Ld, dim), gen, torch.float16, dev)
+    Q = normalized_randn(torch, (B, Lq, dim), gen, torch.float16, dev)
+    idx = torch.randint(1, N + 1, (B, C), generator=gen, device=dev, dtype=torch.int64)
+    n_invalid = (C * B) // 100
+    flat = torch.randperm(C * B, generator=gen, device=dev)[:n_invalid]
+    idx.view(-1)[flat] = 0
+    qmask = torch.ones(B, Lq, dtype=torch.bool, device=dev)
+    dmask = torch.ones(N, Ld, dtype=torch.bool, device=dev)
+    args_t = torch.empty(B, C, Lq, dtype=torch.int32, device=dev)
+    S = torch.empty(B, C, dtype=torch.float32, device=dev)
+    neg = -1.0e4
+
+    def step():
+        boundary.launch_candidates_scan(args_t, None, Q, G, idx, qmask, dmask, N, S, neg)
+
+    wall, launch_ms = timed_steps(torch, step, args.steps, args.warmup)
+    n_valid = C * B - n_invalid
+    bytes_per_launch = (n_valid * (Ld * dim * 2 + Ld) + C * B * (4 * Lq + 4)
+                        + B * (Lq * dim * 2 + Lq) + C * B * 8)
+    res = dict(pairs_per_step=C * B, bytes_per_launch=bytes_per_launch, wall=wall,
+               launch_ms=launch_ms, dtype="f16",
+               config={"workload": "c2_candidates_fp16", "dim": dim, "Lq": Lq, "Ld": Ld,
+                       "C": C, "B": B, "N": N, "invalid_slots": n_invalid, "idx": "int64",
+                       "masks": "all true (device Bool)", "outputs": "scores (C,B) + tape (Lq,C,B)"})
+    res["bound"] = "hbm"
+    if not args.no_cpu or args.check:
+        res.update(cpu_candidates(args, torch, Q, G, idx, qmask, dmask, S, args_t, neg,
+                                  fp16=True))
+    return res
+
+
+def cpu_candidates(args, torch, Q, G, idx, qmask, dmask, S, args_t, neg, fp16=False,
+                   int8=None):
+    """Bounded CPU baseline + full-size parity spot check on a random pair sample."""
+    import numpy as np
+    import oracle
+    torch.cuda.synchronize()
+    B, C = idx.shape
+    rng = np.random.default_rng(0)
+    nthreads = cpu_threads()
+    out = {}
+    idx_h = idx.cpu().numpy()
+    n_gallery = G.shape[0] if int8 is None else int8[0].shape[0]
+
+    def sample_problem(pairs):
+        b = pairs // C
+        j = idx_h.reshape(-1)[pairs]
+        ub = np.unique(b)
+        uj = np.unique(j[(j >= 1) & (j <= n_gallery)])
+        # compact copies of only the referenced queries / documents
+        bmap = {v: i for i, v in enumerate(ub)}
+        jmap = {v: i + 1 for i, v in enumerate(uj)}
+        idx_c = np.zeros((len(ub), C), np.int64)
+        keep = []
+        for p, bb, jj in zip(pairs, b, j):
+            r, c = bmap[bb], p % C
+            idx_c[r, c] = jmap.get(jj, 0)
+            keep.append(r * C + c)
+        return ub, uj, idx_c, np.asarray(keep, np.int64)
+
+    def run_oracle(pairs, threads):
+        ub, uj, idx_c, keep = sample_problem(pairs)
+        ub_t = torch.from_numpy(ub).to(Q.device)
+        uj_t = torch.from_numpy(np.maximum(uj - 1, 0)).to(Q.device)
+        qm = qmask[ub_t].cpu().numpy().astype(np.uint8)
+        if int8 is None:
+            Qh = Q[ub_t].cpu().numpy()
+            Gh = G[uj_t].cpu().numpy() if len(uj) else np.zeros((0,) + tuple(G.shape[1:]), Qh.dtype)
+            dm = dmask[uj_t].cpu().numpy().astype(np.uint8)
+            t0 = time.perf_counter()
+            Sc, ac, _ = oracle.candidates_forward(Qh, Gh, idx_c, qm, dm, neg, subset=keep,
+                                                  nthreads=threads)
+            dt = time.perf_counter() - t0
+        else:
+            Gc, Gs, Qf = int8
+            Qh = Qf[ub_t].cpu().numpy()
+            Gch = Gc[uj_t].cpu().numpy()
+            Gsh = Gs[uj_t].cpu().numpy()
+            dm = dmask[uj_t].cpu().numpy().astype(np.uint8)
+            t0 = time.perf_counter()
+            Qc, Qs = oracle.quantize_int8(Qh)
+            Sc, ac, _ = oracle.int8_candidates_forward(Qc, Qs, Gch, Gsh, idx_c, qm, dm, neg,
+                                                       subset=keep, nthreads=threads)
+            dt = time.perf_counter() - t0
+        return Sc.reshape(-1)[keep], ac.reshape(-1, ac.shape[-1])[keep], dt
+
+    if args.check:
+        pairs = rng.choice(B * C, size=min(args.check, B * C), replace=False)
+        Sc, ac, _ = run_oracle(pairs, nthreads)
+        Sg = S.reshape(-1)[torch.from_numpy(pairs).to(S.device)].cpu().numpy()
+        ag = args_t.reshape(B * C, -1)[torch.from_numpy(pairs).to(S.device)].cpu().numpy()
+        tol = 2e-3 if (fp16 and int8 is None) else 1e-6
+        ok = np.abs(Sg - Sc) <= tol * np.maximum(1.0, np.abs(Sc))
+        out["check"] = {"pairs": int(len(pairs)), "scores_within_tol": bool(ok.all()),
+                        "max_abs_err": float(np.abs(Sg - Sc).max()),
+                        "tape_agreement": float((ag == ac).mean())}
+        log(f"parity spot check: {out['check']}")
+    if not args.no_cpu:
+        calib = rng.choice(B * C, size=64, replace=False)
+        _, _, dt = run_oracle(calib, nthreads)
+        n = int(max(64, min(B * C, 64 * args.cpu_seconds / max(dt, 1e-6))))
+        pairs = rng.choice(B * C, size=n, replace=False)
+        _, _, dt = run_oracle(pairs, nthreads)
+        out["cpu"] = {"value": n / dt, "unit": "pairs/s", "cores": nthreads, "kind": "port",
+                      "sample": f"{n} random (c,b) pairs of the same workload, "
+                                f"{dt:.1f} s on {nthreads} host threads (C oracle, OpenMP)"}
+        log(f"cpu baseline: {out['cpu']}")
+    return out
+
+
+def run_c5(args, torch, fm, boundary, dev):
+    dim, Lq, Ld, C, B, N = 128, 32, 180, 1000, 256, 1_000_000
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(5)
+    log("c5: generating + quantising gallery (1e6 x 180 x 128) in chunks ...")
+    Gc = torch.empty(N, Ld, dim, dtype=torch.int8, device=dev)
+    Gs = torch.empty(N, Ld, dtype=torch.float32, device=dev)
+    chunk = 20000
+    for a in range(0, N, chunk):
+        b = min(N, a + chunk)
+        x = normalized_randn(torch, (b - a, Ld, dim), gen, torch.float32, dev)
+        boundary.int8_quantize(x, Gc[a:b], Gs[a:b])
+        del x
+    Qf = normalized_randn(torch, (B, Lq, dim), gen, torch.float32, dev)
+    idx = torch.randint(1, N + 1, (B, C), generator=gen, device=dev, dtype=torch.int64)
+    qmask = torch.ones(B, Lq, dtype=torch.bool, device=dev)
+    dmask = torch.ones(N, Ld, dtype=torch.bool, device=dev)
+    args_t = torch.empty(B, C, Lq, dtype=torch.int32, device=dev)
+    S = torch.empty(B, C, dtype=torch.float32, device=dev)
+    Qc = torch.empty(B, Lq, dim, dtype=torch.int8, device=dev)
+    Qs = torch.empty(B, Lq, dtype=torch.float32, device=dev)
+
+    def step():  # on-the-fly query quantisation + INT8 candidate scan
+        boundary.int8_quantize(Qf, Qc, Qs)
+        boundary.launch_int8_candidates_scan(args_t, None, Qc, Qs, Gc, Gs, idx, qmask, dmask, N,
+                                             S, -1.0e4)
+
+    wall, launch_ms = timed_steps(torch, step, args.steps, args.warmup)
+    bytes_per_launch = C * B * (Ld * dim + Ld * 4 + Ld + 4 * Lq + 4) + C * B * 8 + B * Lq * (dim * 5 + 4)
+    res = dict(pairs_per_step=C * B, bytes_per_launch=bytes_per_launch, wall=wall,
+               launch_ms=launch_ms, dtype="int8", bound="hbm",
+               config={"workload": "c5_int8_candidates", "dim": dim, "Lq": Lq, "Ld": Ld, "C": C,
+                       "B": B, "N": N, "idx": "int64", "query": "fp32, quantised per step"})
+    if not args.no_cpu or args.check:
+        res.update(cpu_candidates(args, torch, Qf, None, idx, qmask, dmask, S, args_t, -1.0e4,
+                                  int8=(Gc, Gs, Qf)))
+    return res
+
+
+def run_c3(args, torch, fm, boundary, dev):
+    import numpy as np
+    dim, Lq, Ld, Bq, Bd = 128, 32, 180, 512, 512
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(3)
+    Q = normalized_randn(torch, (Bq, Lq, dim), gen, torch.float16, dev)
+    D = normalized_randn(torch, (Bd, Ld, dim), gen, torch.float16, dev)
+    lens = torch.randint(64, Ld + 1, (Bd,), generator=gen, device=dev)
+    dmask = torch.arange(Ld, device=dev)[None, :] < lens[:, None]
+    qmask = torch.ones(Bq, Lq, dtype=torch.bool, device=dev)
+    S = torch.empty(Bq, Bd, dtype=torch.float32, device=dev)
+    args_t = torch.empty(Bq, Bd, Lq, dtype=torch.int32, device=dev)
+
+    def step():
+        boundary.inbatch_device_scan(S, args_t, Q, D, qmask, dmask)
+
+    wall, launch_ms = timed_steps(torch, step, args.steps, args.warmup)
+    valid_flops = 2 * dim * Lq * Bq * int(lens.sum().item())
+    res = dict(pairs_per_step=Bq * Bd, flops_per_launch=valid_flops, wall=wall,
+               launch_ms=launch_ms, dtype="f16", bound="mfma",
+               padded_flops=2 * dim * Lq * Ld * Bq * Bd,
+               config={"workload": "c3_inbatch_fp16", "dim": dim, "Lq": Lq, "Ld": Ld, "Bq": Bq,
+                       "Bd": Bd, "doc_len": "U[64,180], tail masked"})
+    if not args.no_cpu:
+        import oracle
+        rng = np.random.default_rng(0)
+        nthreads = cpu_threads()
+        Qh = Q.cpu().numpy()
+        Dh = D.cpu().numpy()
+        dm = dmask.cpu().numpy().astype(np.uint8)
+
+        def run(n):
+            ii = rng.integers(0, Bq, n)
+            jj = rng.integers(0, Bd, n)
+            t0 = time.perf_counter()
+            oracle.paired_forward(Qh[ii], Dh[jj], None, dm[jj], nthreads=nthreads)
+            return time.perf_counter() - t0
+        dt = run(256)
+        n = int(max(256, min(Bq * Bd, 256 * args.cpu_seconds / max(dt, 1e-6))))
+        dt = run(n)
+        res["cpu"] = {"value": n / dt, "unit": "pairs/s", "cores": nthreads, "kind": "port",
+                      "sample": f"{n} random (i,j) pairs, {dt:.1f} s on {nthreads} threads"}
+    return res
+
+
+def run_c4(args, torch, fm, boundary, dev, dim=128):
+    import numpy as np
+    Lq, nd, nq = 24, 20_000, 64
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(4)
+    lens = torch.randint(700, 1101, (nd,), generator=gen, device=dev)
+    cu = torch.zeros(nd + 1, dtype=torch.int32, device=dev)
+    cu[1:] = torch.cumsum(lens, 0).to(torch.int32)
+    cu += 1
+    ntok = int(lens.sum().item())
+    log(f"c4: packing {nd} docs, {ntok} tokens, d={dim} bf16 ...")
+    tok = normalized_randn(torch, (ntok, dim), gen, torch.bfloat16, dev, chunk_rows=1 << 20)
+    Qs = normalized_randn(torch, (nq, Lq, dim), gen, torch.bfloat16, dev)
+    S = torch.empty(nq, nd, dtype=torch.float32, device=dev)
+    args_t = torch.empty(nq, nd, Lq, dtype=torch.int32, device=dev)
+
+    def step():  # 64 maxsim(q, P) calls, one per query
+        for i in range(nq):
+            boundary.launch_packed_scan(args_t[i], None, Qs[i], tok, cu, None, S[i])
+
+    wall, launch_ms = timed_steps(torch, step, args.steps, args.warmup)
+    bytes_per_call = ntok * dim * 2 + (nd + 1) * 4 + nd * (4 * Lq + 4) + Lq * dim * 2
+    res = dict(pairs_per_step=nq * nd, bytes_per_launch=bytes_per_call, launches_per_step=nq,
+               wall=wall, launch_ms=launch_ms, dtype="bf16", bound="hbm",
+               config={"workload": f"c4_packed_bf16_d{dim}", "dim": dim, "Lq": Lq, "docs": nd,
+                       "doc_len": "U[700,1100]", "tokens": ntok, "queries": nq})
+    if not args.no_cpu:
+        import oracle
+        rng = np.random.default_rng(0)
+        nthreads = cpu_threads()
+        cu_h = cu.cpu().numpy()
+        q0 = Qs[0].view(torch.int16).cpu().numpy().view(np.uint16)
+
+        def run(n):
+            docs = np.sort(rng.choice(nd, size=n, replace=False))
+            a, z = cu_h[docs] - 1, cu_h[docs + 1] - 1
+            sel = np.concatenate([np.arange(x, y) for x, y in zip(a, z)])
+            t_h = tok[torch.from_numpy(sel).to(dev)].view(torch.int16).cpu().numpy().view(np.uint16)
+            cu_c = np.concatenate([[1], 1 + np.cumsum(z - a)]).astype(np.int32)
+            t0 = time.perf_counter()
+            oracle.packed_forward(q0, t_h, cu_c, None, bf16=True, nthreads=nthreads)
+            return time.perf_counter() - t0
+        dt = run(16)
+        n = int(max(16, min(nd, 16 * args.cpu_seconds / max(dt, 1e-6))))
+        dt = run(n)
+        res["cpu"] = {"value": n / dt, "unit": "pairs/s", "cores": nthreads, "kind": "port",
+                      "sample": f"{n} documents of one query, {dt:.1f} s on {nthreads} threads"}
+    return res
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU only (single-GPU box); "
+                                   "run with --gpus 1", "n_gpus": args.gpus}))
+        sys.exit(2)
+    import torch
+    import flashmaxsim as fm
+    from flashmaxsim import boundary
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    runner = {"c2": run_c2, "c3": run_c3, "c4": run_c4, "c5": run_c5,
+              "c4d1024": lambda *a: run_c4(*a, dim=1024)}[args.workload]
+    r = runner(args, torch, fm, boundary, dev)
+    steps = args.steps
+    wall = r["wall"]
+    pairs = r["pairs_per_step"] * steps
+    launches = r.get("launches_per_step", 1)
+    launch_ms = sorted(r["launch_ms"])
+    avg_launch_s = (sum(launch_ms) / len(launch_ms)) / 1e3 / launches
+    if r["bound"] == "hbm":
+        achieved = r["bytes_per_launch"] / avg_launch_s / 1e9
+        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4)}
+    else:
+        peak = FP16_PEAK_TFLOPS
+        achieved = r["flops_per_launch"] / avg_launch_s / 1e12
+        roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak,
+                "unit": "TFLOP/s", "frac": round(achieved / peak, 4)}
+    roof["traffic"] = None
+    prof = os.path.join(ROOT, "profiles", f"traffic_{args.workload}.json")
+    if os.path.exists(prof):
+        with open(prof) as f:
+            roof["traffic"] = json.load(f).get("hbm_bytes_per_launch")
+    out = {
+        "metric": "MaxSim pairs/sec (Lq32 Ld180 d128 fp16 candidates); % HBM roofline",
+        "value": round(pairs / wall, 1),
+        "unit": "pairs/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall / steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": r["dtype"],
+        "data": "synthetic (seeded randn, L2-normalised tokens, generated on device)",
+        "config": r["config"],
+        "roofline": roof,
+        "cpu_baseline": r.get("cpu"),
+    }
+    if "check" in r:
+        out["parity_check"] = r["check"]
+    if r["bound"] == "mfma":
+        out["roofline"]["padded_tflops"] = round(r["padded_flops"] / avg_launch_s / 1e12, 2)
+    if args.workload != "c2":
+        out["metric"] = f"MaxSim pairs/sec ({r['config']['workload']})"
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

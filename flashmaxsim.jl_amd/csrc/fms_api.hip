@@ -1,0 +1,350 @@
+// fms_api.hip -- the extern "C" boundary of libflashmaxsim_hip.so.
+//
+// Validates shapes / pointers on the host (the reference validates in Julia
+// before every launch: DimensionMismatch in forward_layouts.jl:20-47,
+// forward_pair.jl:14-21, quant.jl:62-94, packed.jl:138-151), picks the
+// kernel and enqueues it on the caller's stream without synchronising.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string.h>
+
+#include "../../include/flashmaxsim_hip.h"
+#include "fms_misc.hpp"
+#include "fms_scan_decl.hpp"
+
+#define FMS_VERSION_STRING "flashmaxsim-hip 0.1.0 (gfx950)"
+
+namespace {
+
+using namespace fms;
+
+constexpr int64_t kMaxSeqBytes = (int64_t)1 << 31;  // one buffer resource per sequence
+constexpr int64_t kMaxTokens = ((int64_t)1 << 31) - 1;
+
+hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+fms_status from_hip(hipError_t e) { return e == hipSuccess ? FMS_OK : FMS_EHIP; }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int elem_bytes(int32_t dtype) {
+  switch (dtype) {
+    case FMS_F32: return 4;
+    case FMS_F16: return 2;
+    case FMS_BF16: return 2;
+    default: return 0;
+  }
+}
+
+// Elements per 16-byte fragment for a stored type (row alignment unit).
+int frag_elems(int esz) { return esz == 4 ? 1 : 16 / esz; }
+
+bool seq_ok(int64_t tokens, int64_t dim, int esz) {
+  return tokens >= 0 && tokens <= kMaxTokens && dim >= 0 && tokens * dim * esz < kMaxSeqBytes;
+}
+
+// Rows are 16-byte multiples and every base is 16-byte aligned: the fast
+// fragment loads apply.  fp32 loads 4 bytes per lane and is always "vec".
+bool vec_ok(int esz, int64_t dim, std::initializer_list<const void*> ptrs) {
+  if (esz == 4) return true;
+  if (dim % frag_elems(esz) != 0) return false;
+  for (const void* p : ptrs)
+    if (p && !aligned16(p)) return false;
+  return true;
+}
+
+template <class L>
+fms_status run_float(int32_t dtype, const L& lay, int dim, int rows, int64_t npairs,
+                     int32_t* args, float* partial, float* scores, float neg, bool vec,
+                     hipStream_t st) {
+  hipError_t e;
+  switch (dtype) {
+    case FMS_F16:
+      e = launch_scan<OpF16, L>(lay, dim, rows, npairs, args, partial, scores, neg, vec, false, st);
+      break;
+    case FMS_BF16:
+      e = launch_scan<OpBF16, L>(lay, dim, rows, npairs, args, partial, scores, neg, vec, false, st);
+      break;
+    case FMS_F32:
+      e = launch_scan<OpF32, L>(lay, dim, rows, npairs, args, partial, scores, neg, vec, false, st);
+      break;
+    default:
+      return FMS_EUNSUPPORTED;
+  }
+  return from_hip(e);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* fms_status_string(fms_status s) {
+  switch (s) {
+    case FMS_OK: return "ok";
+    case FMS_EINVAL: return "invalid argument (shape, NULL pointer or alignment)";
+    case FMS_EUNSUPPORTED: return "unsupported dtype or size";
+    case FMS_EHIP: return "HIP runtime error";
+    default: return "unknown status";
+  }
+}
+
+const char* fms_version(void) { return FMS_VERSION_STRING; }
+
+int fms_arch_supported(void) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return 0;
+  return strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : 0;
+}
+
+fms_status fms_launch_paired_scan(int32_t dtype, int32_t* args, float* partial, const void* Q,
+                                  const void* D, const uint8_t* qmask, const uint8_t* dmask,
+                                  int64_t dim, int64_t Tq, int64_t Td, int64_t B, float* scores,
+                                  void* stream) {
+  const int esz = elem_bytes(dtype);
+  if (esz == 0) return FMS_EUNSUPPORTED;
+  if (dim < 0 || Tq < 0 || Td < 0 || B < 0) return FMS_EINVAL;
+  if (!seq_ok(Tq, dim, esz) || !seq_ok(Td, dim, esz)) return FMS_EUNSUPPORTED;
+  if (B == 0 || (Tq == 0 && !scores)) return FMS_OK;
+  if ((Tq * dim > 0 && !Q) || (Td * dim > 0 && !D)) return FMS_EINVAL;
+  LayPaired lay;
+  lay.Q = static_cast<const char*>(Q);
+  lay.D = static_cast<const char*>(D);
+  lay.qm = qmask;
+  lay.dm = dmask;
+  lay.Qs = nullptr;
+  lay.Ds = nullptr;
+  lay.qbytes = Tq * dim * esz;
+  lay.dbytes = Td * dim * esz;
+  lay.Tq = (int)Tq;
+  lay.Td = (int)Td;
+  return run_float(dtype, lay, (int)dim, (int)Tq, B, args, partial, scores, 0.0f,
+                   vec_ok(esz, dim, {Q, D}), as_stream(stream));
+}
+
+fms_status fms_launch_pair_scan(int32_t dtype, int32_t* argmax_u, float* partial, const void* q,
+                                const void* d, const uint8_t* qmask, const uint8_t* dmask,
+                                int64_t dim, int64_t Tq, int64_t Td, float* score, void* stream) {
+  return fms_launch_paired_scan(dtype, argmax_u, partial, q, d, qmask, dmask, dim, Tq, Td, 1,
+                                score, stream);
+}
+
+fms_status fms_launch_candidates_scan(int32_t dtype, int32_t* args, float* partial,
+                                      const void* Q, const void* gallery, const void* idx,
+                                      int32_t idx_bytes, const uint8_t* qmask,
+                                      const uint8_t* dmask, int64_t dim, int64_t Tq, int64_t B,
+                                      int64_t Td, int64_t N, int64_t C, float* scores, float neg,
+                                      void* stream) {
+  const int esz = elem_bytes(dtype);
+  if (esz == 0) return FMS_EUNSUPPORTED;
+  if (dim < 0 || Tq < 0 || Td < 0 || B < 0 || N < 0 || C < 0) return FMS_EINVAL;
+  if (idx_bytes != 4 && idx_bytes != 8) return FMS_EINVAL;
+  if (!seq_ok(Tq, dim, esz) || !seq_ok(Td, dim, esz)) return FMS_EUNSUPPORTED;
+  if (C == 0 || B == 0 || (Tq == 0 && !scores)) return FMS_OK;
+  if (!idx || (Tq * dim > 0 && !Q) || (N * Td * dim > 0 && !gallery)) return FMS_EINVAL;
+  LayCand lay;
+  lay.Q = static_cast<const char*>(Q);
+  lay.G = static_cast<const char*>(gallery);
+  lay.idx = idx;
+  lay.idx64 = idx_bytes == 8;
+  lay.qm = qmask;
+  lay.dm = dmask;
+  lay.Qs = nullptr;
+  lay.Gs = nullptr;
+  lay.qbytes = Tq * dim * esz;
+  lay.dbytes = Td * dim * esz;
+  lay.N = N;
+  lay.C = C;
+  lay.Tq = (int)Tq;
+  lay.Td = (int)Td;
+  return run_float(dtype, lay, (int)dim, (int)Tq, C * B, args, partial, scores, neg,
+                   vec_ok(esz, dim, {Q, gallery}), as_stream(stream));
+}
+
+fms_status fms_inbatch_device_scan(int32_t dtype, float* S, int32_t* args, const void* Q,
+                                   const void* D, const uint8_t* qmask, const uint8_t* dmask,
+                                   int64_t dim, int64_t Tq, int64_t Bq, int64_t Td, int64_t Bd,
+                                   void* stream) {
+  const int esz = elem_bytes(dtype);
+  if (esz == 0) return FMS_EUNSUPPORTED;
+  if (dim < 0 || Tq < 0 || Td < 0 || Bq < 0 || Bd < 0) return FMS_EINVAL;
+  if (!seq_ok(Tq, dim, esz) || !seq_ok(Td, dim, esz)) return FMS_EUNSUPPORTED;
+  if (Bq == 0 || Bd == 0) return FMS_OK;
+  if (!S || (Tq * dim > 0 && !Q) || (Td * dim > 0 && !D)) return FMS_EINVAL;
+  LayInBatch lay;
+  lay.Q = static_cast<const char*>(Q);
+  lay.D = static_cast<const char*>(D);
+  lay.qm = qmask;
+  lay.dm = dmask;
+  lay.qbytes = Tq * dim * esz;
+  lay.dbytes = Td * dim * esz;
+  lay.Bd = Bd;
+  lay.Tq = (int)Tq;
+  lay.Td = (int)Td;
+  return run_float(dtype, lay, (int)dim, (int)Tq, Bq * Bd, args, nullptr, S, 0.0f,
+                   vec_ok(esz, dim, {Q, D}), as_stream(stream));
+}
+
+fms_status fms_launch_packed_scan(int32_t dtype, int32_t* args, float* partial, const void* q,
+                                  const void* tokens, const int32_t* cu, const uint8_t* qmask,
+                                  int64_t dim, int64_t Tq, int64_t B, int64_t ntokens,
+                                  float* scores, void* stream) {
+  const int esz = elem_bytes(dtype);
+  if (esz == 0) return FMS_EUNSUPPORTED;
+  if (dim < 0 || Tq < 0 || B < 0 || ntokens < 0) return FMS_EINVAL;
+  // Each document gets its own buffer resource; one longer than 2^31 bytes
+  // is truncated to that size on device (LayPacked::get).
+  if (!seq_ok(Tq, dim, esz)) return FMS_EUNSUPPORTED;
+  if (B == 0 || (Tq == 0 && !scores)) return FMS_OK;
+  if (!cu || (Tq * dim > 0 && !q) || (ntokens * dim > 0 && !tokens)) return FMS_EINVAL;
+  LayPacked lay;
+  lay.q = static_cast<const char*>(q);
+  lay.tok = static_cast<const char*>(tokens);
+  lay.cu = cu;
+  lay.qm = qmask;
+  lay.ntok = ntokens;
+  lay.rowbytes = dim * esz;
+  lay.Tq = (int)Tq;
+  return run_float(dtype, lay, (int)dim, (int)Tq, B, args, partial, scores, 0.0f,
+                   vec_ok(esz, dim, {q, tokens}), as_stream(stream));
+}
+
+fms_status fms_launch_varlen_scan(int32_t dtype, int32_t* args, float* partial,
+                                  const void* Qtokens, const void* Dtokens, const int32_t* cu_q,
+                                  const int32_t* cu_d, int64_t dim, int64_t max_q, int64_t N,
+                                  int64_t nq_tokens, int64_t nd_tokens, float* scores,
+                                  void* stream) {
+  const int esz = elem_bytes(dtype);
+  if (esz == 0) return FMS_EUNSUPPORTED;
+  if (dim < 0 || max_q < 0 || N < 0 || nq_tokens < 0 || nd_tokens < 0) return FMS_EINVAL;
+  if (!seq_ok(max_q, dim, esz)) return FMS_EUNSUPPORTED;
+  if (N == 0 || (max_q == 0 && !scores)) return FMS_OK;
+  if (!cu_q || !cu_d || (nq_tokens * dim > 0 && !Qtokens) || (nd_tokens * dim > 0 && !Dtokens))
+    return FMS_EINVAL;
+  LayVarlen lay;
+  lay.Qt = static_cast<const char*>(Qtokens);
+  lay.Dt = static_cast<const char*>(Dtokens);
+  lay.cu_q = cu_q;
+  lay.cu_d = cu_d;
+  lay.nq = nq_tokens;
+  lay.nd = nd_tokens;
+  lay.rowbytes = dim * esz;
+  lay.max_q = (int)max_q;
+  return run_float(dtype, lay, (int)dim, (int)max_q, N, args, partial, scores, 0.0f,
+                   vec_ok(esz, dim, {Qtokens, Dtokens}), as_stream(stream));
+}
+
+fms_status fms_int8_quantize(const float* X, int8_t* codes, float* scales, int64_t dim,
+                             int64_t ntok, void* stream) {
+  if (dim < 0 || ntok < 0 || dim > kMaxTokens) return FMS_EINVAL;
+  if (ntok == 0) return FMS_OK;
+  if (!scales || (dim > 0 && (!X || !codes))) return FMS_EINVAL;
+  return from_hip(quantize_int8(X, codes, scales, (int)dim, ntok, as_stream(stream)));
+}
+
+fms_status fms_launch_int8_paired_scan(int32_t* args, float* partial, const int8_t* Qc,
+                                       const float* Qs, const int8_t* Dc, const float* Ds,
+                                       const uint8_t* qmask, const uint8_t* dmask, int64_t dim,
+                                       int64_t Tq, int64_t Td, int64_t B, float* scores,
+                                       void* stream) {
+  if (dim < 0 || Tq < 0 || Td < 0 || B < 0) return FMS_EINVAL;
+  if (!seq_ok(Tq, dim, 4) || !seq_ok(Td, dim, 4)) return FMS_EUNSUPPORTED;
+  if (B == 0 || (Tq == 0 && !scores)) return FMS_OK;
+  if ((Tq > 0 && (!Qs || (dim > 0 && !Qc))) || (Td > 0 && (!Ds || (dim > 0 && !Dc))))
+    return FMS_EINVAL;
+  LayPaired lay;
+  lay.Q = reinterpret_cast<const char*>(Qc);
+  lay.D = reinterpret_cast<const char*>(Dc);
+  lay.qm = qmask;
+  lay.dm = dmask;
+  lay.Qs = Qs;
+  lay.Ds = Ds;
+  lay.qbytes = Tq * dim;
+  lay.dbytes = Td * dim;
+  lay.Tq = (int)Tq;
+  lay.Td = (int)Td;
+  const bool vec = vec_ok(1, dim, {Qc, Dc});
+  const bool ds_vec = (Td % 4 == 0) && aligned16(Ds);
+  return from_hip(launch_scan<OpI8, LayPaired>(lay, (int)dim, (int)Tq, B, args, partial, scores,
+                                               0.0f, vec, ds_vec, as_stream(stream)));
+}
+
+fms_status fms_launch_int8_pair_scan(int32_t* args, float* partial, const int8_t* qc,
+                                     const float* qs, const int8_t* dc, const float* ds,
+                                     const uint8_t* qmask, const uint8_t* dmask, int64_t dim,
+                                     int64_t Tq, int64_t Td, float* score, void* stream) {
+  return fms_launch_int8_paired_scan(args, partial, qc, qs, dc, ds, qmask, dmask, dim, Tq, Td, 1,
+                                     score, stream);
+}
+
+fms_status fms_launch_int8_candidates_scan(int32_t* args, float* partial, const int8_t* Qc,
+                                           const float* Qs, const int8_t* Gc, const float* Gs,
+                                           const void* idx, int32_t idx_bytes,
+                                           const uint8_t* qmask, const uint8_t* dmask,
+                                           int64_t dim, int64_t Tq, int64_t B, int64_t Td,
+                                           int64_t N, int64_t C, float* scores, float neg,
+                                           void* stream) {
+  if (dim < 0 || Tq < 0 || Td < 0 || B < 0 || N < 0 || C < 0) return FMS_EINVAL;
+  if (idx_bytes != 4 && idx_bytes != 8) return FMS_EINVAL;
+  if (!seq_ok(Tq, dim, 4) || !seq_ok(Td, dim, 4)) return FMS_EUNSUPPORTED;
+  if (C == 0 || B == 0 || (Tq == 0 && !scores)) return FMS_OK;
+  if (!idx || (Tq > 0 && (!Qs || (dim > 0 && !Qc))) ||
+      (N * Td > 0 && (!Gs || (dim > 0 && !Gc))))
+    return FMS_EINVAL;
+  LayCand lay;
+  lay.Q = reinterpret_cast<const char*>(Qc);
+  lay.G = reinterpret_cast<const char*>(Gc);
+  lay.idx = idx;
+  lay.idx64 = idx_bytes == 8;
+  lay.qm = qmask;
+  lay.dm = dmask;
+  lay.Qs = Qs;
+  lay.Gs = Gs;
+  lay.qbytes = Tq * dim;
+  lay.dbytes = Td * dim;
+  lay.N = N;
+  lay.C = C;
+  lay.Tq = (int)Tq;
+  lay.Td = (int)Td;
+  const bool vec = vec_ok(1, dim, {Qc, Gc});
+  const bool ds_vec = (Td % 4 == 0) && aligned16(Gs);
+  return from_hip(launch_scan<OpI8, LayCand>(lay, (int)dim, (int)Tq, C * B, args, partial, scores,
+                                             neg, vec, ds_vec, as_stream(stream)));
+}
+
+fms_status fms_int8_dots(int32_t* out, const int8_t* qc, const int8_t* dc, int64_t dim,
+                         int64_t Tq, int64_t Td, void* stream) {
+  if (dim < 0 || Tq < 0 || Td < 0) return FMS_EINVAL;
+  if (!seq_ok(Tq, dim, 1) || !seq_ok(Td, dim, 1) || Tq * Td >= kMaxSeqBytes)
+    return FMS_EUNSUPPORTED;
+  if (Tq == 0 || Td == 0) return FMS_OK;
+  if (!out || (dim > 0 && (!qc || !dc))) return FMS_EINVAL;
+  return from_hip(int8_dots(out, qc, dc, (int)dim, (int)Tq, (int)Td, vec_ok(1, dim, {qc, dc}),
+                            as_stream(stream)));
+}
+
+fms_status fms_length_normalize(float* scores, const uint8_t* qmask, int64_t Tq, int64_t nrows,
+                                int64_t ncols, const void* idx, int32_t idx_bytes, int64_t N,
+                                float neg, void* stream) {
+  if (Tq < 0 || nrows < 0 || ncols < 0 || N < 0 || ncols > kMaxTokens) return FMS_EINVAL;
+  if (idx && idx_bytes != 4 && idx_bytes != 8) return FMS_EINVAL;
+  if (nrows == 0 || ncols == 0) return FMS_OK;
+  if (!scores) return FMS_EINVAL;
+  return from_hip(length_normalize(scores, qmask, Tq, nrows, ncols, idx, idx_bytes == 8, N, neg,
+                                   as_stream(stream)));
+}
+
+fms_status fms_varlen_normalize(float* scores, const int32_t* cu_q, int64_t N, void* stream) {
+  if (N < 0) return FMS_EINVAL;
+  if (N == 0) return FMS_OK;
+  if (!scores || !cu_q) return FMS_EINVAL;
+  return from_hip(varlen_normalize(scores, cu_q, N, as_stream(stream)));
+}
+
+fms_status fms_debug_mfma_layout(float* out, int32_t dtype_or_int8, void* stream) {
+  if (!out || dtype_or_int8 < 0 || dtype_or_int8 > 3) return FMS_EINVAL;
+  return from_hip(mfma_layout_probe(out, dtype_or_int8, as_stream(stream)));
+}
+
+}  // extern "C"

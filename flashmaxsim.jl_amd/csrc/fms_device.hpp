@@ -1,0 +1,197 @@
+// fms_device.hpp -- gfx950 device building blocks shared by every MaxSim scan.
+//
+// Tiling (CDNA4, wave64):
+//   One MFMA 32x32xK instruction per k-block multiplies a 32-token document
+//   chunk (A operand: row i = document token) by a 32-token query tile
+//   (B operand: column j = query token).  The fp32/int32 result lives in 16
+//   accumulator registers per lane:
+//       lane l, register r  <->  row 8*(r/4) + 4*(l/32) + r%4,  column l%32
+//   so every lane owns ONE query token (column) and 16 document tokens of
+//   the chunk, and the per-query-token running max / argmax is a private
+//   per-lane scan; lanes l and l^32 are merged once per (pair, query tile).
+//
+// Operand fragments: lane l supplies row/column l%32 and k-slots
+//   [kb*KB + (l/32)*EPL, +EPL) of k-block kb.  The same slot mapping is used
+//   for A and B, so each MFMA sums whole dot products over its KB k values.
+//
+// Loads go through raw buffer resources (one per document / query / mask),
+// which makes every read past the end of a sequence return zero instead of
+// touching memory: ragged tails need no guards and cannot fault.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fms {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+constexpr int kTile = 32;      // query tokens per tile == document tokens per chunk
+constexpr int kWaves = 4;      // waves per workgroup for the scan kernels
+constexpr int kRsrcWord3 = 0x00020000;  // gfx9-family raw buffer descriptor word 3
+
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kRsrcWord3);
+}
+
+__device__ __forceinline__ u32x4 buf_load16(rsrc_t r, int voff) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0));
+}
+// Four fp32 values.  Bit-cast the whole 128-bit result before extracting
+// lanes: extracting i32 elements first and bit-casting each to float makes
+// this compiler (ROCm 7.2 clang, -O3) shrink the load to a single dword and
+// broadcast it to all four elements.
+__device__ __forceinline__ f32x4 buf_load16f(rsrc_t r, int voff) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0));
+}
+__device__ __forceinline__ uint32_t buf_load4(rsrc_t r, int voff) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, voff, 0, 0);
+}
+__device__ __forceinline__ uint32_t buf_load2(rsrc_t r, int voff) {
+  return __builtin_amdgcn_raw_buffer_load_b16(r, voff, 0, 0);
+}
+__device__ __forceinline__ uint32_t buf_load1(rsrc_t r, int voff) {
+  return __builtin_amdgcn_raw_buffer_load_b8(r, voff, 0, 0);
+}
+
+// ---- MFMA operand traits ------------------------------------------------------
+// kEsz: bytes per stored element; kEpl: elements per lane per k-block;
+// kKb: k values per MFMA (two lane halves x kEpl); Frag: raw register image
+// of one lane's operand; Acc: 16-register accumulator.
+
+struct OpF16 {
+  static constexpr int kEsz = 2, kEpl = 8, kKb = 16;
+  static constexpr bool kInt = false;
+  typedef u32x4 Frag;
+  typedef f32x16 Acc;
+  __device__ static Frag zero() { return u32x4{0u, 0u, 0u, 0u}; }
+  __device__ static Frag load(rsrc_t r, int voff) { return buf_load16(r, voff); }
+  __device__ static Acc mma(Frag a, Frag b, Acc c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  // Element-wise guarded load (dim not a multiple of kEpl): elements with
+  // k >= dim are zero.  `voff` addresses element k0 of the row.
+  __device__ static Frag load_guarded(rsrc_t r, int voff, int k0, int dim) {
+    uint32_t w[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      uint32_t lo = (k0 + 2 * e < dim) ? buf_load2(r, voff + 4 * e) : 0u;
+      uint32_t hi = (k0 + 2 * e + 1 < dim) ? buf_load2(r, voff + 4 * e + 2) : 0u;
+      w[e] = (lo & 0xffffu) | (hi << 16);
+    }
+    return u32x4{w[0], w[1], w[2], w[3]};
+  }
+};
+
+struct OpBF16 : OpF16 {
+  __device__ static Acc mma(Frag a, Frag b, Acc c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+};
+
+struct OpI8 {
+  static constexpr int kEsz = 1, kEpl = 16, kKb = 32;
+  static constexpr bool kInt = true;
+  typedef u32x4 Frag;
+  typedef i32x16 Acc;
+  __device__ static Frag zero() { return u32x4{0u, 0u, 0u, 0u}; }
+  __device__ static Frag load(rsrc_t r, int voff) { return buf_load16(r, voff); }
+  __device__ static Acc mma(Frag a, Frag b, Acc c) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, a),
+                                                 __builtin_bit_cast(i32x4, b), c, 0, 0, 0);
+  }
+  __device__ static Frag load_guarded(rsrc_t r, int voff, int k0, int dim) {
+    uint32_t w[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      uint32_t acc = 0u;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        uint32_t v = (k0 + 4 * e + b < dim) ? buf_load1(r, voff + 4 * e + b) : 0u;
+        acc |= (v & 0xffu) << (8 * b);
+      }
+      w[e] = acc;
+    }
+    return u32x4{w[0], w[1], w[2], w[3]};
+  }
+};
+
+struct OpF32 {
+  static constexpr int kEsz = 4, kEpl = 1, kKb = 2;
+  static constexpr bool kInt = false;
+  typedef uint32_t Frag;
+  typedef f32x16 Acc;
+  __device__ static Frag zero() { return 0u; }
+  __device__ static Frag load(rsrc_t r, int voff) { return buf_load4(r, voff); }
+  __device__ static Acc mma(Frag a, Frag b, Acc c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(__builtin_bit_cast(float, a),
+                                                __builtin_bit_cast(float, b), c, 0, 0, 0);
+  }
+  __device__ static Frag load_guarded(rsrc_t r, int voff, int k0, int dim) {
+    return (k0 < dim) ? buf_load4(r, voff) : 0u;
+  }
+};
+
+// Document row (within a 32-token chunk) held by accumulator register r of
+// a lane in half h (= lane / 32).
+__device__ __forceinline__ constexpr int acc_row(int r, int h) {
+  return 8 * (r >> 2) + 4 * h + (r & 3);
+}
+
+// Running (max, slot) update over one chunk's 16 scores of this lane.
+// slot = chunk*16 + r identifies (chunk, register) until the final merge.
+// A score replaces the running max only when strictly greater, and the
+// running max starts at -inf, so the first valid document token wins and
+// ties keep the lowest token (forward_pair.jl:140-143).  `rowbits` has bit
+// (8*(r/4) + r%4) set for valid registers of this lane (already shifted by
+// 4*h); ALL_VALID skips the mask test.
+template <bool ALL_VALID>
+__device__ __forceinline__ void running_max(const float (&s)[16], uint32_t rowbits, int slot0,
+                                            float& mx, int& slot) {
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int bit = 8 * (r >> 2) + (r & 3);
+    bool take = s[r] > mx;
+    if (!ALL_VALID) take = take && ((rowbits >> bit) & 1u);
+    mx = take ? s[r] : mx;
+    slot = take ? slot0 + r : slot;
+  }
+}
+
+// 1-based document token of a slot for a lane in half h; 0 = none.
+__device__ __forceinline__ int slot_to_token(int slot, int h) {
+  return slot < 0 ? 0 : (slot >> 4) * kTile + acc_row(slot & 15, h) + 1;
+}
+
+// Merge the (max, token) of lanes l and l^32, which hold disjoint document
+// rows of the same query token.  Equal maxima keep the lower token, matching
+// a sequential ascending scan.
+__device__ __forceinline__ void merge_halves(float& mx, int& tok) {
+  const float omx = __shfl_xor(mx, 32);
+  const int otok = __shfl_xor(tok, 32);
+  const bool take = otok != 0 && (tok == 0 || omx > mx || (omx == mx && otok < tok));
+  mx = take ? omx : mx;
+  tok = take ? otok : tok;
+}
+
+// Sum over the 32 lanes of each wave half (after merge_halves both halves
+// hold the same 32 per-token partials, so either half's sum is the score).
+__device__ __forceinline__ float half_sum(float v) {
+#pragma unroll
+  for (int o = 16; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+}  // namespace fms

@@ -1,0 +1,19 @@
+// fms_misc.hpp -- host launchers of the small kernels in fms_misc.hip.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fms {
+
+hipError_t quantize_int8(const float* X, int8_t* codes, float* scales, int dim, int64_t ntok,
+                         hipStream_t stream);
+hipError_t int8_dots(int32_t* out, const int8_t* qc, const int8_t* dc, int dim, int Tq, int Td,
+                     bool vec, hipStream_t stream);
+hipError_t length_normalize(float* scores, const uint8_t* qmask, int64_t Tq, int64_t nrows,
+                            int64_t ncols, const void* idx, int idx64, int64_t N, float neg,
+                            hipStream_t stream);
+hipError_t varlen_normalize(float* scores, const int32_t* cu_q, int64_t N, hipStream_t stream);
+hipError_t mfma_layout_probe(float* out, int op, hipStream_t stream);
+
+}  // namespace fms

@@ -1,0 +1,37 @@
+"""flashmaxsim -- host mirror of FlashMaxSim.jl's forward API over the MI355X library.
+
+Every score is computed by libflashmaxsim_hip.so (hand-written gfx950 HIP
+kernels) through its C ABI; this package only validates arguments, allocates
+outputs on the device and enqueues the kernels on the current torch stream.
+There is no CPU path: host tensors raise ``ArgumentError``.
+
+Array convention: a Julia array of size ``(a, b, c)`` (column-major) is the
+torch tensor of shape ``(c, b, a)`` (row-major) -- the same bytes.  So
+``Q::(dim, Tq, B)`` is ``Q.shape == (B, Tq, dim)``, masks ``(Tq, B)`` are
+``(B, Tq)``, candidate indices ``(C, B)`` are ``(B, C)`` (1-based), and tapes
+``(Tq, C, B)`` are ``(B, C, Tq)``.
+"""
+from .api import AtomicUnified, InBatch, InvGrid, MaxSim, dot_accum, maxsim, score_eltype
+from .boundary import (inbatch_device_scan, launch_candidates_scan, launch_int8_candidates_scan,
+                       launch_int8_pair_scan, launch_int8_paired_scan, launch_packed_scan,
+                       launch_pair_scan, launch_paired_scan, launch_varlen_scan,
+                       tensor_cores_active)
+from .errors import ArgumentError, DimensionMismatch, HIPError, UnsupportedError
+from .forward import (candidates_forward, inbatch_forward, int8_candidates_forward,
+                      int8_pair_forward, int8_paired_forward, packed_forward, paired_forward,
+                      pair_forward, varlen_forward)
+from .packed import PackedSeq, nseq, pack_docs, pack_pairs
+from .quant import Int8Index, dequant_int8, quantize_int8_symmetric
+
+__all__ = [
+    "maxsim", "MaxSim", "InBatch", "AtomicUnified", "InvGrid", "score_eltype", "dot_accum",
+    "PackedSeq", "nseq", "pack_docs", "pack_pairs",
+    "Int8Index", "quantize_int8_symmetric", "dequant_int8",
+    "pair_forward", "paired_forward", "inbatch_forward", "candidates_forward",
+    "packed_forward", "varlen_forward", "int8_pair_forward", "int8_paired_forward",
+    "int8_candidates_forward",
+    "launch_pair_scan", "launch_paired_scan", "launch_candidates_scan", "inbatch_device_scan",
+    "launch_packed_scan", "launch_varlen_scan", "launch_int8_pair_scan",
+    "launch_int8_paired_scan", "launch_int8_candidates_scan", "tensor_cores_active",
+    "ArgumentError", "DimensionMismatch", "HIPError", "UnsupportedError",
+]

@@ -1,0 +1,282 @@
+"""Layout drivers: allocate outputs, call the boundary, finalize.
+
+Each ``*_forward`` mirrors the reference's device driver ``*_forward_ka``
+(outputs allocated with zeros_like, one scan launch, scores kept on device)
+and returns ``(scores, argmax_tape)``.  Σ_t and the candidate ``neg`` fill
+are fused into the scan kernel (the reference runs ``sum(partial; dims=1)``
+and ``ifelse.(valid, S, neg)`` as separate device kernels).
+
+Shapes follow the package convention (Julia ``(a, b, c)`` is torch
+``(c, b, a)``): a paired tape Julia ``(Tq, B)`` is ``(B, Tq)``, a candidate
+score matrix ``(C, B)`` is ``(B, C)``, an in-batch ``S (Bd, Bq)`` is
+``(Bq, Bd)``.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import boundary
+from .errors import DimensionMismatch
+from .packed import PackedSeq
+from .quant import Int8Index, quantize_int8_symmetric, require_int8_index
+
+SCORE_DTYPE = torch.float32
+
+
+def _zeros(like: torch.Tensor, dtype, *shape):
+    return torch.zeros(shape, dtype=dtype, device=like.device)
+
+
+# ---- shape checks (DimensionMismatch, as in the reference) ---------------------------
+
+def require_pair_shapes(q, d, qmask, dmask):
+    """forward_pair.jl:14-21."""
+    if q.dim() != 2 or d.dim() != 2:
+        raise DimensionMismatch("pair features must be (T, dim)")
+    Tq, dim = q.shape
+    Td = d.shape[0]
+    if d.shape[1] != dim:
+        raise DimensionMismatch("feature dim")
+    if qmask is not None and qmask.numel() != Tq:
+        raise DimensionMismatch("qmask")
+    if dmask is not None and dmask.numel() != Td:
+        raise DimensionMismatch("dmask")
+    return dim, Tq, Td
+
+
+def require_paired_shapes(Q, D, qmask, dmask):
+    """forward_layouts.jl:20-28."""
+    B, Tq, dim = Q.shape
+    Td = D.shape[1]
+    if D.shape[2] != dim:
+        raise DimensionMismatch("feature dim")
+    if D.shape[0] != B:
+        raise DimensionMismatch("batch")
+    if qmask is not None and tuple(qmask.shape) != (B, Tq):
+        raise DimensionMismatch("qmask")
+    if dmask is not None and tuple(dmask.shape) != (B, Td):
+        raise DimensionMismatch("dmask")
+    return dim, Tq, Td, B
+
+
+def require_inbatch_shapes(Q, D, qmask, dmask):
+    """forward_layouts.jl:30-37."""
+    Bq, Tq, dim = Q.shape
+    Bd, Td = D.shape[0], D.shape[1]
+    if D.shape[2] != dim:
+        raise DimensionMismatch("feature dim")
+    if qmask is not None and tuple(qmask.shape) != (Bq, Tq):
+        raise DimensionMismatch("qmask")
+    if dmask is not None and tuple(dmask.shape) != (Bd, Td):
+        raise DimensionMismatch("dmask")
+    return dim, Tq, Bq, Td, Bd
+
+
+def require_candidates_shapes(Q, gallery, idxs, qmask, dmask):
+    """forward_layouts.jl:39-47."""
+    B, Tq, dim = Q.shape
+    N, Td = gallery.shape[0], gallery.shape[1]
+    if gallery.shape[2] != dim:
+        raise DimensionMismatch("feature dim")
+    if idxs.dim() != 2 or idxs.shape[0] != B:
+        raise DimensionMismatch("idxs")
+    if qmask is not None and tuple(qmask.shape) != (B, Tq):
+        raise DimensionMismatch("qmask")
+    if dmask is not None and tuple(dmask.shape) != (N, Td):
+        raise DimensionMismatch("dmask")
+    return dim, Tq, B, Td, N
+
+
+def indices_on(prototype: torch.Tensor, idxs: torch.Tensor) -> torch.Tensor:
+    """indices_on (ka.jl:41-46): refuse a host->device copy of idxs in the hot path."""
+    if idxs.device != prototype.device:
+        from .errors import ArgumentError
+        raise ArgumentError(
+            "FlashMaxSim requires idxs on the same KernelAbstractions backend as features "
+            "(e.g. idxs.to('cuda')); refusing a host→device copy in the hot path")
+    return idxs
+
+
+# ---- forward drivers ---------------------------------------------------------------------
+
+def pair_forward(q, d, qmask=None, dmask=None, neg=None):
+    """pair_forward_ka (forward_pair.jl:155-174): (score (1,), argmax_u (Tq,))."""
+    boundary.require_device(q, d, qmask, dmask)
+    _, Tq, _ = require_pair_shapes(q, d, qmask, dmask)
+    argmax_u = _zeros(q, torch.int32, Tq)
+    partial = _zeros(q, SCORE_DTYPE, Tq)
+    score = _zeros(q, SCORE_DTYPE, 1)
+    boundary.launch_pair_scan(argmax_u, partial, q, d, qmask, dmask, score)
+    return score, argmax_u
+
+
+def paired_forward(Q, D, qmask=None, dmask=None, neg=None):
+    """paired_forward_ka (forward_layouts.jl:112-124): (scores (B,), args (B,Tq))."""
+    boundary.require_device(Q, D, qmask, dmask)
+    _, Tq, _, B = require_paired_shapes(Q, D, qmask, dmask)
+    args = _zeros(Q, torch.int32, B, Tq)
+    scores = _zeros(Q, SCORE_DTYPE, B)
+    boundary.launch_paired_scan(args, None, Q, D, qmask, dmask, scores)
+    return scores, args
+
+
+def inbatch_forward(Q, D, qmask=None, dmask=None, neg=None):
+    """inbatch_forward_ka (forward_layouts.jl:188-200): (S (Bq,Bd), args (Bq,Bd,Tq))."""
+    boundary.require_device(Q, D, qmask, dmask)
+    _, Tq, Bq, Td, Bd = require_inbatch_shapes(Q, D, qmask, dmask)
+    S = _zeros(Q, SCORE_DTYPE, Bq, Bd)
+    args = _zeros(Q, torch.int32, Bq, Bd, Tq)
+    if Bd == 0 or Bq == 0 or Tq == 0 or Td == 0:
+        return S, args
+    boundary.inbatch_device_scan(S, args, Q, D, qmask, dmask)
+    return S, args
+
+
+def candidates_forward(Q, gallery, idxs, qmask=None, dmask=None, neg=-1.0e4):
+    """candidates_forward_ka (forward_layouts.jl:272-290): (S (B,C), args (B,C,Tq))."""
+    boundary.require_device(Q, gallery, qmask, dmask)
+    _, Tq, B, _, N = require_candidates_shapes(Q, gallery, idxs, qmask, dmask)
+    idx = indices_on(Q, idxs)
+    C = idx.shape[1]
+    args = _zeros(Q, torch.int32, B, C, Tq)
+    S = _zeros(Q, SCORE_DTYPE, B, C)
+    boundary.launch_candidates_scan(args, None, Q, gallery, idx, qmask, dmask, N, S, neg)
+    return S, args
+
+
+def packed_forward(q, P: PackedSeq, qmask=None, neg=None):
+    """packed_forward_ka (packed.jl:191-202): (scores (B,), args (B,Tq))."""
+    boundary.require_device(q, P.tokens, P.cu, qmask)
+    Tq = q.shape[0]
+    if P.tokens.shape[1] != q.shape[1]:
+        raise DimensionMismatch("feature dim")
+    if qmask is not None and qmask.numel() != Tq:
+        raise DimensionMismatch("qmask")
+    B = P.nseq()
+    args = _zeros(q, torch.int32, B, Tq)
+    scores = _zeros(q, SCORE_DTYPE, B)
+    boundary.launch_packed_scan(args, None, q, P.tokens, P.cu, qmask, scores)
+    return scores, args
+
+
+def varlen_forward(Qp: PackedSeq, Dp: PackedSeq, neg=None):
+    """varlen_forward_ka (packed.jl:274-284): (scores (N,), args (N,max_q))."""
+    boundary.require_device(Qp.tokens, Dp.tokens, Qp.cu, Dp.cu)
+    N = Qp.nseq()
+    if N != Dp.nseq():
+        raise DimensionMismatch("varlen pair count")
+    if Qp.tokens.shape[1] != Dp.tokens.shape[1]:
+        raise DimensionMismatch("feature dim")
+    max_q = Qp.max_len
+    args = _zeros(Qp.tokens, torch.int32, N, max_q)
+    scores = _zeros(Qp.tokens, SCORE_DTYPE, N)
+    boundary.launch_varlen_scan(args, None, Qp.tokens, Dp.tokens, Qp.cu, Dp.cu, scores)
+    return scores, args
+
+
+def int8_pair_forward(q, d: Int8Index, qmask=None, dmask=None):
+    """int8_pair_forward (quant.jl:156-170): quantise q on device, then the INT8 scan."""
+    qq = quantize_int8_symmetric(q)
+    require_int8_index(d)
+    boundary.require_device(q, qq.codes, qq.scales, d.codes, d.scales, qmask, dmask)
+    Tq, dim = qq.codes.shape
+    Td = d.codes.shape[0]
+    if d.codes.shape[1] != dim:
+        raise DimensionMismatch("feature dim")
+    if d.scales.numel() != Td:
+        raise DimensionMismatch("document scales")
+    if qmask is not None and qmask.numel() != Tq:
+        raise DimensionMismatch("qmask")
+    if dmask is not None and dmask.numel() != Td:
+        raise DimensionMismatch("dmask")
+    args = _zeros(q, torch.int32, Tq)
+    score = _zeros(q, SCORE_DTYPE, 1)
+    boundary.launch_int8_pair_scan(args, None, qq.codes, qq.scales, d.codes, d.scales, qmask,
+                                   dmask, score)
+    return score, args
+
+
+def int8_paired_forward(Q, D: Int8Index, qmask=None, dmask=None):
+    """int8_paired_forward (quant.jl:219-226)."""
+    QQ = quantize_int8_symmetric(Q)
+    require_int8_index(D)
+    boundary.require_device(Q, QQ.codes, QQ.scales, D.codes, D.scales, qmask, dmask)
+    B, Tq, dim = QQ.codes.shape
+    Td = D.codes.shape[1]
+    if D.codes.shape[2] != dim:
+        raise DimensionMismatch("feature dim")
+    if D.codes.shape[0] != B:
+        raise DimensionMismatch("batch")
+    if tuple(D.scales.shape) != (B, Td):
+        raise DimensionMismatch("document scales")
+    if qmask is not None and tuple(qmask.shape) != (B, Tq):
+        raise DimensionMismatch("qmask")
+    if dmask is not None and tuple(dmask.shape) != (B, Td):
+        raise DimensionMismatch("dmask")
+    args = _zeros(Q, torch.int32, B, Tq)
+    scores = _zeros(Q, SCORE_DTYPE, B)
+    boundary.launch_int8_paired_scan(args, None, QQ.codes, QQ.scales, D.codes, D.scales, qmask,
+                                     dmask, scores)
+    return scores, args
+
+
+def int8_candidates_forward(Q, G: Int8Index, idxs, qmask=None, dmask=None, neg=-1.0e4):
+    """INT8 candidate layout (no reference method): quantised Q_b vs gallery[idxs[c,b]]."""
+    QQ = quantize_int8_symmetric(Q)
+    boundary.require_device(Q, QQ.codes, QQ.scales, G.codes, G.scales, qmask, dmask)
+    B, Tq, dim = QQ.codes.shape
+    N, Td = G.codes.shape[0], G.codes.shape[1]
+    if G.codes.shape[2] != dim:
+        raise DimensionMismatch("feature dim")
+    if tuple(G.scales.shape) != (N, Td):
+        raise DimensionMismatch("document scales")
+    if idxs.dim() != 2 or idxs.shape[0] != B:
+        raise DimensionMismatch("idxs")
+    if qmask is not None and tuple(qmask.shape) != (B, Tq):
+        raise DimensionMismatch("qmask")
+    if dmask is not None and tuple(dmask.shape) != (N, Td):
+        raise DimensionMismatch("dmask")
+    idx = indices_on(Q, idxs)
+    C = idx.shape[1]
+    args = _zeros(Q, torch.int32, B, C, Tq)
+    S = _zeros(Q, SCORE_DTYPE, B, C)
+    boundary.launch_int8_candidates_scan(args, None, QQ.codes, QQ.scales, G.codes, G.scales, idx,
+                                         qmask, dmask, N, S, neg)
+    return S, args
+
+
+# ---- finalize (normalize.jl, forward_pair.jl:153-173, packed.jl:316-354) ------------------
+
+def length_normalize(scores, qmask, Tq):
+    """scores (ncols,) or (ncols, nrows) with one query per column; returns a new tensor."""
+    out = scores.clone()
+    ncols = out.shape[0] if out.dim() >= 1 else 1
+    nrows = out.numel() // max(ncols, 1)
+    boundary.length_normalize_(out, qmask, Tq, nrows, ncols)
+    return out
+
+
+def length_normalize_candidates(S, qmask, Tq, idxs, N, neg):
+    """length_normalize_candidates (normalize.jl:28-46): invalid idx keep neg."""
+    out = S.clone()
+    B, C = out.shape
+    boundary.length_normalize_(out, qmask, Tq, C, B, idxs, N, neg)
+    return out
+
+
+def packed_finalize(scores, qmask, Tq, normalize: bool):
+    """packed_finalize (packed.jl:333-337): one query count scales every document."""
+    if not normalize:
+        return scores
+    out = scores.clone()
+    boundary.length_normalize_(out, qmask, Tq, out.numel(), 1)
+    return out
+
+
+def varlen_finalize(scores, Qp: PackedSeq, normalize: bool):
+    """varlen_finalize (packed.jl:351-354): scores[n] *= 1/max(Tq_n, 1)."""
+    if not normalize:
+        return scores
+    out = scores.clone()
+    boundary.varlen_normalize_(out, Qp.cu)
+    return out

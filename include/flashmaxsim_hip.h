@@ -1,0 +1,244 @@
+/*
+ * flashmaxsim_hip.h -- C ABI of libflashmaxsim_hip.so, the MI355X (gfx950)
+ * implementation of FlashMaxSim.jl's fused MaxSim forward.
+ *
+ * Each entry point replaces one method of the reference's device plugin
+ * boundary (the `launch_*_scan!` / `inbatch_device_scan!` generic functions
+ * that a weak-dependency extension specialises per backend; the CUDA
+ * extension overrides them in ext/FlashMaxSimCUDAExt.jl:57-167).  A Julia
+ * AMDGPU.jl extension binds them with `ccall` (INTEGRATION.md shows the
+ * binding); the Python host mirror in flashmaxsim.jl_amd/flashmaxsim binds
+ * them with ctypes.
+ *
+ * Conventions (all from the reference):
+ *   - Column-major (Julia) layout.  A feature array of Julia size
+ *     (dim, T, B) has element (k, t, b) at k + dim*(t + T*b).  Tokens are
+ *     therefore contiguous `dim`-vectors.
+ *   - Outputs first; the caller owns every buffer (zeros_like, ka.jl:28-30).
+ *     The library keeps no pointer after the call returns.
+ *   - Asynchronous: work is enqueued on `stream` (a hipStream_t; NULL = the
+ *     legacy default stream).  No host synchronisation (ka.jl:3-5,10-15).
+ *   - Argmax tapes are int32, 1-based, 0 = no valid document token.
+ *     partial[t] is the per-query-token max (0 for a masked query token or
+ *     an empty / fully masked document), exactly like the reference's
+ *     `partial` buffer (kernels_forward.jl:55).
+ *   - Masks are Bool bytes (0 = false, nonzero = true); NULL = all true
+ *     (what true_mask allocates, colocation.jl:4-6).
+ *   - Fused epilogue (an extension over the reference boundary, which leaves
+ *     Sigma_t to a later `sum(partial; dims=1)`): when `scores` is non-NULL
+ *     the kernel also writes scores[p] = Sigma_t partial[t,p] (fp32), and for
+ *     the candidate layouts an invalid index writes `neg` there, fusing
+ *     forward_layouts.jl:285-287.  `partial` and `args` may be NULL when not
+ *     wanted.
+ *   - Zero-size inputs return FMS_OK without launching (ka.jl:12); an empty
+ *     document (Td = 0 or cu[b+1] = cu[b]) still writes zeros.
+ *   - Kernels never trap: an out-of-range candidate index yields tape 0 /
+ *     partial 0 / score `neg`; a malformed device cu is clamped into the
+ *     token range (the reference trusts device cu, packed.jl:65-67).
+ *   - Scores accumulate in fp32 for every feature type (f16/bf16 products
+ *     are exact in fp32; int8 dots accumulate exactly in int32).
+ *
+ * Reentrant: no global mutable state; concurrent calls on different streams
+ * are independent.
+ */
+#ifndef FLASHMAXSIM_HIP_H
+#define FLASHMAXSIM_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef int32_t fms_status;
+#define FMS_OK 0
+#define FMS_EINVAL 1       /* bad shape, NULL required pointer, misaligned buffer */
+#define FMS_EUNSUPPORTED 2 /* dtype / size the library does not implement */
+#define FMS_EHIP 3         /* a HIP runtime call or kernel launch failed */
+
+/* Feature element types.  BF16 has no reference counterpart on device (the
+ * reference's dot_accum(BFloat16) = BFloat16); here it accumulates in fp32. */
+#define FMS_F32 0
+#define FMS_F16 1
+#define FMS_BF16 2
+
+/* Human-readable text for a status code (static storage). */
+const char* fms_status_string(fms_status s);
+
+/* 1 when the current HIP device is gfx950 (the only target built), else 0.
+ * Plays the role of tensor_cores_active(backend, T) (src/ka.jl:71). */
+int fms_arch_supported(void);
+
+/* Library version string. */
+const char* fms_version(void);
+
+/*
+ * Pair scan.  Replaces launch_pair_scan!(backend, argmax_u, partial, q, d,
+ * qmask, dmask) (src/forward_pair.jl:176-190; CUDA override
+ * ext/FlashMaxSimCUDAExt.jl:57-68).  q is (dim,Tq), d is (dim,Td);
+ * argmax_u/partial are (Tq,).  score (nullable, length 1) receives Sigma_t,
+ * replacing sum_length1 (src/ka.jl:49-53).
+ */
+fms_status fms_launch_pair_scan(int32_t dtype, int32_t* argmax_u, float* partial,
+                                const void* q, const void* d,
+                                const uint8_t* qmask, const uint8_t* dmask,
+                                int64_t dim, int64_t Tq, int64_t Td,
+                                float* score, void* stream);
+
+/*
+ * Paired-batch scan.  Replaces launch_paired_scan!(backend, args, partial, Q,
+ * D, qmask, dmask) (src/forward_layouts.jl:126-143; CUDA override
+ * ext/FlashMaxSimCUDAExt.jl:70-82).  Q (dim,Tq,B), D (dim,Td,B), qmask
+ * (Tq,B), dmask (Td,B); args/partial (Tq,B); scores (B,) nullable.
+ */
+fms_status fms_launch_paired_scan(int32_t dtype, int32_t* args, float* partial,
+                                  const void* Q, const void* D,
+                                  const uint8_t* qmask, const uint8_t* dmask,
+                                  int64_t dim, int64_t Tq, int64_t Td, int64_t B,
+                                  float* scores, void* stream);
+
+/*
+ * Candidate scan.  Replaces launch_candidates_scan!(backend, args, partial,
+ * Q, gallery, idx, qmask, dmask, N) (src/forward_layouts.jl:292-310; CUDA
+ * override ext/FlashMaxSimCUDAExt.jl:112-124).  Q (dim,Tq,B), gallery
+ * (dim,Td,N), idx (C,B) 1-based integers of idx_bytes = 4 or 8 bytes
+ * (Int32 / Int64), qmask (Tq,B), dmask (Td,N); args/partial (Tq,C,B);
+ * scores (C,B) nullable: Sigma_t for 1 <= idx <= N, else `neg`.
+ */
+fms_status fms_launch_candidates_scan(int32_t dtype, int32_t* args, float* partial,
+                                      const void* Q, const void* gallery,
+                                      const void* idx, int32_t idx_bytes,
+                                      const uint8_t* qmask, const uint8_t* dmask,
+                                      int64_t dim, int64_t Tq, int64_t B,
+                                      int64_t Td, int64_t N, int64_t C,
+                                      float* scores, float neg, void* stream);
+
+/*
+ * In-batch scan.  Replaces inbatch_device_scan!(backend, S, args, Q, D,
+ * qmask, dmask) (src/forward_layouts.jl:202-225; CUDA override
+ * ext/FlashMaxSimCUDAExt.jl:126-140).  Q (dim,Tq,Bq), D (dim,Td,Bd);
+ * S (Bd,Bq) receives S[j,i] = MaxSim(Q_i, D_j) (overwritten, as the CUDA
+ * override does with `S .= ...`); args (Tq,Bd,Bq) nullable.
+ */
+fms_status fms_inbatch_device_scan(int32_t dtype, float* S, int32_t* args,
+                                   const void* Q, const void* D,
+                                   const uint8_t* qmask, const uint8_t* dmask,
+                                   int64_t dim, int64_t Tq, int64_t Bq,
+                                   int64_t Td, int64_t Bd, void* stream);
+
+/*
+ * Packed scan: one query against B ragged documents.  Replaces
+ * launch_packed_scan!(backend, args, partial, q, packed, cu, qmask)
+ * (src/packed.jl:219-234; CUDA override ext/FlashMaxSimCUDAExt.jl:84-96).
+ * q (dim,Tq), tokens (dim,ntokens), cu (B+1,) int32 1-based CSR (document b
+ * is tokens[:, cu[b]:cu[b+1]-1]); qmask (Tq,) nullable; args/partial (Tq,B)
+ * with document-local 1-based argmax; scores (B,) nullable.
+ */
+fms_status fms_launch_packed_scan(int32_t dtype, int32_t* args, float* partial,
+                                  const void* q, const void* tokens, const int32_t* cu,
+                                  const uint8_t* qmask,
+                                  int64_t dim, int64_t Tq, int64_t B, int64_t ntokens,
+                                  float* scores, void* stream);
+
+/*
+ * Varlen scan: N ragged (query, document) pairs.  Replaces
+ * launch_varlen_scan!(backend, args, partial, Qp, Dp, cu_q, cu_d)
+ * (src/packed.jl:298-314; CUDA override ext/FlashMaxSimCUDAExt.jl:98-110).
+ * args/partial (max_q,N); rows t >= Tq_n are written 0.  scores (N,) nullable.
+ */
+fms_status fms_launch_varlen_scan(int32_t dtype, int32_t* args, float* partial,
+                                  const void* Qtokens, const void* Dtokens,
+                                  const int32_t* cu_q, const int32_t* cu_d,
+                                  int64_t dim, int64_t max_q, int64_t N,
+                                  int64_t nq_tokens, int64_t nd_tokens,
+                                  float* scores, void* stream);
+
+/*
+ * Per-token symmetric INT8 quantisation of fp32 features, bit-exact with
+ * quantize_int8_symmetric (src/quant.jl:42-49): scale = max(max(absmax,
+ * 1f-8)/127f0, floatmin(Float32)) with IEEE division; code =
+ * round-to-nearest-even(clamp(x/scale, -127, 127)).  X (dim,ntok) fp32 ->
+ * codes (dim,ntok) int8, scales (ntok,) fp32.
+ */
+fms_status fms_int8_quantize(const float* X, int8_t* codes, float* scales,
+                             int64_t dim, int64_t ntok, void* stream);
+
+/*
+ * INT8 pair scan.  Replaces launch_int8_pair_scan!(backend, args, partial,
+ * qc, qs, dc, ds, qmask, dmask) (src/quant.jl:139-154; CUDA override
+ * ext/FlashMaxSimCUDAExt.jl:142-153).  Dots accumulate exactly in int32;
+ * s = (qs[t]*ds[u]) * Float32(acc) evaluated left to right (src/quant.jl:113).
+ */
+fms_status fms_launch_int8_pair_scan(int32_t* args, float* partial,
+                                     const int8_t* qc, const float* qs,
+                                     const int8_t* dc, const float* ds,
+                                     const uint8_t* qmask, const uint8_t* dmask,
+                                     int64_t dim, int64_t Tq, int64_t Td,
+                                     float* score, void* stream);
+
+/*
+ * INT8 paired scan.  Replaces launch_int8_paired_scan!(backend, args,
+ * partial, Qc, Qs, Dc, Ds, qmask, dmask) (src/quant.jl:199-217; CUDA
+ * override ext/FlashMaxSimCUDAExt.jl:155-167).
+ */
+fms_status fms_launch_int8_paired_scan(int32_t* args, float* partial,
+                                       const int8_t* Qc, const float* Qs,
+                                       const int8_t* Dc, const float* Ds,
+                                       const uint8_t* qmask, const uint8_t* dmask,
+                                       int64_t dim, int64_t Tq, int64_t Td, int64_t B,
+                                       float* scores, void* stream);
+
+/*
+ * INT8 candidate scan.  No reference counterpart: Int8Index has only pair
+ * and paired methods (src/dispatch.jl:247-296).  Composes the INT8 pair scan
+ * per (c,b) with the candidate conventions of launch_candidates_scan!
+ * (src/forward_layouts.jl:292-310): idx (C,B), invalid -> tape 0 / `neg`.
+ */
+fms_status fms_launch_int8_candidates_scan(int32_t* args, float* partial,
+                                           const int8_t* Qc, const float* Qs,
+                                           const int8_t* Gc, const float* Gs,
+                                           const void* idx, int32_t idx_bytes,
+                                           const uint8_t* qmask, const uint8_t* dmask,
+                                           int64_t dim, int64_t Tq, int64_t B,
+                                           int64_t Td, int64_t N, int64_t C,
+                                           float* scores, float neg, void* stream);
+
+/*
+ * Test-only: raw int32 dots out (Td,Tq) with out[u + Td*t] = <qc_t, dc_u>,
+ * computed by the same int8 MFMA path as the scans.  No reference
+ * counterpart (the reference never exposes dots); used for the bit-exact
+ * check of the int32 accumulation (quant.jl:109-112).
+ */
+fms_status fms_int8_dots(int32_t* out, const int8_t* qc, const int8_t* dc,
+                         int64_t dim, int64_t Tq, int64_t Td, void* stream);
+
+/*
+ * Query-length normalisation epilogues (src/normalize.jl:4-46,
+ * src/forward_pair.jl:222-228, src/packed.jl:316-354).  scores (nrows,ncols)
+ * column-major, scaled in place by inv = 1/max(count, 1) (fp32, multiply):
+ *   fms_length_normalize: count = count(qmask[:,col]) per column (qmask
+ *     (Tq,ncols); NULL = Tq); if idx is non-NULL (candidate layout,
+ *     idx (nrows,ncols)), entries with idx outside 1..N are set to `neg`.
+ *   fms_varlen_normalize: count = cu_q[n+1]-cu_q[n] per entry (N entries).
+ */
+fms_status fms_length_normalize(float* scores, const uint8_t* qmask, int64_t Tq,
+                                int64_t nrows, int64_t ncols,
+                                const void* idx, int32_t idx_bytes, int64_t N, float neg,
+                                void* stream);
+fms_status fms_varlen_normalize(float* scores, const int32_t* cu_q, int64_t N, void* stream);
+
+/*
+ * Test-only: MFMA accumulator layout probe (no reference counterpart).  Runs
+ * one 32x32 MFMA of the given feature type (FMS_F32 / FMS_F16 / FMS_BF16, or
+ * 3 = int8) twice -- A[i][0] = i+1, B[0][j] = 1, then A[i][0] = 1,
+ * B[0][j] = j+1 -- and writes out[(pass*64 + lane)*16 + reg] (2048 floats),
+ * so a test can confirm the (lane, register) -> (row, column) map the scans
+ * rely on.
+ */
+fms_status fms_debug_mfma_layout(float* out, int32_t dtype_or_int8, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLASHMAXSIM_HIP_H */

@@ -1,0 +1,290 @@
+"""GPU parity: every HIP scan layout vs the CPU oracle on the same seeded inputs.
+
+Bars (north star): fp32 scores within 1e-5 relative, fp16/bf16 within 2e-3;
+argmax tapes equal except at near-ties within that tolerance; INT8 int32
+dots and per-token partials bit-exact.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from helpers import (FEATURE_TOL, as_feature, assert_scores, assert_tape, mask_np, to_dev,
+                     tokens, widened)
+
+import flashmaxsim as fm
+from flashmaxsim import _lib, boundary
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = [torch.float16, torch.bfloat16, torch.float32]
+DT_ID = {torch.float16: "f16", torch.bfloat16: "bf16", torch.float32: "f32"}
+
+
+def _acc_row(r, h):
+    return 8 * (r >> 2) + 4 * h + (r & 3)
+
+
+@pytest.mark.parametrize("op", [0, 1, 2, 3], ids=["f32", "f16", "bf16", "i8"])
+def test_mfma_accumulator_layout(device, op):
+    out = torch.zeros(2048, dtype=torch.float32, device=device)
+    _lib.check(_lib.lib().fms_debug_mfma_layout(out.data_ptr(), op,
+                                                torch.cuda.current_stream().cuda_stream),
+               "probe")
+    o = out.cpu().numpy().reshape(2, 64, 16)
+    for lane in range(64):
+        for r in range(16):
+            assert o[0, lane, r] == _acc_row(r, lane // 32) + 1, (lane, r, o[0, lane, r])
+            assert o[1, lane, r] == (lane % 32) + 1, (lane, r, o[1, lane, r])
+
+
+def _masks(rng, B, Tq, Td, kind):
+    if kind == "none":
+        return None, None
+    if kind == "pattern":  # test_ka_cpu.jl:234-236 patterns
+        qm = np.array([[(t + 1) % 2 == 1 for t in range(Tq)] for _ in range(B)])
+        dm = np.array([[(u + 1) % 3 != 0 for u in range(Td)] for _ in range(B)])
+    else:  # random, with one fully masked document row
+        qm = rng.random((B, Tq)) < 0.8
+        dm = rng.random((B, Td)) < 0.7
+        dm[-1, :] = False
+    return torch.from_numpy(qm), torch.from_numpy(dm)
+
+
+def _pair_sims_fn(qf, df, pair_of):
+    """qf (P?, Tq, dim) f64, df(...) -> callable(idx) -> s[u] for (pair, t)."""
+    def sims(idx):
+        *pidx, t = idx
+        q, d = pair_of(tuple(pidx))
+        return d @ q[t]
+    return sims
+
+
+PAIRED_SHAPES = [
+    (128, 32, 180, 8),   # fast kernel, C2-like tokens
+    (40, 33, 65, 2),     # tile-straddling dim/Tq/Td (test_cuda.jl:102-117)
+    (768, 8, 17, 2),     # split-d (test_cuda.jl:174-187)
+    (256, 32, 64, 3),    # fast kernel, second register bucket
+    (16, 12, 130, 3),    # host DOC_TILE straddle (test_regressions.jl:196-206)
+    (8, 3, 5, 2),
+    (12, 5, 9, 2),       # row not a 16-byte multiple for 16-bit types
+]
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: DT_ID[d])
+@pytest.mark.parametrize("shape", PAIRED_SHAPES, ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("masks", ["none", "pattern", "random"])
+def test_paired_parity(device, dtype, shape, masks):
+    dim, Tq, Td, B = shape
+    rng = np.random.default_rng([dim, Tq, Td, B, ["none", "pattern", "random"].index(masks)])
+    Qt, Qo, bf = as_feature(tokens(rng, (B, Tq, dim)), dtype)
+    Dt, Do, _ = as_feature(tokens(rng, (B, Td, dim)), dtype)
+    qm, dm = _masks(rng, B, Tq, Td, masks)
+    s_o, a_o, p_o = oracle.paired_forward(Qo, Do, mask_np(qm), mask_np(dm), bf16=bf)
+    args = torch.zeros(B, Tq, dtype=torch.int32, device=device)
+    part = torch.zeros(B, Tq, dtype=torch.float32, device=device)
+    scores = torch.zeros(B, dtype=torch.float32, device=device)
+    boundary.launch_paired_scan(args, part, Qt.to(device), Dt.to(device), to_dev(qm, device),
+                                to_dev(dm, device), scores)
+    torch.cuda.synchronize()
+    tol = FEATURE_TOL[dtype]
+    assert_scores(scores.cpu(), s_o, tol, what="scores")
+    assert_scores(part.cpu(), p_o, tol, what="partial")
+    Qf, Df = widened(Qo, bf), widened(Do, bf)
+    assert_tape(args.cpu().numpy(), a_o, _pair_sims_fn(Qf, Df, lambda p: (Qf[p[0]], Df[p[0]])), tol)
+    # the driver path (fused scores, no partial) agrees with the boundary path
+    s2, a2 = fm.paired_forward(Qt.to(device), Dt.to(device), to_dev(qm, device), to_dev(dm, device))
+    torch.cuda.synchronize()
+    assert torch.equal(s2.cpu(), scores.cpu()) and torch.equal(a2.cpu(), args.cpu())
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: DT_ID[d])
+@pytest.mark.parametrize("shape", [(128, 32, 180), (40, 33, 65), (8, 6, 7), (128, 24, 100)],
+                         ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("idx_dtype", [torch.int32, torch.int64], ids=["i32", "i64"])
+def test_candidates_parity(device, dtype, shape, idx_dtype):
+    dim, Tq, Td = shape
+    N, C, B = 23, 9, 5
+    rng = np.random.default_rng(dim * 1000 + Tq * 10 + Td)
+    Qt, Qo, bf = as_feature(tokens(rng, (B, Tq, dim)), dtype)
+    Gt, Go, _ = as_feature(tokens(rng, (N, Td, dim)), dtype)
+    idx = rng.integers(1, N + 1, size=(B, C)).astype(np.int64)
+    idx[0, 2] = 0
+    idx[3, 0] = N + 1
+    idx[4, 8] = -5
+    qm = torch.from_numpy(rng.random((B, Tq)) < 0.9)
+    dm = torch.from_numpy(np.array([[(u + 1) % 4 != 0 for u in range(Td)] for _ in range(N)]))
+    neg = -1.0e4
+    S_o, a_o, p_o = oracle.candidates_forward(Qo, Go, idx, mask_np(qm), mask_np(dm), neg, bf16=bf)
+    idx_t = torch.from_numpy(idx).to(idx_dtype).to(device)
+    args = torch.zeros(B, C, Tq, dtype=torch.int32, device=device)
+    part = torch.zeros(B, C, Tq, dtype=torch.float32, device=device)
+    S = torch.zeros(B, C, dtype=torch.float32, device=device)
+    boundary.launch_candidates_scan(args, part, Qt.to(device), Gt.to(device), idx_t,
+                                    qm.to(device), dm.to(device), N, S, neg)
+    torch.cuda.synchronize()
+    tol = FEATURE_TOL[dtype]
+    assert_scores(S.cpu(), S_o, tol, what="scores")
+    assert (S.cpu().numpy()[idx < 1] == np.float32(neg)).all()
+    assert (S.cpu().numpy()[idx > N] == np.float32(neg)).all()
+    assert_scores(part.cpu(), p_o, tol, what="partial")
+    Qf, Gf = widened(Qo, bf), widened(Go, bf)
+    assert_tape(args.cpu().numpy(), a_o,
+                _pair_sims_fn(Qf, Gf, lambda p: (Qf[p[0]], Gf[idx[p[0], p[1]] - 1])), tol)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: DT_ID[d])
+@pytest.mark.parametrize("shape", [(128, 32, 180, 6, 5), (40, 33, 65, 3, 4), (16, 8, 10, 4, 4)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_inbatch_parity(device, dtype, shape):
+    dim, Tq, Td, Bq, Bd = shape
+    rng = np.random.default_rng(sum(shape))
+    Qt, Qo, bf = as_feature(tokens(rng, (Bq, Tq, dim)), dtype)
+    Dt, Do, _ = as_feature(tokens(rng, (Bd, Td, dim)), dtype)
+    lens = rng.integers(min(Td, 3), Td + 1, size=Bd)
+    lens[0] = 0  # an empty document contributes 0 (test_regressions.jl:173-194)
+    dm = torch.from_numpy(np.arange(Td)[None, :] < lens[:, None])
+    qm = torch.from_numpy(rng.random((Bq, Tq)) < 0.9)
+    S_o, a_o = oracle.inbatch_forward(Qo, Do, mask_np(qm), mask_np(dm), bf16=bf)
+    S, args = fm.inbatch_forward(Qt.to(device), Dt.to(device), qm.to(device), dm.to(device))
+    torch.cuda.synchronize()
+    tol = FEATURE_TOL[dtype]
+    assert_scores(S.cpu(), S_o, tol, what="S")
+    assert (S.cpu().numpy()[:, 0] == 0).all()
+    Qf, Df = widened(Qo, bf), widened(Do, bf)
+    assert_tape(args.cpu().numpy(), a_o, _pair_sims_fn(Qf, Df, lambda p: (Qf[p[0]], Df[p[1]])), tol)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: DT_ID[d])
+@pytest.mark.parametrize("case", ["small", "colpali", "splitd"])
+def test_packed_parity(device, dtype, case):
+    rng = np.random.default_rng({"small": 31, "colpali": 4, "splitd": 44}[case])
+    if case == "small":
+        dim, Tq, lens = 16, 7, [5, 0, 3, 9, 1, 33, 64, 65]
+    elif case == "colpali":
+        dim, Tq, lens = 128, 24, list(rng.integers(700, 1101, size=12))
+        lens[3] = 0
+    else:
+        dim, Tq, lens = 1024, 24, [40, 0, 97, 3]
+    docs = [tokens(rng, (n, dim)) for n in lens]
+    q32 = tokens(rng, (Tq, dim))
+    qt, qo, bf = as_feature(q32, dtype)
+    tok_t, tok_o, _ = as_feature(np.concatenate(docs, 0), dtype)
+    cu = np.concatenate([[1], 1 + np.cumsum(lens)]).astype(np.int32)
+    qm = torch.from_numpy(rng.random(Tq) < 0.9)
+    s_o, a_o, p_o = oracle.packed_forward(qo, tok_o, cu, mask_np(qm), bf16=bf)
+    P = fm.PackedSeq(tok_t, torch.from_numpy(cu)).to(device)
+    scores, args = fm.packed_forward(qt.to(device), P, qm.to(device))
+    torch.cuda.synchronize()
+    tol = FEATURE_TOL[dtype]
+    assert_scores(scores.cpu(), s_o, tol)
+    assert scores.cpu()[lens.index(0)] == 0
+    qf, tf = widened(qo, bf), widened(tok_o, bf)
+    assert_tape(args.cpu().numpy(), a_o,
+                _pair_sims_fn(qf, tf, lambda p: (qf, tf[cu[p[0]] - 1: cu[p[0] + 1] - 1])), tol)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: DT_ID[d])
+def test_varlen_parity(device, dtype):
+    rng = np.random.default_rng(32)
+    dim = 12 if dtype == torch.float32 else 64
+    qlens = [4, 2, 35, 1, 0, 7]
+    dlens = [5, 3, 70, 0, 4, 33]
+    qs = [tokens(rng, (n, dim)) for n in qlens]
+    ds = [tokens(rng, (n, dim)) for n in dlens]
+    Qt, Qo, bf = as_feature(np.concatenate(qs, 0), dtype)
+    Dt, Do, _ = as_feature(np.concatenate(ds, 0), dtype)
+    cu_q = np.concatenate([[1], 1 + np.cumsum(qlens)]).astype(np.int32)
+    cu_d = np.concatenate([[1], 1 + np.cumsum(dlens)]).astype(np.int32)
+    max_q = max(qlens)
+    s_o, a_o, p_o = oracle.varlen_forward(Qo, Do, cu_q, cu_d, max_q, bf16=bf)
+    Qp = fm.PackedSeq(Qt, torch.from_numpy(cu_q)).to(device)
+    Dp = fm.PackedSeq(Dt, torch.from_numpy(cu_d)).to(device)
+    scores, args = fm.varlen_forward(Qp, Dp)
+    torch.cuda.synchronize()
+    tol = FEATURE_TOL[dtype]
+    assert_scores(scores.cpu(), s_o, tol)
+    Qf, Df = widened(Qo, bf), widened(Do, bf)
+    assert_tape(args.cpu().numpy(), a_o,
+                _pair_sims_fn(Qf, Df, lambda p: (Qf[cu_q[p[0]] - 1: cu_q[p[0] + 1] - 1],
+                                                 Df[cu_d[p[0]] - 1: cu_d[p[0] + 1] - 1])), tol)
+
+
+# ---- known answers from the reference's own tests, on the device ----------------------
+
+def test_all_negative_dots_keep_true_max(device):
+    """test_regressions.jl:244-254: q = ones(4,3), d = -ones(4,5) => -12, tape > 0."""
+    for dtype in DTYPES:
+        q = torch.ones(3, 4, dtype=dtype, device=device)
+        d = -torch.ones(5, 4, dtype=dtype, device=device)
+        s, a = fm.pair_forward(q, d)
+        assert s.item() == -12.0
+        assert (a.cpu() == 1).all()
+
+
+def test_empty_doc_scores_zero_not_neg(device):
+    """test_regressions.jl:173-194: a fully masked document contributes 0."""
+    rng = np.random.default_rng(11)
+    q = torch.from_numpy(tokens(rng, (5, 8))).to(device)
+    d = torch.from_numpy(tokens(rng, (6, 8))).to(device)
+    dm = torch.zeros(6, dtype=torch.bool, device=device)
+    assert fm.maxsim(q, d, None, dm).item() == 0.0
+    assert fm.maxsim(q, d, None, dm, normalize=True).item() == 0.0
+
+
+def test_candidate_neg_and_normalize(device):
+    """test_forward.jl:41-49 / test_regressions.jl:133-149: invalid idx => neg, kept by normalize."""
+    rng = np.random.default_rng(7)
+    Q = torch.from_numpy(tokens(rng, (2, 4, 8))).to(device)
+    G = torch.from_numpy(tokens(rng, (4, 5, 8))).to(device)
+    idxs = torch.tensor([[1, 0], [2, 1]], dtype=torch.int32, device=device)  # Julia [1 2; 0 1]
+    S = fm.maxsim(Q, G, idxs)
+    assert S[0, 1].item() == -1.0e4
+    Sn = fm.maxsim(Q, G, idxs, normalize=True)
+    assert Sn[0, 1].item() == -1.0e4
+    assert abs(Sn[0, 0].item() - S[0, 0].item() / 4) < 1e-5
+
+
+def test_normalize_layouts(device):
+    rng = np.random.default_rng(5)
+    Q = torch.from_numpy(tokens(rng, (3, 6, 16))).to(device)
+    D = torch.from_numpy(tokens(rng, (3, 9, 16))).to(device)
+    qm = torch.tensor([[1, 1, 0, 1, 0, 1], [0] * 6, [1] * 6], dtype=torch.bool, device=device)
+    s = fm.maxsim(Q, D, qm, None)
+    sn = fm.maxsim(Q, D, qm, None, normalize=True)
+    inv = 1.0 / torch.clamp(qm.sum(1).float(), min=1.0)
+    assert torch.equal(sn, s * inv)
+    S = fm.maxsim(Q, D, qm, None, fm.InBatch())
+    Sn = fm.maxsim(Q, D, qm, None, fm.InBatch(), normalize=True)
+    assert torch.equal(Sn, S * inv[:, None])
+    P = fm.pack_docs([D[0], D[1][:4], D[2][:0]])
+    sp = fm.maxsim(Q[0], P)
+    spn = fm.maxsim(Q[0], P, normalize=True)
+    assert torch.equal(spn, sp * (1.0 / 6.0))
+    Qp, Dp = fm.pack_pairs([Q[0], Q[1][:2]], [D[0], D[1]])
+    sv = fm.maxsim(Qp, Dp)
+    svn = fm.maxsim(Qp, Dp, normalize=True)
+    assert torch.equal(svn, sv * torch.tensor([1 / 6, 1 / 2], device=device, dtype=torch.float32))
+
+
+def test_float16_returns_float32_scores(device):
+    """test_edge_cases.jl:14-24 and the CUDA WMMA checks (test_cuda.jl:154-172)."""
+    rng = np.random.default_rng(20)
+    q = torch.from_numpy(tokens(rng, (17, 32))).to(device)
+    d = torch.from_numpy(tokens(rng, (23, 32))).to(device)
+    s16 = fm.maxsim(q.half(), d.half())
+    assert s16.dtype == torch.float32 and s16.numel() == 1
+    s32 = fm.maxsim(q, d)
+    assert abs(s16.item() - s32.item()) <= 1e-3 * (1 + abs(s32.item()))
+
+
+def test_host_arrays_are_refused(device):
+    """test_cuda.jl:22,90: host masks / host idxs with device features throw ArgumentError."""
+    q = torch.randn(4, 8, device=device)
+    d = torch.randn(5, 8, device=device)
+    with pytest.raises(fm.ArgumentError):
+        fm.maxsim(q, d, torch.ones(4, dtype=torch.bool), torch.ones(5, dtype=torch.bool))
+    Q = torch.randn(2, 4, 8, device=device)
+    G = torch.randn(3, 5, 8, device=device)
+    with pytest.raises(fm.ArgumentError):
+        fm.maxsim(Q, G, torch.ones(2, 2, dtype=torch.int32))

@@ -1,0 +1,105 @@
+"""CPU checks of the host mirror: PackedSeq / pack_docs CSR logic, MaxSim
+config semantics, argument validation, and that no CPU scoring path exists
+(host tensors are refused, as the MI355X library is the only scorer)."""
+import numpy as np
+import pytest
+import torch
+
+import flashmaxsim as fm
+from flashmaxsim import forward as F
+
+
+def test_pack_docs_cu_and_max_len():
+    """test_packed.jl:1-27."""
+    dim = 8
+    docs = [torch.randn(5, dim), torch.randn(0, dim), torch.randn(3, dim)]
+    P = fm.pack_docs(docs)
+    assert P.cu.tolist() == [1, 6, 6, 9]
+    assert P.max_len == 5 and fm.nseq(P) == 3
+    assert tuple(P.tokens.shape) == (8, dim)
+    assert torch.equal(P.tokens[0:5], docs[0]) and torch.equal(P.tokens[5:8], docs[2])
+    assert fm.PackedSeq(P.tokens, P.cu).max_len == 5
+    with pytest.raises(fm.ArgumentError):
+        fm.PackedSeq(P.tokens, torch.tensor([1, 6, 6, 7], dtype=torch.int32))  # does not cover
+    with pytest.raises(fm.ArgumentError):
+        fm.PackedSeq(P.tokens, torch.tensor([2, 6, 6, 9], dtype=torch.int32))  # does not start at 1
+    with pytest.raises(fm.ArgumentError):
+        fm.PackedSeq(P.tokens, torch.tensor([1, 6, 4, 9], dtype=torch.int32))  # decreasing
+    with pytest.raises(fm.ArgumentError):
+        fm.pack_docs([])
+    with pytest.raises(fm.DimensionMismatch):
+        fm.pack_docs([torch.randn(2, 4), torch.randn(2, 5)])
+
+
+def test_pack_pairs():
+    qs = [torch.randn(4, 8), torch.randn(2, 8)]
+    ds = [torch.randn(5, 8), torch.randn(3, 8)]
+    Qp, Dp = fm.pack_pairs(qs, ds)
+    assert Qp.cu.tolist() == [1, 5, 7] and Dp.cu.tolist() == [1, 6, 9]
+    assert Qp.max_len == 4 and Dp.max_len == 5
+    with pytest.raises(fm.DimensionMismatch):
+        fm.pack_pairs(qs, ds[:1])
+
+
+def test_maxsim_config_semantics():
+    cfg = fm.MaxSim(torch.float16)
+    assert cfg.neg == -1.0e4 and not cfg.normalize
+    assert fm.MaxSim(torch.bfloat16).neg == -9984.0  # BFloat16(-1f4) rounds to -9984
+    assert fm.MaxSim(torch.float32, neg=0, normalize=True).normalize
+    assert isinstance(fm.MaxSim(backward=fm.InvGrid).backward, fm.InvGrid)
+    assert fm.score_eltype(torch.float16) == torch.float32
+    assert fm.score_eltype(torch.bfloat16) == torch.float32
+    assert "MaxSim" in repr(cfg)
+
+
+def test_host_tensors_have_no_cpu_path():
+    q, d = torch.randn(3, 8), torch.randn(5, 8)
+    with pytest.raises(fm.ArgumentError):
+        fm.maxsim(q, d)
+    with pytest.raises(fm.ArgumentError):
+        fm.maxsim(q.unsqueeze(0), d.unsqueeze(0), fm.InBatch())
+    with pytest.raises(fm.ArgumentError):
+        fm.maxsim(q, fm.pack_docs([d]))
+
+
+def test_shape_checks_match_reference():
+    """test_forward.jl:77-91 (DimensionMismatch cases), checked before any launch."""
+    Q, D = torch.randn(2, 3, 4), torch.randn(2, 5, 4)
+    with pytest.raises(fm.DimensionMismatch):
+        F.require_paired_shapes(Q, D, torch.ones(2, 3, dtype=torch.bool), torch.ones(3, 5, dtype=torch.bool))
+    with pytest.raises(fm.DimensionMismatch):
+        F.require_paired_shapes(Q, D, torch.ones(2, 2, dtype=torch.bool), None)
+    with pytest.raises(fm.DimensionMismatch):
+        F.require_paired_shapes(Q, torch.randn(2, 5, 5), None, None)
+    with pytest.raises(fm.DimensionMismatch):
+        F.require_paired_shapes(Q, torch.randn(3, 5, 4), None, None)
+    with pytest.raises(fm.DimensionMismatch):
+        F.require_inbatch_shapes(Q, D, torch.ones(2, 3, dtype=torch.bool), torch.ones(2, 4, dtype=torch.bool))
+    G = torch.randn(4, 5, 4)
+    idxs = torch.tensor([[1, 3, 0], [2, 4, 1]])
+    with pytest.raises(fm.DimensionMismatch):
+        F.require_candidates_shapes(Q, G, idxs, torch.ones(3, 3, dtype=torch.bool), None)
+    with pytest.raises(fm.DimensionMismatch):
+        F.require_candidates_shapes(Q, G, torch.tensor([[1, 0], [2, 1], [3, 2]]), None, None)
+    with pytest.raises(fm.DimensionMismatch):
+        F.require_candidates_shapes(Q, torch.randn(4, 5, 5), idxs, None, None)
+    with pytest.raises(fm.DimensionMismatch):
+        F.require_pair_shapes(torch.randn(3, 4), torch.randn(5, 4), torch.ones(2, dtype=torch.bool), None)
+
+
+def test_unsupported_feature_type():
+    from flashmaxsim import boundary
+    with pytest.raises(fm.UnsupportedError):
+        boundary.dtype_code(torch.randn(2, 2, dtype=torch.float64))
+    assert boundary.dtype_code(torch.randn(2, 2).half()) == 1
+
+
+def test_int8index_shape_checks():
+    from flashmaxsim.quant import require_int8_index
+    require_int8_index(fm.Int8Index(torch.zeros(5, 8, dtype=torch.int8), torch.zeros(5)))
+    with pytest.raises(fm.DimensionMismatch):
+        require_int8_index(fm.Int8Index(torch.zeros(5, 8, dtype=torch.int8), torch.zeros(4)))
+    with pytest.raises(fm.DimensionMismatch):
+        require_int8_index(fm.Int8Index(torch.zeros(2, 5, 8, dtype=torch.int8), torch.zeros(3, 5)))
+    deq = fm.dequant_int8(fm.Int8Index(torch.tensor([[1, -2]], dtype=torch.int8), torch.tensor([0.5])))
+    assert deq.tolist() == [[0.5, -1.0]]

@@ -38,7 +38,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="c2", choices=["c2", "c3", "c4", "c4d1024", "c5"])
+    ap.add_argument("--workload", default="c2",
+                    choices=["c2", "c3", "c4", "c4d1024", "c5", "read"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="target duration of the bounded CPU baseline sample")
@@ -341,6 +342,27 @@ def run_c4(args, torch, fm, boundary, dev, dim=128):
     return res
 
 
+def run_read(args, torch, fm, boundary, dev):
+    """Measured HBM read ceiling: fms_debug_read_bandwidth over an 8 GiB buffer (16-byte
+    nontemporal loads, 8192 x 256 threads).  Also the known-size calibration of FETCH_SIZE."""
+    from flashmaxsim import _lib
+    nbytes = 8 << 30
+    buf = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    buf.fill_(7)
+    blocks = 8192
+    out = torch.empty(blocks * 256, dtype=torch.int32, device=dev)
+
+    def step():
+        _lib.check(_lib.lib().fms_debug_read_bandwidth(buf.data_ptr(), nbytes, out.data_ptr(),
+                                                       blocks, torch.cuda.current_stream().cuda_stream),
+                   "read_bandwidth")
+
+    wall, launch_ms = timed_steps(torch, step, args.steps, args.warmup)
+    return dict(pairs_per_step=0, bytes_per_launch=nbytes, wall=wall, launch_ms=launch_ms,
+                dtype="u8", bound="hbm",
+                config={"workload": "hbm_read_ceiling", "bytes": nbytes, "blocks": blocks})
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -352,7 +374,7 @@ def main():
     from flashmaxsim import boundary
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    runner = {"c2": run_c2, "c3": run_c3, "c4": run_c4, "c5": run_c5,
+    runner = {"c2": run_c2, "c3": run_c3, "c4": run_c4, "c5": run_c5, "read": run_read,
               "c4d1024": lambda *a: run_c4(*a, dim=1024)}[args.workload]
     r = runner(args, torch, fm, boundary, dev)
     steps = args.steps
@@ -396,7 +418,11 @@ def main():
         out["parity_check"] = r["check"]
     if r["bound"] == "mfma":
         out["roofline"]["padded_tflops"] = round(r["padded_flops"] / avg_launch_s / 1e12, 2)
-    if args.workload != "c2":
+    if args.workload == "read":
+        out["metric"] = "HBM streaming read GB/s"
+        out["value"] = out["roofline"]["achieved"]
+        out["unit"] = "GB/s"
+    elif args.workload != "c2":
         out["metric"] = f"MaxSim pairs/sec ({r['config']['workload']})"
     print(json.dumps(out), flush=True)
 

@@ -9,6 +9,7 @@
 #include <string.h>
 
 #include "../../include/flashmaxsim_hip.h"
+#include "fms_inbatch.hpp"
 #include "fms_misc.hpp"
 #include "fms_scan_decl.hpp"
 
@@ -172,6 +173,22 @@ fms_status fms_inbatch_device_scan(int32_t dtype, float* S, int32_t* args, const
   if (!seq_ok(Tq, dim, esz) || !seq_ok(Td, dim, esz)) return FMS_EUNSUPPORTED;
   if (Bq == 0 || Bd == 0) return FMS_OK;
   if (!S || (Tq * dim > 0 && !Q) || (Td * dim > 0 && !D)) return FMS_EINVAL;
+  if ((dtype == FMS_F16 || dtype == FMS_BF16) && inbatch_mfma_supported(dim, Tq, Td, Q, D) &&
+      Bq <= kMaxTokens && Bd <= kMaxTokens) {
+    InBatchArgs a;
+    a.Q = static_cast<const char*>(Q);
+    a.D = static_cast<const char*>(D);
+    a.qm = qmask;
+    a.dm = dmask;
+    a.S = S;
+    a.args = args;
+    a.Bq = (int)Bq;
+    a.Bd = (int)Bd;
+    a.Tq = (int)Tq;
+    a.Td = (int)Td;
+    return from_hip(launch_inbatch_mfma(dtype == FMS_BF16, a, as_stream(stream)));
+  }
+  // other shapes / fp32: the per-pair scan over p = j + Bd*i
   LayInBatch lay;
   lay.Q = static_cast<const char*>(Q);
   lay.D = static_cast<const char*>(D);
@@ -345,6 +362,14 @@ fms_status fms_varlen_normalize(float* scores, const int32_t* cu_q, int64_t N, v
 fms_status fms_debug_mfma_layout(float* out, int32_t dtype_or_int8, void* stream) {
   if (!out || dtype_or_int8 < 0 || dtype_or_int8 > 3) return FMS_EINVAL;
   return from_hip(mfma_layout_probe(out, dtype_or_int8, as_stream(stream)));
+}
+
+fms_status fms_debug_read_bandwidth(const void* p, int64_t bytes, uint32_t* out, int32_t blocks,
+                                    void* stream) {
+  if (bytes < 0 || bytes % 16 != 0 || blocks <= 0 || !out || (bytes > 0 && !p) ||
+      !aligned16(p))
+    return FMS_EINVAL;
+  return from_hip(read_bandwidth(p, bytes, out, blocks, as_stream(stream)));
 }
 
 }  // extern "C"

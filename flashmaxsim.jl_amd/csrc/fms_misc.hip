@@ -198,6 +198,37 @@ __global__ void mfma_layout_probe_kernel(float* out, int op) {
   }
 }
 
+// Streaming read of `bytes` (a multiple of 16) with 16-byte loads: the
+// measured HBM read ceiling reported beside the scans' roofline, and the
+// known-size reference that calibrates the FETCH_SIZE counter.  Each thread
+// folds what it read into one word so the loads cannot be removed.
+__global__ void __launch_bounds__(256) read_bandwidth_kernel(const u32x4* __restrict__ p,
+                                                             int64_t n16, uint32_t* out) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  uint32_t acc = 0u;
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  for (; i + 3 * stride < n16; i += 4 * stride) {
+    const u32x4 a = __builtin_nontemporal_load(p + i);
+    const u32x4 b = __builtin_nontemporal_load(p + i + stride);
+    const u32x4 c = __builtin_nontemporal_load(p + i + 2 * stride);
+    const u32x4 d = __builtin_nontemporal_load(p + i + 3 * stride);
+    acc ^= a[0] ^ a[1] ^ a[2] ^ a[3] ^ b[0] ^ b[1] ^ b[2] ^ b[3];
+    acc ^= c[0] ^ c[1] ^ c[2] ^ c[3] ^ d[0] ^ d[1] ^ d[2] ^ d[3];
+  }
+  for (; i < n16; i += stride) {
+    const u32x4 a = __builtin_nontemporal_load(p + i);
+    acc ^= a[0] ^ a[1] ^ a[2] ^ a[3];
+  }
+  out[(int64_t)blockIdx.x * blockDim.x + threadIdx.x] = acc;
+}
+
+hipError_t read_bandwidth(const void* p, int64_t bytes, uint32_t* out, int blocks,
+                          hipStream_t stream) {
+  hipLaunchKernelGGL(read_bandwidth_kernel, dim3((unsigned)blocks), dim3(256), 0, stream,
+                     static_cast<const u32x4*>(p), bytes / 16, out);
+  return hipGetLastError();
+}
+
 hipError_t mfma_layout_probe(float* out, int op, hipStream_t stream) {
   hipLaunchKernelGGL(mfma_layout_probe_kernel, dim3(1), dim3(64), 0, stream, out, op);
   return hipGetLastError();

@@ -298,10 +298,18 @@ __global__ void __launch_bounds__(64 * kWaves) scan_generic(const ScanArgs<L> A)
       for (int ch = 0; ch < nch; ++ch) {
         Acc acc = {};
         const int row = ch * kTile + r32;
-        for (int kb = 0; kb < A.nkb; ++kb) {
-          const typename Op::Frag a = load_frag<Op, VEC>(rd, row, rowbytes, kb, h, dim);
-          const typename Op::Frag b = load_frag<Op, VEC>(rq, t, rowbytes, kb, h, dim);
-          acc = Op::mma(a, b, acc);
+        // split-d: 8 k-blocks of document and query fragments in flight per
+        // batch; blocks past nkb load as zero and add nothing.
+        for (int kb0 = 0; kb0 < A.nkb; kb0 += 8) {
+          typename Op::Frag a[8], b[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const int kb = kb0 + i;
+            a[i] = kb < A.nkb ? load_frag<Op, VEC>(rd, row, rowbytes, kb, h, dim) : Op::zero();
+            b[i] = kb < A.nkb ? load_frag<Op, VEC>(rq, t, rowbytes, kb, h, dim) : Op::zero();
+          }
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc = Op::mma(a[i], b[i], acc);
         }
         uint32_t mbyte = 1u;
         if (v.dm) mbyte = buf_load1(make_rsrc(v.dm, (uint32_t)v.td), row);

@@ -47,6 +47,7 @@ SIGNATURES = {
     "fms_length_normalize": [_p, _p, _i64, _i64, _i64, _p, _i32, _i64, _f, _p],
     "fms_varlen_normalize": [_p, _p, _i64, _p],
     "fms_debug_mfma_layout": [_p, _i32, _p],
+    "fms_debug_read_bandwidth": [_p, _i64, _p, _i32, _p],
 }
 _RESTYPES = {
     "fms_status_string": ctypes.c_char_p,

@@ -237,6 +237,15 @@ fms_status fms_varlen_normalize(float* scores, const int32_t* cu_q, int64_t N, v
  */
 fms_status fms_debug_mfma_layout(float* out, int32_t dtype_or_int8, void* stream);
 
+/*
+ * Test-only: streaming read of `bytes` (multiple of 16, 16-byte aligned)
+ * with `blocks` workgroups of 256 threads; out receives blocks*256 words.
+ * No reference counterpart: it measures the HBM read ceiling reported
+ * beside the scans' roofline and calibrates the FETCH_SIZE counter.
+ */
+fms_status fms_debug_read_bandwidth(const void* p, int64_t bytes, uint32_t* out, int32_t blocks,
+                                    void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -134,7 +134,10 @@ def test_candidates_parity(device, dtype, shape, idx_dtype):
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: DT_ID[d])
-@pytest.mark.parametrize("shape", [(128, 32, 180, 6, 5), (40, 33, 65, 3, 4), (16, 8, 10, 4, 4)],
+@pytest.mark.parametrize("shape", [(128, 32, 180, 6, 5), (40, 33, 65, 3, 4), (16, 8, 10, 4, 4),
+                                   # dim 128: the MFMA-tiled in-batch kernel
+                                   (128, 32, 180, 40, 37), (128, 1, 1, 3, 2), (128, 24, 65, 17, 9),
+                                   (128, 32, 33, 20, 3), (128, 8, 40, 512, 1024)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_inbatch_parity(device, dtype, shape):
     dim, Tq, Td, Bq, Bd = shape

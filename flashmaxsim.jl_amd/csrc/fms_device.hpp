@@ -148,24 +148,52 @@ __device__ __forceinline__ constexpr int acc_row(int r, int h) {
   return 8 * (r >> 2) + 4 * h + (r & 3);
 }
 
-// Running (max, slot) update over one chunk's 16 scores of this lane.
+// Running (max, slot) update over one chunk's 16 scores of this lane;
 // slot = chunk*16 + r identifies (chunk, register) until the final merge.
-// A score replaces the running max only when strictly greater, and the
-// running max starts at -inf, so the first valid document token wins and
-// ties keep the lowest token (forward_pair.jl:140-143).  `rowbits` has bit
-// (8*(r/4) + r%4) set for valid registers of this lane (already shifted by
-// 4*h); ALL_VALID skips the mask test.
-template <bool ALL_VALID>
-__device__ __forceinline__ void running_max(const float (&s)[16], uint32_t rowbits, int slot0,
-                                            float& mx, int& slot) {
+// Registers ascend in document row within a wave half (acc_row), so the
+// reference's sequential rule -- first valid token wins, then only a
+// strictly greater score replaces (forward_pair.jl:140-143) -- is: the
+// chunk's maximum with the LOWEST register among equal maxima, merged into
+// the running max only if strictly greater (earlier chunks win ties).
+//
+// fold_tree: a v_max3 tree gives the chunk maximum, a reverse scan the first
+// register equal to it -- short dependency chains, ~2.6 VALU ops per score.
+// Every row must hold a valid token (callers substitute masked rows).
+__device__ __forceinline__ void fold_tree(const float (&s)[16], int slot0, float& mx, int& slot) {
+  const float m0 = __builtin_fmaxf(__builtin_fmaxf(s[0], s[1]), s[2]);
+  const float m1 = __builtin_fmaxf(__builtin_fmaxf(s[3], s[4]), s[5]);
+  const float m2 = __builtin_fmaxf(__builtin_fmaxf(s[6], s[7]), s[8]);
+  const float m3 = __builtin_fmaxf(__builtin_fmaxf(s[9], s[10]), s[11]);
+  const float m4 = __builtin_fmaxf(__builtin_fmaxf(s[12], s[13]), s[14]);
+  const float m5 = __builtin_fmaxf(__builtin_fmaxf(s[15], m0), m1);
+  const float m6 = __builtin_fmaxf(__builtin_fmaxf(m2, m3), m4);
+  const float cm = __builtin_fmaxf(m5, m6);
+  int ci = 15;
+#pragma unroll
+  for (int r = 14; r >= 0; --r) ci = (s[r] == cm) ? r : ci;
+  const bool take = cm > mx;
+  mx = take ? cm : mx;
+  slot = take ? slot0 + ci : slot;
+}
+
+// running_max_seq: the sequential scan itself, with row masking, for the
+// HBM-bound scans (fewest live registers).  `rowbits` is the
+// chunk validity shifted to this lane half (bit 8*(r/4) + r%4 = register r);
+// kMasked = false skips the test for fully valid chunks.  The register index
+// r is a chunk-local immediate folded into `slot` once per chunk: three VALU
+// ops per score.
+template <bool kMasked>
+__device__ __forceinline__ void running_max_seq(const float (&s)[16], uint32_t rowbits,
+                                                int slot0, float& mx, int& slot) {
+  int rc = -1;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
-    const int bit = 8 * (r >> 2) + (r & 3);
-    bool take = s[r] > mx;
-    if (!ALL_VALID) take = take && ((rowbits >> bit) & 1u);
+    const bool ok = !kMasked || ((rowbits >> (8 * (r >> 2) + (r & 3))) & 1u);
+    const bool take = ok && s[r] > mx;
     mx = take ? s[r] : mx;
-    slot = take ? slot0 + r : slot;
+    rc = take ? r : rc;
   }
+  slot = rc >= 0 ? slot0 + rc : slot;
 }
 
 // 1-based document token of a slot for a lane in half h; 0 = none.

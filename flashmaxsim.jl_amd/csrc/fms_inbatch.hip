@@ -7,24 +7,30 @@
 //
 // Workgroup = 4 waves (one per SIMD), two workgroups per CU, 16 queries x a
 // block of DB documents.
-//   * every wave keeps QPW = 4 query tiles (32 tokens x d=128 fp16/bf16) in
+//   * every wave keeps 4 query tiles (32 tokens x d=128 fp16/bf16) in
 //     registers for the whole workgroup lifetime, so each LDS fragment read
 //     feeds 4 MFMAs;
 //   * the workgroup streams its documents in 32-token chunks: each chunk
-//     (8 KB) is fetched ONCE from L2/HBM (one coalesced 16-byte load per
-//     thread) and stored to one of two LDS buffers, XOR-swizzled so that the
-//     MFMA-layout ds_read_b128s of 8 consecutive lanes hit distinct banks;
+//     (8 KB) is fetched ONCE from L2/HBM (two coalesced 16-byte loads per
+//     thread) and stored to one of two LDS buffers with 272-byte rows, so the
+//     MFMA-layout ds_read_b128s of consecutive lanes hit distinct banks;
+//   * masked rows (dmask = 0, and rows past Td in a document's last chunk)
+//     are replaced AT LOAD TIME by a copy of the document's first valid
+//     token f.  A copy scores exactly what f scores, so the maximum is
+//     unchanged, and with first-occurrence tie breaking a copy can only win
+//     where f ties it: a winning copy maps back to f when the document is
+//     closed.  The fold therefore needs no row masks at all;
 //   * software pipeline: chunk c+3 is requested while chunk c is multiplied
 //     (chunks c+2 and c+3 in flight), chunk c+1 moves register -> LDS at the
 //     start of step c, and one barrier per step publishes it.  Loads are
-//     unconditional (past the end a zero-size buffer resource returns zeros
-//     without touching memory) and the loop has no global stores, so the
-//     compiler's in-order vmcnt accounting waits for exactly one chunk;
-//   * per chunk and wave: 8 LDS fragment reads feed 4 x 8 MFMA 32x32x16,
-//     then the per-lane running max/argmax update (the scans' epilogue,
-//     ~0.75x the MFMA time); the two workgroups on a CU have independent
-//     barriers, so one's epilogue co-executes with the other's MFMAs on each
-//     SIMD; fully masked chunks skip both;
+//     unconditional (the stream position stops at the last chunk, so loads
+//     issued past the end re-read it) and the loop has no global stores, so
+//     the compiler's in-order vmcnt accounting waits for exactly one chunk;
+//   * per chunk and wave: 8 LDS fragment reads feed 4 x 8 MFMA 32x32x16
+//     issued query by query, with each query's running max/argmax update
+//     (fold_tree, ~0.65x its MFMA time on the VALU) interleaved into the
+//     next query's MFMAs; the two workgroups on a CU have independent
+//     barriers, so the rest overlaps across workgroups on each SIMD;
 //   * per-document tape / score go to LDS and leave in one coalesced pass at
 //     the end of the block.
 // Block -> (query block, document block) is XCD-aware: consecutive block ids
@@ -42,28 +48,33 @@ namespace fms {
 namespace {
 
 constexpr int kIbWaves = 4;
-constexpr int kIbQpw = 4;
+constexpr int kIbQpw = 4;                          // query tiles per wave
+constexpr int kIbQueries = kIbWaves * kIbQpw;      // queries per block
 constexpr int kIbNkb = 8;                          // dim == 128
 constexpr int kIbRowBytes = kIbNkb * 32;           // 256 B per token
-constexpr int kIbChunkBytes = kTile * kIbRowBytes;  // 8 KB per chunk
-constexpr int kIbQueries = kIbWaves * kIbQpw;       // 16 queries per block
-constexpr int kIbUnits = kIbChunkBytes / 16 / (64 * kIbWaves);  // 16-byte units per thread
+constexpr int kIbLdsRow = kIbRowBytes + 16;        // padded LDS row (272 B)
+constexpr int kIbLdsChunk = kTile * kIbLdsRow;     // one LDS chunk buffer
+constexpr int kIbUnits = kTile * kIbRowBytes / 16 / (64 * kIbWaves);  // 16-byte units per thread
 constexpr int kXcds = 8;
 constexpr int kIbMaxChunkMasks = 1024;           // DB * nch per block
 constexpr int kIbMaxDocs = 16;                   // documents per block
 
 // LDS byte offset of 16-byte unit `u` (0..15) of chunk row `row` (0..31).
-__device__ __forceinline__ int lds_off(int row, int u) {
-  return row * kIbRowBytes + ((u ^ (row & 7)) << 4);
-}
+// Rows are padded to 272 bytes: the MFMA-layout reads of consecutive lanes
+// (consecutive rows, same unit) start 68 banks apart, i.e. on distinct
+// 16-byte bank groups for 8 (32-bank) or 16 (64-bank) lanes per pass, the
+// staging writes of 16 lanes cover one contiguous row, and the 8 fragment
+// reads of a lane are one base address plus immediate offsets.
+__device__ __forceinline__ int lds_off(int row, int u) { return row * kIbLdsRow + (u << 4); }
 
 }  // namespace
 
 // Workgroup barrier that does not drain in-flight global loads: wait only
-// for this wave's LDS writes (lgkmcnt(0)), then s_barrier.  __syncthreads()
-// would add a release fence, i.e. s_waitcnt vmcnt(0), and stall on the
-// chunk loads that are deliberately kept in flight across the barrier.  The
-// empty asm statements stop the compiler from moving LDS accesses across.
+// for this wave's LDS accesses (lgkmcnt(0)), then s_barrier.
+// __syncthreads() would add a release fence, i.e. s_waitcnt vmcnt(0), and
+// stall on the chunk loads that are deliberately kept in flight across the
+// barrier.  The empty asm statements stop the compiler from moving LDS
+// accesses across.
 __device__ __forceinline__ void lds_barrier() {
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt / expcnt unconstrained
@@ -75,8 +86,12 @@ template <class Op>
 __global__ void __launch_bounds__(64 * kIbWaves, 2) inbatch_mfma(const InBatchArgs A) {
   typedef typename Op::Acc Acc;
   typedef typename Op::Frag Frag;
-  __shared__ __attribute__((aligned(16))) uint8_t lds[2][kIbChunkBytes];
-  __shared__ uint32_t chunk_mask[kIbMaxChunkMasks];  // ballot of valid rows per (doc, chunk)
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2][kIbLdsChunk];
+  __shared__ uint32_t chunk_mask[kIbMaxChunkMasks];  // valid rows per (doc, chunk)
+  __shared__ int32_t doc_first[kIbMaxDocs];          // first valid token, -1 = none
+  __shared__ uint32_t lst_mask[kIbMaxChunkMasks];    // compacted chunk list
+  __shared__ uint32_t lst_info[kIbMaxChunkMasks];
+  __shared__ int lst_count;
   __shared__ int32_t res_tape[kIbWaves][kIbQpw][kIbMaxDocs][kTile];
   __shared__ float res_score[kIbWaves][kIbQpw][kIbMaxDocs];
 
@@ -97,12 +112,13 @@ __global__ void __launch_bounds__(64 * kIbWaves, 2) inbatch_mfma(const InBatchAr
   }
   if (qb >= nqb) return;
   const int j0 = db * A.db, j1 = (j0 + A.db < A.Bd) ? j0 + A.db : A.Bd;
+  const int ndoc = j1 - j0;
   const int Tq = A.Tq, Td = A.Td;
-  const int nch = Td > 0 ? (Td + kTile - 1) / kTile : 1;
-  const int nsteps = (j1 - j0) * nch;
+  const int nch = Td > 0 ? (Td + kTile - 1) / kTile : 1;  // <= 64
+  const int nall = ndoc * nch;
 
-  // ---- chunk validity masks of this block's documents (one ballot each) -----
-  for (int c = wave; c < nsteps; c += kIbWaves) {
+  // ---- row validity of this block's chunks (one ballot each) ----------------
+  for (int c = wave; c < nall; c += kIbWaves) {
     const int j = uniform(j0 + c / nch), ch = uniform(c % nch);
     uint32_t mb = 1u;
     if (A.dm) mb = buf_load1(make_rsrc(A.dm + (int64_t)j * Td, (uint32_t)Td), ch * kTile + r32);
@@ -129,25 +145,86 @@ __global__ void __launch_bounds__(64 * kIbWaves, 2) inbatch_mfma(const InBatchAr
     tvalid[q] = live && r32 < Tq && mb != 0u;
   }
 
+  __syncthreads();  // chunk_mask complete
+  // ---- first valid token of each document; defaults of the results ----------
+  for (int jj = wave; jj < ndoc; jj += kIbWaves) {
+    const uint32_t m = lane < nch ? chunk_mask[jj * nch + lane] : 0u;
+    const uint64_t nz = __ballot(m != 0u);
+    int f = -1;
+    if (nz != 0u) {
+      const int k = uniform(__builtin_ctzll(nz));
+      f = k * kTile + __builtin_ctz((uint32_t)uniform((int)chunk_mask[jj * nch + k]));
+    }
+    if (lane == 0) doc_first[jj] = f;
+  }
+  // A document without a valid token never closes: score 0, tape 0.
+  for (int e = tid; e < kIbWaves * kIbQpw * kIbMaxDocs * kTile; e += 64 * kIbWaves)
+    (&res_tape[0][0][0][0])[e] = 0;
+  for (int e = tid; e < kIbWaves * kIbQpw * kIbMaxDocs; e += 64 * kIbWaves)
+    (&res_score[0][0][0])[e] = 0.0f;
+  __syncthreads();  // doc_first complete
+
+  // ---- compacted chunk list ------------------------------------------------------
+  // Only chunks with at least one valid row are streamed and multiplied (a
+  // document's fully masked tail costs nothing).  Entry i: row validity
+  // lst_mask[i]; lst_info[i] = ch | jj << 6 | (last chunk of its document)
+  // << 10 | (first valid token + 1) << 11.
+  if (wave == 0) {
+    int base = 0;
+    for (int c0 = 0; c0 < nall; c0 += 64) {
+      const int c = c0 + lane;
+      const uint32_t m = c < nall ? chunk_mask[c] : 0u;
+      const uint64_t bal = __ballot(m != 0u);
+      if (m != 0u) {
+        const int pos = base + __builtin_popcountll(bal & ((1ull << lane) - 1ull));
+        const int jj = c / nch, ch = c - jj * nch;
+        lst_mask[pos] = m;
+        lst_info[pos] = (uint32_t)(ch | (jj << 6) | ((doc_first[jj] + 1) << 11));
+      }
+      base += __builtin_popcountll(bal);
+    }
+    if (lane == 0) lst_count = base;
+  }
+  __syncthreads();
+  const int nsteps = uniform(lst_count);
+  bool last[kIbMaxChunkMasks / (64 * kIbWaves)];
+#pragma unroll
+  for (int k = 0; k < kIbMaxChunkMasks / (64 * kIbWaves); ++k) {
+    const int i = tid + k * 64 * kIbWaves;
+    last[k] = i < nsteps && (i + 1 == nsteps ||
+                             ((lst_info[i + 1] >> 6) & 15u) != ((lst_info[i] >> 6) & 15u));
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < kIbMaxChunkMasks / (64 * kIbWaves); ++k)
+    if (last[k]) lst_info[tid + k * 64 * kIbWaves] |= 1u << 10;
+  __syncthreads();
+
   // ---- chunk stream -------------------------------------------------------------
-  // Thread tid moves kIbUnits 16-byte units of every chunk: unit
-  // tid + i*256 is row (tid>>4) + 16*i, column tid&15.
+  // One buffer resource spans the block's documents [j0, j1) (contiguous in
+  // D).  Thread tid moves kIbUnits 16-byte units of every chunk: unit
+  // tid + i*256 is row (tid>>4) + 16*i, column tid&15; a masked row loads
+  // the document's first valid token instead.  The stream position stops at
+  // the last list entry, so loads issued past the end re-read it.
+  const rsrc_t rd = make_rsrc(A.D + (int64_t)j0 * Td * kIbRowBytes, (uint32_t)(ndoc * Td * kIbRowBytes));
   const int urow = tid >> 4, ucol = tid & 15;
   typedef u32x4 Stage[kIbUnits];
-  auto chunk_load = [&](int c, Stage& g) {
-    const bool in = c < nsteps;
-    const int cc = in ? c : 0;
-    const int j = uniform(j0 + cc / nch), ch = uniform(cc % nch);
-    const rsrc_t rd = make_rsrc(A.D + (int64_t)j * Td * kIbRowBytes,
-                                in ? (uint32_t)Td * kIbRowBytes : 0u);
+  int ld_i = 0;  // next list entry to request
+  auto chunk_load = [&](Stage& g, uint32_t m, uint32_t info) {
+    const int ch = info & 63u, jj = (info >> 6) & 15u, f = (int)(info >> 11) - 1;
+    const int fsrc = f < 0 ? 0 : f;  // (never: listed chunks have a valid row)
 #pragma unroll
-    for (int i = 0; i < kIbUnits; ++i)
-      g[i] = buf_load16(rd, (ch * kTile + urow + 16 * i) * kIbRowBytes + ucol * 16);
+    for (int i = 0; i < kIbUnits; ++i) {
+      const int row = urow + 16 * i;
+      const int src = ((m >> row) & 1u) ? ch * kTile + row : fsrc;
+      g[i] = buf_load16(rd, (jj * Td + src) * kIbRowBytes + ucol * 16);
+    }
+    if (ld_i + 1 < nsteps) ++ld_i;
   };
-  auto lds_store = [&](int c, const Stage& g) {
+  auto lds_store = [&](int i, const Stage& g) {
 #pragma unroll
-    for (int i = 0; i < kIbUnits; ++i)
-      *reinterpret_cast<u32x4*>(&lds[c & 1][lds_off(urow + 16 * i, ucol)]) = g[i];
+    for (int u = 0; u < kIbUnits; ++u)
+      *reinterpret_cast<u32x4*>(&lds[i & 1][lds_off(urow + 16 * u, ucol)]) = g[u];
   };
 
   float mx[kIbQpw];
@@ -155,71 +232,98 @@ __global__ void __launch_bounds__(64 * kIbWaves, 2) inbatch_mfma(const InBatchAr
 #pragma unroll
   for (int q = 0; q < kIbQpw; ++q) { mx[q] = -INFINITY; slot[q] = -1; }
 
-  // One step: chunk c+1 register -> LDS, refill that register stage with
-  // chunk c+3, multiply chunk c (LDS buffer c%2) against the wave's query
-  // tiles, fold it into the running max, close its document after its last
-  // chunk.  Fully masked chunks skip the MFMAs and the fold.
-  auto step = [&](int c, Stage& g_next) {
-    lds_store(c + 1, g_next);
-    chunk_load(c + 3, g_next);
-    const int jj = uniform(c / nch), ch = uniform(c % nch);
-    const uint32_t m32 = (uint32_t)uniform((int)chunk_mask[c]);
-    if (m32 != 0u) {
-      Acc acc[kIbQpw];
+  // Close query q's document jj: merge the wave halves, map a winning
+  // substituted row back to the first valid token f, reduce the score,
+  // stage tape and score in LDS, reset the running max.
+  auto close = [&](int q, int jj, int f) {
+    int tok = slot_to_token(slot[q], h);
+    float m = mx[q];
+    merge_halves(m, tok);
+    const int t0 = tok > 0 ? tok - 1 : 0;
+    const bool real = tok > 0 && ((chunk_mask[jj * nch + (t0 >> 5)] >> (t0 & 31)) & 1u);
+    tok = real ? tok : f + 1;
+    const float part = (tvalid[q] && tok != 0) ? m : 0.0f;
+    const float score = half_sum(part);
+    if (h == 0) res_tape[wave][q][jj][r32] = tvalid[q] ? tok : 0;
+    if (lane == 0) res_score[wave][q][jj] = score;
+    mx[q] = -INFINITY;
+    slot[q] = -1;
+  };
+
+  // One step: entry i+1 register -> LDS, refill that register stage with
+  // entry i+3, multiply entry i (LDS buffer i%2) query by query with the
+  // previous query's fold interleaved, close the document after its last
+  // entry, read the list info for the next step, publish.
+  uint32_t ld_m = 0u, ld_info = 0u;  // list entry ld_i, read one step ahead
+  uint32_t cur_info = 0u;            // list entry i
+  auto step = [&](int i, Stage& g_next) {
+    lds_store(i + 1, g_next);
+    chunk_load(g_next, (uint32_t)uniform((int)ld_m), (uint32_t)uniform((int)ld_info));
+    const uint32_t info = (uint32_t)uniform((int)cur_info);
+    const int ch = info & 63u;
+    Frag a[kIbNkb];
 #pragma unroll
-      for (int q = 0; q < kIbQpw; ++q) acc[q] = Acc{};
+    for (int kb = 0; kb < kIbNkb; ++kb)
+      a[kb] = *reinterpret_cast<const Frag*>(&lds[i & 1][lds_off(r32, 2 * kb + h)]);
+    Acc acc[kIbQpw];
+    auto fold = [&](int q) {
+      float s[16];
 #pragma unroll
-      for (int kb = 0; kb < kIbNkb; ++kb) {
-        const Frag a = *reinterpret_cast<const Frag*>(&lds[c & 1][lds_off(r32, 2 * kb + h)]);
+      for (int r = 0; r < 16; ++r) s[r] = acc[q][r];
+      fold_tree(s, ch * 16, mx[q], slot[q]);
+    };
 #pragma unroll
-        for (int q = 0; q < kIbQpw; ++q) acc[q] = Op::mma(a, qf[q][kb], acc[q]);
-      }
+    for (int q = 0; q < kIbQpw; ++q) {
+      acc[q] = Acc{};
 #pragma unroll
-      for (int q = 0; q < kIbQpw; ++q) {
-        float s[16];
+      for (int kb = 0; kb < kIbNkb; ++kb) acc[q] = Op::mma(a[kb], qf[q][kb], acc[q]);
+      if (q > 0) fold(q - 1);
+    }
+    fold(kIbQpw - 1);
+    // Issue order: fragment reads, query 0's MFMAs, then per later query two
+    // MFMAs followed by (one MFMA, a slice of the previous query's fold) x 6.
+    __builtin_amdgcn_sched_group_barrier(0x100, kIbNkb, 0);  // DS reads
+    __builtin_amdgcn_sched_group_barrier(0x008, kIbNkb, 0);  // MFMA
 #pragma unroll
-        for (int r = 0; r < 16; ++r) s[r] = acc[q][r];
-        if (m32 == 0xffffffffu) {
-          running_max<true>(s, 0u, ch * 16, mx[q], slot[q]);
-        } else {
-          running_max<false>(s, m32 >> (4 * h), ch * 16, mx[q], slot[q]);
-        }
+    for (int q = 1; q < kIbQpw; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+#pragma unroll
+      for (int k = 0; k < kIbNkb - 2; ++k) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 7, 0);  // VALU
       }
     }
-    if (ch == nch - 1) {  // document done: stage tape + score in LDS
+    if (info & (1u << 10)) {
+      const int jj = (info >> 6) & 15u, f = (int)(info >> 11) - 1;
 #pragma unroll
-      for (int q = 0; q < kIbQpw; ++q) {
-        int tok = slot_to_token(slot[q], h);
-        float m = mx[q];
-        merge_halves(m, tok);
-        const float part = (tvalid[q] && tok != 0) ? m : 0.0f;
-        const float score = half_sum(part);
-        if (h == 0) res_tape[wave][q][jj][r32] = tvalid[q] ? tok : 0;
-        if (lane == 0) res_score[wave][q][jj] = score;
-        mx[q] = -INFINITY;
-        slot[q] = -1;
-      }
+      for (int q = 0; q < kIbQpw; ++q) close(q, jj, f);
     }
+    ld_m = lst_mask[ld_i];
+    ld_info = lst_info[ld_i];
+    cur_info = lst_info[i + 1 < nsteps ? i + 1 : i];
     lds_barrier();
   };
 
   if (nsteps > 0) {
     Stage g0, g1;
-    chunk_load(0, g0);
-    chunk_load(1, g1);
+    chunk_load(g0, lst_mask[0], lst_info[0]);           // entry 0
+    chunk_load(g1, lst_mask[ld_i], lst_info[ld_i]);     // entry 1
     lds_store(0, g0);
-    chunk_load(2, g0);
-    lds_barrier();  // also publishes chunk_mask
-    int c = 0;
-    for (; c + 1 < nsteps; c += 2) {  // both steps unconditional: exact vmcnt waits
-      step(c, g1);      // g1 held chunk c+1, now requests c+3
-      step(c + 1, g0);  // g0 held chunk c+2, now requests c+4
+    chunk_load(g0, lst_mask[ld_i], lst_info[ld_i]);     // entry 2
+    ld_m = lst_mask[ld_i];
+    ld_info = lst_info[ld_i];
+    cur_info = lst_info[0];
+    lds_barrier();
+    int i = 0;
+    for (; i + 1 < nsteps; i += 2) {  // both steps unconditional: exact vmcnt waits
+      step(i, g1);      // g1 held entry i+1, now requests i+3
+      step(i + 1, g0);  // g0 held entry i+2, now requests i+4
     }
-    if (c < nsteps) step(c, g1);
+    if (i < nsteps) step(i, g1);
   }
+  __syncthreads();  // results of every wave staged
 
   // ---- write the block's tape and scores (coalesced) ------------------------------
-  const int ndoc = j1 - j0;
 #pragma unroll
   for (int q = 0; q < kIbQpw; ++q) {
     if (qi[q] >= A.Bq) continue;
@@ -241,17 +345,18 @@ hipError_t launch_inbatch_mfma(int dtype_bf16, const InBatchArgs& args_in, hipSt
   A.ndb = (A.Bd + db - 1) / db;
   const dim3 grid((unsigned)(A.nqb * A.ndb)), block(64 * kIbWaves);
   if (dtype_bf16)
-    hipLaunchKernelGGL(inbatch_mfma<OpBF16>, grid, block, 0, stream, A);
+    hipLaunchKernelGGL((inbatch_mfma<OpBF16>), grid, block, 0, stream, A);
   else
-    hipLaunchKernelGGL(inbatch_mfma<OpF16>, grid, block, 0, stream, A);
+    hipLaunchKernelGGL((inbatch_mfma<OpF16>), grid, block, 0, stream, A);
   return hipGetLastError();
 }
 
+// A block's documents span one buffer resource: ndoc * Td * 256 bytes <=
+// 16 * 2048 * 256 = 8 MB under the chunk-count limit.
 bool inbatch_mfma_supported(int64_t dim, int64_t Tq, int64_t Td, const void* Q, const void* D) {
   const bool al = ((reinterpret_cast<uintptr_t>(Q) | reinterpret_cast<uintptr_t>(D)) & 15u) == 0;
   return dim == kIbNkb * 16 && Tq >= 1 && Tq <= kTile && Td >= 0 &&
-         (Td + kTile - 1) / kTile <= kIbMaxChunkMasks / kIbMaxDocs &&
-         Td * kIbRowBytes < ((int64_t)1 << 31) && al;
+         (Td + kTile - 1) / kTile <= kIbMaxChunkMasks / kIbMaxDocs && al;
 }
 
 }  // namespace fms

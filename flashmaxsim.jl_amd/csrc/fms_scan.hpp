@@ -106,11 +106,10 @@ __device__ __forceinline__ void acc_to_scores(const typename Op::Acc& acc, float
 
 __device__ __forceinline__ void update_chunk(const float (&s)[16], uint32_t m32, int h, int ch,
                                              float& mx, int& slot) {
-  if (m32 == 0xffffffffu) {
-    running_max<true>(s, 0u, ch * 16, mx, slot);
-  } else if (m32 != 0u) {
-    running_max<false>(s, m32 >> (4 * h), ch * 16, mx, slot);
-  }
+  if (m32 == 0xffffffffu)
+    running_max_seq<false>(s, 0u, ch * 16, mx, slot);
+  else if (m32 != 0u)
+    running_max_seq<true>(s, m32 >> (4 * h), ch * 16, mx, slot);
 }
 
 // Close one (pair, query tile): merge halves, write tape / partial, return

@@ -158,6 +158,57 @@ def test_inbatch_parity(device, dtype, shape):
     assert_tape(args.cpu().numpy(), a_o, _pair_sims_fn(Qf, Df, lambda p: (Qf[p[0]], Df[p[1]])), tol)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=lambda d: DT_ID[d])
+@pytest.mark.parametrize("shape", [(32, 180, 24, 21), (17, 65, 40, 33), (32, 32, 16, 16),
+                                   (8, 300, 20, 17), (5, 7, 18, 6)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_inbatch_masks_and_ties(device, dtype, shape):
+    """Non-prefix document masks, leading masked tokens, fully masked and
+    single-token documents, and exact duplicate tokens (exact ties must keep
+    the first occurrence, forward_pair.jl:140-143) on the MFMA-tiled kernel,
+    which substitutes masked rows by copies of the first valid token."""
+    Tq, Td, Bq, Bd = shape
+    dim = 128
+    rng = np.random.default_rng(Tq * 1000 + Td)
+    q32 = tokens(rng, (Bq, Tq, dim))
+    d32 = tokens(rng, (Bd, Td, dim))
+    dm = rng.random((Bd, Td)) < 0.7
+    for j in range(Bd):  # later rows copy earlier ones: exact ties
+        for _ in range(3):
+            a, b = np.sort(rng.choice(Td, 2, replace=False)) if Td > 1 else (0, 0)
+            d32[j, b] = d32[j, a]
+    dm[0, : min(Td - 1, 40)] = False          # leading masked tokens
+    dm[1, :] = False                           # no valid token
+    dm[2, :] = False
+    dm[2, Td - 1] = True                       # only the last token
+    if Td > 3:                                 # first valid token also at a later valid row
+        first = int(np.argmax(dm[3])) if dm[3].any() else 0
+        dm[3, first] = True
+        d32[3, Td - 1] = d32[3, first]
+        dm[3, Td - 1] = True
+    Qt, Qo, bf = as_feature(q32, dtype)
+    Dt, Do, _ = as_feature(d32, dtype)
+    qm = torch.from_numpy(rng.random((Bq, Tq)) < 0.9)
+    dmt = torch.from_numpy(dm)
+    S_o, a_o = oracle.inbatch_forward(Qo, Do, mask_np(qm), mask_np(dmt), bf16=bf)
+    S, args = fm.inbatch_forward(Qt.to(device), Dt.to(device), qm.to(device), dmt.to(device))
+    torch.cuda.synchronize()
+    tol = FEATURE_TOL[dtype]
+    assert_scores(S.cpu(), S_o, tol, what="S")
+    assert (S.cpu().numpy()[:, 1] == 0).all()
+    got = args.cpu().numpy()
+    assert (got[:, 1] == 0).all()
+    # every recorded token is a valid document token
+    ii, jj, tt = np.nonzero(got)
+    assert dm[jj, got[ii, jj, tt] - 1].all()
+    # mismatches only at near-ties between tokens that are not exact copies
+    Qf, Df = widened(Qo, bf), widened(Do, bf)
+    assert_tape(got, a_o, _pair_sims_fn(Qf, Df, lambda p: (Qf[p[0]], Df[p[1]])), tol)
+    for i, j, t in np.argwhere(got != a_o):
+        g, w = got[i, j, t] - 1, a_o[i, j, t] - 1
+        assert not np.array_equal(Do[j, g], Do[j, w]), (i, j, t, g, w)
+
+
 @pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: DT_ID[d])
 @pytest.mark.parametrize("case", ["small", "colpali", "splitd"])
 def test_packed_parity(device, dtype, case):

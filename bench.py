@@ -9,7 +9,7 @@ launch_candidates_scan over the whole batch (scores + argmax tape), inputs
 resident in HBM, outputs preallocated.  Prints ONE JSON line.
 
 Other workloads (--workload c3 | c4 | c4d1024 | c5) measure the in-batch,
-packed and INT8 scans the same way; they are reported in DESIGN.md.
+packed and INT8 scans the same way (each prints its own JSON line).
 """
 from __future__ import annotations
 

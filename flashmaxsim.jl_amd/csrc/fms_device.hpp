@@ -152,7 +152,7 @@ __device__ __forceinline__ constexpr int acc_row(int r, int h) {
 // slot = chunk*16 + r identifies (chunk, register) until the final merge.
 // Registers ascend in document row within a wave half (acc_row), so the
 // reference's sequential rule -- first valid token wins, then only a
-// strictly greater score replaces (forward_pair.jl:140-143) -- is: the
+// strictly greater score replaces (forward_pair.jl:82-85) -- is: the
 // chunk's maximum with the LOWEST register among equal maxima, merged into
 // the running max only if strictly greater (earlier chunks win ties).
 //

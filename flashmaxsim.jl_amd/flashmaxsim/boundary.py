@@ -7,7 +7,7 @@ package (Julia ``(dim, T, B)`` == torch ``(B, T, dim)``).
 
 | here                      | reference                                         |
 |---------------------------|---------------------------------------------------|
-| launch_pair_scan          | launch_pair_scan!        (forward_pair.jl:176-190)   |
+| launch_pair_scan          | launch_pair_scan!        (forward_pair.jl:118-132)   |
 | launch_paired_scan        | launch_paired_scan!      (forward_layouts.jl:126-143)|
 | launch_candidates_scan    | launch_candidates_scan!  (forward_layouts.jl:292-310)|
 | inbatch_device_scan       | inbatch_device_scan!     (forward_layouts.jl:202-225)|

@@ -100,7 +100,7 @@ def indices_on(prototype: torch.Tensor, idxs: torch.Tensor) -> torch.Tensor:
 # ---- forward drivers ---------------------------------------------------------------------
 
 def pair_forward(q, d, qmask=None, dmask=None, neg=None):
-    """pair_forward_ka (forward_pair.jl:155-174): (score (1,), argmax_u (Tq,))."""
+    """pair_forward_ka (forward_pair.jl:104-116): (score (1,), argmax_u (Tq,))."""
     boundary.require_device(q, d, qmask, dmask)
     _, Tq, _ = require_pair_shapes(q, d, qmask, dmask)
     argmax_u = _zeros(q, torch.int32, Tq)

@@ -1,0 +1,202 @@
+# FlashMaxSimHIPExt.jl -- weak-dependency extension of FlashMaxSim.jl that
+# routes the fused MaxSim forward on AMDGPU.jl arrays (MI355X / gfx950) to
+# libflashmaxsim_hip.so through `ccall`.
+#
+# It specialises exactly the device plugin boundary that the CUDA extension
+# specialises (ext/FlashMaxSimCUDAExt.jl:57-167 in FlashMaxSim.jl):
+#   launch_pair_scan!        src/forward_pair.jl:118-132
+#   launch_paired_scan!      src/forward_layouts.jl:126-143
+#   launch_candidates_scan!  src/forward_layouts.jl:292-310
+#   inbatch_device_scan!     src/forward_layouts.jl:202-203
+#   launch_packed_scan!      src/packed.jl:219-234
+#   launch_varlen_scan!      src/packed.jl:298-314
+#   launch_int8_pair_scan!   src/quant.jl:139-154
+#   launch_int8_paired_scan! src/quant.jl:199-217
+#   tensor_cores_active      src/ka.jl:71
+# and additionally candidates_forward_ka (src/forward_layouts.jl:272-290), so
+# the candidate layout uses the library's fused Σ_t + `neg` epilogue instead
+# of the separate `sum(partial; dims=1)` and `ifelse.` kernels.
+#
+# Arrays are passed as raw device pointers in Julia's own column-major
+# layout, which is the layout the C ABI documents; nothing is copied or
+# transposed.  Every call is enqueued on AMDGPU.jl's task-local stream and
+# returns without synchronising (src/ka.jl:3-5).  A nonzero status becomes
+# an ArgumentError, like the reference's pre-launch checks.
+#
+# Julia is not installed in the build container, so this file is written to
+# the AMDGPU.jl 1.x API and is not exercised by the repository's tests; the
+# Python host mirror (flashmaxsim.jl_amd/flashmaxsim) drives the same C ABI
+# in the test suite.
+module FlashMaxSimHIPExt
+
+using AMDGPU
+using FlashMaxSim
+
+const libfms = get(ENV, "FLASHMAXSIM_HIP_LIB",
+                   joinpath(@__DIR__, "..", "..", "lib", "libflashmaxsim_hip.so"))
+
+const FMS_F32 = Int32(0)
+const FMS_F16 = Int32(1)
+const FMS_BF16 = Int32(2)
+
+const ROCBackend = AMDGPU.ROCBackend
+
+@static if isdefined(Core, :BFloat16)
+    const FloatFeature = Union{Float16, Float32, Core.BFloat16}
+    dtype_code(::Type{Core.BFloat16}) = FMS_BF16
+else
+    const FloatFeature = Union{Float16, Float32}
+end
+dtype_code(::Type{Float32}) = FMS_F32
+dtype_code(::Type{Float16}) = FMS_F16
+
+stream_ptr() = AMDGPU.stream().stream
+dptr(x::ROCArray) = Ptr{Cvoid}(UInt(pointer(x)))
+dptr(::Nothing) = C_NULL
+
+function check(status::Int32, what::AbstractString)
+    status == 0 && return nothing
+    msg = unsafe_string(ccall((:fms_status_string, libfms), Cstring, (Int32,), status))
+    throw(ArgumentError("FlashMaxSim HIP $what: $msg"))
+end
+
+gfx950() = ccall((:fms_arch_supported, libfms), Cint, ()) == 1
+
+FlashMaxSim.tensor_cores_active(::ROCBackend, ::Type{T}) where {T<:FloatFeature} = gfx950()
+FlashMaxSim.tensor_cores_active(::ROCBackend, ::Type{Int8}) = gfx950()
+
+# ---- float scans -------------------------------------------------------------
+
+function FlashMaxSim.launch_pair_scan!(::ROCBackend, argmax_u, partial,
+                                       q::ROCMatrix{T}, d::ROCMatrix{T},
+                                       qmask, dmask) where {T<:FloatFeature}
+    dim, Tq = size(q)
+    check(ccall((:fms_launch_pair_scan, libfms), Int32,
+                (Int32, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid},
+                 Int64, Int64, Int64, Ptr{Cvoid}, Ptr{Cvoid}),
+                dtype_code(T), dptr(argmax_u), dptr(partial), dptr(q), dptr(d),
+                dptr(qmask), dptr(dmask), dim, Tq, size(d, 2), C_NULL, stream_ptr()),
+          "pair scan")
+    nothing
+end
+
+function FlashMaxSim.launch_paired_scan!(::ROCBackend, args, partial,
+                                         Q::ROCArray{T,3}, D::ROCArray{T,3},
+                                         qmask, dmask) where {T<:FloatFeature}
+    dim, Tq, B = size(Q)
+    check(ccall((:fms_launch_paired_scan, libfms), Int32,
+                (Int32, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid},
+                 Int64, Int64, Int64, Int64, Ptr{Cvoid}, Ptr{Cvoid}),
+                dtype_code(T), dptr(args), dptr(partial), dptr(Q), dptr(D),
+                dptr(qmask), dptr(dmask), dim, Tq, size(D, 2), B, C_NULL, stream_ptr()),
+          "paired scan")
+    nothing
+end
+
+function candidates_call(args, partial, scores, Q::ROCArray{T,3}, gallery, idx,
+                         qmask, dmask, N, neg) where {T<:FloatFeature}
+    dim, Tq, B = size(Q)
+    check(ccall((:fms_launch_candidates_scan, libfms), Int32,
+                (Int32, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Int32,
+                 Ptr{Cvoid}, Ptr{Cvoid}, Int64, Int64, Int64, Int64, Int64, Int64,
+                 Ptr{Cvoid}, Float32, Ptr{Cvoid}),
+                dtype_code(T), dptr(args), dptr(partial), dptr(Q), dptr(gallery),
+                dptr(idx), Int32(sizeof(eltype(idx))), dptr(qmask), dptr(dmask),
+                dim, Tq, B, size(gallery, 2), N, size(idx, 1),
+                dptr(scores), Float32(neg), stream_ptr()),
+          "candidate scan")
+    nothing
+end
+
+FlashMaxSim.launch_candidates_scan!(::ROCBackend, args, partial, Q::ROCArray{T,3},
+                                    gallery::ROCArray{T,3}, idx, qmask, dmask,
+                                    N) where {T<:FloatFeature} =
+    candidates_call(args, partial, nothing, Q, gallery, idx, qmask, dmask, N, 0)
+
+# Fused driver: Σ_t and the `neg` fill happen inside the scan kernel
+# (replaces src/forward_layouts.jl:285-287).  Same outputs as the reference
+# driver: (scores (C,B) in score_eltype(T), args (Tq,C,B)).
+function FlashMaxSim.candidates_forward_ka(backend::ROCBackend, Q::ROCArray{T,3},
+                                           gallery::ROCArray{T,3},
+                                           idxs::AbstractMatrix{<:Integer},
+                                           qmask::AbstractMatrix{Bool},
+                                           dmask::AbstractMatrix{Bool},
+                                           neg::T) where {T<:FloatFeature}
+    _, Tq, B, _, N = FlashMaxSim.require_candidates_shapes(Q, gallery, idxs, qmask, dmask)
+    idx = FlashMaxSim.indices_on(Q, idxs)
+    C = size(idx, 1)
+    args = FlashMaxSim.zeros_like(Q, Int32, Tq, C, B)
+    S = similar(Q, FlashMaxSim.score_eltype(T), C, B)
+    candidates_call(args, nothing, S, Q, gallery, idx, qmask, dmask, N, neg)
+    S, args
+end
+
+function FlashMaxSim.inbatch_device_scan!(::ROCBackend, S, args,
+                                          Q::ROCArray{T,3}, D::ROCArray{T,3},
+                                          qmask, dmask) where {T<:FloatFeature}
+    dim, Tq, Bq = size(Q)
+    check(ccall((:fms_inbatch_device_scan, libfms), Int32,
+                (Int32, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid},
+                 Int64, Int64, Int64, Int64, Int64, Ptr{Cvoid}),
+                dtype_code(T), dptr(S), dptr(args), dptr(Q), dptr(D),
+                dptr(qmask), dptr(dmask), dim, Tq, Bq, size(D, 2), size(D, 3), stream_ptr()),
+          "in-batch scan")
+    nothing
+end
+
+function FlashMaxSim.launch_packed_scan!(::ROCBackend, args, partial, q::ROCMatrix{T},
+                                         packed::ROCMatrix{T}, cu::ROCVector{Int32},
+                                         qmask) where {T<:FloatFeature}
+    dim, Tq = size(q)
+    check(ccall((:fms_launch_packed_scan, libfms), Int32,
+                (Int32, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid},
+                 Int64, Int64, Int64, Int64, Ptr{Cvoid}, Ptr{Cvoid}),
+                dtype_code(T), dptr(args), dptr(partial), dptr(q), dptr(packed), dptr(cu),
+                dptr(qmask), dim, Tq, length(cu) - 1, size(packed, 2), C_NULL, stream_ptr()),
+          "packed scan")
+    nothing
+end
+
+function FlashMaxSim.launch_varlen_scan!(::ROCBackend, args, partial, Qp::ROCMatrix{T},
+                                         Dp::ROCMatrix{T}, cu_q::ROCVector{Int32},
+                                         cu_d::ROCVector{Int32}) where {T<:FloatFeature}
+    check(ccall((:fms_launch_varlen_scan, libfms), Int32,
+                (Int32, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid},
+                 Int64, Int64, Int64, Int64, Int64, Ptr{Cvoid}, Ptr{Cvoid}),
+                dtype_code(T), dptr(args), dptr(partial), dptr(Qp), dptr(Dp),
+                dptr(cu_q), dptr(cu_d), size(Qp, 1), size(args, 1), size(args, 2),
+                size(Qp, 2), size(Dp, 2), C_NULL, stream_ptr()),
+          "varlen scan")
+    nothing
+end
+
+# ---- INT8 scans ----------------------------------------------------------------
+
+function FlashMaxSim.launch_int8_pair_scan!(::ROCBackend, args, partial, qc::ROCMatrix{Int8},
+                                            qs::ROCVector{Float32}, dc::ROCMatrix{Int8},
+                                            ds::ROCVector{Float32}, qmask, dmask)
+    dim, Tq = size(qc)
+    check(ccall((:fms_launch_int8_pair_scan, libfms), Int32,
+                (Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid},
+                 Ptr{Cvoid}, Ptr{Cvoid}, Int64, Int64, Int64, Ptr{Cvoid}, Ptr{Cvoid}),
+                dptr(args), dptr(partial), dptr(qc), dptr(qs), dptr(dc), dptr(ds),
+                dptr(qmask), dptr(dmask), dim, Tq, size(dc, 2), C_NULL, stream_ptr()),
+          "INT8 pair scan")
+    nothing
+end
+
+function FlashMaxSim.launch_int8_paired_scan!(::ROCBackend, args, partial,
+                                              Qc::ROCArray{Int8,3}, Qs::ROCMatrix{Float32},
+                                              Dc::ROCArray{Int8,3}, Ds::ROCMatrix{Float32},
+                                              qmask, dmask)
+    dim, Tq, B = size(Qc)
+    check(ccall((:fms_launch_int8_paired_scan, libfms), Int32,
+                (Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid},
+                 Ptr{Cvoid}, Ptr{Cvoid}, Int64, Int64, Int64, Int64, Ptr{Cvoid}, Ptr{Cvoid}),
+                dptr(args), dptr(partial), dptr(Qc), dptr(Qs), dptr(Dc), dptr(Ds),
+                dptr(qmask), dptr(dmask), dim, Tq, size(Dc, 2), B, C_NULL, stream_ptr()),
+          "INT8 paired scan")
+    nothing
+end
+
+end # module

@@ -6,9 +6,9 @@
  * boundary (the `launch_*_scan!` / `inbatch_device_scan!` generic functions
  * that a weak-dependency extension specialises per backend; the CUDA
  * extension overrides them in ext/FlashMaxSimCUDAExt.jl:57-167).  A Julia
- * AMDGPU.jl extension binds them with `ccall` (INTEGRATION.md shows the
- * binding); the Python host mirror in flashmaxsim.jl_amd/flashmaxsim binds
- * them with ctypes.
+ * AMDGPU.jl extension binds them with `ccall`
+ * (flashmaxsim.jl_amd/julia/ext/FlashMaxSimHIPExt.jl); the Python host
+ * mirror in flashmaxsim.jl_amd/flashmaxsim binds them with ctypes.
  *
  * Conventions (all from the reference):
  *   - Column-major (Julia) layout.  A feature array of Julia size
@@ -74,7 +74,7 @@ const char* fms_version(void);
 
 /*
  * Pair scan.  Replaces launch_pair_scan!(backend, argmax_u, partial, q, d,
- * qmask, dmask) (src/forward_pair.jl:176-190; CUDA override
+ * qmask, dmask) (src/forward_pair.jl:118-132; CUDA override
  * ext/FlashMaxSimCUDAExt.jl:57-68).  q is (dim,Tq), d is (dim,Td);
  * argmax_u/partial are (Tq,).  score (nullable, length 1) receives Sigma_t,
  * replacing sum_length1 (src/ka.jl:49-53).
@@ -214,7 +214,7 @@ fms_status fms_int8_dots(int32_t* out, const int8_t* qc, const int8_t* dc,
 
 /*
  * Query-length normalisation epilogues (src/normalize.jl:4-46,
- * src/forward_pair.jl:222-228, src/packed.jl:316-354).  scores (nrows,ncols)
+ * src/forward_pair.jl:153-173, src/packed.jl:316-354).  scores (nrows,ncols)
  * column-major, scaled in place by inv = 1/max(count, 1) (fp32, multiply):
  *   fms_length_normalize: count = count(qmask[:,col]) per column (qmask
  *     (Tq,ncols); NULL = Tq); if idx is non-NULL (candidate layout,

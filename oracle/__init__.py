@@ -153,7 +153,7 @@ def widen(x: np.ndarray, bf16: bool = False) -> np.ndarray:
 # ---- layouts ---------------------------------------------------------------------
 
 def pair_forward(q, d, qmask=None, dmask=None, bf16=False):
-    """pair_forward_host (src/forward_pair.jl:103-153). q (Tq,dim), d (Td,dim)."""
+    """pair_forward_host (src/forward_pair.jl:45-95). q (Tq,dim), d (Td,dim)."""
     q, d = _c(q), _c(d)
     code = _dtype_code(q, bf16)
     Tq, dim = q.shape

@@ -18,12 +18,12 @@
  *     sums run in fp32 (dot_accum, src/kernels_forward.jl:16-21).  The
  *     reference itself accumulates BFloat16 in BFloat16 (dot_accum(T)=T);
  *     this oracle pins the fp32-accumulate mathematics instead.
- *   - The per-tile GEMM (src/forward_pair.jl:134, BLAS mul!) is restated as
+ *   - The per-tile GEMM (src/forward_pair.jl:76, BLAS mul!) is restated as
  *     an in-order k loop, which is exactly the KA token kernels' order
  *     (src/kernels_forward.jl:45-48).  BLAS's blocked order is not pinned.
  *   - Running max per query token: first valid document token wins, then
- *     strictly greater replaces (src/forward_pair.jl:140-143).
- *   - Sigma_t in fp32, ascending t (src/forward_pair.jl:148-151).
+ *     strictly greater replaces (src/forward_pair.jl:82-85).
+ *   - Sigma_t in fp32, ascending t (src/forward_pair.jl:90-93).
  *
  * Build: see oracle/Makefile (gcc -O2 -fopenmp -ffp-contract=off).
  */
@@ -121,7 +121,7 @@ static const char* advance(const void* base, int64_t elems, int dtype) {
 /* ---- pair core ----------------------------------------------------------- */
 
 /*
- * Restates pair_forward_host! (src/forward_pair.jl:117-153) for fp32
+ * Restates pair_forward_host! (src/forward_pair.jl:59-95) for fp32
  * accumulation.  q is (dim, Tq), d is (dim, Td), masks are Bool bytes
  * (NULL = all true, as true_mask, src/colocation.jl:4-6).  Writes argmax_u
  * (Tq) and mx (Tq); mx is the per-token partial (0 for a masked token or an
@@ -224,7 +224,7 @@ int fmso_max_threads(void) {
 #endif
 }
 
-/* pair_forward_host (src/forward_pair.jl:103-109).  partial may be NULL. */
+/* pair_forward_host (src/forward_pair.jl:45-51).  partial may be NULL. */
 float fmso_pair_forward(int dtype, const void* q, const void* d,
                         const uint8_t* qmask, const uint8_t* dmask,
                         int64_t dim, int64_t Tq, int64_t Td,

@@ -6,7 +6,7 @@ C oracle, by materialising the similarity matrix in numpy fp64 and taking
 the first maximum (np.argmax) over valid document tokens -- the definition
 MaxSim(q, d) = sum_t max_u <q_t, d_u> with first-valid-wins ties
 (src/dense.jl:26-56).  The closed-form cases come from the reference's
-tests (test_regressions.jl:173-194, 244-254).
+tests (test_regressions.jl:65-86, 136-147).
 
 Run:  python tests/golden/make_golden.py
 """

@@ -41,7 +41,7 @@ def test_mfma_accumulator_layout(device, op):
 def _masks(rng, B, Tq, Td, kind):
     if kind == "none":
         return None, None
-    if kind == "pattern":  # test_ka_cpu.jl:234-236 patterns
+    if kind == "pattern":  # test_ka_cpu.jl:19-21 patterns
         qm = np.array([[(t + 1) % 2 == 1 for t in range(Tq)] for _ in range(B)])
         dm = np.array([[(u + 1) % 3 != 0 for u in range(Td)] for _ in range(B)])
     else:  # random, with one fully masked document row
@@ -65,7 +65,7 @@ PAIRED_SHAPES = [
     (40, 33, 65, 2),     # tile-straddling dim/Tq/Td (test_cuda.jl:102-117)
     (768, 8, 17, 2),     # split-d (test_cuda.jl:174-187)
     (256, 32, 64, 3),    # fast kernel, second register bucket
-    (16, 12, 130, 3),    # host DOC_TILE straddle (test_regressions.jl:196-206)
+    (16, 12, 130, 3),    # host DOC_TILE straddle (test_regressions.jl:88-98)
     (8, 3, 5, 2),
     (12, 5, 9, 2),       # row not a 16-byte multiple for 16-bit types
 ]
@@ -145,7 +145,7 @@ def test_inbatch_parity(device, dtype, shape):
     Qt, Qo, bf = as_feature(tokens(rng, (Bq, Tq, dim)), dtype)
     Dt, Do, _ = as_feature(tokens(rng, (Bd, Td, dim)), dtype)
     lens = rng.integers(min(Td, 3), Td + 1, size=Bd)
-    lens[0] = 0  # an empty document contributes 0 (test_regressions.jl:173-194)
+    lens[0] = 0  # an empty document contributes 0 (test_regressions.jl:65-86)
     dm = torch.from_numpy(np.arange(Td)[None, :] < lens[:, None])
     qm = torch.from_numpy(rng.random((Bq, Tq)) < 0.9)
     S_o, a_o = oracle.inbatch_forward(Qo, Do, mask_np(qm), mask_np(dm), bf16=bf)
@@ -165,7 +165,7 @@ def test_inbatch_parity(device, dtype, shape):
 def test_inbatch_masks_and_ties(device, dtype, shape):
     """Non-prefix document masks, leading masked tokens, fully masked and
     single-token documents, and exact duplicate tokens (exact ties must keep
-    the first occurrence, forward_pair.jl:140-143) on the MFMA-tiled kernel,
+    the first occurrence, forward_pair.jl:82-85) on the MFMA-tiled kernel,
     which substitutes masked rows by copies of the first valid token."""
     Tq, Td, Bq, Bd = shape
     dim = 128
@@ -267,7 +267,7 @@ def test_varlen_parity(device, dtype):
 # ---- known answers from the reference's own tests, on the device ----------------------
 
 def test_all_negative_dots_keep_true_max(device):
-    """test_regressions.jl:244-254: q = ones(4,3), d = -ones(4,5) => -12, tape > 0."""
+    """test_regressions.jl:136-147: q = ones(4,3), d = -ones(4,5) => -12, tape > 0."""
     for dtype in DTYPES:
         q = torch.ones(3, 4, dtype=dtype, device=device)
         d = -torch.ones(5, 4, dtype=dtype, device=device)
@@ -277,7 +277,7 @@ def test_all_negative_dots_keep_true_max(device):
 
 
 def test_empty_doc_scores_zero_not_neg(device):
-    """test_regressions.jl:173-194: a fully masked document contributes 0."""
+    """test_regressions.jl:65-86: a fully masked document contributes 0."""
     rng = np.random.default_rng(11)
     q = torch.from_numpy(tokens(rng, (5, 8))).to(device)
     d = torch.from_numpy(tokens(rng, (6, 8))).to(device)
@@ -287,7 +287,7 @@ def test_empty_doc_scores_zero_not_neg(device):
 
 
 def test_candidate_neg_and_normalize(device):
-    """test_forward.jl:41-49 / test_regressions.jl:133-149: invalid idx => neg, kept by normalize."""
+    """test_forward.jl:41-49 / test_regressions.jl:25-41: invalid idx => neg, kept by normalize."""
     rng = np.random.default_rng(7)
     Q = torch.from_numpy(tokens(rng, (2, 4, 8))).to(device)
     G = torch.from_numpy(tokens(rng, (4, 5, 8))).to(device)

@@ -68,14 +68,14 @@ def check_tape(got, want, S, valid_u, rtol=1e-5):
 # ---- known answers from the reference's tests -----------------------------------------------
 
 def test_all_negative_dots():
-    """test_regressions.jl:244-254: q=ones(4,3), d=-ones(4,5) => -12, every tape entry 1."""
+    """test_regressions.jl:136-147: q=ones(4,3), d=-ones(4,5) => -12, every tape entry 1."""
     s, a, p = oracle.pair_forward(np.ones((3, 4), np.float32), -np.ones((5, 4), np.float32))
     assert s == np.float32(-12.0)
     assert (a == 1).all() and (p == -4.0).all()
 
 
 def test_empty_document_scores_zero():
-    """test_regressions.jl:173-194: all-false dmask => score 0 (not neg), tape 0."""
+    """test_regressions.jl:65-86: all-false dmask => score 0 (not neg), tape 0."""
     rng = np.random.default_rng(11)
     q, d = tokens(rng, (5, 8)), tokens(rng, (6, 8))
     s, a, p = oracle.pair_forward(q, d, None, np.zeros(6, np.uint8))
@@ -85,7 +85,7 @@ def test_empty_document_scores_zero():
 
 
 def test_invalid_candidate_gets_neg():
-    """test_forward.jl:40-49 / test_ka_cpu.jl:265-272: idx 0 => neg, tape 0."""
+    """test_forward.jl:41-49 / test_ka_cpu.jl:50-57: idx 0 => neg, tape 0."""
     rng = np.random.default_rng(3)
     Q, G = tokens(rng, (4, 8, 16)), tokens(rng, (12, 10, 16))
     idxs = np.array([[1, 5, 0], [2, 6, 1], [3, 7, 2], [4, 8, 3]], np.int64)  # Julia [1 2 3 4; 5 6 7 8; 0 1 2 3]
@@ -100,7 +100,7 @@ def test_invalid_candidate_gets_neg():
 
 
 def test_inbatch_doc_chunk_known_answers():
-    """test_regressions.jl:257-262."""
+    """test_regressions.jl:149-154."""
     assert oracle.inbatch_doc_chunk(4, 128, 32, 32, 10_000) == 128
     assert oracle.inbatch_doc_chunk(8, 128, 32, 32, 10_000) == 64
     assert oracle.inbatch_doc_chunk(4, 128, 32, 32, 0) == 1

@@ -43,6 +43,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="target duration of the bounded CPU baseline sample")
+    ap.add_argument("--grouping", default="auto", choices=["auto", "always", "never"],
+                    help="candidate pair order (document-grouped or output order)")
     ap.add_argument("--check", type=int, default=256,
                     help="pairs re-scored by the CPU oracle as a full-size parity spot check")
     return ap.parse_args()
@@ -374,6 +376,7 @@ def main():
     from flashmaxsim import boundary
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    boundary.candidates_grouping(args.grouping)
     runner = {"c2": run_c2, "c3": run_c3, "c4": run_c4, "c5": run_c5, "read": run_read,
               "c4d1024": lambda *a: run_c4(*a, dim=1024)}[args.workload]
     r = runner(args, torch, fm, boundary, dev)

@@ -5,10 +5,14 @@
 // forward_pair.jl:14-21, quant.jl:62-94, packed.jl:138-151), picks the
 // kernel and enqueues it on the caller's stream without synchronising.
 #include <hip/hip_runtime.h>
+#include <math.h>
 #include <stdint.h>
 #include <string.h>
 
+#include <atomic>
+
 #include "../../include/flashmaxsim_hip.h"
+#include "fms_group.hpp"
 #include "fms_inbatch.hpp"
 #include "fms_misc.hpp"
 #include "fms_scan_decl.hpp"
@@ -54,25 +58,73 @@ bool vec_ok(int esz, int64_t dim, std::initializer_list<const void*> ptrs) {
   return true;
 }
 
+// Launches the scan for a float feature type (dtype already validated).
+template <class L>
+hipError_t launch_float(int32_t dtype, const L& lay, int dim, int rows, int64_t npairs,
+                        int32_t* args, float* partial, float* scores, float neg, bool vec,
+                        hipStream_t st) {
+  switch (dtype) {
+    case FMS_F16:
+      return launch_scan<OpF16, L>(lay, dim, rows, npairs, args, partial, scores, neg, vec, false, st);
+    case FMS_BF16:
+      return launch_scan<OpBF16, L>(lay, dim, rows, npairs, args, partial, scores, neg, vec, false, st);
+    default:
+      return launch_scan<OpF32, L>(lay, dim, rows, npairs, args, partial, scores, neg, vec, false, st);
+  }
+}
+
 template <class L>
 fms_status run_float(int32_t dtype, const L& lay, int dim, int rows, int64_t npairs,
                      int32_t* args, float* partial, float* scores, float neg, bool vec,
                      hipStream_t st) {
-  hipError_t e;
-  switch (dtype) {
-    case FMS_F16:
-      e = launch_scan<OpF16, L>(lay, dim, rows, npairs, args, partial, scores, neg, vec, false, st);
-      break;
-    case FMS_BF16:
-      e = launch_scan<OpBF16, L>(lay, dim, rows, npairs, args, partial, scores, neg, vec, false, st);
-      break;
-    case FMS_F32:
-      e = launch_scan<OpF32, L>(lay, dim, rows, npairs, args, partial, scores, neg, vec, false, st);
-      break;
-    default:
-      return FMS_EUNSUPPORTED;
+  if (elem_bytes(dtype) == 0) return FMS_EUNSUPPORTED;
+  return from_hip(launch_float(dtype, lay, dim, rows, npairs, args, partial, scores, neg, vec, st));
+}
+
+// Candidate pair grouping (fms_candidates_grouping): 0 auto, 1 always, 2 never.
+std::atomic<int> g_grouping{0};
+
+// Smallest candidate batch worth the five extra launches of the document sort.
+constexpr int64_t kGroupMinPairs = 16384;
+
+// Whether a candidate scan of P pairs over N documents of dbytes each runs in
+// document order.  Auto: P >= kGroupMinPairs; the O(N) counter passes of the
+// sort (16 bytes per document) stay under 5% of the document bytes the
+// ungrouped scan would read; and the document reads saved are worth giving
+// up the query-tile reuse of output order (consecutive candidates of one
+// query): at least 30% of the reads, estimated for indices drawn uniformly
+// over 1..N, where P draws hit N*(1 - exp(-P/N)) distinct documents.
+// Pair ids and document ids must fit 32 bits.
+bool group_candidates(int64_t P, int64_t N, int64_t dbytes) {
+  if (P < 1 || P >= INT32_MAX || N < 1 || N >= INT32_MAX) return false;
+  const int mode = g_grouping.load(std::memory_order_relaxed);
+  if (mode == 2) return false;
+  if (mode == 1) return true;
+  if (P < kGroupMinPairs || (double)(N + 1) * 16.0 > 0.05 * (double)P * (double)dbytes)
+    return false;
+  const double distinct = -(double)N * expm1(-(double)P / (double)N);
+  return distinct <= 0.7 * (double)P;
+}
+
+// Runs launch(layout) on the candidate layout, in document order when
+// group_candidates says so (workspace from the library pool, released on
+// the same stream), otherwise in output order.  An allocation failure falls
+// back to output order: the results are identical either way.
+template <class Launch>
+fms_status run_candidates(const LayCand& lay, int64_t npairs, hipStream_t st, Launch&& launch) {
+  if (group_candidates(npairs, lay.N, lay.dbytes)) {
+    void* ws = nullptr;
+    if (workspace_alloc(&ws, group_workspace_bytes(npairs, lay.N), st) == hipSuccess) {
+      LayCandSorted sl;
+      sl.c = lay;
+      hipError_t e = group_pairs_by_document(lay.idx, lay.idx64, npairs, lay.N, ws, &sl.order, st);
+      if (e == hipSuccess) e = launch(sl);
+      const hipError_t ef = workspace_free(ws, st);
+      return from_hip(e != hipSuccess ? e : ef);
+    }
+    (void)hipGetLastError();  // clear the failed allocation; scan in output order
   }
-  return from_hip(e);
+  return from_hip(launch(lay));
 }
 
 }  // namespace
@@ -159,8 +211,11 @@ fms_status fms_launch_candidates_scan(int32_t dtype, int32_t* args, float* parti
   lay.C = C;
   lay.Tq = (int)Tq;
   lay.Td = (int)Td;
-  return run_float(dtype, lay, (int)dim, (int)Tq, C * B, args, partial, scores, neg,
-                   vec_ok(esz, dim, {Q, gallery}), as_stream(stream));
+  const bool vec = vec_ok(esz, dim, {Q, gallery});
+  const hipStream_t st = as_stream(stream);
+  return run_candidates(lay, C * B, st, [&](const auto& L) -> hipError_t {
+    return launch_float(dtype, L, (int)dim, (int)Tq, C * B, args, partial, scores, neg, vec, st);
+  });
 }
 
 fms_status fms_inbatch_device_scan(int32_t dtype, float* S, int32_t* args, const void* Q,
@@ -326,8 +381,17 @@ fms_status fms_launch_int8_candidates_scan(int32_t* args, float* partial, const 
   lay.Td = (int)Td;
   const bool vec = vec_ok(1, dim, {Qc, Gc});
   const bool ds_vec = (Td % 4 == 0) && aligned16(Gs);
-  return from_hip(launch_scan<OpI8, LayCand>(lay, (int)dim, (int)Tq, C * B, args, partial, scores,
-                                             neg, vec, ds_vec, as_stream(stream)));
+  const hipStream_t st = as_stream(stream);
+  return run_candidates(lay, C * B, st, [&](const auto& L) -> hipError_t {
+    typedef typename std::decay<decltype(L)>::type Lay;
+    return launch_scan<OpI8, Lay>(L, (int)dim, (int)Tq, C * B, args, partial, scores, neg, vec,
+                                  ds_vec, st);
+  });
+}
+
+int32_t fms_candidates_grouping(int32_t mode) {
+  if (mode < 0 || mode > 2) return -1;
+  return g_grouping.exchange(mode);
 }
 
 fms_status fms_int8_dots(int32_t* out, const int8_t* qc, const int8_t* dc, int64_t dim,

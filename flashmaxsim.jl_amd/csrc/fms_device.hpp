@@ -42,6 +42,26 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kRsrcWord3);
 }
 
+// Resource whose base and size are forced into scalar registers.  Every
+// sequence a wave reads is uniform across the wave; when the compiler
+// cannot prove that for a loop-carried value it builds the descriptor in
+// vector registers and wraps each load in a waterfall loop, which also
+// defeats the in-order vmcnt accounting the prefetch relies on.
+// Wave-uniform copies of 32- / 64-bit values.  __builtin_amdgcn_readfirstlane
+// returns a signed int: it must become uint32_t before any widening, or a
+// low word with bit 31 set sign-extends into the high word.
+__device__ __forceinline__ uint32_t rfl32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_readfirstlane((int)v);
+}
+__device__ __forceinline__ uint64_t rfl64(uint64_t v) {
+  return ((uint64_t)rfl32((uint32_t)(v >> 32)) << 32) | (uint64_t)rfl32((uint32_t)v);
+}
+
+__device__ __forceinline__ rsrc_t make_rsrc_u(const void* base, uint32_t bytes) {
+  return make_rsrc(reinterpret_cast<const void*>(rfl64(reinterpret_cast<uint64_t>(base))),
+                   rfl32(bytes));
+}
+
 __device__ __forceinline__ u32x4 buf_load16(rsrc_t r, int voff) {
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0));
 }

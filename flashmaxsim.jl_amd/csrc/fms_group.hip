@@ -1,0 +1,228 @@
+// fms_group.hip -- counting sort of candidate pairs by document, and the
+// workspace pool it draws from.
+//
+// Five small launches: zero the N+1 counters, histogram the pairs (one
+// atomic per pair), exclusive scan of the counters (tile sums, scan of the
+// tile sums, apply), atomic scatter of the pair ids.  Cost is linear in
+// C*B + N and small next to the scan it feeds (~1.5 MB of traffic for
+// C*B = 256k, N = 100k).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <mutex>
+
+#include "fms_group.hpp"
+
+namespace fms {
+
+namespace {
+
+constexpr int kScanThreads = 1024;                  // one block = 16 waves
+constexpr int kScanPer = 4;                         // counters per thread
+constexpr int kScanTile = kScanThreads * kScanPer;  // counters per block
+constexpr int kFlat = 256;                          // threads of the flat kernels
+
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+inline unsigned flat_blocks(int64_t n) {
+  const int64_t b = cdiv(n, kFlat);
+  return (unsigned)(b < 1 ? 1 : (b > 65536 ? 65536 : b));
+}
+
+__device__ __forceinline__ int64_t load_index(const void* idx, int idx64, int64_t p) {
+  return idx64 ? static_cast<const int64_t*>(idx)[p] : (int64_t) static_cast<const int32_t*>(idx)[p];
+}
+
+// Exclusive scan of one value per thread over a kScanThreads block; *total
+// receives the block sum.  Every thread of the block must call it.
+__device__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* total) {
+  __shared__ uint32_t wsum[kScanThreads / 64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  uint32_t x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t y = __shfl_up(x, o);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) wsum[w] = x;
+  __syncthreads();
+  if (w == 0) {
+    uint32_t s = lane < kScanThreads / 64 ? wsum[lane] : 0u;
+#pragma unroll
+    for (int o = 1; o < kScanThreads / 64; o <<= 1) {
+      const uint32_t y = __shfl_up(s, o);
+      if (lane >= o) s += y;
+    }
+    if (lane < kScanThreads / 64) wsum[lane] = s;  // inclusive wave totals
+  }
+  __syncthreads();
+  const uint32_t r = (w > 0 ? wsum[w - 1] : 0u) + x - v;
+  *total = wsum[kScanThreads / 64 - 1];
+  __syncthreads();  // wsum is reused by the next call
+  return r;
+}
+
+}  // namespace
+
+__global__ void __launch_bounds__(kFlat) group_zero_kernel(uint32_t* c, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * kFlat;
+  for (int64_t i = (int64_t)blockIdx.x * kFlat + threadIdx.x; i < n; i += stride) c[i] = 0u;
+}
+
+// counts[j-1] += 1 for every pair with 1 <= j <= N, counts[N] += 1 otherwise.
+__global__ void __launch_bounds__(kFlat) group_hist_kernel(const void* idx, int idx64, int64_t P,
+                                                           int64_t N, uint32_t* counts) {
+  const int64_t stride = (int64_t)gridDim.x * kFlat;
+  for (int64_t p = (int64_t)blockIdx.x * kFlat + threadIdx.x; p < P; p += stride) {
+    const int64_t j = load_index(idx, idx64, p);
+    atomicAdd(&counts[(j >= 1 && j <= N) ? j - 1 : N], 1u);
+  }
+}
+
+// sums[b] = sum of counters of tile b.
+__global__ void __launch_bounds__(kScanThreads) scan_tile_sums_kernel(const uint32_t* c, int64_t n,
+                                                                      uint32_t* sums) {
+  const int64_t base = (int64_t)blockIdx.x * kScanTile + (int64_t)threadIdx.x * kScanPer;
+  uint32_t s = 0u;
+#pragma unroll
+  for (int i = 0; i < kScanPer; ++i)
+    if (base + i < n) s += c[base + i];
+  uint32_t tot;
+  block_exclusive_scan(s, &tot);
+  if (threadIdx.x == 0) sums[blockIdx.x] = tot;
+}
+
+// Exclusive scan of the nb tile sums in place (one block, carried over
+// 1024-entry slices).
+__global__ void __launch_bounds__(kScanThreads) scan_sums_kernel(uint32_t* sums, int64_t nb) {
+  uint32_t carry = 0u;
+  for (int64_t b0 = 0; b0 < nb; b0 += kScanThreads) {
+    const int64_t i = b0 + threadIdx.x;
+    const uint32_t v = i < nb ? sums[i] : 0u;
+    uint32_t tot;
+    const uint32_t ex = block_exclusive_scan(v, &tot);
+    if (i < nb) sums[i] = carry + ex;
+    carry += tot;
+  }
+}
+
+// Counters -> exclusive offsets, in place.
+__global__ void __launch_bounds__(kScanThreads) scan_apply_kernel(uint32_t* c, int64_t n,
+                                                                  const uint32_t* sums) {
+  const int64_t base = (int64_t)blockIdx.x * kScanTile + (int64_t)threadIdx.x * kScanPer;
+  uint32_t v[kScanPer];
+  uint32_t s = 0u;
+#pragma unroll
+  for (int i = 0; i < kScanPer; ++i) {
+    v[i] = base + i < n ? c[base + i] : 0u;
+    s += v[i];
+  }
+  uint32_t tot;
+  uint32_t ex = block_exclusive_scan(s, &tot) + sums[blockIdx.x];
+#pragma unroll
+  for (int i = 0; i < kScanPer; ++i) {
+    if (base + i < n) c[base + i] = ex;
+    ex += v[i];
+  }
+}
+
+// order[cursor[key]++] = (p, document of p).
+__global__ void __launch_bounds__(kFlat) group_scatter_kernel(const void* idx, int idx64, int64_t P,
+                                                              int64_t N, uint32_t* cursor,
+                                                              PairRef* order) {
+  const int64_t stride = (int64_t)gridDim.x * kFlat;
+  for (int64_t p = (int64_t)blockIdx.x * kFlat + threadIdx.x; p < P; p += stride) {
+    const int64_t j = load_index(idx, idx64, p);
+    const bool valid = j >= 1 && j <= N;
+    const uint32_t pos = atomicAdd(&cursor[valid ? j - 1 : N], 1u);
+    PairRef r;
+    r.p = (int32_t)p;
+    r.j = valid ? (int32_t)(j - 1) : -1;
+    order[pos] = r;
+  }
+}
+
+size_t group_workspace_bytes(int64_t npairs, int64_t N) {
+  const int64_t ncount = N + 1;
+  return align256((size_t)npairs * sizeof(PairRef)) + align256((size_t)ncount * 4) +
+         align256((size_t)cdiv(ncount, kScanTile) * 4);
+}
+
+hipError_t group_pairs_by_document(const void* idx, int idx64, int64_t npairs, int64_t N,
+                                   void* workspace, const PairRef** order_out,
+                                   hipStream_t stream) {
+  const int64_t ncount = N + 1;
+  const int64_t nb = cdiv(ncount, kScanTile);
+  char* w = static_cast<char*>(workspace);
+  PairRef* order = reinterpret_cast<PairRef*>(w);
+  uint32_t* counts = reinterpret_cast<uint32_t*>(w + align256((size_t)npairs * sizeof(PairRef)));
+  uint32_t* sums = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(counts) +
+                                               align256((size_t)ncount * 4));
+  hipLaunchKernelGGL(group_zero_kernel, dim3(flat_blocks(ncount)), dim3(kFlat), 0, stream, counts,
+                     ncount);
+  hipLaunchKernelGGL(group_hist_kernel, dim3(flat_blocks(npairs)), dim3(kFlat), 0, stream, idx,
+                     idx64, npairs, N, counts);
+  hipLaunchKernelGGL(scan_tile_sums_kernel, dim3((unsigned)nb), dim3(kScanThreads), 0, stream,
+                     counts, ncount, sums);
+  hipLaunchKernelGGL(scan_sums_kernel, dim3(1), dim3(kScanThreads), 0, stream, sums, nb);
+  hipLaunchKernelGGL(scan_apply_kernel, dim3((unsigned)nb), dim3(kScanThreads), 0, stream, counts,
+                     ncount, sums);
+  hipLaunchKernelGGL(group_scatter_kernel, dim3(flat_blocks(npairs)), dim3(kFlat), 0, stream, idx,
+                     idx64, npairs, N, counts, order);
+  *order_out = order;
+  return hipGetLastError();
+}
+
+// ---- workspace pool -------------------------------------------------------------
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_pool_mutex;
+hipMemPool_t g_pool[kMaxDevices] = {};
+
+hipError_t stream_device(hipStream_t stream, int* dev) {
+  if (stream == nullptr) return hipGetDevice(dev);
+  hipDevice_t d;
+  const hipError_t e = hipStreamGetDevice(stream, &d);
+  *dev = (int)d;
+  return e;
+}
+
+hipError_t device_pool(int dev, hipMemPool_t* pool) {
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_pool_mutex);
+  if (!g_pool[dev]) {
+    hipMemPoolProps props = {};
+    props.allocType = hipMemAllocationTypePinned;
+    props.handleTypes = hipMemHandleTypeNone;
+    props.location.type = hipMemLocationTypeDevice;
+    props.location.id = dev;
+    hipMemPool_t p = nullptr;
+    hipError_t e = hipMemPoolCreate(&p, &props);
+    if (e != hipSuccess) return e;
+    uint64_t keep = UINT64_MAX;  // never trim at synchronisation points
+    e = hipMemPoolSetAttribute(p, hipMemPoolAttrReleaseThreshold, &keep);
+    if (e != hipSuccess) return e;
+    g_pool[dev] = p;
+  }
+  *pool = g_pool[dev];
+  return hipSuccess;
+}
+
+}  // namespace
+
+hipError_t workspace_alloc(void** ptr, size_t bytes, hipStream_t stream) {
+  int dev = 0;
+  hipError_t e = stream_device(stream, &dev);
+  if (e != hipSuccess) return e;
+  hipMemPool_t pool;
+  e = device_pool(dev, &pool);
+  if (e != hipSuccess) return e;
+  return hipMallocFromPoolAsync(ptr, bytes, pool, stream);
+}
+
+hipError_t workspace_free(void* ptr, hipStream_t stream) { return hipFreeAsync(ptr, stream); }
+
+}  // namespace fms

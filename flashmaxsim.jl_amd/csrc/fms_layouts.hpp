@@ -1,13 +1,15 @@
-// fms_layouts.hpp -- how each reference layout maps a linear pair id p to
-// one (query, document) pair.  Output cells are always p-major: the tape /
-// partial of pair p occupy [p*rows, (p+1)*rows) and its score is scores[p],
-// which is exactly the reference's column-major (Tq, C, B) / (Tq, B) /
-// (Tq, Bd, Bq) / (max_q, N) layouts.
+// fms_layouts.hpp -- how each reference layout maps a scan position k to
+// one (query, document) pair and its output slot.  Output cells are always
+// pair-major: the tape / partial of output slot o occupy [o*rows,
+// (o+1)*rows) and its score is scores[o], which is exactly the reference's
+// column-major (Tq, C, B) / (Tq, B) / (Tq, Bd, Bq) / (max_q, N) layouts.
+// Every layout but LayCandSorted scans in output order (o = k).
 #pragma once
 
 #include <stdint.h>
 
 #include "fms_device.hpp"
+#include "fms_group.hpp"
 
 namespace fms {
 
@@ -22,7 +24,42 @@ struct PairView {
   const float* ds;    // int8 document scales
   int td;             // document tokens (0 = empty / invalid)
   bool valid;         // false only for an out-of-range candidate index
+  int64_t out;        // output slot (pair id) of this pair
 };
+
+// Read-only element at a wave-uniform index through the constant address
+// space, so the backend reads it with a scalar load.  A vector load here
+// would be followed by a full vmcnt drain of the wave's chunk prefetch.
+template <class T>
+__device__ __forceinline__ T sload(const T* p, int64_t i) {
+  typedef __attribute__((address_space(4))) const T* cptr;
+  return ((cptr)p)[i];
+}
+
+// The same view with every field moved to scalar registers.  A view is a
+// function of uniform values only, but the compiler cannot always prove
+// that after it has been carried through a loop; a buffer resource built
+// from a pointer it believes divergent becomes a per-lane waterfall loop
+// around every load.
+template <class T>
+__device__ __forceinline__ T* uniform_ptr(T* p) {
+  return reinterpret_cast<T*>(rfl64(reinterpret_cast<uint64_t>(p)));
+}
+
+__device__ __forceinline__ PairView uniform_view(const PairView& v) {
+  PairView u;
+  u.q = uniform_ptr(v.q);
+  u.qm = uniform_ptr(v.qm);
+  u.qs = uniform_ptr(v.qs);
+  u.tq = (int)rfl32((uint32_t)v.tq);
+  u.d = uniform_ptr(v.d);
+  u.dm = uniform_ptr(v.dm);
+  u.ds = uniform_ptr(v.ds);
+  u.td = (int)rfl32((uint32_t)v.td);
+  u.valid = rfl32(v.valid ? 1u : 0u) != 0u;
+  u.out = (int64_t)rfl64((uint64_t)v.out);
+  return u;
+}
 
 __device__ __forceinline__ int64_t clamp64(int64_t v, int64_t lo, int64_t hi) {
   return v < lo ? lo : (v > hi ? hi : v);
@@ -46,7 +83,7 @@ struct LayPaired {
     v.q = Q + b * qbytes; v.qm = qm ? qm + b * Tq : nullptr; v.qs = Qs ? Qs + b * Tq : nullptr;
     v.tq = Tq;
     v.d = D + b * dbytes; v.dm = dm ? dm + b * Td : nullptr; v.ds = Ds ? Ds + b * Td : nullptr;
-    v.td = Td; v.valid = true;
+    v.td = Td; v.valid = true; v.out = b;
     return v;
   }
 };
@@ -61,8 +98,8 @@ struct LayCand {
   int Tq, Td, idx64;
   __device__ PairView get(int64_t p) const {
     const int64_t b = p / C;
-    const int64_t j = idx64 ? static_cast<const int64_t*>(idx)[p]
-                            : (int64_t) static_cast<const int32_t*>(idx)[p];
+    const int64_t j = idx64 ? sload(static_cast<const int64_t*>(idx), p)
+                            : (int64_t)sload(static_cast<const int32_t*>(idx), p);
     PairView v;
     v.q = Q + b * qbytes; v.qm = qm ? qm + b * Tq : nullptr; v.qs = Qs ? Qs + b * Tq : nullptr;
     v.tq = Tq;
@@ -70,6 +107,32 @@ struct LayCand {
     const int64_t jj = v.valid ? j - 1 : 0;
     v.d = G + jj * dbytes; v.dm = dm ? dm + jj * Td : nullptr; v.ds = Gs ? Gs + jj * Td : nullptr;
     v.td = v.valid ? Td : 0;
+    v.out = p;
+    return v;
+  }
+};
+
+// The candidate layout scanned in document order (group_pairs_by_document):
+// position k is pair order[k].p, so the pairs that share a document are
+// adjacent and the waves that score them read it together.
+struct LayCandSorted {
+  LayCand c;
+  const PairRef* order;
+  __device__ PairView get(int64_t k) const {
+    PairRef r;
+    r.p = sload(&order[k].p, 0);
+    r.j = sload(&order[k].j, 0);
+    const int64_t p = r.p, b = p / c.C;
+    PairView v;
+    v.q = c.Q + b * c.qbytes; v.qm = c.qm ? c.qm + b * c.Tq : nullptr;
+    v.qs = c.Qs ? c.Qs + b * c.Tq : nullptr;
+    v.tq = c.Tq;
+    v.valid = r.j >= 0;
+    const int64_t jj = v.valid ? r.j : 0;
+    v.d = c.G + jj * c.dbytes; v.dm = c.dm ? c.dm + jj * c.Td : nullptr;
+    v.ds = c.Gs ? c.Gs + jj * c.Td : nullptr;
+    v.td = v.valid ? c.Td : 0;
+    v.out = p;
     return v;
   }
 };
@@ -85,7 +148,7 @@ struct LayInBatch {
     PairView v;
     v.q = Q + i * qbytes; v.qm = qm ? qm + i * Tq : nullptr; v.qs = nullptr; v.tq = Tq;
     v.d = D + j * dbytes; v.dm = dm ? dm + j * Td : nullptr; v.ds = nullptr; v.td = Td;
-    v.valid = true;
+    v.valid = true; v.out = p;
     return v;
   }
 };
@@ -98,13 +161,13 @@ struct LayPacked {
   int64_t ntok, rowbytes;
   int Tq;
   __device__ PairView get(int64_t b) const {
-    const int64_t a = clamp64((int64_t)cu[b] - 1, 0, ntok);
-    const int64_t z = clamp64(clamp64((int64_t)cu[b + 1] - 1, a, ntok), a,
+    const int64_t a = clamp64((int64_t)sload(cu, b) - 1, 0, ntok);
+    const int64_t z = clamp64(clamp64((int64_t)sload(cu, b + 1) - 1, a, ntok), a,
                               a + max_seq_tokens(rowbytes));
     PairView v;
     v.q = q; v.qm = qm; v.qs = nullptr; v.tq = Tq;
     v.d = tok + a * rowbytes; v.dm = nullptr; v.ds = nullptr; v.td = (int)(z - a);
-    v.valid = true;
+    v.valid = true; v.out = b;
     return v;
   }
 };
@@ -116,15 +179,15 @@ struct LayVarlen {
   int64_t nq, nd, rowbytes;
   int max_q;
   __device__ PairView get(int64_t n) const {
-    const int64_t qa = clamp64((int64_t)cu_q[n] - 1, 0, nq);
-    const int64_t qz = clamp64(clamp64((int64_t)cu_q[n + 1] - 1, qa, nq), qa, qa + max_seq_tokens(rowbytes));
-    const int64_t da = clamp64((int64_t)cu_d[n] - 1, 0, nd);
-    const int64_t dz = clamp64(clamp64((int64_t)cu_d[n + 1] - 1, da, nd), da, da + max_seq_tokens(rowbytes));
+    const int64_t qa = clamp64((int64_t)sload(cu_q, n) - 1, 0, nq);
+    const int64_t qz = clamp64(clamp64((int64_t)sload(cu_q, n + 1) - 1, qa, nq), qa, qa + max_seq_tokens(rowbytes));
+    const int64_t da = clamp64((int64_t)sload(cu_d, n) - 1, 0, nd);
+    const int64_t dz = clamp64(clamp64((int64_t)sload(cu_d, n + 1) - 1, da, nd), da, da + max_seq_tokens(rowbytes));
     PairView v;
     v.q = Qt + qa * rowbytes; v.qm = nullptr; v.qs = nullptr;
     v.tq = (int)((qz - qa) < max_q ? (qz - qa) : max_q);
     v.d = Dt + da * rowbytes; v.dm = nullptr; v.ds = nullptr; v.td = (int)(dz - da);
-    v.valid = true;
+    v.valid = true; v.out = n;
     return v;
   }
 };

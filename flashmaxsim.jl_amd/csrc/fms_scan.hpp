@@ -1,16 +1,24 @@
 // fms_scan.hpp -- fused MaxSim scan kernels (pair / paired / candidates /
 // in-batch-by-pair / packed / varlen), fp16 / bf16 / fp32 / int8.
 //
-// One wave owns a contiguous run of pairs and processes them one after the
-// other (candidate pairs p = c + C*b of one query b are consecutive, so the
-// query tile stays in registers across them).  Per pair and 32-token query
+// One wave owns a run of scan positions and processes their pairs one after
+// the other.  In output order (every layout but LayCandSorted) the run is
+// contiguous: candidate pairs p = c + C*b of one query b are consecutive, so
+// the query tile stays in registers across them.  In document order
+// (LayCandSorted) the waves of a workgroup take interleaved positions, so
+// the kWaves waves of a workgroup score kWaves consecutive entries of the
+// document order at the same time: pairs that share a document read it
+// together, through one L2, once.  Per pair and 32-token query
 // tile, the document streams through in 32-token chunks; each chunk is one
 // MFMA per k-block and one running max/argmax update per accumulator
 // register.  Nothing of size Tq x Td ever reaches HBM.
 //
 // Two kernel shapes:
-//   scan_fast<Op, L, NKB>: dim == NKB' * KB for NKB' <= NKB, 16-byte aligned
-//     rows.  The query tile is register resident (NKB fragments), the next
+//   scan_fast<Op, L, NKB>: dim == NKB * KB exactly, 16-byte aligned rows.
+//     The loads and MFMAs of a step are unconditional, so the compiler's
+//     in-order vmcnt accounting waits for exactly the chunk it multiplies
+//     and never drains the prefetch.  The query tile is register resident
+//     (NKB fragments), the next
 //     chunk (possibly of the next pair) is prefetched into a second register
 //     buffer while the current one is multiplied.
 //   scan_generic<Op, L, VEC>: any dim (split-d: the query fragment is
@@ -26,6 +34,12 @@
 #include "fms_layouts.hpp"
 
 namespace fms {
+
+// Layouts whose positions are interleaved across the waves of a workgroup.
+template <class L>
+struct interleaved { static constexpr bool value = false; };
+template <>
+struct interleaved<LayCandSorted> { static constexpr bool value = true; };
 
 template <class L>
 struct ScanArgs {
@@ -46,7 +60,8 @@ struct ScanArgs {
 template <class Op, int NKB>
 struct Chunk {
   typename Op::Frag a[NKB];
-  uint32_t mbyte;                 // document mask byte of row lane%32
+  uint32_t mbyte;                 // document mask byte of row lane%32 (0 when the
+                                  // pair has no mask: test with mask_ok)
   float ds[Op::kInt ? 16 : 1];    // int8: document scale of each accumulator row
 };
 
@@ -54,16 +69,43 @@ struct Chunk {
 template <class Op, int NKB>
 struct QTile {
   typename Op::Frag f[NKB];
-  float qscale;   // int8 query scale of this lane's token
-  bool tvalid;    // this lane's query token exists and is unmasked
+  float qscale;    // int8 query scale of this lane's token
+  uint32_t mbyte;  // query mask byte of this lane's token, raw (0 when there is
+                   // no mask).  Tested only at tile close, so nothing waits for
+                   // the load before the MFMAs.
+  int t;           // this lane's query token
 };
 
 // ---- shared pieces ---------------------------------------------------------------
 
+// Scan positions of this wave: first, first + stride, ... (cnt of them).
+template <class L>
+__device__ __forceinline__ void wave_positions(const ScanArgs<L>& A, int64_t& first,
+                                               int64_t& stride, int& cnt) {
+  const int wib = uniform((int)(threadIdx.x >> 6));
+  int64_t rem;
+  if constexpr (interleaved<L>::value) {
+    first = (int64_t)blockIdx.x * kWaves * A.ppw + wib;
+    stride = kWaves;
+    rem = A.npairs > first ? (A.npairs - first + kWaves - 1) / kWaves : 0;
+  } else {
+    first = ((int64_t)blockIdx.x * kWaves + wib) * A.ppw;
+    stride = 1;
+    rem = A.npairs > first ? A.npairs - first : 0;
+  }
+  cnt = (int)(rem < A.ppw ? rem : A.ppw);
+}
+
+// A raw mask byte (read unconditionally from a zero-size resource when the
+// mask pointer is NULL) and whether it marks a valid token.
+__device__ __forceinline__ bool mask_ok(const void* mask, uint32_t raw) {
+  return mask == nullptr || raw != 0u;
+}
+
 // Validity of this lane's chunk row (row lane%32 of chunk ch) -> wave ballot.
 __device__ __forceinline__ uint32_t chunk_rows_valid(const PairView& v, int ch, int r32,
                                                      uint32_t mbyte) {
-  const bool ok = (ch * kTile + r32 < v.td) && (mbyte != 0u);
+  const bool ok = (ch * kTile + r32 < v.td) && mask_ok(v.dm, mbyte);
   return (uint32_t)__ballot(ok);
 }
 
@@ -71,7 +113,7 @@ template <class Op>
 __device__ __forceinline__ void load_ds(float (&ds)[Op::kInt ? 16 : 1], const PairView& v, int ch,
                                         int h, bool vec) {
   if constexpr (Op::kInt) {
-    const rsrc_t rs = make_rsrc(v.ds, (uint32_t)v.td * 4u);
+    const rsrc_t rs = make_rsrc_u(v.ds, (uint32_t)v.td * 4u);
     if (vec) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
@@ -115,7 +157,7 @@ __device__ __forceinline__ void update_chunk(const float (&s)[16], uint32_t m32,
 // Close one (pair, query tile): merge halves, write tape / partial, return
 // this tile's contribution to the pair score (same value in every lane).
 template <class L>
-__device__ __forceinline__ float finish_tile(const ScanArgs<L>& A, int64_t p, int qt, int r32,
+__device__ __forceinline__ float finish_tile(const ScanArgs<L>& A, int64_t out, int qt, int r32,
                                              int h, bool tvalid, float mx, int slot) {
   int tok = slot_to_token(slot, h);
   merge_halves(mx, tok);
@@ -123,7 +165,7 @@ __device__ __forceinline__ float finish_tile(const ScanArgs<L>& A, int64_t p, in
   const int arg = tvalid ? tok : 0;
   const int t = qt * kTile + r32;
   if (h == 0 && t < A.rows) {
-    const int64_t o = p * (int64_t)A.rows + t;
+    const int64_t o = out * (int64_t)A.rows + t;
     if (A.args) A.args[o] = arg;
     if (A.partial) A.partial[o] = part;
   }
@@ -131,9 +173,9 @@ __device__ __forceinline__ float finish_tile(const ScanArgs<L>& A, int64_t p, in
 }
 
 template <class L>
-__device__ __forceinline__ void write_score(const ScanArgs<L>& A, int64_t p, bool valid,
+__device__ __forceinline__ void write_score(const ScanArgs<L>& A, int64_t out, bool valid,
                                             float score, int lane) {
-  if (A.scores && lane == 0) A.scores[p] = valid ? score : A.neg;
+  if (A.scores && lane == 0) A.scores[out] = valid ? score : A.neg;
 }
 
 // ---- fast kernel ------------------------------------------------------------------
@@ -142,53 +184,55 @@ template <class Op, int NKB>
 __device__ __forceinline__ void load_chunk(Chunk<Op, NKB>& c, const PairView& v, int ch, int nkb,
                                            int rowbytes, int lane_off, int r32, int h,
                                            bool ds_vec) {
-  const rsrc_t rd = make_rsrc(v.d, (uint32_t)v.td * (uint32_t)rowbytes);
+  const rsrc_t rd = make_rsrc_u(v.d, (uint32_t)v.td * (uint32_t)rowbytes);
   const int base = ch * kTile * rowbytes + lane_off;
 #pragma unroll
-  for (int kb = 0; kb < NKB; ++kb)
-    if (kb < nkb) c.a[kb] = Op::load(rd, base + kb * Op::kKb * Op::kEsz);
-  if (v.dm) {
-    const rsrc_t rm = make_rsrc(v.dm, (uint32_t)v.td);
-    c.mbyte = buf_load1(rm, ch * kTile + r32);
-  } else {
-    c.mbyte = 1u;
-  }
+  for (int kb = 0; kb < NKB; ++kb) c.a[kb] = Op::load(rd, base + kb * Op::kKb * Op::kEsz);
+  // Unconditional load (a zero-size resource reads 0 when there is no
+  // mask): conditional loads make the compiler's vmcnt count path
+  // dependent, and it then drains the prefetch.
+  const bool has_m = v.dm != nullptr;
+  const uint32_t mraw = buf_load1(make_rsrc_u(has_m ? (const void*)v.dm : (const void*)v.d,
+                                              has_m ? (uint32_t)v.td : 0u),
+                                  ch * kTile + r32);
+  c.mbyte = mraw;
   load_ds<Op>(c.ds, v, ch, h, ds_vec);
 }
 
 template <class Op, int NKB>
 __device__ __forceinline__ void load_qtile(QTile<Op, NKB>& q, const PairView& v, int qt, int nkb,
                                            int rowbytes, int lane_off, int r32) {
-  const rsrc_t rq = make_rsrc(v.q, (uint32_t)v.tq * (uint32_t)rowbytes);
+  const rsrc_t rq = make_rsrc_u(v.q, (uint32_t)v.tq * (uint32_t)rowbytes);
   const int base = qt * kTile * rowbytes + lane_off;
 #pragma unroll
-  for (int kb = 0; kb < NKB; ++kb)
-    q.f[kb] = (kb < nkb) ? Op::load(rq, base + kb * Op::kKb * Op::kEsz) : Op::zero();
-  const int t = qt * kTile + r32;
-  uint32_t mb = 1u;
-  if (v.qm) mb = buf_load1(make_rsrc(v.qm, (uint32_t)v.tq), t);
-  q.tvalid = (t < v.tq) && (mb != 0u);
+  for (int kb = 0; kb < NKB; ++kb) q.f[kb] = Op::load(rq, base + kb * Op::kKb * Op::kEsz);
+  q.t = qt * kTile + r32;
+  const bool has_m = v.qm != nullptr;
+  const uint32_t mraw = buf_load1(make_rsrc_u(has_m ? (const void*)v.qm : (const void*)v.q,
+                                              has_m ? (uint32_t)v.tq : 0u),
+                                  q.t);
+  q.mbyte = mraw;
   q.qscale = 0.0f;
-  if constexpr (Op::kInt) q.qscale = __builtin_bit_cast(float, buf_load4(make_rsrc(v.qs, (uint32_t)v.tq * 4u), t * 4));
+  if constexpr (Op::kInt) q.qscale = __builtin_bit_cast(float, buf_load4(make_rsrc_u(v.qs, (uint32_t)v.tq * 4u), q.t * 4));
 }
 
 template <class Op, class L, int NKB>
 __global__ void __launch_bounds__(64 * kWaves) scan_fast(const ScanArgs<L> A) {
   typedef typename Op::Acc Acc;
   const int lane = threadIdx.x & 63, r32 = lane & 31, h = lane >> 5;
-  const int wave = uniform((int)(blockIdx.x * kWaves + (threadIdx.x >> 6)));
-  const int64_t p0 = (int64_t)wave * A.ppw;
-  if (p0 >= A.npairs) return;
-  const int64_t p1 = (p0 + A.ppw < A.npairs) ? p0 + A.ppw : A.npairs;
+  int64_t first, stride;
+  int cnt;
+  wave_positions(A, first, stride, cnt);
+  if (cnt <= 0) return;
   const int rowbytes = A.dim * Op::kEsz;
   const int lane_off = r32 * rowbytes + h * Op::kEpl * Op::kEsz;
   const int nkb = A.nkb;
   const bool ds_vec = A.ds_vec != 0;
 
-  // wave cursor: pair p, query tile qt, chunk ch of nch
-  int64_t p = p0;
+  // wave cursor: position index pi (pair view v), query tile qt, chunk ch of nch
+  int pi = 0;
   int qt = 0, ch = 0;
-  PairView v = A.lay.get(p);
+  PairView v = uniform_view(A.lay.get(first));
   int nch = v.td > 0 ? (v.td + kTile - 1) / kTile : 1;
 
   Chunk<Op, NKB> bufA, bufB;
@@ -205,48 +249,67 @@ __global__ void __launch_bounds__(64 * kWaves) scan_fast(const ScanArgs<L> A) {
   // tile / pair when this was its last chunk.  Returns false after the
   // wave's final chunk.
   auto step = [&](Chunk<Op, NKB>& cur, Chunk<Op, NKB>& nxt) -> bool {
+    // Row validity of `cur` first: its mask byte is the last load of the
+    // previous step, so this waits for `cur` (needed next anyway) and for
+    // nothing issued in this step.
+    const uint32_t m32 = chunk_rows_valid(v, ch, r32, cur.mbyte);
     if (ch == 0 && (v.q != q_src || qt != q_qt)) {
       load_qtile<Op, NKB>(q, v, qt, nkb, rowbytes, lane_off, r32);
       q_src = v.q;
       q_qt = qt;
     }
     // advance a copy of the cursor and prefetch its chunk
-    int64_t np = p;
+    int npi = pi;
     int nqt_i = qt, nch_i = ch + 1, nnch = nch;
     PairView nv = v;
     if (nch_i >= nch) {
       nch_i = 0;
       if (++nqt_i >= A.nqt) {
         nqt_i = 0;
-        ++np;
-        if (np < p1) {
-          nv = A.lay.get(np);
+        ++npi;
+        // The layouts read idx / order / cu with unchecked scalar loads; the
+        // position stays valid even if such a load is speculated.
+        const int64_t kpos = first + (int64_t)(npi < cnt ? npi : pi) * stride;
+        if (npi < cnt) {
+          nv = uniform_view(A.lay.get(kpos));
           nnch = nv.td > 0 ? (nv.td + kTile - 1) / kTile : 1;
         }
       }
     }
-    const bool more = np < p1;
-    if (more) load_chunk<Op, NKB>(nxt, nv, nch_i, nkb, rowbytes, lane_off, r32, h, ds_vec);
+    const bool more = npi < cnt;
+    // Unconditional: after the wave's last chunk it re-reads the current one
+    // (an L2 hit), so every step issues the same loads and the MFMAs below
+    // wait only for the chunk they multiply.
+    if (more)
+      load_chunk<Op, NKB>(nxt, nv, nch_i, nkb, rowbytes, lane_off, r32, h, ds_vec);
+    else
+      load_chunk<Op, NKB>(nxt, v, ch, nkb, rowbytes, lane_off, r32, h, ds_vec);
+    // Keep the prefetch ahead of the MFMAs: the scheduler would otherwise
+    // sink the independent loads below them and nothing would overlap.
+    __builtin_amdgcn_sched_barrier(0);
 
     Acc acc = {};
 #pragma unroll
-    for (int kb = 0; kb < NKB; ++kb)
-      if (kb < nkb) acc = Op::mma(cur.a[kb], q.f[kb], acc);
+    for (int kb = 0; kb < NKB; ++kb) acc = Op::mma(cur.a[kb], q.f[kb], acc);
     float s[16];
     acc_to_scores<Op>(acc, q.qscale, cur.ds, s);
-    const uint32_t m32 = chunk_rows_valid(v, ch, r32, cur.mbyte);
     update_chunk(s, m32, h, ch, mx, slot);
 
     if (ch == nch - 1) {
-      score += finish_tile(A, p, qt, r32, h, q.tvalid, mx, slot);
+      // The empty asm pins the query-mask test here: hoisted next to its
+      // load, it would make the compiler wait for the whole prefetch.
+      uint32_t qmb = q.mbyte;
+      asm volatile("" : "+v"(qmb));
+      const bool tvalid = q.t < v.tq && mask_ok(v.qm, qmb);
+      score += finish_tile(A, v.out, qt, r32, h, tvalid, mx, slot);
       mx = -INFINITY;
       slot = -1;
       if (qt == A.nqt - 1) {
-        write_score(A, p, v.valid, score, lane);
+        write_score(A, v.out, v.valid, score, lane);
         score = 0.0f;
       }
     }
-    p = np; qt = nqt_i; ch = nch_i; nch = nnch; v = nv;
+    pi = npi; qt = nqt_i; ch = nch_i; nch = nnch; v = nv;
     return more;
   };
 
@@ -272,26 +335,25 @@ template <class Op, class L, bool VEC>
 __global__ void __launch_bounds__(64 * kWaves) scan_generic(const ScanArgs<L> A) {
   typedef typename Op::Acc Acc;
   const int lane = threadIdx.x & 63, r32 = lane & 31, h = lane >> 5;
-  const int wave = uniform((int)(blockIdx.x * kWaves + (threadIdx.x >> 6)));
-  const int64_t p0 = (int64_t)wave * A.ppw;
-  if (p0 >= A.npairs) return;
-  const int64_t p1 = (p0 + A.ppw < A.npairs) ? p0 + A.ppw : A.npairs;
+  int64_t first, stride;
+  int cnt;
+  wave_positions(A, first, stride, cnt);
   const int dim = A.dim;
   const int rowbytes = dim * Op::kEsz;
 
-  for (int64_t p = p0; p < p1; ++p) {
-    const PairView v = A.lay.get(p);
+  for (int pi = 0; pi < cnt; ++pi) {
+    const PairView v = uniform_view(A.lay.get(first + pi * stride));
     const int nch = v.td > 0 ? (v.td + kTile - 1) / kTile : 1;
-    const rsrc_t rq = make_rsrc(v.q, (uint32_t)v.tq * (uint32_t)rowbytes);
-    const rsrc_t rd = make_rsrc(v.d, (uint32_t)v.td * (uint32_t)rowbytes);
+    const rsrc_t rq = make_rsrc_u(v.q, (uint32_t)v.tq * (uint32_t)rowbytes);
+    const rsrc_t rd = make_rsrc_u(v.d, (uint32_t)v.td * (uint32_t)rowbytes);
     float score = 0.0f;
     for (int qt = 0; qt < A.nqt; ++qt) {
       const int t = qt * kTile + r32;
       uint32_t mb = 1u;
-      if (v.qm) mb = buf_load1(make_rsrc(v.qm, (uint32_t)v.tq), t);
+      if (v.qm) mb = buf_load1(make_rsrc_u(v.qm, (uint32_t)v.tq), t);
       const bool tvalid = (t < v.tq) && (mb != 0u);
       float qscale = 0.0f;
-      if constexpr (Op::kInt) qscale = __builtin_bit_cast(float, buf_load4(make_rsrc(v.qs, (uint32_t)v.tq * 4u), t * 4));
+      if constexpr (Op::kInt) qscale = __builtin_bit_cast(float, buf_load4(make_rsrc_u(v.qs, (uint32_t)v.tq * 4u), t * 4));
       float mx = -INFINITY;
       int slot = -1;
       for (int ch = 0; ch < nch; ++ch) {
@@ -311,28 +373,29 @@ __global__ void __launch_bounds__(64 * kWaves) scan_generic(const ScanArgs<L> A)
           for (int i = 0; i < 8; ++i) acc = Op::mma(a[i], b[i], acc);
         }
         uint32_t mbyte = 1u;
-        if (v.dm) mbyte = buf_load1(make_rsrc(v.dm, (uint32_t)v.td), row);
+        if (v.dm) mbyte = buf_load1(make_rsrc_u(v.dm, (uint32_t)v.td), row);
         float ds[Op::kInt ? 16 : 1];
         load_ds<Op>(ds, v, ch, h, false);
         float s[16];
         acc_to_scores<Op>(acc, qscale, ds, s);
         update_chunk(s, chunk_rows_valid(v, ch, r32, mbyte), h, ch, mx, slot);
       }
-      score += finish_tile(A, p, qt, r32, h, tvalid, mx, slot);
+      score += finish_tile(A, v.out, qt, r32, h, tvalid, mx, slot);
     }
-    write_score(A, p, v.valid, score, lane);
+    write_score(A, v.out, v.valid, score, lane);
   }
 }
 
 // ---- host-side launcher -------------------------------------------------------------
 
-// Fast-kernel bucket (register-resident k-blocks) for a given nkb; 0 = none.
+// Fast-kernel instantiation for a given nkb (k-blocks per token); 0 = none,
+// use the generic kernel.  16-bit features: dim 64 / 128 / 256; int8: dim
+// 64 / 128 / 256; fp32 always uses the generic kernel.
 template <class Op>
-constexpr int fast_bucket(int nkb) {
-  if (Op::kEsz == 4) return 0;  // fp32 uses the generic kernel
-  const int b1 = (Op::kKb == 16) ? 8 : 4;   // dim <= 128
-  const int b2 = 2 * b1;                    // dim <= 256
-  return nkb <= b1 ? b1 : (nkb <= b2 ? b2 : 0);
+constexpr int fast_nkb(int nkb) {
+  if (Op::kEsz == 4) return 0;
+  const int b = (Op::kKb == 16) ? 4 : 2;
+  return (nkb == b || nkb == 2 * b || nkb == 4 * b) ? nkb : 0;
 }
 
 inline int pairs_per_wave(int64_t npairs) {
@@ -365,15 +428,19 @@ hipError_t launch_scan(const L& lay, int dim, int rows, int64_t npairs, int32_t*
   const dim3 grid((unsigned)((waves + kWaves - 1) / kWaves));
   const dim3 block(64 * kWaves);
   const bool fast_ok = vec && (dim % Op::kKb == 0) && dim > 0;
-  const int bucket = fast_ok ? fast_bucket<Op>(A.nkb) : 0;
+  const int nkb_fast = fast_ok ? fast_nkb<Op>(A.nkb) : 0;
   if constexpr (Op::kEsz != 4) {
-    constexpr int b1 = (Op::kKb == 16) ? 8 : 4;
-    if (bucket == b1) {
-      hipLaunchKernelGGL((scan_fast<Op, L, b1>), grid, block, 0, stream, A);
+    constexpr int b = (Op::kKb == 16) ? 4 : 2;
+    if (nkb_fast == b) {
+      hipLaunchKernelGGL((scan_fast<Op, L, b>), grid, block, 0, stream, A);
       return hipGetLastError();
     }
-    if (bucket == 2 * b1) {
-      hipLaunchKernelGGL((scan_fast<Op, L, 2 * b1>), grid, block, 0, stream, A);
+    if (nkb_fast == 2 * b) {
+      hipLaunchKernelGGL((scan_fast<Op, L, 2 * b>), grid, block, 0, stream, A);
+      return hipGetLastError();
+    }
+    if (nkb_fast == 4 * b) {
+      hipLaunchKernelGGL((scan_fast<Op, L, 4 * b>), grid, block, 0, stream, A);
       return hipGetLastError();
     }
   }

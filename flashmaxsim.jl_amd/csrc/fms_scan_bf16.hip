@@ -7,6 +7,7 @@ namespace fms {
                                             float*, float, bool, bool, hipStream_t);
 FMS_INST(LayPaired)
 FMS_INST(LayCand)
+FMS_INST(LayCandSorted)
 FMS_INST(LayInBatch)
 FMS_INST(LayPacked)
 FMS_INST(LayVarlen)

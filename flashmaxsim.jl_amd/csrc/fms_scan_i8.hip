@@ -7,4 +7,7 @@ template hipError_t launch_scan<OpI8, LayPaired>(const LayPaired&, int, int, int
                                                  float*, float*, float, bool, bool, hipStream_t);
 template hipError_t launch_scan<OpI8, LayCand>(const LayCand&, int, int, int64_t, int32_t*,
                                                float*, float*, float, bool, bool, hipStream_t);
+template hipError_t launch_scan<OpI8, LayCandSorted>(const LayCandSorted&, int, int, int64_t,
+                                                     int32_t*, float*, float*, float, bool, bool,
+                                                     hipStream_t);
 }  // namespace fms

@@ -120,6 +120,20 @@ def launch_candidates_scan(args, partial, Q, gallery, idx, qmask, dmask, N, scor
     _lib.check(st, "launch_candidates_scan")
 
 
+GROUPING_MODES = {"auto": 0, "always": 1, "never": 2}
+
+
+def candidates_grouping(mode: str) -> str:
+    """Set how candidate scans order their pairs ("auto", "always", "never"); returns
+    the previous mode.  In document order the pairs that share a gallery document are
+    scored together, so the document leaves HBM once per group; results are
+    bit-identical either way.  Process-wide (fms_candidates_grouping)."""
+    if mode not in GROUPING_MODES:
+        raise ArgumentError(f"grouping mode must be one of {sorted(GROUPING_MODES)}")
+    prev = _lib.lib().fms_candidates_grouping(GROUPING_MODES[mode])
+    return {v: k for k, v in GROUPING_MODES.items()}[prev]
+
+
 def inbatch_device_scan(S, args, Q, D, qmask, dmask):
     dev = require_device(S, args, Q, D, qmask, dmask)
     Bq, Tq, dim = Q.shape

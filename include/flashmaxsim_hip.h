@@ -38,8 +38,10 @@
  *   - Scores accumulate in fp32 for every feature type (f16/bf16 products
  *     are exact in fp32; int8 dots accumulate exactly in int32).
  *
- * Reentrant: no global mutable state; concurrent calls on different streams
- * are independent.
+ * Reentrant: concurrent calls on different streams are independent.  The
+ * only process-wide state is a per-device memory pool that the candidate
+ * scans draw their stream-ordered workspace from (kept for the life of the
+ * process) and the grouping mode of fms_candidates_grouping.
  */
 #ifndef FLASHMAXSIM_HIP_H
 #define FLASHMAXSIM_HIP_H
@@ -112,6 +114,20 @@ fms_status fms_launch_candidates_scan(int32_t dtype, int32_t* args, float* parti
                                       int64_t dim, int64_t Tq, int64_t B,
                                       int64_t Td, int64_t N, int64_t C,
                                       float* scores, float neg, void* stream);
+
+/*
+ * Document-order grouping of the candidate scans (float and INT8).  No
+ * reference counterpart: a tuning switch of this library.  In document order
+ * the pairs that share a gallery document are scored together and the
+ * document is read from HBM once per group instead of once per pair; the
+ * results are bit-identical to output order.  Grouping needs a workspace of
+ * about 8*C*B + 4*N bytes, allocated stream-ordered from a library-owned
+ * pool and released on the same stream.  mode: 0 = automatic (C*B >= 16384,
+ * the sort's O(N) passes cheap next to the scan, and uniformly drawn
+ * indices would repeat enough to save >= 30% of the document reads),
+ * 1 = always, 2 = never.  Returns the previous mode, or -1 for an invalid mode.
+ */
+int32_t fms_candidates_grouping(int32_t mode);
 
 /*
  * In-batch scan.  Replaces inbatch_device_scan!(backend, S, args, Q, D,

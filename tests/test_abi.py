@@ -91,3 +91,17 @@ def test_status_maps_to_reference_exceptions():
     with pytest.raises(fm.HIPError):
         _lib.check(_lib.FMS_EHIP, "x")
     _lib.check(OK, "x")
+
+
+def test_candidates_grouping_mode_switch():
+    """fms_candidates_grouping is host-only state: returns the previous mode, rejects others."""
+    L = _lib.lib()
+    prev = L.fms_candidates_grouping(1)
+    try:
+        assert L.fms_candidates_grouping(2) == 1
+        assert L.fms_candidates_grouping(0) == 2
+        assert L.fms_candidates_grouping(3) == -1
+        assert L.fms_candidates_grouping(-1) == -1
+        assert L.fms_candidates_grouping(0) == 0
+    finally:
+        L.fms_candidates_grouping(prev)

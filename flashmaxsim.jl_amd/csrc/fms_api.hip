@@ -428,6 +428,11 @@ fms_status fms_debug_mfma_layout(float* out, int32_t dtype_or_int8, void* stream
   return from_hip(mfma_layout_probe(out, dtype_or_int8, as_stream(stream)));
 }
 
+fms_status fms_debug_cross_lane(float* out, void* stream) {
+  if (!out) return FMS_EINVAL;
+  return from_hip(cross_lane_probe(out, as_stream(stream)));
+}
+
 fms_status fms_debug_read_bandwidth(const void* p, int64_t bytes, uint32_t* out, int32_t blocks,
                                     void* stream) {
   if (bytes < 0 || bytes % 16 != 0 || blocks <= 0 || !out || (bytes > 0 && !p) ||

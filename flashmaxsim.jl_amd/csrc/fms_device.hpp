@@ -221,23 +221,50 @@ __device__ __forceinline__ int slot_to_token(int slot, int h) {
   return slot < 0 ? 0 : (slot >> 4) * kTile + acc_row(slot & 15, h) + 1;
 }
 
+// Cross-lane exchanges without LDS.  v_permlane32_swap(a, b) trades lanes
+// 32-63 of `a` with lanes 0-31 of `b` and returns both; with a = b = x that
+// gives {[x_lo, x_lo], [x_hi, x_hi]}, so lane l finds x[l ^ 32] in the
+// second result when it is in the low half (h = 0) and in the first when it
+// is in the high half.  (ds_bpermute, behind __shfl_xor, costs an LDS round
+// trip per step of a reduction.)
+__device__ __forceinline__ uint32_t lane_xor32(uint32_t x, int h) {
+  const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+  return h ? r[0] : r[1];
+}
+
+// v + v[lane dpp-permuted] for a DPP control (quad_perm / row_ror).
+template <int kCtrl>
+__device__ __forceinline__ float dpp_add(float v) {
+  return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                           0, __builtin_bit_cast(int, v), kCtrl, 0xf, 0xf, false));
+}
+
 // Merge the (max, token) of lanes l and l^32, which hold disjoint document
 // rows of the same query token.  Equal maxima keep the lower token, matching
-// a sequential ascending scan.
-__device__ __forceinline__ void merge_halves(float& mx, int& tok) {
-  const float omx = __shfl_xor(mx, 32);
-  const int otok = __shfl_xor(tok, 32);
-  const bool take = otok != 0 && (tok == 0 || omx > mx || (omx == mx && otok < tok));
+// a sequential ascending scan.  h = lane / 32.
+__device__ __forceinline__ void merge_halves(float& mx, int& tok, int h) {
+  const float omx = __builtin_bit_cast(float, lane_xor32(__builtin_bit_cast(uint32_t, mx), h));
+  const int otok = (int)lane_xor32((uint32_t)tok, h);
+  // Bitwise, not short-circuit: no exec-mask branches.
+  const bool take = (otok != 0) & ((tok == 0) | (omx > mx) | ((omx == mx) & (otok < tok)));
   mx = take ? omx : mx;
   tok = take ? otok : tok;
 }
 
-// Sum over the 32 lanes of each wave half (after merge_halves both halves
-// hold the same 32 per-token partials, so either half's sum is the score).
+// Sum over lanes 0-31, returned in every lane (wave-uniform).  After
+// merge_halves both wave halves hold the same 32 per-token partials, so this
+// is the score.  Quad butterflies and row rotations by DPP leave each row
+// of 16 lanes holding its sum; rows 0 and 1 are then read with v_readlane.
+// (v_permlane16_swap would do the last step in vector registers, but this
+// compiler folds `r[0] + r[1]` of its two results into `r[0] + r[0]`.)
 __device__ __forceinline__ float half_sum(float v) {
-#pragma unroll
-  for (int o = 16; o >= 1; o >>= 1) v += __shfl_xor(v, o);
-  return v;
+  v = dpp_add<0xB1>(v);   // quad_perm [1,0,3,2]: lane ^ 1
+  v = dpp_add<0x4E>(v);   // quad_perm [2,3,0,1]: lane ^ 2
+  v = dpp_add<0x124>(v);  // row_ror:4
+  v = dpp_add<0x128>(v);  // row_ror:8 -> each row of 16 holds its sum
+  const int bits = __builtin_bit_cast(int, v);
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(bits, 0)) +
+         __builtin_bit_cast(float, __builtin_amdgcn_readlane(bits, 16));
 }
 
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }

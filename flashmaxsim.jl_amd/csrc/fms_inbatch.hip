@@ -27,17 +27,24 @@
 //     issued past the end re-read it) and the loop has no global stores, so
 //     the compiler's in-order vmcnt accounting waits for exactly one chunk;
 //   * per chunk and wave: 8 LDS fragment reads feed 4 x 8 MFMA 32x32x16
-//     issued query by query, with each query's running max/argmax update
-//     (fold_tree, ~0.65x its MFMA time on the VALU) interleaved into the
-//     next query's MFMAs; the two workgroups on a CU have independent
-//     barriers, so the rest overlaps across workgroups on each SIMD;
-//   * per-document tape / score go to LDS and leave in one coalesced pass at
-//     the end of the block.
-// Block -> (query block, document block) is XCD-aware: consecutive block ids
-// go to different XCDs, so each XCD's blocks share one slice of documents
-// (<= 4 MB, its L2) and iterate over all query blocks.
+//     issued k-block by k-block across the 4 query tiles, i.e. 4 independent
+//     accumulation chains (a dependent 32x32x16 MFMA issues at about half the
+//     rate of an independent one), then each tile's running max/argmax
+//     update (fold_tree); the two workgroups on a CU have independent
+//     barriers, so one's folds overlap the other's MFMAs on each SIMD;
+//   * the document close (merge of the wave halves, score) uses v_permlane32
+//     and DPP, not LDS shuffles, and no branches;
+//   * per-document tape (int16, Td <= 2048) / score go to LDS and leave in
+//     one coalesced pass at the end of the block.
+// Documents per block are chosen so the grid is a whole number (>= 2) of
+// rounds of the resident block slots.  Block -> (query block, document
+// block) is XCD-aware: consecutive block ids go to different XCDs, so each
+// XCD's blocks share one slice of documents (its L2) and iterate over all
+// query blocks.
 #include <hip/hip_runtime.h>
 #include <math.h>
+
+#include <algorithm>
 #include <stdint.h>
 
 #include "fms_device.hpp"
@@ -56,8 +63,14 @@ constexpr int kIbLdsRow = kIbRowBytes + 16;        // padded LDS row (272 B)
 constexpr int kIbLdsChunk = kTile * kIbLdsRow;     // one LDS chunk buffer
 constexpr int kIbUnits = kTile * kIbRowBytes / 16 / (64 * kIbWaves);  // 16-byte units per thread
 constexpr int kXcds = 8;
-constexpr int kIbMaxChunkMasks = 1024;           // DB * nch per block
-constexpr int kIbMaxDocs = 16;                   // documents per block
+constexpr int kIbMaxChunkMasks = 512;            // documents x chunks per block
+constexpr int kIbMaxDocs = 24;                   // documents per block
+constexpr int kIbMaxChunks = 64;                 // chunks per document (Td <= 2048)
+constexpr int kIbBlocksPerCu = 2;                // occupancy the launch bounds ask for
+// List entry: chunk (6 bits) | document in block (5) | last chunk of its
+// document (1) | first valid token + 1 (20).
+constexpr int kInfoDocShift = 6, kInfoLastBit = 11, kInfoFirstShift = 12;
+constexpr uint32_t kInfoDocMask = 31u;
 
 // LDS byte offset of 16-byte unit `u` (0..15) of chunk row `row` (0..31).
 // Rows are padded to 272 bytes: the MFMA-layout reads of consecutive lanes
@@ -83,7 +96,7 @@ __device__ __forceinline__ void lds_barrier() {
 }
 
 template <class Op>
-__global__ void __launch_bounds__(64 * kIbWaves, 2) inbatch_mfma(const InBatchArgs A) {
+__global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(const InBatchArgs A) {
   typedef typename Op::Acc Acc;
   typedef typename Op::Frag Frag;
   __shared__ __attribute__((aligned(16))) uint8_t lds[2][kIbLdsChunk];
@@ -92,7 +105,7 @@ __global__ void __launch_bounds__(64 * kIbWaves, 2) inbatch_mfma(const InBatchAr
   __shared__ uint32_t lst_mask[kIbMaxChunkMasks];    // compacted chunk list
   __shared__ uint32_t lst_info[kIbMaxChunkMasks];
   __shared__ int lst_count;
-  __shared__ int32_t res_tape[kIbWaves][kIbQpw][kIbMaxDocs][kTile];
+  __shared__ int16_t res_tape[kIbWaves][kIbQpw][kIbMaxDocs][kTile];  // Td <= 2048
   __shared__ float res_score[kIbWaves][kIbQpw][kIbMaxDocs];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = uniform(tid >> 6);
@@ -167,8 +180,8 @@ __global__ void __launch_bounds__(64 * kIbWaves, 2) inbatch_mfma(const InBatchAr
   // ---- compacted chunk list ------------------------------------------------------
   // Only chunks with at least one valid row are streamed and multiplied (a
   // document's fully masked tail costs nothing).  Entry i: row validity
-  // lst_mask[i]; lst_info[i] = ch | jj << 6 | (last chunk of its document)
-  // << 10 | (first valid token + 1) << 11.
+  // lst_mask[i]; lst_info[i] packs (chunk, document, last chunk of its
+  // document, first valid token + 1) as the kInfo* constants describe.
   if (wave == 0) {
     int base = 0;
     for (int c0 = 0; c0 < nall; c0 += 64) {
@@ -179,7 +192,8 @@ __global__ void __launch_bounds__(64 * kIbWaves, 2) inbatch_mfma(const InBatchAr
         const int pos = base + __builtin_popcountll(bal & ((1ull << lane) - 1ull));
         const int jj = c / nch, ch = c - jj * nch;
         lst_mask[pos] = m;
-        lst_info[pos] = (uint32_t)(ch | (jj << 6) | ((doc_first[jj] + 1) << 11));
+        lst_info[pos] = (uint32_t)(ch | (jj << kInfoDocShift) |
+                                   ((doc_first[jj] + 1) << kInfoFirstShift));
       }
       base += __builtin_popcountll(bal);
     }
@@ -192,12 +206,13 @@ __global__ void __launch_bounds__(64 * kIbWaves, 2) inbatch_mfma(const InBatchAr
   for (int k = 0; k < kIbMaxChunkMasks / (64 * kIbWaves); ++k) {
     const int i = tid + k * 64 * kIbWaves;
     last[k] = i < nsteps && (i + 1 == nsteps ||
-                             ((lst_info[i + 1] >> 6) & 15u) != ((lst_info[i] >> 6) & 15u));
+                             ((lst_info[i + 1] >> kInfoDocShift) & kInfoDocMask) !=
+                                 ((lst_info[i] >> kInfoDocShift) & kInfoDocMask));
   }
   __syncthreads();
 #pragma unroll
   for (int k = 0; k < kIbMaxChunkMasks / (64 * kIbWaves); ++k)
-    if (last[k]) lst_info[tid + k * 64 * kIbWaves] |= 1u << 10;
+    if (last[k]) lst_info[tid + k * 64 * kIbWaves] |= 1u << kInfoLastBit;
   __syncthreads();
 
   // ---- chunk stream -------------------------------------------------------------
@@ -211,7 +226,8 @@ __global__ void __launch_bounds__(64 * kIbWaves, 2) inbatch_mfma(const InBatchAr
   typedef u32x4 Stage[kIbUnits];
   int ld_i = 0;  // next list entry to request
   auto chunk_load = [&](Stage& g, uint32_t m, uint32_t info) {
-    const int ch = info & 63u, jj = (info >> 6) & 15u, f = (int)(info >> 11) - 1;
+    const int ch = info & 63u, jj = (info >> kInfoDocShift) & kInfoDocMask;
+    const int f = (int)(info >> kInfoFirstShift) - 1;
     const int fsrc = f < 0 ? 0 : f;  // (never: listed chunks have a valid row)
 #pragma unroll
     for (int i = 0; i < kIbUnits; ++i) {
@@ -238,13 +254,16 @@ __global__ void __launch_bounds__(64 * kIbWaves, 2) inbatch_mfma(const InBatchAr
   auto close = [&](int q, int jj, int f) {
     int tok = slot_to_token(slot[q], h);
     float m = mx[q];
-    merge_halves(m, tok);
+    merge_halves(m, tok, h);
+    // Branch-free: the mask word is read for every lane (t0 is always a
+    // valid token index of the document).
     const int t0 = tok > 0 ? tok - 1 : 0;
-    const bool real = tok > 0 && ((chunk_mask[jj * nch + (t0 >> 5)] >> (t0 & 31)) & 1u);
+    const uint32_t mw = chunk_mask[jj * nch + (t0 >> 5)];
+    const bool real = (tok > 0) & (((mw >> (t0 & 31)) & 1u) != 0u);
     tok = real ? tok : f + 1;
-    const float part = (tvalid[q] && tok != 0) ? m : 0.0f;
+    const float part = (tvalid[q] & (tok != 0)) ? m : 0.0f;
     const float score = half_sum(part);
-    if (h == 0) res_tape[wave][q][jj][r32] = tvalid[q] ? tok : 0;
+    if (h == 0) res_tape[wave][q][jj][r32] = (int16_t)(tvalid[q] ? tok : 0);
     if (lane == 0) res_score[wave][q][jj] = score;
     mx[q] = -INFINITY;
     slot[q] = -1;
@@ -259,6 +278,11 @@ __global__ void __launch_bounds__(64 * kIbWaves, 2) inbatch_mfma(const InBatchAr
   auto step = [&](int i, Stage& g_next) {
     lds_store(i + 1, g_next);
     chunk_load(g_next, (uint32_t)uniform((int)ld_m), (uint32_t)uniform((int)ld_info));
+    // List entries for the next step, read now so the LDS latency hides
+    // behind this step's MFMAs instead of stalling before the barrier.
+    ld_m = lst_mask[ld_i];
+    ld_info = lst_info[ld_i];
+    const uint32_t next_info = lst_info[i + 1 < nsteps ? i + 1 : i];
     const uint32_t info = (uint32_t)uniform((int)cur_info);
     const int ch = info & 63u;
     Frag a[kIbNkb];
@@ -266,41 +290,30 @@ __global__ void __launch_bounds__(64 * kIbWaves, 2) inbatch_mfma(const InBatchAr
     for (int kb = 0; kb < kIbNkb; ++kb)
       a[kb] = *reinterpret_cast<const Frag*>(&lds[i & 1][lds_off(r32, 2 * kb + h)]);
     Acc acc[kIbQpw];
-    auto fold = [&](int q) {
+    // The query tiles' accumulations interleave k-block by k-block:
+    // kIbQpw independent MFMA chains, so no MFMA waits for the result of
+    // the one issued just before it (a dependent 32x32x16 MFMA issues at
+    // about half the rate of independent ones).
+#pragma unroll
+    for (int q = 0; q < kIbQpw; ++q) acc[q] = Acc{};
+#pragma unroll
+    for (int kb = 0; kb < kIbNkb; ++kb)
+#pragma unroll
+      for (int q = 0; q < kIbQpw; ++q) acc[q] = Op::mma(a[kb], qf[q][kb], acc[q]);
+#pragma unroll
+    for (int q = 0; q < kIbQpw; ++q) {
       float s[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[r] = acc[q][r];
       fold_tree(s, ch * 16, mx[q], slot[q]);
-    };
-#pragma unroll
-    for (int q = 0; q < kIbQpw; ++q) {
-      acc[q] = Acc{};
-#pragma unroll
-      for (int kb = 0; kb < kIbNkb; ++kb) acc[q] = Op::mma(a[kb], qf[q][kb], acc[q]);
-      if (q > 0) fold(q - 1);
     }
-    fold(kIbQpw - 1);
-    // Issue order: fragment reads, query 0's MFMAs, then per later query two
-    // MFMAs followed by (one MFMA, a slice of the previous query's fold) x 6.
-    __builtin_amdgcn_sched_group_barrier(0x100, kIbNkb, 0);  // DS reads
-    __builtin_amdgcn_sched_group_barrier(0x008, kIbNkb, 0);  // MFMA
-#pragma unroll
-    for (int q = 1; q < kIbQpw; ++q) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-#pragma unroll
-      for (int k = 0; k < kIbNkb - 2; ++k) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 7, 0);  // VALU
-      }
-    }
-    if (info & (1u << 10)) {
-      const int jj = (info >> 6) & 15u, f = (int)(info >> 11) - 1;
+    if (info & (1u << kInfoLastBit)) {
+      const int jj = (info >> kInfoDocShift) & kInfoDocMask;
+      const int f = (int)(info >> kInfoFirstShift) - 1;
 #pragma unroll
       for (int q = 0; q < kIbQpw; ++q) close(q, jj, f);
     }
-    ld_m = lst_mask[ld_i];
-    ld_info = lst_info[ld_i];
-    cur_info = lst_info[i + 1 < nsteps ? i + 1 : i];
+    cur_info = next_info;
     lds_barrier();
   };
 
@@ -338,9 +351,26 @@ __global__ void __launch_bounds__(64 * kIbWaves, 2) inbatch_mfma(const InBatchAr
 hipError_t launch_inbatch_mfma(int dtype_bf16, const InBatchArgs& args_in, hipStream_t stream) {
   InBatchArgs A = args_in;
   A.nqb = (A.Bq + kIbQueries - 1) / kIbQueries;
-  // documents per block: enough blocks to fill 256 CUs several times over
-  int db = kIbMaxDocs;
-  while (db > 1 && (int64_t)A.nqb * ((A.Bd + db - 1) / db) < 2048) db >>= 1;
+  // Documents per block: the grid should be a whole number of rounds of the
+  // resident block slots (kIbBlocksPerCu per CU) -- a last round that
+  // fills only part of the GPU idles the rest -- with at least two rounds
+  // for balance, as few blocks as that allows (each block pays one set-up),
+  // and the block's chunk list within kIbMaxChunkMasks.
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus < 1)
+    cus = 256;
+  const int64_t slots = (int64_t)cus * kIbBlocksPerCu;
+  const int nch = A.Td > 0 ? (A.Td + kTile - 1) / kTile : 1;
+  const int db_cap = std::min(kIbMaxDocs, std::max(1, kIbMaxChunkMasks / nch));
+  int db = 1;
+  for (int64_t rounds = 2; rounds <= 64; ++rounds) {
+    const int64_t ndb_want = (rounds * slots + A.nqb - 1) / A.nqb;
+    db = (int)std::max<int64_t>(1, (A.Bd + ndb_want - 1) / ndb_want);
+    if (db <= db_cap) break;
+  }
+  db = std::min(db, db_cap);
   A.db = db;
   A.ndb = (A.Bd + db - 1) / db;
   const dim3 grid((unsigned)(A.nqb * A.ndb)), block(64 * kIbWaves);
@@ -352,11 +382,11 @@ hipError_t launch_inbatch_mfma(int dtype_bf16, const InBatchArgs& args_in, hipSt
 }
 
 // A block's documents span one buffer resource: ndoc * Td * 256 bytes <=
-// 16 * 2048 * 256 = 8 MB under the chunk-count limit.
+// kIbMaxChunkMasks * 32 * 256 = 4 MB.  Tape entries are staged as int16.
 bool inbatch_mfma_supported(int64_t dim, int64_t Tq, int64_t Td, const void* Q, const void* D) {
   const bool al = ((reinterpret_cast<uintptr_t>(Q) | reinterpret_cast<uintptr_t>(D)) & 15u) == 0;
   return dim == kIbNkb * 16 && Tq >= 1 && Tq <= kTile && Td >= 0 &&
-         (Td + kTile - 1) / kTile <= kIbMaxChunkMasks / kIbMaxDocs && al;
+         (Td + kTile - 1) / kTile <= kIbMaxChunks && al;
 }
 
 }  // namespace fms

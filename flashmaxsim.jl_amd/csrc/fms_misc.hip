@@ -229,6 +229,26 @@ hipError_t read_bandwidth(const void* p, int64_t bytes, uint32_t* out, int block
   return hipGetLastError();
 }
 
+// Cross-lane helper probe (one wave): out[l] = lane_xor32(l), out[64 + l] =
+// half_sum(l) (the sum of lanes 0-31 in every lane), out[128 + l] /
+// out[192 + l] = the (token, max) merge_halves keeps when lane l holds
+// (max = l % 7, token = l + 1).
+__global__ void cross_lane_probe_kernel(float* out) {
+  const int lane = threadIdx.x & 63, h = lane >> 5;
+  out[lane] = (float)lane_xor32((uint32_t)lane, h);
+  out[64 + lane] = half_sum((float)lane);
+  float mx = (float)(lane % 7);
+  int tok = lane + 1;
+  merge_halves(mx, tok, h);
+  out[128 + lane] = (float)tok;
+  out[192 + lane] = mx;
+}
+
+hipError_t cross_lane_probe(float* out, hipStream_t stream) {
+  hipLaunchKernelGGL(cross_lane_probe_kernel, dim3(1), dim3(64), 0, stream, out);
+  return hipGetLastError();
+}
+
 hipError_t mfma_layout_probe(float* out, int op, hipStream_t stream) {
   hipLaunchKernelGGL(mfma_layout_probe_kernel, dim3(1), dim3(64), 0, stream, out, op);
   return hipGetLastError();

@@ -15,6 +15,7 @@ hipError_t length_normalize(float* scores, const uint8_t* qmask, int64_t Tq, int
                             hipStream_t stream);
 hipError_t varlen_normalize(float* scores, const int32_t* cu_q, int64_t N, hipStream_t stream);
 hipError_t mfma_layout_probe(float* out, int op, hipStream_t stream);
+hipError_t cross_lane_probe(float* out, hipStream_t stream);
 hipError_t read_bandwidth(const void* p, int64_t bytes, uint32_t* out, int blocks,
                           hipStream_t stream);
 

@@ -160,7 +160,7 @@ template <class L>
 __device__ __forceinline__ float finish_tile(const ScanArgs<L>& A, int64_t out, int qt, int r32,
                                              int h, bool tvalid, float mx, int slot) {
   int tok = slot_to_token(slot, h);
-  merge_halves(mx, tok);
+  merge_halves(mx, tok, h);
   const float part = (tvalid && tok != 0) ? mx : 0.0f;
   const int arg = tvalid ? tok : 0;
   const int t = qt * kTile + r32;

@@ -49,6 +49,7 @@ SIGNATURES = {
     "fms_debug_mfma_layout": [_p, _i32, _p],
     "fms_debug_read_bandwidth": [_p, _i64, _p, _i32, _p],
     "fms_candidates_grouping": [_i32],
+    "fms_debug_cross_lane": [_p, _p],
 }
 _RESTYPES = {
     "fms_status_string": ctypes.c_char_p,

@@ -254,6 +254,15 @@ fms_status fms_varlen_normalize(float* scores, const int32_t* cu_q, int64_t N, v
 fms_status fms_debug_mfma_layout(float* out, int32_t dtype_or_int8, void* stream);
 
 /*
+ * Test-only: cross-lane helper probe (no reference counterpart).  One wave
+ * writes 256 floats: out[l] = the lane its l ^ 32 exchange reads, out[64+l]
+ * = the sum of the lane ids 0..31 (in every lane), out[128+l] / out[192+l] =
+ * the (token, max) kept by the half merge when lane l holds max l % 7 and
+ * token l + 1 -- what the scans' tile close relies on.
+ */
+fms_status fms_debug_cross_lane(float* out, void* stream);
+
+/*
  * Test-only: streaming read of `bytes` (multiple of 16, 16-byte aligned)
  * with `blocks` workgroups of 256 threads; out receives blocks*256 words.
  * No reference counterpart: it measures the HBM read ceiling reported

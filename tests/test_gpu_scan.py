@@ -38,6 +38,22 @@ def test_mfma_accumulator_layout(device, op):
             assert o[1, lane, r] == (lane % 32) + 1, (lane, r, o[1, lane, r])
 
 
+def test_cross_lane_helpers(device):
+    """The lane exchanges the tile close relies on (v_permlane32/16_swap, DPP): xor-32
+    partner, the sum over lanes 0-31 broadcast to every lane, and the half merge's tie
+    rule (larger max wins, equal maxima keep the lower token)."""
+    out = torch.zeros(256, dtype=torch.float32, device=device)
+    _lib.check(_lib.lib().fms_debug_cross_lane(out.data_ptr(),
+                                               torch.cuda.current_stream().cuda_stream), "probe")
+    o = out.cpu().numpy()
+    for lane in range(64):
+        assert o[lane] == lane ^ 32, (lane, o[lane])
+        assert o[64 + lane] == 496.0, (lane, o[64 + lane])
+        mine, other = (lane % 7, lane + 1), ((lane ^ 32) % 7, (lane ^ 32) + 1)
+        want = other if (other[0] > mine[0] or (other[0] == mine[0] and other[1] < mine[1])) else mine
+        assert (o[128 + lane], o[192 + lane]) == (want[1], want[0]), (lane, o[128 + lane], o[192 + lane])
+
+
 def _masks(rng, B, Tq, Td, kind):
     if kind == "none":
         return None, None

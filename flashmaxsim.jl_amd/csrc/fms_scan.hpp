@@ -280,10 +280,8 @@ __global__ void __launch_bounds__(64 * kWaves) scan_fast(const ScanArgs<L> A) {
     // Unconditional: after the wave's last chunk it re-reads the current one
     // (an L2 hit), so every step issues the same loads and the MFMAs below
     // wait only for the chunk they multiply.
-    if (more)
-      load_chunk<Op, NKB>(nxt, nv, nch_i, nkb, rowbytes, lane_off, r32, h, ds_vec);
-    else
-      load_chunk<Op, NKB>(nxt, v, ch, nkb, rowbytes, lane_off, r32, h, ds_vec);
+    load_chunk<Op, NKB>(nxt, more ? nv : v, more ? nch_i : ch, nkb, rowbytes, lane_off, r32, h,
+                        ds_vec);
     // Keep the prefetch ahead of the MFMAs: the scheduler would otherwise
     // sink the independent loads below them and nothing would overlap.
     __builtin_amdgcn_sched_barrier(0);
@@ -316,6 +314,17 @@ __global__ void __launch_bounds__(64 * kWaves) scan_fast(const ScanArgs<L> A) {
   while (step(bufA, bufB) && step(bufB, bufA)) {
   }
 }
+
+// ---- split-d kernel: fms_split.hpp (its own translation units) ----------------------
+
+// k-blocks per split-d batch: 128 bytes of each operand per lane per step.
+template <class Op>
+constexpr int split_kbat() {
+  return 128 / (Op::kEpl * Op::kEsz);
+}
+
+template <class Op, class L>
+hipError_t launch_split(const ScanArgs<L>& A, dim3 grid, dim3 block, hipStream_t stream);
 
 // ---- generic kernel ---------------------------------------------------------------
 
@@ -398,6 +407,7 @@ constexpr int fast_nkb(int nkb) {
   return (nkb == b || nkb == 2 * b || nkb == 4 * b) ? nkb : 0;
 }
 
+
 inline int pairs_per_wave(int64_t npairs) {
   // Aim for ~32k waves (8 resident per SIMD over 1024 SIMDs, several rounds)
   // so that each wave keeps its query tile across a handful of pairs.
@@ -444,6 +454,9 @@ hipError_t launch_scan(const L& lay, int dim, int rows, int64_t npairs, int32_t*
       return hipGetLastError();
     }
   }
+  // Split-d: any dim that is a whole number of KBAT-k-block batches.
+  constexpr int kbat = split_kbat<Op>();
+  if (vec && dim > 0 && dim % (kbat * Op::kKb) == 0) return launch_split<Op, L>(A, grid, block, stream);
   if (vec) {
     hipLaunchKernelGGL((scan_generic<Op, L, true>), grid, block, 0, stream, A);
   } else {

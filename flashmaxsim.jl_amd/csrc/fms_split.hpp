@@ -1,0 +1,157 @@
+// fms_split.hpp -- the split-d scan kernel, built in its own translation
+// units (fms_split_<type>.hip) with MFMA accumulators in ordinary VGPRs:
+// it carries two accumulation chains across loop iterations, which in AGPRs
+// would be copied back and forth every step.  The launcher in fms_scan.hpp
+// dispatches to it for dims that are whole batches and whose query tile
+// does not fit in registers.
+#pragma once
+
+#include "fms_scan.hpp"
+
+namespace fms {
+
+// scan_split<Op, L, KBAT>: dim == nbat * KBAT * KB exactly (16-byte aligned
+// rows), for dims whose query tile does not fit in registers (and fp32).
+// One step multiplies one batch of KBAT k-blocks of one (pair, query tile,
+// chunk): the batch's document AND query fragments are loaded the step
+// before (the query tile is re-read per chunk from L1/L2), so every step
+// issues the same loads and the MFMAs wait only for the batch they use.
+// Even and odd k-blocks accumulate into two independent chains, added when
+// the chunk's last batch is done.
+
+template <class Op, int KBAT>
+struct SplitBatch {
+  typename Op::Frag a[KBAT];     // document fragments
+  typename Op::Frag b[KBAT];     // query fragments
+  uint32_t mbyte;                // raw document mask byte of row lane%32
+  uint32_t qmbyte;               // raw query mask byte of token lane%32
+  float qscale;                  // int8 query scale of token lane%32
+  float ds[Op::kInt ? 16 : 1];   // int8 document scales of the accumulator rows
+};
+
+template <class Op, int KBAT>
+__device__ __forceinline__ void load_split(SplitBatch<Op, KBAT>& c, const PairView& v, int qt,
+                                           int ch, int bi, int rowbytes, int h, int r32,
+                                           bool ds_vec) {
+  const int kofs = (bi * KBAT * Op::kKb + h * Op::kEpl) * Op::kEsz;
+  const rsrc_t rd = make_rsrc_u(v.d, (uint32_t)v.td * (uint32_t)rowbytes);
+  const rsrc_t rq = make_rsrc_u(v.q, (uint32_t)v.tq * (uint32_t)rowbytes);
+  const int dbase = (ch * kTile + r32) * rowbytes + kofs;
+  const int qbase = (qt * kTile + r32) * rowbytes + kofs;
+#pragma unroll
+  for (int k = 0; k < KBAT; ++k) {
+    c.a[k] = Op::load(rd, dbase + k * Op::kKb * Op::kEsz);
+    c.b[k] = Op::load(rq, qbase + k * Op::kKb * Op::kEsz);
+  }
+  // Masks read unconditionally (zero-size resource when absent, see mask_ok).
+  const bool has_dm = v.dm != nullptr, has_qm = v.qm != nullptr;
+  c.mbyte = buf_load1(make_rsrc_u(has_dm ? (const void*)v.dm : (const void*)v.d,
+                                  has_dm ? (uint32_t)v.td : 0u),
+                      ch * kTile + r32);
+  c.qmbyte = buf_load1(make_rsrc_u(has_qm ? (const void*)v.qm : (const void*)v.q,
+                                   has_qm ? (uint32_t)v.tq : 0u),
+                       qt * kTile + r32);
+  c.qscale = 0.0f;
+  if constexpr (Op::kInt)
+    c.qscale = __builtin_bit_cast(float, buf_load4(make_rsrc_u(v.qs, (uint32_t)v.tq * 4u),
+                                                   (qt * kTile + r32) * 4));
+  load_ds<Op>(c.ds, v, ch, h, ds_vec);
+}
+
+template <class Op, class L, int KBAT>
+__global__ void __launch_bounds__(64 * kWaves) scan_split(const ScanArgs<L> A) {
+  typedef typename Op::Acc Acc;
+  const int lane = threadIdx.x & 63, r32 = lane & 31, h = lane >> 5;
+  int64_t first, stride;
+  int cnt;
+  wave_positions(A, first, stride, cnt);
+  if (cnt <= 0) return;
+  const int rowbytes = A.dim * Op::kEsz;
+  const int nbat = A.nkb / KBAT;
+  const bool ds_vec = A.ds_vec != 0;
+
+  // wave cursor: position index pi (view v), query tile qt, chunk ch of
+  // nch, batch bi of nbat
+  int pi = 0, qt = 0, ch = 0, bi = 0;
+  PairView v = uniform_view(A.lay.get(first));
+  int nch = v.td > 0 ? (v.td + kTile - 1) / kTile : 1;
+
+  SplitBatch<Op, KBAT> bufA, bufB;
+  Acc acc0 = {}, acc1 = {};
+  float mx = -INFINITY, score = 0.0f;
+  int slot = -1;
+
+  load_split<Op, KBAT>(bufA, v, 0, 0, 0, rowbytes, h, r32, ds_vec);
+
+  auto step = [&](SplitBatch<Op, KBAT>& cur, SplitBatch<Op, KBAT>& nxt) -> bool {
+    // advance a copy of the cursor and prefetch its batch
+    int npi = pi, nqt_i = qt, nch_i = ch, nbi = bi + 1, nnch = nch;
+    PairView nv = v;
+    if (nbi >= nbat) {
+      nbi = 0;
+      if (++nch_i >= nch) {
+        nch_i = 0;
+        if (++nqt_i >= A.nqt) {
+          nqt_i = 0;
+          ++npi;
+          const int64_t kpos = first + (int64_t)(npi < cnt ? npi : pi) * stride;
+          if (npi < cnt) {
+            nv = uniform_view(A.lay.get(kpos));
+            nnch = nv.td > 0 ? (nv.td + kTile - 1) / kTile : 1;
+          }
+        }
+      }
+    }
+    const bool more = npi < cnt;
+    // One call on a selected cursor (after the wave's last batch it re-reads
+    // the current one): two calls under `if (more)` get merged with their
+    // arguments as divergent phis, and the loads become waterfall loops.
+    load_split<Op, KBAT>(nxt, more ? nv : v, more ? nqt_i : qt, more ? nch_i : ch,
+                         more ? nbi : bi, rowbytes, h, r32, ds_vec);
+    __builtin_amdgcn_sched_barrier(0);
+
+#pragma unroll
+    for (int k = 0; k < KBAT; ++k) {
+      if (k & 1)
+        acc1 = Op::mma(cur.a[k], cur.b[k], acc1);
+      else
+        acc0 = Op::mma(cur.a[k], cur.b[k], acc0);
+    }
+
+    if (bi == nbat - 1) {  // chunk complete: fold it
+      Acc acc;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[r] = acc0[r] + acc1[r];
+      acc0 = Acc{};
+      acc1 = Acc{};
+      float s[16];
+      acc_to_scores<Op>(acc, cur.qscale, cur.ds, s);
+      update_chunk(s, chunk_rows_valid(v, ch, r32, cur.mbyte), h, ch, mx, slot);
+      if (ch == nch - 1) {
+        uint32_t qmb = cur.qmbyte;
+        asm volatile("" : "+v"(qmb));
+        const bool tvalid = (qt * kTile + r32) < v.tq && mask_ok(v.qm, qmb);
+        score += finish_tile(A, v.out, qt, r32, h, tvalid, mx, slot);
+        mx = -INFINITY;
+        slot = -1;
+        if (qt == A.nqt - 1) {
+          write_score(A, v.out, v.valid, score, lane);
+          score = 0.0f;
+        }
+      }
+    }
+    pi = npi; qt = nqt_i; ch = nch_i; bi = nbi; nch = nnch; v = nv;
+    return more;
+  };
+
+  while (step(bufA, bufB) && step(bufB, bufA)) {
+  }
+}
+
+template <class Op, class L>
+hipError_t launch_split(const ScanArgs<L>& A, dim3 grid, dim3 block, hipStream_t stream) {
+  hipLaunchKernelGGL((scan_split<Op, L, split_kbat<Op>()>), grid, block, 0, stream, A);
+  return hipGetLastError();
+}
+
+}  // namespace fms

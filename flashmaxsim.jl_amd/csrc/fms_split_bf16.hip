@@ -1,0 +1,11 @@
+// Explicit instantiation of the BF16 split-d scan for every layout it serves.
+#include "fms_split.hpp"
+
+namespace fms {
+template hipError_t launch_split<OpBF16, LayPaired>(const ScanArgs<LayPaired>&, dim3, dim3, hipStream_t);
+template hipError_t launch_split<OpBF16, LayCand>(const ScanArgs<LayCand>&, dim3, dim3, hipStream_t);
+template hipError_t launch_split<OpBF16, LayCandSorted>(const ScanArgs<LayCandSorted>&, dim3, dim3, hipStream_t);
+template hipError_t launch_split<OpBF16, LayInBatch>(const ScanArgs<LayInBatch>&, dim3, dim3, hipStream_t);
+template hipError_t launch_split<OpBF16, LayPacked>(const ScanArgs<LayPacked>&, dim3, dim3, hipStream_t);
+template hipError_t launch_split<OpBF16, LayVarlen>(const ScanArgs<LayVarlen>&, dim3, dim3, hipStream_t);
+}  // namespace fms

@@ -1,11 +1,11 @@
 // fms_group.hip -- counting sort of candidate pairs by document, and the
 // workspace pool it draws from.
 //
-// Five small launches: zero the N+1 counters, histogram the pairs (one
+// Six small launches: zero the N+1 counters, histogram the pairs (one
 // atomic per pair), exclusive scan of the counters (tile sums, scan of the
 // tile sums, apply), atomic scatter of the pair ids.  Cost is linear in
-// C*B + N and small next to the scan it feeds (~1.5 MB of traffic for
-// C*B = 256k, N = 100k).
+// C*B + N and small next to the scan it feeds: for C*B = 256k, N = 100k
+// about 30 MB of HBM traffic (mostly atomic write-backs) and ~85 us.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 

@@ -13,7 +13,7 @@
 // MFMA per k-block and one running max/argmax update per accumulator
 // register.  Nothing of size Tq x Td ever reaches HBM.
 //
-// Two kernel shapes:
+// Three kernel shapes, tried in this order:
 //   scan_fast<Op, L, NKB>: dim == NKB * KB exactly, 16-byte aligned rows.
 //     The loads and MFMAs of a step are unconditional, so the compiler's
 //     in-order vmcnt accounting waits for exactly the chunk it multiplies
@@ -21,6 +21,9 @@
 //     (NKB fragments), the next
 //     chunk (possibly of the next pair) is prefetched into a second register
 //     buffer while the current one is multiplied.
+//   scan_split<Op, L, KBAT> (fms_split.hpp): dims that are whole batches of
+//     KBAT k-blocks but whose query tile does not fit in registers (and
+//     fp32); document and query fragments stream one batch ahead.
 //   scan_generic<Op, L, VEC>: any dim (split-d: the query fragment is
 //     re-read per k-block from L1/L2) and, with VEC = false, rows that are
 //     not 16-byte multiples (element-wise guarded loads).

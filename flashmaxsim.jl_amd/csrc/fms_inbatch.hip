@@ -5,42 +5,51 @@
 // argmax-accumulate, forward_layouts.jl:202-225; here nothing but S and the
 // tape leaves the chip).
 //
-// Workgroup = 4 waves (one per SIMD), two workgroups per CU, 16 queries x a
-// block of DB documents.
+// Two launches.  A plan kernel reads the document masks once per call: the
+// valid rows of every 32-token chunk, each document's count of chunks with a
+// valid row and its first valid token.  The in-batch kernel then runs one
+// workgroup per CU (a single round of the grid):
+//
+// Workgroup = 8 waves (two per SIMD), 32 queries x a range of documents.
+//   * document ranges split the documents by work (chunk steps plus one per
+//     document, from the plan), so the workgroups finish together; every
+//     workgroup checks the split against the per-block document limit and
+//     all fall back to an even split otherwise;
 //   * every wave keeps 4 query tiles (32 tokens x d=128 fp16/bf16) in
 //     registers for the whole workgroup lifetime, so each LDS fragment read
-//     feeds 4 MFMAs;
+//     feeds 4 MFMAs; the eight waves share one chunk stream (a barrier per
+//     step keeps the two waves of each SIMD in step);
 //   * the workgroup streams its documents in 32-token chunks: each chunk
-//     (8 KB) is fetched ONCE from L2/HBM (two coalesced 16-byte loads per
-//     thread) and stored to one of two LDS buffers with 272-byte rows, so the
-//     MFMA-layout ds_read_b128s of consecutive lanes hit distinct banks;
+//     (8 KB) is fetched ONCE from L2/HBM straight into LDS (buffer_load ...
+//     lds, one 16-byte load per thread, no registers), in MFMA fragment
+//     order: the 64 lanes of one fragment read cover 1 KB contiguously (no
+//     bank conflicts) and a lane's 8 reads are one address plus immediates;
 //   * masked rows (dmask = 0, and rows past Td in a document's last chunk)
 //     are replaced AT LOAD TIME by a copy of the document's first valid
 //     token f.  A copy scores exactly what f scores, so the maximum is
 //     unchanged, and with first-occurrence tie breaking a copy can only win
 //     where f ties it: a winning copy maps back to f when the document is
 //     closed.  The fold therefore needs no row masks at all;
-//   * software pipeline: chunk c+3 is requested while chunk c is multiplied
-//     (chunks c+2 and c+3 in flight), chunk c+1 moves register -> LDS at the
-//     start of step c, and one barrier per step publishes it.  Loads are
-//     unconditional (the stream position stops at the last chunk, so loads
-//     issued past the end re-read it) and the loop has no global stores, so
-//     the compiler's in-order vmcnt accounting waits for exactly one chunk;
-//   * per chunk and wave: 8 LDS fragment reads feed 4 x 8 MFMA 32x32x16
-//     issued k-block by k-block across the 4 query tiles, i.e. 4 independent
-//     accumulation chains (a dependent 32x32x16 MFMA issues at about half the
-//     rate of an independent one), then each tile's running max/argmax
-//     update (fold_tree); the two workgroups on a CU have independent
-//     barriers, so one's folds overlap the other's MFMAs on each SIMD;
+//   * software pipeline over three LDS buffers: chunk c+2 is requested while
+//     chunk c is multiplied, and one barrier per step (after each wave's
+//     own load of chunk c+1 has landed) publishes the next chunk.  Loads
+//     are unconditional (the stream is padded to whole rounds of the
+//     buffers and stops at its last entry, so loads past the end re-read
+//     it), so the in-order vmcnt accounting waits for exactly one chunk;
+//   * per chunk and wave: 8 LDS fragment reads feed 4 x 8 MFMA 32x32x16 in
+//     two phases of two independent accumulation chains (a dependent
+//     32x32x16 MFMA issues at about half the rate of an independent one).
+//     Each phase's MFMAs overlap the running max/argmax update (fold_tree)
+//     of the two tiles multiplied before them: phase 1 multiplies tiles 0,1
+//     while tiles 2,3 of the previous chunk fold, phase 2 multiplies tiles
+//     2,3 while tiles 0,1 fold;
 //   * the document close (merge of the wave halves, score) uses v_permlane32
 //     and DPP, not LDS shuffles, and no branches;
 //   * per-document tape (int16, Td <= 2048) / score go to LDS and leave in
 //     one coalesced pass at the end of the block.
-// Documents per block are chosen so the grid is a whole number (>= 2) of
-// rounds of the resident block slots.  Block -> (query block, document
-// block) is XCD-aware: consecutive block ids go to different XCDs, so each
-// XCD's blocks share one slice of documents (its L2) and iterate over all
-// query blocks.
+// Block -> (query block, document range) is XCD-aware: consecutive block ids
+// go to different XCDs, so each XCD's blocks share one slice of documents
+// (its L2) and iterate over all query blocks.
 #include <hip/hip_runtime.h>
 #include <math.h>
 
@@ -48,37 +57,35 @@
 #include <stdint.h>
 
 #include "fms_device.hpp"
+#include "fms_group.hpp"
 #include "fms_inbatch.hpp"
 
 namespace fms {
 
 namespace {
 
-constexpr int kIbWaves = 4;
+constexpr int kIbWaves = 8;
 constexpr int kIbQpw = 4;                          // query tiles per wave
+static_assert(kIbQpw == 4, "the step is written for two phases of two query tiles");
 constexpr int kIbQueries = kIbWaves * kIbQpw;      // queries per block
 constexpr int kIbNkb = 8;                          // dim == 128
 constexpr int kIbRowBytes = kIbNkb * 32;           // 256 B per token
-constexpr int kIbLdsRow = kIbRowBytes + 16;        // padded LDS row (272 B)
-constexpr int kIbLdsChunk = kTile * kIbLdsRow;     // one LDS chunk buffer
-constexpr int kIbUnits = kTile * kIbRowBytes / 16 / (64 * kIbWaves);  // 16-byte units per thread
+constexpr int kIbFrags = kIbNkb * 64;              // 16-byte fragments per chunk (8 KB)
+constexpr int kIbKbPerWave = kIbNkb / kIbWaves;    // k-blocks each wave moves into LDS
+constexpr int kIbBufs = 3;                         // LDS chunk buffers (kIbBufs - 1 chunks in flight)
+static_assert(kIbBufs == 3 || kIbBufs == 4, "the step loop rotates 3 or 4 buffers");
 constexpr int kXcds = 8;
 constexpr int kIbMaxChunkMasks = 512;            // documents x chunks per block
-constexpr int kIbMaxDocs = 24;                   // documents per block
+constexpr int kIbMaxDocs = 40;                   // documents per block
 constexpr int kIbMaxChunks = 64;                 // chunks per document (Td <= 2048)
-constexpr int kIbBlocksPerCu = 2;                // occupancy the launch bounds ask for
-// List entry: chunk (6 bits) | document in block (5) | last chunk of its
-// document (1) | first valid token + 1 (20).
-constexpr int kInfoDocShift = 6, kInfoLastBit = 11, kInfoFirstShift = 12;
-constexpr uint32_t kInfoDocMask = 31u;
-
-// LDS byte offset of 16-byte unit `u` (0..15) of chunk row `row` (0..31).
-// Rows are padded to 272 bytes: the MFMA-layout reads of consecutive lanes
-// (consecutive rows, same unit) start 68 banks apart, i.e. on distinct
-// 16-byte bank groups for 8 (32-bank) or 16 (64-bank) lanes per pass, the
-// staging writes of 16 lanes cover one contiguous row, and the 8 fragment
-// reads of a lane are one base address plus immediate offsets.
-__device__ __forceinline__ int lds_off(int row, int u) { return row * kIbLdsRow + (u << 4); }
+constexpr int kIbMaxList = (kIbMaxChunkMasks + kIbBufs - 1) / kIbBufs * kIbBufs;  // padded stream
+constexpr int kIbBlocksPerCu = 1;                // occupancy the launch bounds ask for
+constexpr int kIbBalanceMaxDocs = 6144;          // partition weights fit the result area
+// List entry: chunk (6 bits) | document in block (6) | last chunk of its
+// document (1) | first valid token + 1 (19).
+constexpr int kInfoDocShift = 6, kInfoLastBit = 12, kInfoFirstShift = 13;
+constexpr uint32_t kInfoDocMask = 63u;
+static_assert(kIbMaxDocs <= (int)kInfoDocMask + 1, "document index fits its field");
 
 }  // namespace
 
@@ -95,15 +102,95 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("" ::: "memory");
 }
 
+// Workgroup barrier after this wave's LDS accesses AND all but its last
+// kVm buffer loads have completed: the loads of the chunk the next step
+// reads (each wave's own share of it) are in LDS before any wave passes.
+template <int kVm>
+__device__ __forceinline__ void dma_barrier() {
+  static_assert(kVm >= 0 && kVm < 16, "vmcnt field");
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0x0070 | kVm);  // vmcnt(kVm) lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// Per-document chunk plan, computed once per call rather than once per query
+// block: one wave per document, lane = chunk (nch <= 64).  cmask[j*nch + ch]
+// holds the valid rows of chunk ch of document j (rows past Td clear),
+// dcount[j] the chunks with a valid row, dfirst[j] the first valid token
+// (-1 = none).
+__global__ void __launch_bounds__(256) inbatch_plan_kernel(const uint8_t* dm, int Bd, int Td,
+                                                           int nch, uint32_t* cmask,
+                                                           int32_t* dcount, int32_t* dfirst) {
+  const int lane = threadIdx.x & 63;
+  const int j = blockIdx.x * 4 + uniform(threadIdx.x >> 6);
+  if (j >= Bd) return;
+  const int rows = Td - lane * kTile;
+  uint32_t m = rows >= kTile ? 0xffffffffu : (rows > 0 ? (1u << rows) - 1u : 0u);
+  if (dm) {
+    // 32 byte loads per lane, all in flight; bytes past the document read 0.
+    const rsrc_t r = make_rsrc(dm + (int64_t)j * Td, (uint32_t)Td);
+    uint32_t b[kTile];
+#pragma unroll
+    for (int t = 0; t < kTile; ++t) b[t] = buf_load1(r, lane * kTile + t);
+    uint32_t bits = 0u;
+#pragma unroll
+    for (int t = 0; t < kTile; ++t) bits |= (b[t] & 0xffu) ? (1u << t) : 0u;
+    m &= bits;
+  }
+  if (lane < nch) cmask[(int64_t)j * nch + lane] = m;
+  const uint64_t nz = __ballot(m != 0u);
+  if (lane == 0) {
+    dcount[j] = __builtin_popcountll(nz);
+    int f = -1;
+    if (nz != 0u) {
+      const int k = __builtin_ctzll(nz);
+      f = k * kTile + __builtin_ctz((uint32_t)__builtin_amdgcn_readlane((int)m, k));
+    }
+    dfirst[j] = f;
+  }
+}
+
+// Exclusive scan over the 64 * kIbWaves threads of a block; every thread
+// must call it.  *total receives the block sum.
+__device__ int block_exclusive_scan_i32(int v, int* total) {
+  __shared__ int wsum[kIbWaves];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) wsum[wave] = x;
+  __syncthreads();
+  int before = 0, all = 0;
+#pragma unroll
+  for (int w = 0; w < kIbWaves; ++w) {
+    const int sw = wsum[w];
+    before += w < wave ? sw : 0;
+    all += sw;
+  }
+  __syncthreads();
+  *total = all;
+  return before + x - v;
+}
+
 template <class Op>
 __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(const InBatchArgs A) {
   typedef typename Op::Acc Acc;
   typedef typename Op::Frag Frag;
-  __shared__ __attribute__((aligned(16))) uint8_t lds[2][kIbLdsChunk];
+  // Chunk buffers, in MFMA fragment order: fragment (kb, lane) at
+  // [kb * 64 + lane].  Four separate arrays, so the compiler can tell which
+  // buffer each load-to-LDS writes.
+  __shared__ u32x4 cbuf0[kIbFrags], cbuf1[kIbFrags], cbuf2[kIbFrags];
+  __shared__ u32x4 cbuf3[kIbBufs == 4 ? kIbFrags : 1];
   __shared__ uint32_t chunk_mask[kIbMaxChunkMasks];  // valid rows per (doc, chunk)
   __shared__ int32_t doc_first[kIbMaxDocs];          // first valid token, -1 = none
-  __shared__ uint32_t lst_mask[kIbMaxChunkMasks];    // compacted chunk list
-  __shared__ uint32_t lst_info[kIbMaxChunkMasks];
+  __shared__ uint32_t lst_mask[kIbMaxList];          // compacted chunk list
+  __shared__ uint32_t lst_info[kIbMaxList];
   __shared__ int lst_count;
   __shared__ int16_t res_tape[kIbWaves][kIbQpw][kIbMaxDocs][kTile];  // Td <= 2048
   __shared__ float res_score[kIbWaves][kIbQpw][kIbMaxDocs];
@@ -124,58 +211,102 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
     qb = id / ndb;
   }
   if (qb >= nqb) return;
-  const int j0 = db * A.db, j1 = (j0 + A.db < A.Bd) ? j0 + A.db : A.Bd;
+
+  // ---- this block's documents -------------------------------------------------
+  // Uniform: A.db per block.  Balanced (A.balance): the document blocks split
+  // the documents by weight dcount + 1 (chunk steps plus the close), block b
+  // taking the documents whose weight prefix lies in [b, b+1) * total / ndb;
+  // every block checks that no block would exceed A.dbcap documents and
+  // falls back to the uniform split otherwise, so all blocks agree.
+  __shared__ int part_j0, part_j1, part_bad;
+  int j0 = db * A.db, j1 = (j0 + A.db < A.Bd) ? j0 + A.db : A.Bd;
+  if (A.balance) {
+    int32_t* const wpre = reinterpret_cast<int32_t*>(&res_tape[0][0][0][0]);  // (Bd + 1,)
+    const int Bd = A.Bd;
+    const int per = (Bd + 64 * kIbWaves - 1) / (64 * kIbWaves);  // documents per thread
+    const int jb = tid * per, je = jb + per < Bd ? jb + per : Bd;
+    int local = 0;
+    for (int j = jb; j < je; ++j) local += A.dcount[j] + 1;
+    if (tid == 0) { part_j0 = Bd; part_j1 = Bd; part_bad = 0; }
+    int total;
+    int run = block_exclusive_scan_i32(local, &total);
+    for (int j = jb; j < je; ++j) {
+      wpre[j] = run;
+      run += A.dcount[j] + 1;
+    }
+    __syncthreads();
+    const int ndbk = A.ndb, cap = A.dbcap;
+    auto bucket = [&](int j) { return (int)(((int64_t)wpre[j] * ndbk) / total); };
+    for (int j = tid; j < Bd; j += 64 * kIbWaves) {
+      const int bj = bucket(j);
+      const int bp = j > 0 ? bucket(j - 1) : -1;
+      if (bj >= db && bp < db) part_j0 = j;
+      if (bj >= db + 1 && bp < db + 1) part_j1 = j;
+      if (j + cap < Bd && bucket(j + cap) == bj) part_bad = 1;
+    }
+    __syncthreads();
+    if (!part_bad) {  // (LDS values: made wave-uniform for the buffer descriptors)
+      j0 = uniform(part_j0);
+      j1 = uniform(part_j1);
+    }
+    __syncthreads();  // partition scratch (result area) free again
+  }
   const int ndoc = j1 - j0;
   const int Tq = A.Tq, Td = A.Td;
   const int nch = Td > 0 ? (Td + kTile - 1) / kTile : 1;  // <= 64
   const int nall = ndoc * nch;
 
-  // ---- row validity of this block's chunks (one ballot each) ----------------
-  for (int c = wave; c < nall; c += kIbWaves) {
-    const int j = uniform(j0 + c / nch), ch = uniform(c % nch);
-    uint32_t mb = 1u;
-    if (A.dm) mb = buf_load1(make_rsrc(A.dm + (int64_t)j * Td, (uint32_t)Td), ch * kTile + r32);
-    const uint32_t m = (uint32_t)__ballot((ch * kTile + r32 < Td) && mb != 0u);
-    if (lane == 0) chunk_mask[c] = m;
+  // ---- this block's chunk masks and first tokens, from the plan ------------------
+  // (issued before the query loads, so waiting for them leaves those in flight)
+  uint32_t cm[kIbMaxChunkMasks / (64 * kIbWaves)];
+#pragma unroll
+  for (int k = 0; k < kIbMaxChunkMasks / (64 * kIbWaves); ++k) {
+    const int c = tid + k * 64 * kIbWaves;
+    cm[k] = c < nall ? A.cmask[(int64_t)j0 * nch + c] : 0u;
   }
+  const int dfv = tid < ndoc ? A.dfirst[j0 + tid] : -1;
 
   // ---- resident query tiles --------------------------------------------------
+  // Query masks are loaded unconditionally (an empty resource when absent
+  // reads 0) and tested only when a document closes.
   Frag qf[kIbQpw][kIbNkb];
-  bool tvalid[kIbQpw];
+  uint32_t qmb[kIbQpw];
+  bool qlive[kIbQpw];
   int qi[kIbQpw];
 #pragma unroll
   for (int q = 0; q < kIbQpw; ++q) {
     qi[q] = qb * kIbQueries + wave * kIbQpw + q;
     const bool live = qi[q] < A.Bq;
+    qlive[q] = live;
     const int iq = live ? qi[q] : 0;
     const rsrc_t rq = make_rsrc(A.Q + (int64_t)iq * Tq * kIbRowBytes,
                                 live ? (uint32_t)Tq * kIbRowBytes : 0u);
     const int base = r32 * kIbRowBytes + h * 16;
 #pragma unroll
     for (int kb = 0; kb < kIbNkb; ++kb) qf[q][kb] = Op::load(rq, base + kb * 32);
-    uint32_t mb = 1u;
-    if (A.qm) mb = buf_load1(make_rsrc(A.qm + (int64_t)iq * Tq, live ? (uint32_t)Tq : 0u), r32);
-    tvalid[q] = live && r32 < Tq && mb != 0u;
+    qmb[q] = buf_load1(make_rsrc(A.qm ? (const void*)(A.qm + (int64_t)iq * Tq) : (const void*)A.Q,
+                                 (A.qm && live) ? (uint32_t)Tq : 0u), r32);
   }
+  const bool has_qm = A.qm != nullptr;
+  auto token_valid = [&](int q) {
+    return qlive[q] && r32 < Tq && (!has_qm || qmb[q] != 0u);
+  };
+#pragma unroll
+  for (int k = 0; k < kIbMaxChunkMasks / (64 * kIbWaves); ++k) {
+    const int c = tid + k * 64 * kIbWaves;
+    if (c < nall) chunk_mask[c] = cm[k];
+  }
+  if (tid < ndoc) doc_first[tid] = dfv;
 
-  __syncthreads();  // chunk_mask complete
-  // ---- first valid token of each document; defaults of the results ----------
-  for (int jj = wave; jj < ndoc; jj += kIbWaves) {
-    const uint32_t m = lane < nch ? chunk_mask[jj * nch + lane] : 0u;
-    const uint64_t nz = __ballot(m != 0u);
-    int f = -1;
-    if (nz != 0u) {
-      const int k = uniform(__builtin_ctzll(nz));
-      f = k * kTile + __builtin_ctz((uint32_t)uniform((int)chunk_mask[jj * nch + k]));
-    }
-    if (lane == 0) doc_first[jj] = f;
-  }
+  // ---- defaults of the results --------------------------------------------------
   // A document without a valid token never closes: score 0, tape 0.
-  for (int e = tid; e < kIbWaves * kIbQpw * kIbMaxDocs * kTile; e += 64 * kIbWaves)
-    (&res_tape[0][0][0][0])[e] = 0;
+  static_assert(sizeof(res_tape) % (16 * 64 * kIbWaves) == 0, "whole 16-byte stores");
+#pragma unroll
+  for (int k = 0; k < (int)(sizeof(res_tape) / (16 * 64 * kIbWaves)); ++k)
+    reinterpret_cast<u32x4*>(&res_tape[0][0][0][0])[tid + k * 64 * kIbWaves] = u32x4{0u, 0u, 0u, 0u};
   for (int e = tid; e < kIbWaves * kIbQpw * kIbMaxDocs; e += 64 * kIbWaves)
     (&res_score[0][0][0])[e] = 0.0f;
-  __syncthreads();  // doc_first complete
+  __syncthreads();  // chunk_mask, doc_first complete
 
   // ---- compacted chunk list ------------------------------------------------------
   // Only chunks with at least one valid row are streamed and multiplied (a
@@ -214,33 +345,41 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
   for (int k = 0; k < kIbMaxChunkMasks / (64 * kIbWaves); ++k)
     if (last[k]) lst_info[tid + k * 64 * kIbWaves] |= 1u << kInfoLastBit;
   __syncthreads();
+  // Pad the stream to whole rounds of the kIbBufs buffers with repeats of
+  // its last entry, close bit cleared: folding a chunk again changes no
+  // result (a running max only moves on a strictly greater score, and after
+  // the document's close nothing reads it).  The lists hold kIbMaxList.
+  const int nsteps_pad = (nsteps + kIbBufs - 1) / kIbBufs * kIbBufs;
+  static_assert(kIbBufs <= 64 * kIbWaves, "one thread per padding entry");
+  if (tid < nsteps_pad - nsteps) {
+    lst_mask[nsteps + tid] = lst_mask[nsteps - 1];
+    lst_info[nsteps + tid] = lst_info[nsteps - 1] & ~(1u << kInfoLastBit);
+  }
+  __syncthreads();
 
   // ---- chunk stream -------------------------------------------------------------
   // One buffer resource spans the block's documents [j0, j1) (contiguous in
-  // D).  Thread tid moves kIbUnits 16-byte units of every chunk: unit
-  // tid + i*256 is row (tid>>4) + 16*i, column tid&15; a masked row loads
-  // the document's first valid token instead.  The stream position stops at
-  // the last list entry, so loads issued past the end re-read it.
+  // D).  A chunk goes HBM/L2 -> LDS with no registers in between: wave w
+  // fills k-blocks kb = kIbKbPerWave*w + k, one 16-byte load per lane: lane
+  // l loads units 2kb + l/32 of chunk row l%32 (a masked row loads the
+  // document's first valid token instead) into fragment slot kb*64 + l.
+  // The stream position stops at the last (padded) entry, so loads issued
+  // past the end re-read it.
   const rsrc_t rd = make_rsrc(A.D + (int64_t)j0 * Td * kIbRowBytes, (uint32_t)(ndoc * Td * kIbRowBytes));
-  const int urow = tid >> 4, ucol = tid & 15;
-  typedef u32x4 Stage[kIbUnits];
   int ld_i = 0;  // next list entry to request
-  auto chunk_load = [&](Stage& g, uint32_t m, uint32_t info) {
+  auto chunk_load = [&](u32x4* buf, uint32_t m, uint32_t info) {
     const int ch = info & 63u, jj = (info >> kInfoDocShift) & kInfoDocMask;
     const int f = (int)(info >> kInfoFirstShift) - 1;
     const int fsrc = f < 0 ? 0 : f;  // (never: listed chunks have a valid row)
+    const int src = ((m >> r32) & 1u) ? ch * kTile + r32 : fsrc;
+    const int voff = (jj * Td + src) * kIbRowBytes + h * 16;
 #pragma unroll
-    for (int i = 0; i < kIbUnits; ++i) {
-      const int row = urow + 16 * i;
-      const int src = ((m >> row) & 1u) ? ch * kTile + row : fsrc;
-      g[i] = buf_load16(rd, (jj * Td + src) * kIbRowBytes + ucol * 16);
+    for (int k = 0; k < kIbKbPerWave; ++k) {
+      const int kb = kIbKbPerWave * wave + k;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rd, (lds_ptr_t)(buf + kb * 64), 16,
+                                               voff + kb * 32, 0, 0, 0);
     }
-    if (ld_i + 1 < nsteps) ++ld_i;
-  };
-  auto lds_store = [&](int i, const Stage& g) {
-#pragma unroll
-    for (int u = 0; u < kIbUnits; ++u)
-      *reinterpret_cast<u32x4*>(&lds[i & 1][lds_off(urow + 16 * u, ucol)]) = g[u];
+    if (ld_i + 1 < nsteps_pad) ++ld_i;
   };
 
   float mx[kIbQpw];
@@ -261,90 +400,135 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
     const uint32_t mw = chunk_mask[jj * nch + (t0 >> 5)];
     const bool real = (tok > 0) & (((mw >> (t0 & 31)) & 1u) != 0u);
     tok = real ? tok : f + 1;
-    const float part = (tvalid[q] & (tok != 0)) ? m : 0.0f;
+    const bool tv = token_valid(q);
+    const float part = (tv & (tok != 0)) ? m : 0.0f;
     const float score = half_sum(part);
-    if (h == 0) res_tape[wave][q][jj][r32] = (int16_t)(tvalid[q] ? tok : 0);
+    if (h == 0) res_tape[wave][q][jj][r32] = (int16_t)(tv ? tok : 0);
     if (lane == 0) res_score[wave][q][jj] = score;
     mx[q] = -INFINITY;
     slot[q] = -1;
   };
 
+  // Fold one query tile's chunk scores into its running max/argmax, and
+  // close the document when `inf` is its last chunk.
+  auto fold_close = [&](int q, const Acc& ac, uint32_t inf) {
+    float sc[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sc[r] = ac[r];
+    fold_tree(sc, (int)(inf & 63u) * 16, mx[q], slot[q]);
+  };
+  auto close_if_last = [&](int q0, int q1, uint32_t inf) {
+    if (inf & (1u << kInfoLastBit)) {
+      const int jj = (inf >> kInfoDocShift) & kInfoDocMask;
+      const int f = (int)(inf >> kInfoFirstShift) - 1;
+      close(q0, jj, f);
+      close(q1, jj, f);
+    }
+  };
+
   // One step: entry i+1 register -> LDS, refill that register stage with
-  // entry i+3, multiply entry i (LDS buffer i%2) query by query with the
-  // previous query's fold interleaved, close the document after its last
-  // entry, read the list info for the next step, publish.
+  // entry i+3, read the list info for the next step, then two phases of 16
+  // MFMAs (two independent accumulation chains each):
+  //   phase 1: tiles 0,1 x entry i  while tiles 2,3 of entry i-1 are folded;
+  //   phase 2: tiles 2,3 x entry i  while tiles 0,1 of entry i are folded.
+  // Every phase's VALU work is independent of its MFMAs, so the two overlap
+  // within the wave, and only 4 accumulator tiles are ever live.
   uint32_t ld_m = 0u, ld_info = 0u;  // list entry ld_i, read one step ahead
   uint32_t cur_info = 0u;            // list entry i
-  auto step = [&](int i, Stage& g_next) {
-    lds_store(i + 1, g_next);
-    chunk_load(g_next, (uint32_t)uniform((int)ld_m), (uint32_t)uniform((int)ld_info));
+  uint32_t prev_info = 0u;           // list entry i-1 (no close bit before step 0)
+  Acc lag2, lag3;                    // tiles 2,3 of entry i-1
+#pragma unroll
+  for (int r = 0; r < 16; ++r) { lag2[r] = -INFINITY; lag3[r] = -INFINITY; }
+  // Step i multiplies buffer `cur` (entry i) and requests entry
+  // i + kIbBufs - 1 into buffer `ahead` (the one entry i-1 used).
+  auto step = [&](int i, const u32x4* cur, u32x4* ahead) {
+    chunk_load(ahead, (uint32_t)uniform((int)ld_m), (uint32_t)uniform((int)ld_info));
     // List entries for the next step, read now so the LDS latency hides
     // behind this step's MFMAs instead of stalling before the barrier.
     ld_m = lst_mask[ld_i];
     ld_info = lst_info[ld_i];
-    const uint32_t next_info = lst_info[i + 1 < nsteps ? i + 1 : i];
+    const uint32_t next_info = lst_info[i + 1 < nsteps_pad ? i + 1 : i];
     const uint32_t info = (uint32_t)uniform((int)cur_info);
-    const int ch = info & 63u;
+    const uint32_t pinfo = (uint32_t)uniform((int)prev_info);
     Frag a[kIbNkb];
 #pragma unroll
-    for (int kb = 0; kb < kIbNkb; ++kb)
-      a[kb] = *reinterpret_cast<const Frag*>(&lds[i & 1][lds_off(r32, 2 * kb + h)]);
-    Acc acc[kIbQpw];
-    // The query tiles' accumulations interleave k-block by k-block:
-    // kIbQpw independent MFMA chains, so no MFMA waits for the result of
-    // the one issued just before it (a dependent 32x32x16 MFMA issues at
-    // about half the rate of independent ones).
+    for (int kb = 0; kb < kIbNkb; ++kb) a[kb] = cur[kb * 64 + lane];
+    Acc n0 = Acc{}, n1 = Acc{};
 #pragma unroll
-    for (int q = 0; q < kIbQpw; ++q) acc[q] = Acc{};
-#pragma unroll
-    for (int kb = 0; kb < kIbNkb; ++kb)
-#pragma unroll
-      for (int q = 0; q < kIbQpw; ++q) acc[q] = Op::mma(a[kb], qf[q][kb], acc[q]);
-#pragma unroll
-    for (int q = 0; q < kIbQpw; ++q) {
-      float s[16];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s[r] = acc[q][r];
-      fold_tree(s, ch * 16, mx[q], slot[q]);
+    for (int kb = 0; kb < kIbNkb; ++kb) {
+      n0 = Op::mma(a[kb], qf[0][kb], n0);
+      n1 = Op::mma(a[kb], qf[1][kb], n1);
     }
-    if (info & (1u << kInfoLastBit)) {
-      const int jj = (info >> kInfoDocShift) & kInfoDocMask;
-      const int f = (int)(info >> kInfoFirstShift) - 1;
+    fold_close(2, lag2, pinfo);
+    fold_close(3, lag3, pinfo);
+    close_if_last(2, 3, pinfo);
+    Acc n2 = Acc{}, n3 = Acc{};
 #pragma unroll
-      for (int q = 0; q < kIbQpw; ++q) close(q, jj, f);
+    for (int kb = 0; kb < kIbNkb; ++kb) {
+      n2 = Op::mma(a[kb], qf[2][kb], n2);
+      n3 = Op::mma(a[kb], qf[3][kb], n3);
     }
+    fold_close(0, n0, info);
+    fold_close(1, n1, info);
+    close_if_last(0, 1, info);
+    lag2 = n2;
+    lag3 = n3;
+    prev_info = info;
     cur_info = next_info;
-    lds_barrier();
+    // Entry i+1's loads were issued before those of entries i+2 .. i+kIbBufs-1,
+    // which alone may remain.
+    dma_barrier<(kIbBufs - 2) * kIbKbPerWave>();
   };
 
-  if (nsteps > 0) {
-    Stage g0, g1;
-    chunk_load(g0, lst_mask[0], lst_info[0]);           // entry 0
-    chunk_load(g1, lst_mask[ld_i], lst_info[ld_i]);     // entry 1
-    lds_store(0, g0);
-    chunk_load(g0, lst_mask[ld_i], lst_info[ld_i]);     // entry 2
+  if (nsteps_pad > 0) {
+    chunk_load(cbuf0, lst_mask[0], lst_info[0]);         // entry 0
+    chunk_load(cbuf1, lst_mask[ld_i], lst_info[ld_i]);   // entry 1
+    if constexpr (kIbBufs == 4)
+      chunk_load(cbuf2, lst_mask[ld_i], lst_info[ld_i]); // entry 2
     ld_m = lst_mask[ld_i];
     ld_info = lst_info[ld_i];
     cur_info = lst_info[0];
-    lds_barrier();
-    int i = 0;
-    for (; i + 1 < nsteps; i += 2) {  // both steps unconditional: exact vmcnt waits
-      step(i, g1);      // g1 held entry i+1, now requests i+3
-      step(i + 1, g0);  // g0 held entry i+2, now requests i+4
+    dma_barrier<(kIbBufs - 2) * kIbKbPerWave>();  // entry 0 in LDS
+    // Every load is unconditional and the buffers rotate statically.
+    for (int i = 0; i < nsteps_pad; i += kIbBufs) {
+      if constexpr (kIbBufs == 4) {
+        step(i, cbuf0, cbuf3);
+        step(i + 1, cbuf1, cbuf0);
+        step(i + 2, cbuf2, cbuf1);
+        step(i + 3, cbuf3, cbuf2);
+      } else {
+        step(i, cbuf0, cbuf2);
+        step(i + 1, cbuf1, cbuf0);
+        step(i + 2, cbuf2, cbuf1);
+      }
     }
-    if (i < nsteps) step(i, g1);
+    // No load into LDS may outlive the workgroup.
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    // tiles 2,3 of the last entry
+    const uint32_t pinfo = (uint32_t)uniform((int)prev_info);
+    fold_close(2, lag2, pinfo);
+    fold_close(3, lag3, pinfo);
+    close_if_last(2, 3, pinfo);
   }
   __syncthreads();  // results of every wave staged
 
   // ---- write the block's tape and scores (coalesced) ------------------------------
+  // Query qi's tape for documents j0..j1-1 is one contiguous run of ndoc * Tq
+  // int32 in A.args; its scores are ndoc contiguous floats in A.S.
 #pragma unroll
   for (int q = 0; q < kIbQpw; ++q) {
     if (qi[q] >= A.Bq) continue;
-    for (int jj = 0; jj < ndoc; ++jj) {
-      const int64_t p = (int64_t)qi[q] * A.Bd + (j0 + jj);
-      if (A.args && h == 0 && r32 < Tq) A.args[p * Tq + r32] = res_tape[wave][q][jj][r32];
-      if (lane == 0) A.S[p] = res_score[wave][q][jj];
+    const int64_t p0 = (int64_t)qi[q] * A.Bd + j0;
+    if (A.args) {
+      int32_t* const out = A.args + p0 * Tq;
+      const int n = ndoc * Tq;
+#pragma unroll 4
+      for (int e = lane; e < n; e += 64) {
+        const int jj = e / Tq, t = e - jj * Tq;
+        out[e] = res_tape[wave][q][jj][t];
+      }
     }
+    if (lane < ndoc) A.S[p0 + lane] = res_score[wave][q][lane];
   }
 }
 
@@ -353,9 +537,9 @@ hipError_t launch_inbatch_mfma(int dtype_bf16, const InBatchArgs& args_in, hipSt
   A.nqb = (A.Bq + kIbQueries - 1) / kIbQueries;
   // Documents per block: the grid should be a whole number of rounds of the
   // resident block slots (kIbBlocksPerCu per CU) -- a last round that
-  // fills only part of the GPU idles the rest -- with at least two rounds
-  // for balance, as few blocks as that allows (each block pays one set-up),
-  // and the block's chunk list within kIbMaxChunkMasks.
+  // fills only part of the GPU idles the rest -- as few blocks as that
+  // allows (each block pays one set-up), and the block's chunk list within
+  // kIbMaxChunkMasks.
   int dev = 0, cus = 256;
   if (hipGetDevice(&dev) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
@@ -364,21 +548,47 @@ hipError_t launch_inbatch_mfma(int dtype_bf16, const InBatchArgs& args_in, hipSt
   const int64_t slots = (int64_t)cus * kIbBlocksPerCu;
   const int nch = A.Td > 0 ? (A.Td + kTile - 1) / kTile : 1;
   const int db_cap = std::min(kIbMaxDocs, std::max(1, kIbMaxChunkMasks / nch));
+  // With the balanced split (blocks of equal work) one round is enough; the
+  // uniform split keeps two, so the dispatcher can even out lengths.
+  const int balance = A.Bd <= kIbBalanceMaxDocs ? 1 : 0;
   int db = 1;
-  for (int64_t rounds = 2; rounds <= 64; ++rounds) {
+  for (int64_t rounds = balance ? 1 : 2; rounds <= 64; ++rounds) {
     const int64_t ndb_want = (rounds * slots + A.nqb - 1) / A.nqb;
     db = (int)std::max<int64_t>(1, (A.Bd + ndb_want - 1) / ndb_want);
     if (db <= db_cap) break;
   }
   db = std::min(db, db_cap);
   A.db = db;
+  A.dbcap = db_cap;
   A.ndb = (A.Bd + db - 1) / db;
-  const dim3 grid((unsigned)(A.nqb * A.ndb)), block(64 * kIbWaves);
-  if (dtype_bf16)
-    hipLaunchKernelGGL((inbatch_mfma<OpBF16>), grid, block, 0, stream, A);
-  else
-    hipLaunchKernelGGL((inbatch_mfma<OpF16>), grid, block, 0, stream, A);
-  return hipGetLastError();
+  A.balance = balance;
+
+  // Plan workspace: chunk masks, chunk counts, first tokens.
+  auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
+  const size_t mask_bytes = al((size_t)A.Bd * nch * 4), vec_bytes = al((size_t)A.Bd * 4);
+  void* ws = nullptr;
+  hipError_t e = workspace_alloc(&ws, mask_bytes + 2 * vec_bytes, stream);
+  if (e != hipSuccess) return e;
+  char* w = static_cast<char*>(ws);
+  uint32_t* cmask = reinterpret_cast<uint32_t*>(w);
+  int32_t* dcount = reinterpret_cast<int32_t*>(w + mask_bytes);
+  int32_t* dfirst = reinterpret_cast<int32_t*>(w + mask_bytes + vec_bytes);
+  A.cmask = cmask;
+  A.dcount = dcount;
+  A.dfirst = dfirst;
+  hipLaunchKernelGGL(inbatch_plan_kernel, dim3((unsigned)((A.Bd + 3) / 4)), dim3(256), 0, stream,
+                     A.dm, A.Bd, A.Td, nch, cmask, dcount, dfirst);
+  e = hipGetLastError();
+  if (e == hipSuccess) {
+    const dim3 grid((unsigned)(A.nqb * A.ndb)), block(64 * kIbWaves);
+    if (dtype_bf16)
+      hipLaunchKernelGGL((inbatch_mfma<OpBF16>), grid, block, 0, stream, A);
+    else
+      hipLaunchKernelGGL((inbatch_mfma<OpF16>), grid, block, 0, stream, A);
+    e = hipGetLastError();
+  }
+  const hipError_t ef = workspace_free(ws, stream);
+  return e != hipSuccess ? e : ef;
 }
 
 // A block's documents span one buffer resource: ndoc * Td * 256 bytes <=

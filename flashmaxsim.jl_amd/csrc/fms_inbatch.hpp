@@ -14,11 +14,20 @@ struct InBatchArgs {
   float* S;            // (Bq, Bd): S[i*Bd + j] = MaxSim(Q_i, D_j)
   int32_t* args;       // (Bq, Bd, Tq) nullable
   int Bq, Bd, Tq, Td;
-  int nqb, ndb, db;    // filled by the launcher
+  // filled by the launcher
+  int nqb, ndb;        // query blocks, document blocks
+  int db;              // documents per block of the uniform partition
+  int dbcap;           // most documents a block can hold
+  int balance;         // 1: partition documents by chunk count (Bd <= kIbBalanceMaxDocs)
+  const uint32_t* cmask;  // (Bd, nch) valid rows per chunk (plan kernel)
+  const int32_t* dcount;  // (Bd,) chunks with a valid row
+  const int32_t* dfirst;  // (Bd,) first valid token, -1 = none
 };
 
 // dim == 128, 1 <= Tq <= 32, 16-byte aligned features.
 bool inbatch_mfma_supported(int64_t dim, int64_t Tq, int64_t Td, const void* Q, const void* D);
+// Runs the plan kernel (per-document chunk masks, in a workspace from the
+// library pool) and the in-batch kernel on `stream`.
 hipError_t launch_inbatch_mfma(int dtype_bf16, const InBatchArgs& args, hipStream_t stream);
 
 }  // namespace fms

@@ -16,7 +16,8 @@ import torch  # noqa: F401  (must precede the CDLL load, see module docstring)
 from .errors import ArgumentError, DimensionMismatch, HIPError, UnsupportedError
 
 _PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-LIB_PATH = os.path.join(_PKG_DIR, "lib", "libflashmaxsim_hip.so")
+# FLASHMAXSIM_HIP_LIB names another build of the same library (same ABI).
+LIB_PATH = os.environ.get("FLASHMAXSIM_HIP_LIB") or os.path.join(_PKG_DIR, "lib", "libflashmaxsim_hip.so")
 
 FMS_OK, FMS_EINVAL, FMS_EUNSUPPORTED, FMS_EHIP = 0, 1, 2, 3
 FMS_F32, FMS_F16, FMS_BF16 = 0, 1, 2

@@ -153,7 +153,10 @@ def test_candidates_parity(device, dtype, shape, idx_dtype):
 @pytest.mark.parametrize("shape", [(128, 32, 180, 6, 5), (40, 33, 65, 3, 4), (16, 8, 10, 4, 4),
                                    # dim 128: the MFMA-tiled in-batch kernel
                                    (128, 32, 180, 40, 37), (128, 1, 1, 3, 2), (128, 24, 65, 17, 9),
-                                   (128, 32, 33, 20, 3), (128, 8, 40, 512, 1024)],
+                                   (128, 32, 33, 20, 3), (128, 8, 40, 512, 1024),
+                                   # long documents: a block's chunk stream holds the
+                                   # full 512-entry list (padded past it)
+                                   (128, 32, 1000, 20, 40), (128, 16, 2048, 17, 9)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_inbatch_parity(device, dtype, shape):
     dim, Tq, Td, Bq, Bd = shape
@@ -218,6 +221,46 @@ def test_inbatch_masks_and_ties(device, dtype, shape):
     ii, jj, tt = np.nonzero(got)
     assert dm[jj, got[ii, jj, tt] - 1].all()
     # mismatches only at near-ties between tokens that are not exact copies
+    Qf, Df = widened(Qo, bf), widened(Do, bf)
+    assert_tape(got, a_o, _pair_sims_fn(Qf, Df, lambda p: (Qf[p[0]], Df[p[1]])), tol)
+    for i, j, t in np.argwhere(got != a_o):
+        g, w = got[i, j, t] - 1, a_o[i, j, t] - 1
+        assert not np.array_equal(Do[j, g], Do[j, w]), (i, j, t, g, w)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=lambda d: DT_ID[d])
+@pytest.mark.parametrize("shape", [(32, 180, 24, 21), (17, 65, 40, 33), (8, 300, 20, 17)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_inbatch_negative_maxima(device, dtype, shape):
+    """Every dot product negative (queries in the positive orthant, documents
+    in the negative one), with exact duplicate tokens: every chunk maximum is
+    below zero, which the MFMA-tiled kernel folds on its exact path; exact
+    ties must still keep the first occurrence (forward_pair.jl:82-85) and
+    the all-negative maxima stay negative (test_regressions.jl:136-147)."""
+    Tq, Td, Bq, Bd = shape
+    dim = 128
+    rng = np.random.default_rng(Tq * 7 + Td)
+    q32 = np.abs(tokens(rng, (Bq, Tq, dim)))
+    d32 = -np.abs(tokens(rng, (Bd, Td, dim)))
+    q32 /= np.linalg.norm(q32, axis=-1, keepdims=True)
+    d32 /= np.linalg.norm(d32, axis=-1, keepdims=True)
+    for j in range(Bd):  # later rows copy earlier ones: exact ties
+        for _ in range(4):
+            a, b = np.sort(rng.choice(Td, 2, replace=False))
+            d32[j, b] = d32[j, a]
+    dm = rng.random((Bd, Td)) < 0.8
+    dm[:, 0] = True
+    Qt, Qo, bf = as_feature(q32.astype(np.float32), dtype)
+    Dt, Do, _ = as_feature(d32.astype(np.float32), dtype)
+    qm = torch.ones(Bq, Tq, dtype=torch.bool)
+    dmt = torch.from_numpy(dm)
+    S_o, a_o = oracle.inbatch_forward(Qo, Do, mask_np(qm), mask_np(dmt), bf16=bf)
+    S, args = fm.inbatch_forward(Qt.to(device), Dt.to(device), qm.to(device), dmt.to(device))
+    torch.cuda.synchronize()
+    tol = FEATURE_TOL[dtype]
+    assert (S_o < 0).all()
+    assert_scores(S.cpu(), S_o, tol, what="S")
+    got = args.cpu().numpy()
     Qf, Df = widened(Qo, bf), widened(Do, bf)
     assert_tape(got, a_o, _pair_sims_fn(Qf, Df, lambda p: (Qf[p[0]], Df[p[1]])), tol)
     for i, j, t in np.argwhere(got != a_o):

@@ -19,6 +19,18 @@ namespace fms {
 // Even and odd k-blocks accumulate into two independent chains, added when
 // the chunk's last batch is done.
 
+// Layouts whose positions all score the same query (a packed call scores
+// one query against every document): the split kernel stages that query in
+// LDS once per workgroup, in MFMA fragment order, instead of re-reading it
+// from L1/L2 for every chunk.  Fragment (qt, kb, lane) sits at
+// (qt * nkb + kb) * 64 + lane.
+template <class L>
+struct shared_query { static constexpr bool value = false; };
+template <>
+struct shared_query<LayPacked> { static constexpr bool value = true; };
+
+constexpr int kSplitLdsQBytes = 64 * 1024;  // largest staged query (nqt * nkb KB)
+
 template <class Op, int KBAT>
 struct SplitBatch {
   typename Op::Frag a[KBAT];     // document fragments
@@ -29,10 +41,10 @@ struct SplitBatch {
   float ds[Op::kInt ? 16 : 1];   // int8 document scales of the accumulator rows
 };
 
-template <class Op, int KBAT>
+template <class Op, int KBAT, bool kLdsQ>
 __device__ __forceinline__ void load_split(SplitBatch<Op, KBAT>& c, const PairView& v, int qt,
                                            int ch, int bi, int rowbytes, int h, int r32,
-                                           bool ds_vec) {
+                                           bool ds_vec, const u32x4* qlds, int nkb) {
   const int kofs = (bi * KBAT * Op::kKb + h * Op::kEpl) * Op::kEsz;
   const rsrc_t rd = make_rsrc_u(v.d, (uint32_t)v.td * (uint32_t)rowbytes);
   const rsrc_t rq = make_rsrc_u(v.q, (uint32_t)v.tq * (uint32_t)rowbytes);
@@ -41,7 +53,10 @@ __device__ __forceinline__ void load_split(SplitBatch<Op, KBAT>& c, const PairVi
 #pragma unroll
   for (int k = 0; k < KBAT; ++k) {
     c.a[k] = Op::load(rd, dbase + k * Op::kKb * Op::kEsz);
-    c.b[k] = Op::load(rq, qbase + k * Op::kKb * Op::kEsz);
+    if constexpr (kLdsQ)
+      c.b[k] = qlds[(qt * nkb + bi * KBAT + k) * 64 + h * 32 + r32];
+    else
+      c.b[k] = Op::load(rq, qbase + k * Op::kKb * Op::kEsz);
   }
   // Masks read unconditionally (zero-size resource when absent, see mask_ok).
   const bool has_dm = v.dm != nullptr, has_qm = v.qm != nullptr;
@@ -58,10 +73,35 @@ __device__ __forceinline__ void load_split(SplitBatch<Op, KBAT>& c, const PairVi
   load_ds<Op>(c.ds, v, ch, h, ds_vec);
 }
 
-template <class Op, class L, int KBAT>
+template <class Op, class L, int KBAT, bool kLdsQ>
 __global__ void __launch_bounds__(64 * kWaves) scan_split(const ScanArgs<L> A) {
   typedef typename Op::Acc Acc;
   const int lane = threadIdx.x & 63, r32 = lane & 31, h = lane >> 5;
+  extern __shared__ u32x4 qlds[];  // kLdsQ: the shared query, nqt * nkb * 64 fragments
+  if constexpr (kLdsQ) {
+    // Every thread of the block takes part (before any wave may leave):
+    // fragment (qt, kb, lane) = 16 bytes of query row qt*32 + lane%32 at
+    // element kb*KB + (lane/32)*kEpl; rows past tq read 0.
+    const PairView v0 = uniform_view(A.lay.get(0));
+    const int rb = A.dim * Op::kEsz;
+    const rsrc_t rq = make_rsrc_u(v0.q, (uint32_t)v0.tq * (uint32_t)rb);
+    const int nfrag = A.nqt * A.nkb * 64;
+    constexpr int kBatch = 8;  // loads in flight per thread
+    for (int u0 = threadIdx.x; u0 < nfrag; u0 += kBatch * 64 * kWaves) {
+      typename Op::Frag f[kBatch];
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        const int u = u0 + j * 64 * kWaves;
+        const int fl = u & 63, kb = (u >> 6) % A.nkb, qt = (u >> 6) / A.nkb;
+        // (u past nfrag: qt == A.nqt, a row past tq, which reads 0 and is not stored)
+        f[j] = Op::load(rq, (qt * kTile + (fl & 31)) * rb + (kb * Op::kKb + (fl >> 5) * Op::kEpl) * Op::kEsz);
+      }
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j)
+        if (u0 + j * 64 * kWaves < nfrag) qlds[u0 + j * 64 * kWaves] = f[j];
+    }
+    __syncthreads();
+  }
   int64_t first, stride;
   int cnt;
   wave_positions(A, first, stride, cnt);
@@ -81,7 +121,7 @@ __global__ void __launch_bounds__(64 * kWaves) scan_split(const ScanArgs<L> A) {
   float mx = -INFINITY, score = 0.0f;
   int slot = -1;
 
-  load_split<Op, KBAT>(bufA, v, 0, 0, 0, rowbytes, h, r32, ds_vec);
+  load_split<Op, KBAT, kLdsQ>(bufA, v, 0, 0, 0, rowbytes, h, r32, ds_vec, qlds, A.nkb);
 
   auto step = [&](SplitBatch<Op, KBAT>& cur, SplitBatch<Op, KBAT>& nxt) -> bool {
     // advance a copy of the cursor and prefetch its batch
@@ -106,8 +146,8 @@ __global__ void __launch_bounds__(64 * kWaves) scan_split(const ScanArgs<L> A) {
     // One call on a selected cursor (after the wave's last batch it re-reads
     // the current one): two calls under `if (more)` get merged with their
     // arguments as divergent phis, and the loads become waterfall loops.
-    load_split<Op, KBAT>(nxt, more ? nv : v, more ? nqt_i : qt, more ? nch_i : ch,
-                         more ? nbi : bi, rowbytes, h, r32, ds_vec);
+    load_split<Op, KBAT, kLdsQ>(nxt, more ? nv : v, more ? nqt_i : qt, more ? nch_i : ch,
+                                more ? nbi : bi, rowbytes, h, r32, ds_vec, qlds, A.nkb);
     __builtin_amdgcn_sched_barrier(0);
 
 #pragma unroll
@@ -150,7 +190,14 @@ __global__ void __launch_bounds__(64 * kWaves) scan_split(const ScanArgs<L> A) {
 
 template <class Op, class L>
 hipError_t launch_split(const ScanArgs<L>& A, dim3 grid, dim3 block, hipStream_t stream) {
-  hipLaunchKernelGGL((scan_split<Op, L, split_kbat<Op>()>), grid, block, 0, stream, A);
+  if constexpr (shared_query<L>::value && Op::kEsz == 2) {
+    const size_t qbytes = (size_t)A.nqt * A.nkb * 64 * 16;
+    if (A.npairs > 0 && qbytes <= (size_t)kSplitLdsQBytes) {
+      hipLaunchKernelGGL((scan_split<Op, L, split_kbat<Op>(), true>), grid, block, qbytes, stream, A);
+      return hipGetLastError();
+    }
+  }
+  hipLaunchKernelGGL((scan_split<Op, L, split_kbat<Op>(), false>), grid, block, 0, stream, A);
   return hipGetLastError();
 }
 

@@ -113,3 +113,28 @@ def test_split_varlen_parity(device):
     Qf, Df = widened(Qo, bf), widened(Do, bf)
     assert_tape(args.cpu().numpy(), a_o,
                 lambda p: Df[cu_d[p[0]] - 1: cu_d[p[0] + 1] - 1] @ Qf[cu_q[p[0]] - 1 + p[1]], tol)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=lambda d: DT_ID[d])
+@pytest.mark.parametrize("dim,Tq", [(1024, 24), (512, 64), (1024, 40), (384, 7)],
+                         ids=lambda x: str(x))
+def test_split_packed_query_staging(device, dtype, dim, Tq):
+    """Packed calls score one query against every document; the split kernel
+    stages that query in LDS when it fits (1024x24, 512x64: two query tiles,
+    384x7) and reads it from global memory otherwise (1024x40)."""
+    rng = np.random.default_rng(dim + Tq)
+    lens = [40, 0, 97, 3, 33, 64, 1]
+    docs = [tokens(rng, (n, dim)) for n in lens]
+    Qt, Qo, bf = as_feature(tokens(rng, (Tq, dim)), dtype)
+    Tt, To, _ = as_feature(np.concatenate(docs, 0), dtype)
+    cu = np.concatenate([[1], 1 + np.cumsum(lens)]).astype(np.int32)
+    qm = torch.from_numpy(rng.random(Tq) < 0.9)
+    s_o, a_o, _ = oracle.packed_forward(Qo, To, cu, mask_np(qm), bf16=bf)
+    P = fm.PackedSeq(Tt, torch.from_numpy(cu)).to(device)
+    scores, args = fm.packed_forward(Qt.to(device), P, qm.to(device))
+    torch.cuda.synchronize()
+    tol = FEATURE_TOL[dtype]
+    assert_scores(scores.cpu(), s_o, tol)
+    Qf, Tf = widened(Qo, bf), widened(To, bf)
+    assert_tape(args.cpu().numpy(), a_o,
+                lambda p: Tf[cu[p[0]] - 1: cu[p[0] + 1] - 1] @ Qf[p[1]], tol)

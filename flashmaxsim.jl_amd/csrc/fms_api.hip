@@ -12,6 +12,7 @@
 #include <atomic>
 
 #include "../../include/flashmaxsim_hip.h"
+#include "fms_backward.hpp"
 #include "fms_group.hpp"
 #include "fms_inbatch.hpp"
 #include "fms_misc.hpp"
@@ -125,6 +126,48 @@ fms_status run_candidates(const LayCand& lay, int64_t npairs, hipStream_t st, La
     (void)hipGetLastError();  // clear the failed allocation; scan in output order
   }
   return from_hip(launch(lay));
+}
+
+}  // namespace
+
+// ---- backward helpers ----------------------------------------------------------
+
+namespace {
+
+// Sources are numbered p * rows + t in 32 bits; destination rows index in 32 bits.
+bool pullback_ok(int64_t npairs, int64_t rows, int64_t nd_rows) {
+  return npairs * rows < ((int64_t)1 << 31) && nd_rows < ((int64_t)1 << 31);
+}
+
+PullbackArgs pullback_args(int32_t dtype, void* dQ, void* dD, const void* Q, const void* D,
+                           const int32_t* args, const void* Delta, const void* inv_n,
+                           int64_t npairs, int64_t G, int64_t nq_rows, int64_t nd_rows,
+                           int64_t rows, int64_t dim) {
+  PullbackArgs a;
+  a.dtype = dtype;
+  a.dQ = static_cast<char*>(dQ);
+  a.dD = static_cast<char*>(dD);
+  a.Qbase = static_cast<const char*>(Q);
+  a.Dbase = static_cast<const char*>(D);
+  a.args = args;
+  a.Delta = Delta;
+  a.inv_n = inv_n;
+  a.npairs = npairs;
+  a.G = npairs > 0 ? G : 1;
+  a.nq_rows = nq_rows;
+  a.nd_rows = nd_rows;
+  a.rows = (int)rows;
+  a.dim = (int)dim;
+  a.zero_dq = false;
+  return a;
+}
+
+// The pointers an output of `rows` rows needs, and the inputs the pairs read.
+bool pullback_ptrs(int64_t nq_rows, const void* Q, const void* dQ, int64_t nd_rows, const void* D,
+                   const void* dD, int64_t npairs, const void* args, const void* Delta) {
+  if (nq_rows > 0 && (!Q || !dQ)) return false;
+  if (nd_rows > 0 && (!D || !dD)) return false;
+  return npairs == 0 || (args && Delta);
 }
 
 }  // namespace
@@ -439,6 +482,164 @@ fms_status fms_debug_read_bandwidth(const void* p, int64_t bytes, uint32_t* out,
       !aligned16(p))
     return FMS_EINVAL;
   return from_hip(read_bandwidth(p, bytes, out, blocks, as_stream(stream)));
+}
+
+// ---- backward on the argmax tape ----------------------------------------------
+
+fms_status fms_paired_pullback(int32_t dtype, void* dQ, void* dD, const void* Q, const void* D,
+                               const uint8_t* qmask, const int32_t* args, const void* Delta,
+                               const void* inv_n, int64_t dim, int64_t Tq, int64_t Td, int64_t B,
+                               void* stream) {
+  const int esz = elem_bytes(dtype);
+  if (esz == 0) return FMS_EUNSUPPORTED;
+  if (dim < 0 || Tq < 0 || Td < 0 || B < 0) return FMS_EINVAL;
+  if (!seq_ok(Tq, dim, esz) || !seq_ok(Td, dim, esz) || !pullback_ok(B, Tq, B * Td))
+    return FMS_EUNSUPPORTED;
+  if (dim == 0 || B == 0 || (Tq == 0 && Td == 0)) return FMS_OK;
+  const int64_t npairs = (Tq > 0 && Td > 0) ? B : 0;
+  if (!pullback_ptrs(B * Tq, Q, dQ, B * Td, D, dD, npairs, args, Delta)) return FMS_EINVAL;
+  LayPaired lay;
+  lay.Q = static_cast<const char*>(Q);
+  lay.D = static_cast<const char*>(D);
+  lay.qm = qmask;
+  lay.dm = nullptr;
+  lay.Qs = nullptr;
+  lay.Ds = nullptr;
+  lay.qbytes = Tq * dim * esz;
+  lay.dbytes = Td * dim * esz;
+  lay.Tq = (int)Tq;
+  lay.Td = (int)Td;
+  const PullbackArgs a =
+      pullback_args(dtype, dQ, dD, Q, D, args, Delta, inv_n, npairs, 1, B * Tq, B * Td, Tq, dim);
+  return from_hip(launch_pullback(lay, a, as_stream(stream)));
+}
+
+fms_status fms_pair_pullback(int32_t dtype, void* dq, void* dd, const void* q, const void* d,
+                             const uint8_t* qmask, const int32_t* argmax_u, const void* delta,
+                             int64_t dim, int64_t Tq, int64_t Td, void* stream) {
+  return fms_paired_pullback(dtype, dq, dd, q, d, qmask, argmax_u, delta, nullptr, dim, Tq, Td, 1,
+                             stream);
+}
+
+fms_status fms_inbatch_pullback(int32_t dtype, void* dQ, void* dD, const void* Q, const void* D,
+                                const uint8_t* qmask, const int32_t* args, const void* Delta,
+                                const void* inv_n, int64_t dim, int64_t Tq, int64_t Td,
+                                int64_t Bq, int64_t Bd, void* stream) {
+  const int esz = elem_bytes(dtype);
+  if (esz == 0) return FMS_EUNSUPPORTED;
+  if (dim < 0 || Tq < 0 || Td < 0 || Bq < 0 || Bd < 0) return FMS_EINVAL;
+  if (!seq_ok(Tq, dim, esz) || !seq_ok(Td, dim, esz) || Bq > kMaxTokens || Bd > kMaxTokens ||
+      !pullback_ok(Bq * Bd, Tq, Bd * Td))
+    return FMS_EUNSUPPORTED;
+  if (dim == 0 || (Bq * Tq == 0 && Bd * Td == 0)) return FMS_OK;
+  const int64_t npairs = (Tq > 0 && Td > 0) ? Bq * Bd : 0;
+  if (!pullback_ptrs(Bq * Tq, Q, dQ, Bd * Td, D, dD, npairs, args, Delta)) return FMS_EINVAL;
+  LayInBatch lay;
+  lay.Q = static_cast<const char*>(Q);
+  lay.D = static_cast<const char*>(D);
+  lay.qm = qmask;
+  lay.dm = nullptr;
+  lay.qbytes = Tq * dim * esz;
+  lay.dbytes = Td * dim * esz;
+  lay.Bd = Bd > 0 ? Bd : 1;
+  lay.Tq = (int)Tq;
+  lay.Td = (int)Td;
+  const PullbackArgs a = pullback_args(dtype, dQ, dD, Q, D, args, Delta, inv_n, npairs, Bd, Bq * Tq,
+                                       Bd * Td, Tq, dim);
+  return from_hip(launch_pullback(lay, a, as_stream(stream)));
+}
+
+fms_status fms_candidates_pullback(int32_t dtype, void* dQ, void* dG, const void* Q,
+                                   const void* gallery, const void* idx, int32_t idx_bytes,
+                                   const uint8_t* qmask, const int32_t* args, const void* Delta,
+                                   const void* inv_n, int64_t dim, int64_t Tq, int64_t B,
+                                   int64_t Td, int64_t N, int64_t C, void* stream) {
+  const int esz = elem_bytes(dtype);
+  if (esz == 0) return FMS_EUNSUPPORTED;
+  if (dim < 0 || Tq < 0 || Td < 0 || B < 0 || N < 0 || C < 0) return FMS_EINVAL;
+  if (idx_bytes != 4 && idx_bytes != 8) return FMS_EINVAL;
+  if (!seq_ok(Tq, dim, esz) || !seq_ok(Td, dim, esz) || !pullback_ok(C * B, Tq, N * Td))
+    return FMS_EUNSUPPORTED;
+  if (dim == 0 || (B * Tq == 0 && N * Td == 0)) return FMS_OK;
+  const int64_t npairs = (Tq > 0 && Td > 0) ? C * B : 0;
+  if (!pullback_ptrs(B * Tq, Q, dQ, N * Td, gallery, dG, npairs, args, Delta) || (npairs > 0 && !idx))
+    return FMS_EINVAL;
+  LayCand lay;
+  lay.Q = static_cast<const char*>(Q);
+  lay.G = static_cast<const char*>(gallery);
+  lay.idx = idx;
+  lay.idx64 = idx_bytes == 8;
+  lay.qm = qmask;
+  lay.dm = nullptr;
+  lay.Qs = nullptr;
+  lay.Gs = nullptr;
+  lay.qbytes = Tq * dim * esz;
+  lay.dbytes = Td * dim * esz;
+  lay.N = N;
+  lay.C = C > 0 ? C : 1;
+  lay.Tq = (int)Tq;
+  lay.Td = (int)Td;
+  const PullbackArgs a = pullback_args(dtype, dQ, dG, Q, gallery, args, Delta, inv_n, npairs, C,
+                                       B * Tq, N * Td, Tq, dim);
+  return from_hip(launch_pullback(lay, a, as_stream(stream)));
+}
+
+fms_status fms_packed_pullback(int32_t dtype, void* dq, void* dP, const void* q,
+                               const void* tokens, const int32_t* cu, const uint8_t* qmask,
+                               const int32_t* args, const void* Delta, const void* inv_n,
+                               int64_t dim, int64_t Tq, int64_t B, int64_t ntokens,
+                               void* stream) {
+  const int esz = elem_bytes(dtype);
+  if (esz == 0) return FMS_EUNSUPPORTED;
+  if (dim < 0 || Tq < 0 || B < 0 || ntokens < 0) return FMS_EINVAL;
+  if (!seq_ok(Tq, dim, esz) || ntokens > kMaxTokens || !pullback_ok(B, Tq, ntokens))
+    return FMS_EUNSUPPORTED;
+  if (dim == 0 || (Tq == 0 && ntokens == 0)) return FMS_OK;
+  const int64_t npairs = (Tq > 0 && ntokens > 0) ? B : 0;
+  if (!pullback_ptrs(Tq, q, dq, ntokens, tokens, dP, npairs, args, Delta) || (npairs > 0 && !cu))
+    return FMS_EINVAL;
+  LayPacked lay;
+  lay.q = static_cast<const char*>(q);
+  lay.tok = static_cast<const char*>(tokens);
+  lay.cu = cu;
+  lay.qm = qmask;
+  lay.ntok = ntokens;
+  lay.rowbytes = dim * esz;
+  lay.Tq = (int)Tq;
+  const PullbackArgs a =
+      pullback_args(dtype, dq, dP, q, tokens, args, Delta, inv_n, npairs, B, Tq, ntokens, Tq, dim);
+  return from_hip(launch_pullback(lay, a, as_stream(stream)));
+}
+
+fms_status fms_varlen_pullback(int32_t dtype, void* dQ, void* dD, const void* Qtokens,
+                               const void* Dtokens, const int32_t* cu_q, const int32_t* cu_d,
+                               const int32_t* args, const void* Delta, const void* inv_n,
+                               int64_t dim, int64_t max_q, int64_t N, int64_t nq_tokens,
+                               int64_t nd_tokens, void* stream) {
+  const int esz = elem_bytes(dtype);
+  if (esz == 0) return FMS_EUNSUPPORTED;
+  if (dim < 0 || max_q < 0 || N < 0 || nq_tokens < 0 || nd_tokens < 0) return FMS_EINVAL;
+  if (!seq_ok(max_q, dim, esz) || nq_tokens > kMaxTokens || nd_tokens > kMaxTokens ||
+      !pullback_ok(N, max_q, nd_tokens))
+    return FMS_EUNSUPPORTED;
+  if (dim == 0 || (nq_tokens == 0 && nd_tokens == 0)) return FMS_OK;
+  const int64_t npairs = (max_q > 0 && nq_tokens > 0 && nd_tokens > 0) ? N : 0;
+  if (!pullback_ptrs(nq_tokens, Qtokens, dQ, nd_tokens, Dtokens, dD, npairs, args, Delta) ||
+      (npairs > 0 && (!cu_q || !cu_d)))
+    return FMS_EINVAL;
+  LayVarlen lay;
+  lay.Qt = static_cast<const char*>(Qtokens);
+  lay.Dt = static_cast<const char*>(Dtokens);
+  lay.cu_q = cu_q;
+  lay.cu_d = cu_d;
+  lay.nq = nq_tokens;
+  lay.nd = nd_tokens;
+  lay.rowbytes = dim * esz;
+  lay.max_q = (int)max_q;
+  PullbackArgs a = pullback_args(dtype, dQ, dD, Qtokens, Dtokens, args, Delta, inv_n, npairs, 1,
+                                 nq_tokens, nd_tokens, max_q, dim);
+  a.zero_dq = true;  // query tokens outside every pair's range get no gather
+  return from_hip(launch_pullback(lay, a, as_stream(stream)));
 }
 
 }  // extern "C"

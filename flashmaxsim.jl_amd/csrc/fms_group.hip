@@ -174,6 +174,19 @@ hipError_t group_pairs_by_document(const void* idx, int idx64, int64_t npairs, i
   return hipGetLastError();
 }
 
+size_t scan_workspace_bytes(int64_t n) { return align256((size_t)cdiv(n > 0 ? n : 1, kScanTile) * 4); }
+
+hipError_t exclusive_scan_u32(uint32_t* counts, int64_t n, uint32_t* sums, hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  const int64_t nb = cdiv(n, kScanTile);
+  hipLaunchKernelGGL(scan_tile_sums_kernel, dim3((unsigned)nb), dim3(kScanThreads), 0, stream,
+                     counts, n, sums);
+  hipLaunchKernelGGL(scan_sums_kernel, dim3(1), dim3(kScanThreads), 0, stream, sums, nb);
+  hipLaunchKernelGGL(scan_apply_kernel, dim3((unsigned)nb), dim3(kScanThreads), 0, stream, counts,
+                     n, sums);
+  return hipGetLastError();
+}
+
 // ---- workspace pool -------------------------------------------------------------
 
 namespace {

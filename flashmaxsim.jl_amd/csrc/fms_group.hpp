@@ -32,6 +32,11 @@ size_t group_workspace_bytes(int64_t npairs, int64_t N);
 hipError_t group_pairs_by_document(const void* idx, int idx64, int64_t npairs, int64_t N,
                                    void* workspace, const PairRef** order, hipStream_t stream);
 
+// In-place exclusive prefix sum of n counters on `stream`; `sums` holds
+// scan_workspace_bytes(n) bytes.
+size_t scan_workspace_bytes(int64_t n);
+hipError_t exclusive_scan_u32(uint32_t* counts, int64_t n, uint32_t* sums, hipStream_t stream);
+
 // Stream-ordered workspace from a library-owned memory pool of the stream's
 // device (created on first use, kept for the life of the process so repeated
 // calls do not return memory to the driver between synchronisations).

@@ -1,4 +1,4 @@
-"""flashmaxsim -- host mirror of FlashMaxSim.jl's forward API over the MI355X library.
+"""flashmaxsim -- host mirror of FlashMaxSim.jl's forward and pullback API over the MI355X library.
 
 Every score is computed by libflashmaxsim_hip.so (hand-written gfx950 HIP
 kernels) through its C ABI; this package only validates arguments, allocates
@@ -12,6 +12,8 @@ torch tensor of shape ``(c, b, a)`` (row-major) -- the same bytes.  So
 ``(Tq, C, B)`` are ``(B, C, Tq)``.
 """
 from .api import AtomicUnified, InBatch, InvGrid, MaxSim, dot_accum, maxsim, score_eltype
+from .backward import (candidates_pullback, inbatch_pullback, packed_pullback, pair_pullback,
+                       paired_pullback, varlen_pullback)
 from .boundary import (inbatch_device_scan, launch_candidates_scan, launch_int8_candidates_scan,
                        launch_int8_pair_scan, launch_int8_paired_scan, launch_packed_scan,
                        launch_pair_scan, launch_paired_scan, launch_varlen_scan,
@@ -30,6 +32,8 @@ __all__ = [
     "pair_forward", "paired_forward", "inbatch_forward", "candidates_forward",
     "packed_forward", "varlen_forward", "int8_pair_forward", "int8_paired_forward",
     "int8_candidates_forward",
+    "pair_pullback", "paired_pullback", "inbatch_pullback", "candidates_pullback",
+    "packed_pullback", "varlen_pullback",
     "launch_pair_scan", "launch_paired_scan", "launch_candidates_scan", "inbatch_device_scan",
     "launch_packed_scan", "launch_varlen_scan", "launch_int8_pair_scan",
     "launch_int8_paired_scan", "launch_int8_candidates_scan", "tensor_cores_active",

@@ -17,6 +17,17 @@ package (Julia ``(dim, T, B)`` == torch ``(B, T, dim)``).
 | launch_int8_paired_scan   | launch_int8_paired_scan! (quant.jl:199-217)          |
 | launch_int8_candidates_scan | (no reference method; candidate conventions)    |
 | tensor_cores_active       | tensor_cores_active      (ka.jl:71)                  |
+| pair_apply_pullback       | pair_apply_pullback!     (backward_pair.jl:73-87)    |
+| paired_apply_pullback     | paired_apply_pullback!   (backward_layouts.jl:45-60) |
+| inbatch_apply_pullback    | inbatch_apply_pullback!  (backward_layouts.jl:113-127)|
+| candidates_apply_pullback | candidates_apply_pullback! (backward_layouts.jl:187-202)|
+| packed_apply_pullback     | packed_apply_pullback!   (packed.jl:384-417)         |
+| varlen_apply_pullback     | varlen_apply_pullback!   (packed.jl:449-485)         |
+
+The pullbacks overwrite their gradient outputs in full (the reference
+accumulates into zeros_like buffers); all of them run the InvGrid form
+(gather for dQ, destination CSR for dD) whatever strategy marker the caller
+holds, since both strategies compute the same sums.
 """
 from __future__ import annotations
 
@@ -252,3 +263,102 @@ def varlen_normalize_(scores, cu_q):
     st = _lib.lib().fms_varlen_normalize(ptr(scores), ptr(cu_q), scores.numel(),
                                          stream_handle(dev))
     _lib.check(st, "varlen_normalize")
+
+
+# ---- backward on the argmax tape -------------------------------------------------
+
+def _tape(args):
+    if args.dtype != torch.int32:
+        raise ArgumentError("argmax tapes are Int32 on device")
+    return args
+
+
+def _like(t, proto, what):
+    """Cotangents, inv_n and gradient buffers carry the feature eltype (Vector{T})."""
+    if t is not None and t.dtype != proto.dtype:
+        raise ArgumentError(f"{what} must have the feature eltype {proto.dtype}, got {t.dtype}")
+    return t
+
+
+def pair_apply_pullback(dq, dd, q, d, qmask, argmax_u, delta):
+    """dq (Tq,dim), dd (Td,dim) <- pullback of one pair; delta is a (1,) device array."""
+    dev = require_device(dq, dd, q, d, qmask, argmax_u, delta)
+    Tq, dim = q.shape
+    Td = d.shape[0]
+    for t, w in ((dq, "dq"), (dd, "dd"), (d, "d"), (delta, "delta")):
+        _like(t, q, w)
+    st = _lib.lib().fms_pair_pullback(
+        dtype_code(q), ptr(dq), ptr(dd), ptr(q), ptr(d), ptr(_mask(qmask)), ptr(_tape(argmax_u)),
+        ptr(delta), dim, Tq, Td, stream_handle(dev))
+    _lib.check(st, "pair_apply_pullback")
+
+
+def paired_apply_pullback(dQ, dD, Q, D, qmask, args, Delta, inv_n):
+    dev = require_device(dQ, dD, Q, D, qmask, args, Delta, inv_n)
+    B, Tq, dim = Q.shape
+    Td = D.shape[1]
+    for t, w in ((dQ, "dQ"), (dD, "dD"), (D, "D"), (Delta, "Delta"), (inv_n, "inv_n")):
+        _like(t, Q, w)
+    st = _lib.lib().fms_paired_pullback(
+        dtype_code(Q), ptr(dQ), ptr(dD), ptr(Q), ptr(D), ptr(_mask(qmask)), ptr(_tape(args)),
+        ptr(Delta), ptr(inv_n), dim, Tq, Td, B, stream_handle(dev))
+    _lib.check(st, "paired_apply_pullback")
+
+
+def inbatch_apply_pullback(dQ, dD, Q, D, qmask, args, Delta, inv_n):
+    """Delta is the torch (Bq, Bd) cotangent (Julia (Bd, Bq)); args (Bq, Bd, Tq)."""
+    dev = require_device(dQ, dD, Q, D, qmask, args, Delta, inv_n)
+    Bq, Tq, dim = Q.shape
+    Bd, Td = D.shape[0], D.shape[1]
+    for t, w in ((dQ, "dQ"), (dD, "dD"), (D, "D"), (Delta, "Delta"), (inv_n, "inv_n")):
+        _like(t, Q, w)
+    st = _lib.lib().fms_inbatch_pullback(
+        dtype_code(Q), ptr(dQ), ptr(dD), ptr(Q), ptr(D), ptr(_mask(qmask)), ptr(_tape(args)),
+        ptr(Delta), ptr(inv_n), dim, Tq, Td, Bq, Bd, stream_handle(dev))
+    _lib.check(st, "inbatch_apply_pullback")
+
+
+def candidates_apply_pullback(dQ, dG, Q, gallery, idx, qmask, args, Delta, inv_n):
+    """Delta (B, C) (Julia (C, B)); args (B, C, Tq); dG like gallery (N, Td, dim)."""
+    dev = require_device(dQ, dG, Q, gallery, idx, qmask, args, Delta, inv_n)
+    B, Tq, dim = Q.shape
+    N, Td = gallery.shape[0], gallery.shape[1]
+    C = idx.shape[1]
+    for t, w in ((dQ, "dQ"), (dG, "dG"), (gallery, "gallery"), (Delta, "Delta"), (inv_n, "inv_n")):
+        _like(t, Q, w)
+    st = _lib.lib().fms_candidates_pullback(
+        dtype_code(Q), ptr(dQ), ptr(dG), ptr(Q), ptr(gallery), ptr(idx), _idx_bytes(idx),
+        ptr(_mask(qmask)), ptr(_tape(args)), ptr(Delta), ptr(inv_n), dim, Tq, B, Td, N, C,
+        stream_handle(dev))
+    _lib.check(st, "candidates_apply_pullback")
+
+
+def packed_apply_pullback(dq, dP, q, tokens, cu, qmask, args, Delta, inv_n):
+    dev = require_device(dq, dP, q, tokens, cu, qmask, args, Delta, inv_n)
+    Tq, dim = q.shape
+    B = cu.shape[0] - 1
+    if cu.dtype != torch.int32:
+        raise ArgumentError("PackedSeq cu must be Int32 on device")
+    for t, w in ((dq, "dq"), (dP, "dP"), (tokens, "tokens"), (Delta, "Delta"), (inv_n, "inv_n")):
+        _like(t, q, w)
+    st = _lib.lib().fms_packed_pullback(
+        dtype_code(q), ptr(dq), ptr(dP), ptr(q), ptr(tokens), ptr(cu), ptr(_mask(qmask)),
+        ptr(_tape(args)), ptr(Delta), ptr(inv_n), dim, Tq, B, tokens.shape[0],
+        stream_handle(dev))
+    _lib.check(st, "packed_apply_pullback")
+
+
+def varlen_apply_pullback(dQ, dD, Qp, Dp, cu_q, cu_d, args, Delta, inv_n):
+    """args (N, max_q) (Julia (max_q, N))."""
+    dev = require_device(dQ, dD, Qp, Dp, cu_q, cu_d, args, Delta, inv_n)
+    N, max_q = args.shape
+    dim = Qp.shape[1]
+    if cu_q.dtype != torch.int32 or cu_d.dtype != torch.int32:
+        raise ArgumentError("PackedSeq cu must be Int32 on device")
+    for t, w in ((dQ, "dQ"), (dD, "dD"), (Dp, "D tokens"), (Delta, "Delta"), (inv_n, "inv_n")):
+        _like(t, Qp, w)
+    st = _lib.lib().fms_varlen_pullback(
+        dtype_code(Qp), ptr(dQ), ptr(dD), ptr(Qp), ptr(Dp), ptr(cu_q), ptr(cu_d),
+        ptr(_tape(args)), ptr(Delta), ptr(inv_n), dim, max_q, N, Qp.shape[0], Dp.shape[0],
+        stream_handle(dev))
+    _lib.check(st, "varlen_apply_pullback")

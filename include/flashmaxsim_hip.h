@@ -244,6 +244,84 @@ fms_status fms_length_normalize(float* scores, const uint8_t* qmask, int64_t Tq,
 fms_status fms_varlen_normalize(float* scores, const int32_t* cu_q, int64_t N, void* stream);
 
 /*
+ * Backward on the argmax tape (paper Eqs. 2-3).  For every pair p and query
+ * token t with qmask[t] and a tape entry 1 <= u = args[t,p] <= Td(p):
+ *     dQ[:, t of p's query]     += delta_p * D[:, u of p's document]
+ *     dD[:, u of p's document]  += delta_p * Q[:, t of p's query]
+ * with delta_p = Delta[p] * inv_n[query of p] (inv_n NULL = all ones).
+ * Replaces the device method `*_apply_pullback!` of each layout, the
+ * InvGrid strategy (gather for dQ, destination CSR for dD).  Differences
+ * from the reference boundary:
+ *   - dQ and dD are OUTPUTS, overwritten in full (rows no source reaches are
+ *     written 0), so the caller need not zero them (the reference allocates
+ *     them with zeros_like and accumulates into them).
+ *   - Sums run in fp32 for every feature type and are rounded once into the
+ *     feature type (the reference accumulates in T).
+ *   - Delta and inv_n are in the feature type (Julia's Vector{T}).
+ *   - dQ sums a query token's pairs in pair order (deterministic).  dD sums
+ *     a destination row's sources in the order a device CSR fill gave them,
+ *     so its last bits may differ between runs, as the reference's device
+ *     CSR's do (src/invgrid.jl:10-14).
+ * Workspace (about 4*npairs*Tq + 4*ndest + 4*npairs bytes) comes from the
+ * library's stream-ordered pool.  Masked or out-of-range tape entries and
+ * pairs with delta 0 contribute nothing (src/backward_pair.jl:21-29).
+ */
+
+/* pair_apply_pullback!(mode, backend, dq, dd, q, d, qmask, argmax_u, δ, dim,
+ * Tq, Td) (src/backward_pair.jl:73-87).  q (dim,Tq), d (dim,Td), delta (1,). */
+fms_status fms_pair_pullback(int32_t dtype, void* dq, void* dd, const void* q, const void* d,
+                             const uint8_t* qmask, const int32_t* argmax_u, const void* delta,
+                             int64_t dim, int64_t Tq, int64_t Td, void* stream);
+
+/* paired_apply_pullback!(mode, backend, dQ, dD, Q, D, qmask, args, Δ, inv_n,
+ * dim, Tq, B, Td) (src/backward_layouts.jl:45-60).  Q (dim,Tq,B), D
+ * (dim,Td,B), args (Tq,B), Delta (B,), inv_n (B,) nullable. */
+fms_status fms_paired_pullback(int32_t dtype, void* dQ, void* dD, const void* Q, const void* D,
+                               const uint8_t* qmask, const int32_t* args, const void* Delta,
+                               const void* inv_n, int64_t dim, int64_t Tq, int64_t Td, int64_t B,
+                               void* stream);
+
+/* inbatch_apply_pullback!(mode, backend, dQ, dD, Q, D, qmask, args, Δ, inv_n,
+ * dim, Tq, Bq, Td, Bd) (src/backward_layouts.jl:113-127).  Q (dim,Tq,Bq), D
+ * (dim,Td,Bd), args (Tq,Bd,Bq), Delta (Bd,Bq) (pair (j,i) = query i against
+ * document j), inv_n (Bq,) nullable. */
+fms_status fms_inbatch_pullback(int32_t dtype, void* dQ, void* dD, const void* Q, const void* D,
+                                const uint8_t* qmask, const int32_t* args, const void* Delta,
+                                const void* inv_n, int64_t dim, int64_t Tq, int64_t Td,
+                                int64_t Bq, int64_t Bd, void* stream);
+
+/* candidates_apply_pullback!(mode, backend, dQ, dG, Q, gallery, idx, qmask,
+ * args, Δ, inv_n, dim, Tq, B, Td, C, N) (src/backward_layouts.jl:187-202).
+ * Q (dim,Tq,B), gallery (dim,Td,N), idx (C,B) of idx_bytes = 4 or 8,
+ * args (Tq,C,B), Delta (C,B), inv_n (B,) nullable; dG (dim,Td,N).  An index
+ * outside 1..N contributes nothing; a document chosen several times sums. */
+fms_status fms_candidates_pullback(int32_t dtype, void* dQ, void* dG, const void* Q,
+                                   const void* gallery, const void* idx, int32_t idx_bytes,
+                                   const uint8_t* qmask, const int32_t* args, const void* Delta,
+                                   const void* inv_n, int64_t dim, int64_t Tq, int64_t B,
+                                   int64_t Td, int64_t N, int64_t C, void* stream);
+
+/* packed_apply_pullback!(mode, backend, Δ, q, P, qmask, args, inv_n)
+ * (src/packed.jl:384-417).  q (dim,Tq), tokens (dim,ntokens) with device cu
+ * (B+1,) 1-based, args (Tq,B), Delta (B,), inv_n (1,) nullable; dP
+ * (dim,ntokens).  cu is clamped into the token range as in the forward. */
+fms_status fms_packed_pullback(int32_t dtype, void* dq, void* dP, const void* q,
+                               const void* tokens, const int32_t* cu, const uint8_t* qmask,
+                               const int32_t* args, const void* Delta, const void* inv_n,
+                               int64_t dim, int64_t Tq, int64_t B, int64_t ntokens,
+                               void* stream);
+
+/* varlen_apply_pullback!(mode, backend, Δ, Q, D, args, inv_n)
+ * (src/packed.jl:449-485).  Query tokens (dim,nq_tokens) with cu_q (N+1,),
+ * document tokens (dim,nd_tokens) with cu_d (N+1,), args (max_q,N) (rows
+ * past a query's length unread), Delta (N,), inv_n (N,) nullable. */
+fms_status fms_varlen_pullback(int32_t dtype, void* dQ, void* dD, const void* Qtokens,
+                               const void* Dtokens, const int32_t* cu_q, const int32_t* cu_d,
+                               const int32_t* args, const void* Delta, const void* inv_n,
+                               int64_t dim, int64_t max_q, int64_t N, int64_t nq_tokens,
+                               int64_t nd_tokens, void* stream);
+
+/*
  * Test-only: MFMA accumulator layout probe (no reference counterpart).  Runs
  * one 32x32 MFMA of the given feature type (FMS_F32 / FMS_F16 / FMS_BF16, or
  * 3 = int8) twice -- A[i][0] = i+1, B[0][j] = 1, then A[i][0] = 1,

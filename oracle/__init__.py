@@ -24,6 +24,9 @@ Function-level parity pins (each is exercised in ``tests/test_oracle.py``):
   floors) and numpy's round-half-even on random data.
 * int8 dots / int8 scans -- exact integer arithmetic vs numpy int32 matmul,
   fixed dequant order ``(qs*ds)*float(acc)``.
+* backward (``*_backward``) -- an independent numpy scatter (``np.add.at``)
+  on the same tapes, finite differences of the forward score, linearity in
+  the cotangent, and the layout invariants the forward has.
 """
 from __future__ import annotations
 
@@ -93,6 +96,20 @@ def _declare(L):
     L.fmso_inv_token_counts.argtypes = [_p, _i64, _i64, _p]
     L.fmso_dense_pair_f64.restype = ctypes.c_double
     L.fmso_dense_pair_f64.argtypes = [_int, _p, _p, _p, _p, _i64, _i64, _i64, _int, _p]
+    L.fmso_paired_backward.restype = None
+    L.fmso_paired_backward.argtypes = [_int, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _p]
+    L.fmso_inbatch_backward.restype = None
+    L.fmso_inbatch_backward.argtypes = [_int, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64,
+                                        _p, _p]
+    L.fmso_candidates_backward.restype = None
+    L.fmso_candidates_backward.argtypes = [_int, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64,
+                                           _i64, _i64, _p, _p]
+    L.fmso_packed_backward.restype = None
+    L.fmso_packed_backward.argtypes = [_int, _p, _p, _p, _p, _p, _p, ctypes.c_double, _i64, _i64,
+                                       _i64, _i64, _p, _p]
+    L.fmso_varlen_backward.restype = None
+    L.fmso_varlen_backward.argtypes = [_int, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64,
+                                       _i64, _p, _p]
 
 
 def max_threads() -> int:
@@ -336,3 +353,96 @@ def dense_pair_f64(q, d, qmask=None, dmask=None, normalize=False, bf16=False):
     s = lib().fmso_dense_pair_f64(code, _ptr(q), _ptr(d), _ptr(qm), _ptr(dm), dim, Tq, Td,
                                   int(bool(normalize)), _ptr(args))
     return float(s), args
+
+
+# ---- backward on the argmax tape ---------------------------------------------------
+
+def _f64(a):
+    return None if a is None else np.ascontiguousarray(a, dtype=np.float64)
+
+
+def paired_backward(Q, D, args, Delta, inv_n=None, qmask=None, bf16=False):
+    """paired_pullback (src/backward_layouts.jl:13-26), fp64.  Q (B,Tq,dim), D (B,Td,dim),
+    args (B,Tq) 1-based tape, Delta (B,), inv_n (B,) or None.  Returns (dQ, dD) fp64."""
+    Q, D = _c(Q), _c(D)
+    code = _dtype_code(Q, bf16)
+    B, Tq, dim = Q.shape
+    Td = D.shape[1]
+    args = _c(args, np.int32)
+    dQ = np.zeros((B, Tq, dim), np.float64)
+    dD = np.zeros((B, Td, dim), np.float64)
+    qm, De, iv = _mask(qmask), _f64(Delta), _f64(inv_n)
+    lib().fmso_paired_backward(code, _ptr(Q), _ptr(D), _ptr(qm), _ptr(args), _ptr(De), _ptr(iv),
+                               dim, Tq, Td, B, _ptr(dQ), _ptr(dD))
+    return dQ, dD
+
+
+def inbatch_backward(Q, D, args, Delta, inv_n=None, qmask=None, bf16=False):
+    """inbatch_pullback (src/backward_layouts.jl:68-94), fp64.  Q (Bq,Tq,dim), D (Bd,Td,dim),
+    args (Bq,Bd,Tq), Delta (Bq,Bd) [Julia (Bd,Bq)], inv_n (Bq,)."""
+    Q, D = _c(Q), _c(D)
+    code = _dtype_code(Q, bf16)
+    Bq, Tq, dim = Q.shape
+    Bd, Td = D.shape[0], D.shape[1]
+    args = _c(args, np.int32)
+    dQ = np.zeros((Bq, Tq, dim), np.float64)
+    dD = np.zeros((Bd, Td, dim), np.float64)
+    qm, De, iv = _mask(qmask), _f64(Delta), _f64(inv_n)
+    lib().fmso_inbatch_backward(code, _ptr(Q), _ptr(D), _ptr(qm), _ptr(args), _ptr(De), _ptr(iv),
+                                dim, Tq, Td, Bq, Bd, _ptr(dQ), _ptr(dD))
+    return dQ, dD
+
+
+def candidates_backward(Q, G, idxs, args, Delta, inv_n=None, qmask=None, bf16=False):
+    """candidates_pullback (src/backward_layouts.jl:136-165), fp64.  Q (B,Tq,dim),
+    G (N,Td,dim), idxs (B,C) 1-based, args (B,C,Tq), Delta (B,C), inv_n (B,)."""
+    Q, G = _c(Q), _c(G)
+    code = _dtype_code(Q, bf16)
+    B, Tq, dim = Q.shape
+    N, Td = G.shape[0], G.shape[1]
+    C = idxs.shape[1]
+    idxs = _c(idxs, np.int64)
+    args = _c(args, np.int32)
+    dQ = np.zeros((B, Tq, dim), np.float64)
+    dG = np.zeros((N, Td, dim), np.float64)
+    qm, De, iv = _mask(qmask), _f64(Delta), _f64(inv_n)
+    lib().fmso_candidates_backward(code, _ptr(Q), _ptr(G), _ptr(idxs), _ptr(qm), _ptr(args),
+                                   _ptr(De), _ptr(iv), dim, Tq, Td, B, C, N, _ptr(dQ), _ptr(dG))
+    return dQ, dG
+
+
+def packed_backward(q, tokens, cu, args, Delta, inv_n=1.0, qmask=None, bf16=False):
+    """packed_pullback (src/packed.jl:361-377), fp64.  q (Tq,dim), tokens (ntok,dim),
+    cu (B+1,) 1-based, args (B,Tq), Delta (B,), inv_n scalar."""
+    q, tokens = _c(q), _c(tokens)
+    code = _dtype_code(q, bf16)
+    Tq, dim = q.shape
+    ntok = tokens.shape[0]
+    cu = _c(cu, np.int32)
+    B = cu.shape[0] - 1
+    args = _c(args, np.int32)
+    dq = np.zeros((Tq, dim), np.float64)
+    dP = np.zeros((ntok, dim), np.float64)
+    qm, De = _mask(qmask), _f64(Delta)
+    lib().fmso_packed_backward(code, _ptr(q), _ptr(tokens), _ptr(cu), _ptr(qm), _ptr(args),
+                               _ptr(De), float(inv_n), dim, Tq, B, ntok, _ptr(dq), _ptr(dP))
+    return dq, dP
+
+
+def varlen_backward(Qt, Dt, cu_q, cu_d, args, Delta, inv_n=None, bf16=False):
+    """varlen_pullback (src/packed.jl:424-442), fp64.  Qt (nq,dim), Dt (nd,dim),
+    cu_q/cu_d (N+1,) 1-based, args (N,max_q), Delta (N,), inv_n (N,)."""
+    Qt, Dt = _c(Qt), _c(Dt)
+    code = _dtype_code(Qt, bf16)
+    nq, dim = Qt.shape
+    nd = Dt.shape[0]
+    cu_q, cu_d = _c(cu_q, np.int32), _c(cu_d, np.int32)
+    N = cu_q.shape[0] - 1
+    args = _c(args, np.int32)
+    max_q = args.shape[1]
+    dQ = np.zeros((nq, dim), np.float64)
+    dD = np.zeros((nd, dim), np.float64)
+    De, iv = _f64(Delta), _f64(inv_n)
+    lib().fmso_varlen_backward(code, _ptr(Qt), _ptr(Dt), _ptr(cu_q), _ptr(cu_d), _ptr(args),
+                               _ptr(De), _ptr(iv), dim, max_q, N, nq, nd, _ptr(dQ), _ptr(dD))
+    return dQ, dD

@@ -609,3 +609,124 @@ double fmso_dense_pair_f64(int dtype, const void* q, const void* d,
     }
     return normalize ? score / (double)(nq > 1 ? nq : 1) : score;
 }
+
+/* ---- backward on the argmax tape (src/backward_pair.jl, src/backward_layouts.jl,
+ *      src/packed.jl:361-377, :424-442) ---------------------------------------- */
+
+/*
+ * The reference's CPU pullback for one pair (pair_pullback, backward_pair.jl:14-37,
+ * with accumulate_doc! AtomicUnified, accumulate.jl:12-29): for every query token t
+ * with qmask[t] and 1 <= u = argmax[t] <= Td,
+ *     dq[:, t] += delta * d[:, u]      and      dd[:, u] += delta * q[:, t],
+ * t ascending.  InvGrid (accumulate.jl:31-39, invgrid.jl:43-65) visits the same
+ * sources of each destination in the same (ascending t) order.
+ * The reference computes in the feature type T; this restatement pins the
+ * mathematics: delta and both accumulations in fp64.  dq/dd are ADDED to.
+ */
+static void pair_pullback_f64(int dtype, double delta, const void* q, const void* d,
+                              const uint8_t* qmask, const int32_t* args,
+                              int64_t dim, int64_t Tq, int64_t Td, double* dq, double* dd) {
+    int64_t t, k;
+    if (delta == 0.0) return; /* backward_pair.jl:21 */
+    for (t = 0; t < Tq; ++t) {
+        if (qmask && !qmask[t]) continue;
+        const int64_t u = (int64_t)args[t];
+        if (u < 1 || u > Td) continue;
+        for (k = 0; k < dim; ++k) {
+            dq[t * dim + k] += delta * load_f64(dtype, d, (u - 1) * dim + k);
+            dd[(u - 1) * dim + k] += delta * load_f64(dtype, q, t * dim + k);
+        }
+    }
+}
+
+/* paired_pullback CPU (backward_layouts.jl:13-26): pair b, delta = Delta[b] * inv_n[b].
+ * dQ (B,Tq,dim) and dD (B,Td,dim) are overwritten.  inv_n NULL = all ones. */
+void fmso_paired_backward(int dtype, const void* Q, const void* D, const uint8_t* qmask,
+                          const int32_t* args, const double* Delta, const double* inv_n,
+                          int64_t dim, int64_t Tq, int64_t Td, int64_t B,
+                          double* dQ, double* dD) {
+    int64_t b;
+    memset(dQ, 0, sizeof(double) * (size_t)(B * Tq * dim));
+    memset(dD, 0, sizeof(double) * (size_t)(B * Td * dim));
+    for (b = 0; b < B; ++b)
+        pair_pullback_f64(dtype, Delta[b] * (inv_n ? inv_n[b] : 1.0),
+                          advance(Q, b * Tq * dim, dtype), advance(D, b * Td * dim, dtype),
+                          qmask ? qmask + b * Tq : NULL, args + b * Tq, dim, Tq, Td,
+                          dQ + b * Tq * dim, dD + b * Td * dim);
+}
+
+/* inbatch_pullback CPU (backward_layouts.jl:68-94): j outer, i inner; pair (i, j) has
+ * delta = Delta[j, i] * inv_n[i] (Delta (Bd, Bq) column-major: j + Bd*i) and tape
+ * args[t, j, i] at t + Tq*(j + Bd*i). */
+void fmso_inbatch_backward(int dtype, const void* Q, const void* D, const uint8_t* qmask,
+                           const int32_t* args, const double* Delta, const double* inv_n,
+                           int64_t dim, int64_t Tq, int64_t Td, int64_t Bq, int64_t Bd,
+                           double* dQ, double* dD) {
+    int64_t i, j;
+    memset(dQ, 0, sizeof(double) * (size_t)(Bq * Tq * dim));
+    memset(dD, 0, sizeof(double) * (size_t)(Bd * Td * dim));
+    for (j = 0; j < Bd; ++j)
+        for (i = 0; i < Bq; ++i) {
+            const int64_t p = j + Bd * i;
+            pair_pullback_f64(dtype, Delta[p] * (inv_n ? inv_n[i] : 1.0),
+                              advance(Q, i * Tq * dim, dtype), advance(D, j * Td * dim, dtype),
+                              qmask ? qmask + i * Tq : NULL, args + p * Tq, dim, Tq, Td,
+                              dQ + i * Tq * dim, dD + j * Td * dim);
+        }
+}
+
+/* candidates_pullback CPU (backward_layouts.jl:136-165): b outer, c inner; pair
+ * p = c + C*b scores Q_b against gallery doc idxs[p] (1-based; outside 1..N the
+ * pair contributes nothing); delta = Delta[p] * inv_n[b]. */
+void fmso_candidates_backward(int dtype, const void* Q, const void* G, const int64_t* idxs,
+                              const uint8_t* qmask, const int32_t* args, const double* Delta,
+                              const double* inv_n, int64_t dim, int64_t Tq, int64_t Td,
+                              int64_t B, int64_t C, int64_t N, double* dQ, double* dG) {
+    int64_t b, c;
+    memset(dQ, 0, sizeof(double) * (size_t)(B * Tq * dim));
+    memset(dG, 0, sizeof(double) * (size_t)(N * Td * dim));
+    for (b = 0; b < B; ++b)
+        for (c = 0; c < C; ++c) {
+            const int64_t p = c + C * b, j = idxs[p];
+            if (j < 1 || j > N) continue;
+            pair_pullback_f64(dtype, Delta[p] * (inv_n ? inv_n[b] : 1.0),
+                              advance(Q, b * Tq * dim, dtype), advance(G, (j - 1) * Td * dim, dtype),
+                              qmask ? qmask + b * Tq : NULL, args + p * Tq, dim, Tq, Td,
+                              dQ + b * Tq * dim, dG + (j - 1) * Td * dim);
+        }
+}
+
+/* packed_pullback CPU (packed.jl:361-377): document b = tokens[cu[b]..cu[b+1]-1]
+ * (1-based cu), delta = Delta[b] * inv_n (one value for the single query). */
+void fmso_packed_backward(int dtype, const void* q, const void* tokens, const int32_t* cu,
+                          const uint8_t* qmask, const int32_t* args, const double* Delta,
+                          double inv_n, int64_t dim, int64_t Tq, int64_t B, int64_t ntok,
+                          double* dq, double* dP) {
+    int64_t b;
+    memset(dq, 0, sizeof(double) * (size_t)(Tq * dim));
+    memset(dP, 0, sizeof(double) * (size_t)(ntok * dim));
+    for (b = 0; b < B; ++b) {
+        const int64_t a = (int64_t)cu[b] - 1, z = (int64_t)cu[b + 1] - 1;
+        pair_pullback_f64(dtype, Delta[b] * inv_n, q, advance(tokens, a * dim, dtype), qmask,
+                          args + b * Tq, dim, Tq, z - a, dq, dP + a * dim);
+    }
+}
+
+/* varlen_pullback CPU (packed.jl:424-442): pair n = (Q tokens cu_q[n]..cu_q[n+1]-1,
+ * D tokens cu_d[n]..cu_d[n+1]-1), no masks, tape column n of args (max_q, N);
+ * delta = Delta[n] * inv_n[n]. */
+void fmso_varlen_backward(int dtype, const void* Qt, const void* Dt, const int32_t* cu_q,
+                          const int32_t* cu_d, const int32_t* args, const double* Delta,
+                          const double* inv_n, int64_t dim, int64_t max_q, int64_t N,
+                          int64_t nq, int64_t nd, double* dQ, double* dD) {
+    int64_t n;
+    memset(dQ, 0, sizeof(double) * (size_t)(nq * dim));
+    memset(dD, 0, sizeof(double) * (size_t)(nd * dim));
+    for (n = 0; n < N; ++n) {
+        const int64_t qa = (int64_t)cu_q[n] - 1, qz = (int64_t)cu_q[n + 1] - 1;
+        const int64_t da = (int64_t)cu_d[n] - 1, dz = (int64_t)cu_d[n + 1] - 1;
+        pair_pullback_f64(dtype, Delta[n] * (inv_n ? inv_n[n] : 1.0), advance(Qt, qa * dim, dtype),
+                          advance(Dt, da * dim, dtype), NULL, args + n * max_q, dim, qz - qa,
+                          dz - da, dQ + qa * dim, dD + da * dim);
+    }
+}

@@ -77,6 +77,18 @@ EINVAL, EUNSUP, OK = _lib.FMS_EINVAL, _lib.FMS_EUNSUPPORTED, _lib.FMS_OK
     (lambda L: L.fms_length_normalize(None, None, 4, 0, 2, None, 0, 0, 0.0, None), OK),
     (lambda L: L.fms_varlen_normalize(None, None, 3, None), EINVAL),
     (lambda L: L.fms_debug_mfma_layout(None, 1, None), EINVAL),
+    # pullbacks: bad dtype, NULL buffers, empty batches, bad index width, negative sizes
+    (lambda L: L.fms_paired_pullback(9, None, None, None, None, None, None, None, None, 8, 4, 5, 2, None), EUNSUP),
+    (lambda L: L.fms_paired_pullback(1, None, None, None, None, None, None, None, None, 8, 4, 5, 2, None), EINVAL),
+    (lambda L: L.fms_paired_pullback(1, None, None, None, None, None, None, None, None, 8, 4, 5, 0, None), OK),
+    (lambda L: L.fms_pair_pullback(1, None, None, 1, 1, None, None, None, 8, 4, 5, None), EINVAL),
+    (lambda L: L.fms_inbatch_pullback(2, None, None, None, None, None, None, None, None, 8, 4, 5, 0, 0, None), OK),
+    (lambda L: L.fms_inbatch_pullback(2, 1, 1, 1, 1, None, None, None, None, 8, 4, 5, 3, 2, None), EINVAL),
+    (lambda L: L.fms_candidates_pullback(1, 1, 1, 1, 1, 1, 3, None, 1, 1, None, 8, 4, 2, 5, 7, 3, None), EINVAL),
+    (lambda L: L.fms_candidates_pullback(1, 1, 1, 1, 1, None, 8, None, 1, 1, None, 8, 4, 2, 5, 7, 3, None), EINVAL),
+    (lambda L: L.fms_packed_pullback(0, None, None, None, None, None, None, None, None, None, -1, 4, 3, 10, None), EINVAL),
+    (lambda L: L.fms_varlen_pullback(0, 1, 1, 1, 1, None, None, 1, 1, None, 8, 4, 3, 10, 10, None), EINVAL),
+    (lambda L: L.fms_varlen_pullback(0, None, None, None, None, None, None, None, None, None, 8, 4, 3, 0, 0, None), OK),
 ])
 def test_validation_status_codes(call, expect):
     assert call(_lib.lib()) == expect

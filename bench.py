@@ -9,7 +9,8 @@ launch_candidates_scan over the whole batch (scores + argmax tape), inputs
 resident in HBM, outputs preallocated.  Prints ONE JSON line.
 
 Other workloads (--workload c3 | c4 | c4d1024 | c5) measure the in-batch,
-packed and INT8 scans the same way (each prints its own JSON line).
+packed and INT8 scans the same way (each prints its own JSON line); c3bwd
+measures the pullback of the c3 scores on their argmax tape (dQ and dD).
 """
 from __future__ import annotations
 
@@ -39,7 +40,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="c2",
-                    choices=["c2", "c3", "c4", "c4d1024", "c5", "read"])
+                    choices=["c2", "c3", "c3bwd", "c4", "c4d1024", "c5", "read"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="target duration of the bounded CPU baseline sample")
@@ -294,6 +295,69 @@ def run_c3(args, torch, fm, boundary, dev):
     return res
 
 
+def run_c3bwd(args, torch, fm, boundary, dev):
+    """Pullback of the c3 in-batch scores on their argmax tape (one training step's
+    backward through MaxSim): dQ and dD from Delta (Bq, Bd) fp16 and inv_n (Bq,)."""
+    import numpy as np
+    dim, Lq, Ld, Bq, Bd = 128, 32, 180, 512, 512
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(3)
+    Q = normalized_randn(torch, (Bq, Lq, dim), gen, torch.float16, dev)
+    D = normalized_randn(torch, (Bd, Ld, dim), gen, torch.float16, dev)
+    lens = torch.randint(64, Ld + 1, (Bd,), generator=gen, device=dev)
+    dmask = torch.arange(Ld, device=dev)[None, :] < lens[:, None]
+    qmask = torch.ones(Bq, Lq, dtype=torch.bool, device=dev)
+    S = torch.empty(Bq, Bd, dtype=torch.float32, device=dev)
+    args_t = torch.empty(Bq, Bd, Lq, dtype=torch.int32, device=dev)
+    boundary.inbatch_device_scan(S, args_t, Q, D, qmask, dmask)
+    Delta = (torch.randn(Bq, Bd, generator=gen, device=dev) / Bd).to(torch.float16)
+    inv_n = torch.full((Bq,), 1.0 / Lq, dtype=torch.float16, device=dev)
+    dQ = torch.empty_like(Q)
+    dD = torch.empty_like(D)
+
+    def step():
+        boundary.inbatch_apply_pullback(dQ, dD, Q, D, qmask, args_t, Delta, inv_n)
+
+    wall, launch_ms = timed_steps(torch, step, args.steps, args.warmup)
+    nsrc = int(((args_t >= 1) & (args_t <= Ld)).sum().item())
+    row = dim * 2
+    # per source: one D row gathered into dQ, one Q row gathered into dD, its tape entry;
+    # per call: Delta, inv_n, both gradients written once
+    bytes_per_launch = nsrc * (2 * row + 4) + Bq * Bd * 2 + Bq * 2 + (Bq * Lq + Bd * Ld) * row
+    res = dict(pairs_per_step=Bq * Bd, bytes_per_launch=bytes_per_launch, wall=wall,
+               launch_ms=launch_ms, dtype="f16", bound="hbm",
+               unique_bytes=(Bq * Lq + Bd * Ld) * row * 2 + Bq * Bd * Lq * 4 + Bq * Bd * 2,
+               config={"workload": "c3bwd_inbatch_pullback_fp16", "dim": dim, "Lq": Lq,
+                       "Ld": Ld, "Bq": Bq, "Bd": Bd, "doc_len": "U[64,180], tail masked",
+                       "sources": nsrc, "outputs": "dQ (Bq,Lq,dim) + dD (Bd,Ld,dim) fp16"})
+    import oracle
+    rng = np.random.default_rng(0)
+    Qh = Q.cpu().numpy()
+    Dh = D.cpu().numpy()
+    ah = args_t.cpu().numpy()
+    Dlh = Delta.float().cpu().numpy().astype(np.float64)
+    ivh = inv_n.float().cpu().numpy().astype(np.float64)
+    # full-size spot check: dQ of a query depends only on its own row of pairs
+    ii = np.sort(rng.choice(Bq, size=4, replace=False))
+    wq, _ = oracle.inbatch_backward(Qh[ii], Dh, ah[ii], Dlh[ii], ivh[ii])
+    got = dQ[torch.from_numpy(ii).to(dev)].float().cpu().numpy().astype(np.float64)
+    err = np.abs(got - wq) / (np.abs(wq) + 1e-3)
+    res["check"] = {"queries": ii.tolist(), "dQ_max_rel_err": float(err.max()),
+                    "ok": bool(err.max() < 4e-3)}
+    if not args.no_cpu:
+        def run(n):
+            sel = rng.choice(Bq, size=n, replace=False)
+            t0 = time.perf_counter()
+            oracle.inbatch_backward(Qh[sel], Dh, ah[sel], Dlh[sel], ivh[sel])
+            return time.perf_counter() - t0
+        dt = run(2)
+        n = int(max(2, min(Bq, 2 * args.cpu_seconds / max(dt, 1e-6))))
+        dt = run(n)
+        res["cpu"] = {"value": n * Bd / dt, "unit": "pairs/s", "cores": 1, "kind": "port",
+                      "sample": f"{n} queries x {Bd} documents, {dt:.1f} s, one thread"}
+    return res
+
+
 def run_c4(args, torch, fm, boundary, dev, dim=128):
     import numpy as np
     Lq, nd, nq = 24, 20_000, 64
@@ -377,7 +441,8 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     boundary.candidates_grouping(args.grouping)
-    runner = {"c2": run_c2, "c3": run_c3, "c4": run_c4, "c5": run_c5, "read": run_read,
+    runner = {"c2": run_c2, "c3": run_c3, "c3bwd": run_c3bwd, "c4": run_c4, "c5": run_c5,
+              "read": run_read,
               "c4d1024": lambda *a: run_c4(*a, dim=1024)}[args.workload]
     r = runner(args, torch, fm, boundary, dev)
     steps = args.steps
@@ -419,6 +484,8 @@ def main():
     }
     if "check" in r:
         out["parity_check"] = r["check"]
+    if "unique_bytes" in r:
+        out["roofline"]["unique_bytes"] = r["unique_bytes"]
     if r["bound"] == "mfma":
         out["roofline"]["padded_tflops"] = round(r["padded_flops"] / avg_launch_s / 1e12, 2)
     if args.workload == "read":

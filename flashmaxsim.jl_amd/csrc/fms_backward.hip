@@ -1,10 +1,29 @@
 // fms_backward.hip -- pullback of the fused MaxSim forward on its argmax tape
-// (see fms_backward.hpp for the mathematics and the two halves).
+// (the mathematics and the output contract are in fms_backward.hpp).
 //
-// Launches per call: delta (delta_p = Delta[p] * inv_n[query of p], fp32),
-// [clear dQ], dQ gather, count -> prefix sum -> fill of the destination CSR,
-// dD per destination row.  A wave owns one output row in the two row
-// kernels; lane l holds features l, l + 64, ... of it (KI per lane).
+// Vector path (feature rows of 64..2048 bytes, a multiple of 16, buffers
+// 16-byte aligned).  A row is read and written in 16-byte chunks; Lr lanes
+// cover one row (Lr = the power of two >= chunks per row, at most 64, with
+// two chunks per lane past 64), so one wave instruction moves 64 / Lr rows.
+// Per call:
+//   delta     delta_p = Delta[p] * inv_n[query of p], fp32.
+//   dQ        bwd_dq_vec: a wave owns a block of tokens of one query group and
+//             a share of the group's pairs; per pair it reads the tape block
+//             once (one dword per lane), hands each lane its tokens' entries
+//             by ds_bpermute, and gathers the chosen document rows.  The four
+//             waves of a workgroup split the pairs and sum in LDS in a fixed
+//             order; across workgroups (pair splits, split index = block
+//             index mod nsplit, so split s runs on XCD s mod 8 and keeps its
+//             share of the documents in that XCD's L2) fp32 partials are
+//             summed in split order by bwd_dq_reduce.  Deterministic.
+//   dD        bwd_doc_csr: a workgroup per document sorts the document's
+//             sources (pair, token) by destination row in LDS (count, scan,
+//             fill) and writes the row lists; bwd_dd_vec then sums each row's
+//             source query rows in registers.  Rows of no document (and
+//             documents of no pair) are written 0.  The order within a row
+//             is the LDS fill order (not fixed).
+// Other row sizes take the generic path: one wave per output row, features
+// strided over the lanes, and a destination CSR built with global atomics.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -17,8 +36,12 @@ namespace fms {
 
 namespace {
 
-constexpr int kBwdThreads = 256;            // 4 waves
-constexpr int kBwdUnroll = 8;               // source rows in flight per wave
+constexpr int kBwdThreads = 256;  // 4 waves
+constexpr int kBwdUnroll = 8;     // source rows in flight per wave (generic kernels)
+constexpr int kDocTile = 4096;    // destination rows per LDS tile of bwd_doc_csr
+constexpr int kDocThreads = 1024; // threads of bwd_doc_csr (16 waves)
+constexpr int kDocUnroll = 4;     // sources in flight per thread (bwd_doc_csr)
+constexpr int kDdUnroll = 8;      // sources in flight per row group (bwd_dd_vec)
 
 inline int64_t bcdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 inline size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -27,30 +50,149 @@ inline unsigned grid_for(int64_t waves) {
   return (unsigned)(b < 1 ? 1 : (b > 1048576 ? 1048576 : b));
 }
 
-// Feature element <-> fp32.
+// Feature element <-> fp32, one element (generic kernels) or one 16-byte
+// chunk of kV elements (vector kernels).
 struct EF32 {
-  static constexpr int kSz = 4;
+  static constexpr int kSz = 4, kV = 4;
   __device__ static float ld(const char* p) { return *reinterpret_cast<const float*>(p); }
   __device__ static void st(char* p, float v) { *reinterpret_cast<float*>(p) = v; }
+  __device__ static void unpack(const uint4& r, float* x) {
+    x[0] = __uint_as_float(r.x);
+    x[1] = __uint_as_float(r.y);
+    x[2] = __uint_as_float(r.z);
+    x[3] = __uint_as_float(r.w);
+  }
+  __device__ static uint4 pack(const float* x) {
+    return make_uint4(__float_as_uint(x[0]), __float_as_uint(x[1]), __float_as_uint(x[2]),
+                      __float_as_uint(x[3]));
+  }
 };
 struct EF16 {
-  static constexpr int kSz = 2;
+  static constexpr int kSz = 2, kV = 8;
   __device__ static float ld(const char* p) { return (float)*reinterpret_cast<const _Float16*>(p); }
   __device__ static void st(char* p, float v) { *reinterpret_cast<_Float16*>(p) = (_Float16)v; }
+  __device__ static float lo(uint32_t w) { return (float)__builtin_bit_cast(_Float16, (uint16_t)w); }
+  __device__ static float hi(uint32_t w) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+  }
+  __device__ static uint32_t two(float a, float b) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)a) |
+           ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)b) << 16);
+  }
+  __device__ static void unpack(const uint4& r, float* x) {
+    x[0] = lo(r.x); x[1] = hi(r.x); x[2] = lo(r.y); x[3] = hi(r.y);
+    x[4] = lo(r.z); x[5] = hi(r.z); x[6] = lo(r.w); x[7] = hi(r.w);
+  }
+  __device__ static uint4 pack(const float* x) {
+    return make_uint4(two(x[0], x[1]), two(x[2], x[3]), two(x[4], x[5]), two(x[6], x[7]));
+  }
 };
 struct EBF16 {
-  static constexpr int kSz = 2;
+  static constexpr int kSz = 2, kV = 8;
   __device__ static float ld(const char* p) {
     return __builtin_bit_cast(float, (uint32_t)*reinterpret_cast<const uint16_t*>(p) << 16);
   }
-  __device__ static void st(char* p, float v) {  // round to nearest even
+  __device__ static uint16_t round(float v) {  // round to nearest even
     const uint32_t u = __builtin_bit_cast(uint32_t, v);
-    const uint16_t r = (v != v) ? (uint16_t)0x7FC0u : (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
-    *reinterpret_cast<uint16_t*>(p) = r;
+    return (v != v) ? (uint16_t)0x7FC0u : (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+  }
+  __device__ static void st(char* p, float v) { *reinterpret_cast<uint16_t*>(p) = round(v); }
+  __device__ static float lo(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
+  __device__ static float hi(uint32_t w) { return __builtin_bit_cast(float, w & 0xFFFF0000u); }
+  __device__ static uint32_t two(float a, float b) {
+    return (uint32_t)round(a) | ((uint32_t)round(b) << 16);
+  }
+  __device__ static void unpack(const uint4& r, float* x) {
+    x[0] = lo(r.x); x[1] = hi(r.x); x[2] = lo(r.y); x[3] = hi(r.y);
+    x[4] = lo(r.z); x[5] = hi(r.z); x[6] = lo(r.w); x[7] = hi(r.w);
+  }
+  __device__ static uint4 pack(const float* x) {
+    return make_uint4(two(x[0], x[1]), two(x[2], x[3]), two(x[4], x[5]), two(x[6], x[7]));
   }
 };
 
 __device__ __forceinline__ int64_t uni64(int64_t v) { return (int64_t)rfl64((uint64_t)v); }
+
+__device__ __forceinline__ uint4 load16(const char* p) { return *reinterpret_cast<const uint4*>(p); }
+
+// Row geometry of the vector kernels (uniform kernel argument).
+struct RowGeo {
+  int lg_lr;  // log2(lanes per row)
+  int cpl;    // chunks per lane (1 or 2)
+  int nch;    // 16-byte chunks per row
+  int tpl;    // dQ: tokens per lane
+  int tpw;    // dQ: tokens per wave (tpl * 64 / lanes per row, <= 64)
+};
+
+// ---- documents as the dD kernels see them -----------------------------------------
+// A document owns a run of dD rows (found from the view of its first pair) and
+// the pairs that score it; its sources are (pair k, query token t), numbered
+// p * rows + t, with list slots from slot0(d) on.  npairs / first / slot0 take
+// a wave-uniform document; pair / qok / qoff take per-lane arguments.
+struct DocsInBatch {  // document j: pairs p = j + Bd * i, i < Bq
+  int64_t ndocs;
+  uint32_t Bd, Bq;
+  int rows, Tq;
+  const uint8_t* qm;
+  int64_t qbytes;
+  __device__ int64_t npairs(int64_t) const { return Bq; }
+  __device__ int64_t first(int64_t d) const { return d; }
+  __device__ int64_t pair(int64_t d, uint32_t k) const { return d + (int64_t)Bd * k; }
+  __device__ int64_t slot0(int64_t d) const { return d * (int64_t)Bq * rows; }
+  __device__ bool qok(uint32_t p, int t) const { return !qm || qm[(int64_t)(p / Bd) * Tq + t]; }
+  __device__ int64_t qoff(uint32_t p) const { return (int64_t)(p / Bd) * qbytes; }
+};
+struct DocsPaired {  // document b: pair b
+  int64_t ndocs;
+  int rows, Tq;
+  const uint8_t* qm;
+  int64_t qbytes;
+  __device__ int64_t npairs(int64_t) const { return 1; }
+  __device__ int64_t first(int64_t d) const { return d; }
+  __device__ int64_t pair(int64_t d, uint32_t) const { return d; }
+  __device__ int64_t slot0(int64_t d) const { return d * rows; }
+  __device__ bool qok(uint32_t p, int t) const { return !qm || qm[(int64_t)p * Tq + t]; }
+  __device__ int64_t qoff(uint32_t p) const { return (int64_t)p * qbytes; }
+};
+struct DocsCand {  // gallery document j: the pairs the document order lists for it
+  int64_t ndocs;
+  const uint32_t* end;
+  const PairRef* order;
+  uint32_t C;
+  int rows, Tq;
+  const uint8_t* qm;
+  int64_t qbytes;
+  __device__ int64_t start(int64_t d) const { return d > 0 ? (int64_t)sload(end, d - 1) : 0; }
+  __device__ int64_t npairs(int64_t d) const { return (int64_t)sload(end, d) - start(d); }
+  __device__ int64_t first(int64_t d) const { return sload(&order[start(d)].p, 0); }
+  __device__ int64_t pair(int64_t d, uint32_t k) const { return order[start(d) + k].p; }
+  __device__ int64_t slot0(int64_t d) const { return start(d) * rows; }
+  __device__ bool qok(uint32_t p, int t) const { return !qm || qm[(int64_t)(p / C) * Tq + t]; }
+  __device__ int64_t qoff(uint32_t p) const { return (int64_t)(p / C) * qbytes; }
+};
+struct DocsPacked {  // document b: pair b; one shared query
+  int64_t ndocs;
+  int rows;
+  const uint8_t* qm;
+  __device__ int64_t npairs(int64_t) const { return 1; }
+  __device__ int64_t first(int64_t d) const { return d; }
+  __device__ int64_t pair(int64_t d, uint32_t) const { return d; }
+  __device__ int64_t slot0(int64_t d) const { return d * rows; }
+  __device__ bool qok(uint32_t, int t) const { return !qm || qm[t]; }
+  __device__ int64_t qoff(uint32_t) const { return 0; }
+};
+struct DocsVarlen {  // document segment n: pair n
+  int64_t ndocs;
+  int rows;
+  const int32_t* cu_q;
+  int64_t nq, rb;
+  __device__ int64_t npairs(int64_t) const { return 1; }
+  __device__ int64_t first(int64_t d) const { return d; }
+  __device__ int64_t pair(int64_t d, uint32_t) const { return d; }
+  __device__ int64_t slot0(int64_t d) const { return d * rows; }
+  __device__ bool qok(uint32_t, int) const { return true; }
+  __device__ int64_t qoff(uint32_t p) const { return clamp64((int64_t)cu_q[p] - 1, 0, nq) * rb; }
+};
 
 template <class E>
 __global__ void __launch_bounds__(kBwdThreads) bwd_delta_kernel(const char* Delta, const char* inv_n,
@@ -69,6 +211,356 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_zero16_kernel(uint16_t* w, in
   const int64_t stride = (int64_t)gridDim.x * kBwdThreads;
   for (int64_t i = (int64_t)blockIdx.x * kBwdThreads + threadIdx.x; i < n; i += stride) w[i] = 0u;
 }
+
+// ---- vector path: dQ --------------------------------------------------------------------
+
+// Work item = (query group g, token block tb).  kWaveSplit: a workgroup owns
+// one (item, split) and its four waves split the split's pairs (the pairs of
+// split s of group g are g*G + [s*ps, (s+1)*ps)); otherwise each wave owns
+// one item and all its pairs (nsplit == 1).  nsplit == 1 writes dQ in the
+// feature type; nsplit > 1 writes fp32 partials part[s][query row][dim].
+template <class L, class E, bool kWaveSplit>
+__global__ void __launch_bounds__(kBwdThreads) bwd_dq_vec_kernel(
+    const L lay, const float* delta, const int32_t* args, int64_t G, int rows, int ntb, int nsplit,
+    int64_t nitems, RowGeo geo, int64_t rb, int dim, const char* Qbase, char* dQ, float* part,
+    int64_t nq_rows) {
+  constexpr int kV = E::kV, kSL = 64 / kV;  // 16-byte slots per lane (64 fp32 accumulators)
+  const int lane = threadIdx.x & 63;
+  const int w = uniform((int)(threadIdx.x >> 6));
+  int64_t item;
+  int split;
+  if constexpr (kWaveSplit) {
+    split = (int)(blockIdx.x % (unsigned)nsplit);
+    item = (int64_t)(blockIdx.x / (unsigned)nsplit);
+  } else {
+    split = 0;
+    item = (int64_t)blockIdx.x * 4 + w;
+    if (item >= nitems) return;  // whole wave
+  }
+  const int64_t g = item / ntb;
+  const int tb = (int)(item - g * ntb);
+  const int64_t gend = (g + 1) * G;
+  const int64_t ps = (G + nsplit - 1) / nsplit;
+  int64_t pa = std::min(gend, g * G + (int64_t)split * ps);
+  int64_t pb = std::min(gend, pa + ps);
+  if constexpr (kWaveSplit) {
+    const int64_t q = (pb - pa + 3) / 4;
+    pa = std::min(pb, pa + w * q);
+    pb = std::min(pb, pa + q);
+  }
+  const PairView v0 = uniform_view(lay.get(g * G));
+  const int lg = geo.lg_lr, rpi = 64 >> lg;
+  const int gid = lane >> lg, c0 = lane & ((1 << lg) - 1);
+  const int t0 = tb * geo.tpw;
+  const int tend = std::min(v0.tq, t0 + geo.tpw);
+  // slot s of a lane: token t0 + srcl(s), 16-byte chunk ch(s) of the row
+  const int cm = geo.cpl - 1, cs = geo.cpl - 1 == 0 ? 0 : 1;
+  auto srcl = [&](int s) { return gid + rpi * (s >> cs); };
+  auto choff = [&](int s) { return (c0 + ((s & cm) << lg)) * 16; };
+  uint32_t actm = 0u, wrm = 0u;  // slot bits: accumulate / write
+#pragma unroll
+  for (int s = 0; s < kSL; ++s) {
+    const int t = t0 + srcl(s);
+    const bool wr = (s >> cs) < geo.tpl && t < tend && choff(s) < geo.nch * 16;
+    wrm |= (uint32_t)wr << s;
+    actm |= (uint32_t)(wr && (v0.qm == nullptr || v0.qm[t] != 0)) << s;
+  }
+  float acc[kSL][kV];
+#pragma unroll
+  for (int s = 0; s < kSL; ++s)
+#pragma unroll
+    for (int e = 0; e < kV; ++e) acc[s][e] = 0.0f;
+  const bool tlane = lane < geo.tpw && t0 + lane < tend;
+  // the tape block of pair p + 1 is loaded while pair p's rows are gathered
+  int tnext = (tlane && pa < pb) ? args[pa * rows + t0 + lane] : 0;
+  for (int64_t p = pa; p < pb; ++p) {
+    const int tv = tnext;
+    if (tlane && p + 1 < pb) tnext = args[(p + 1) * rows + t0 + lane];
+    const PairView v = uniform_view(lay.get(p));
+    const float dl = sload(delta, p);
+    if (!v.valid || dl == 0.0f) continue;
+    uint4 raw[kSL];
+#pragma unroll
+    for (int s = 0; s < kSL; ++s) {
+      const int u = __shfl(tv, srcl(s));
+      raw[s] = (((actm >> s) & 1u) && u >= 1 && u <= v.td)
+                   ? load16(v.d + (int64_t)(u - 1) * rb + choff(s))
+                   : make_uint4(0u, 0u, 0u, 0u);
+    }
+#pragma unroll
+    for (int s = 0; s < kSL; ++s) {
+      float x[kV];
+      E::unpack(raw[s], x);
+#pragma unroll
+      for (int e = 0; e < kV; ++e) acc[s][e] += dl * x[e];
+    }
+  }
+  if constexpr (kWaveSplit) {  // (w0 + w2) + (w1 + w3), element-major LDS rows of 64 lanes
+    __shared__ float red[2][64 * 64];
+    if (w >= 2) {
+#pragma unroll
+      for (int s = 0; s < kSL; ++s)
+#pragma unroll
+        for (int e = 0; e < kV; ++e) red[w - 2][(s * kV + e) * 64 + lane] = acc[s][e];
+    }
+    __syncthreads();
+    if (w < 2) {
+#pragma unroll
+      for (int s = 0; s < kSL; ++s)
+#pragma unroll
+        for (int e = 0; e < kV; ++e) acc[s][e] += red[w][(s * kV + e) * 64 + lane];
+    }
+    __syncthreads();
+    if (w == 1) {
+#pragma unroll
+      for (int s = 0; s < kSL; ++s)
+#pragma unroll
+        for (int e = 0; e < kV; ++e) red[0][(s * kV + e) * 64 + lane] = acc[s][e];
+    }
+    __syncthreads();
+    if (w != 0) return;
+#pragma unroll
+    for (int s = 0; s < kSL; ++s)
+#pragma unroll
+      for (int e = 0; e < kV; ++e) acc[s][e] += red[0][(s * kV + e) * 64 + lane];
+  }
+  const int64_t qrow0 = (int64_t)(v0.q - Qbase) / rb;
+#pragma unroll
+  for (int s = 0; s < kSL; ++s) {
+    if (!((wrm >> s) & 1u)) continue;
+    const int t = t0 + srcl(s);
+    if (nsplit == 1) {
+      *reinterpret_cast<uint4*>(dQ + (qrow0 + t) * rb + choff(s)) = E::pack(acc[s]);
+    } else {
+      float* dst = part + ((int64_t)split * nq_rows + qrow0 + t) * dim + (choff(s) / 16) * kV;
+#pragma unroll
+      for (int e = 0; e < kV; e += 4)
+        *reinterpret_cast<float4*>(dst + e) =
+            make_float4(acc[s][e], acc[s][e + 1], acc[s][e + 2], acc[s][e + 3]);
+    }
+  }
+}
+
+// dQ chunk c (16 bytes of the feature type) = sum over splits, in split order,
+// of the fp32 partials.
+template <class E>
+__global__ void __launch_bounds__(kBwdThreads) bwd_dq_reduce_kernel(const float* part, int nsplit,
+                                                                   int64_t nchunks, int64_t stride,
+                                                                   char* dQ) {
+  constexpr int kV = E::kV;
+  const int64_t step = (int64_t)gridDim.x * kBwdThreads;
+  for (int64_t c = (int64_t)blockIdx.x * kBwdThreads + threadIdx.x; c < nchunks; c += step) {
+    float acc[kV];
+#pragma unroll
+    for (int e = 0; e < kV; ++e) acc[e] = 0.0f;
+    for (int s = 0; s < nsplit; ++s) {
+      const float* src = part + (int64_t)s * stride + c * kV;
+#pragma unroll
+      for (int e = 0; e < kV; e += 4) {
+        const float4 x = *reinterpret_cast<const float4*>(src + e);
+        acc[e] += x.x;
+        acc[e + 1] += x.y;
+        acc[e + 2] += x.z;
+        acc[e + 3] += x.w;
+      }
+    }
+    *reinterpret_cast<uint4*>(dQ + c * 16) = E::pack(acc);
+  }
+}
+
+// ---- vector path: dD ---------------------------------------------------------------------
+
+// Exclusive scan of cnt[0, n) (n <= kDocTile) into out[]; returns the total.
+// Every thread of the (kDocThreads) block calls it.
+__device__ uint32_t block_scan_tile(const uint32_t* cnt, uint32_t* out, int n) {
+  constexpr int kWaves = kDocThreads / 64, kPer = kDocTile / kDocThreads;
+  __shared__ uint32_t wsum[kWaves];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int i0 = tid * kPer;
+  uint32_t loc[kPer];
+  uint32_t sum = 0u;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    loc[j] = (i0 + j < n) ? cnt[i0 + j] : 0u;
+    sum += loc[j];
+  }
+  uint32_t x = sum;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t y = __shfl_up(x, o);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) wsum[w] = x;
+  __syncthreads();
+  uint32_t before = x - sum, total = 0u;
+#pragma unroll
+  for (int j = 0; j < kWaves; ++j) {
+    if (j < w) before += wsum[j];
+    total += wsum[j];
+  }
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    if (i0 + j < n) out[i0 + j] = before;
+    before += loc[j];
+  }
+  __syncthreads();  // wsum and out are read by the caller / next call
+  return total;
+}
+
+// Sources f = k * tq + t (pair k of the document, query token t) of one
+// document, kDocUnroll per thread at a time: calls fn(p, t, u) for those with
+// a nonzero delta, a true qmask and a tape entry u0 < u <= u0 + ut.
+template <class Docs, class Fn>
+__device__ __forceinline__ void for_doc_sources(const Docs& docs, int64_t d, uint32_t nsrc, int tq,
+                                                const float* delta, const int32_t* args, int rows,
+                                                int u0, int ut, Fn fn) {
+  for (uint32_t f0 = 0; f0 < nsrc; f0 += kDocUnroll * kDocThreads) {
+    int64_t p[kDocUnroll];
+    int t[kDocUnroll], u[kDocUnroll];
+    bool ok[kDocUnroll];
+#pragma unroll
+    for (int q = 0; q < kDocUnroll; ++q) {
+      const uint32_t f = f0 + q * kDocThreads + threadIdx.x;
+      ok[q] = f < nsrc;
+      const uint32_t k = ok[q] ? f / (uint32_t)tq : 0u;
+      t[q] = ok[q] ? (int)(f - k * (uint32_t)tq) : 0;
+      p[q] = docs.pair(d, k);
+      u[q] = ok[q] ? args[p[q] * rows + t[q]] : 0;
+    }
+#pragma unroll
+    for (int q = 0; q < kDocUnroll; ++q) {
+      if (ok[q] && u[q] > u0 && u[q] <= u0 + ut && delta[p[q]] != 0.0f &&
+          docs.qok((uint32_t)p[q], t[q]))
+        fn(p[q], t[q], u[q]);
+    }
+  }
+}
+
+// One workgroup per document (grid-stride): sources of the document with a
+// nonzero delta, a true qmask and a tape entry 1 <= u <= td, sorted by u in
+// LDS tiles of kDocTile rows; writes rstart/rcount of the document's rows and
+// each source as (query row, delta bits) into list[slot0(d) ...].
+template <class L, class Docs>
+__global__ void __launch_bounds__(kDocThreads) bwd_doc_csr_kernel(const L lay, const Docs docs,
+                                                                 const float* delta,
+                                                                 const int32_t* args, int rows,
+                                                                 const char* Dbase, int64_t rb,
+                                                                 uint32_t* rstart, uint32_t* rcount,
+                                                                 uint2* list) {
+  __shared__ uint32_t cnt[kDocTile], cur[kDocTile];
+  const int tid = threadIdx.x;
+  for (int64_t d = blockIdx.x; d < docs.ndocs; d += gridDim.x) {
+    const int64_t np = uni64(docs.npairs(d));
+    if (np == 0) continue;
+    const PairView v = uniform_view(lay.get(uni64(docs.first(d))));
+    const int64_t r0 = (int64_t)(v.d - Dbase) / rb;
+    const int td = v.td, tq = v.tq;
+    const uint32_t nsrc = (uint32_t)(np * tq);
+    int64_t slot = docs.slot0(d);
+    for (int u0 = 0; u0 < td; u0 += kDocTile) {
+      const int ut = std::min(kDocTile, td - u0);
+      for (int i = tid; i < ut; i += kDocThreads) cnt[i] = 0u;
+      __syncthreads();
+      for_doc_sources(docs, d, nsrc, tq, delta, args, rows, u0, ut,
+                      [&](int64_t, int, int u) { atomicAdd(&cnt[u - 1 - u0], 1u); });
+      __syncthreads();
+      const uint32_t total = block_scan_tile(cnt, cur, ut);
+      for (int i = tid; i < ut; i += kDocThreads) {
+        rstart[r0 + u0 + i] = (uint32_t)slot + cur[i];
+        rcount[r0 + u0 + i] = cnt[i];
+      }
+      for_doc_sources(docs, d, nsrc, tq, delta, args, rows, u0, ut, [&](int64_t p, int t, int u) {
+        const uint32_t pos = atomicAdd(&cur[u - 1 - u0], 1u);
+        list[slot + pos] = make_uint2((uint32_t)(docs.qoff((uint32_t)p) / rb + t),
+                                      __float_as_uint(delta[p]));
+      });
+      __syncthreads();
+      slot += total;
+    }
+  }
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = std::max(v, (uint32_t)__shfl_xor((int)v, o));
+  return v;
+}
+
+// dD row r = sum over its listed sources of delta_p * Q[query row].  A wave
+// covers 64 / Lr consecutive rows, Lr lanes per row; every row of [0, nrows)
+// is written.  Each lane of a row group reads one list entry of a batch of Lr
+// (the next batch is loaded while this one is gathered); the group gathers
+// the batch's query rows kDdUnroll at a time, taking row and delta by
+// ds_bpermute.  Entries are checked against the list and the query rows, so
+// a malformed tape or cu cannot send a read out of bounds.
+template <class E, int kCPL>
+__global__ void __launch_bounds__(kBwdThreads) bwd_dd_vec_kernel(
+    const uint32_t* rstart, const uint32_t* rcount, const uint2* list, uint32_t nlist,
+    int64_t nrows, RowGeo geo, int64_t rb, const char* Qbase, int64_t nq_rows, char* dD) {
+  constexpr int kV = E::kV;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lg = geo.lg_lr, lr = 1 << lg, rpi = 64 >> lg;
+  const int gid = lane >> lg, c0 = lane & (lr - 1), gbase = gid << lg;
+  const int64_t per_block = 4 * (int64_t)rpi;
+  auto fetch = [&](uint32_t jj, uint32_t n, uint32_t base) {
+    return (jj < n && base + jj < nlist) ? list[base + jj] : make_uint2(0u, 0u);
+  };
+  for (int64_t rb0 = (int64_t)blockIdx.x * per_block; rb0 < nrows; rb0 += (int64_t)gridDim.x * per_block) {
+    const int64_t r = rb0 + w * rpi + gid;
+    const bool rv = r < nrows;
+    const uint32_t n = rv ? rcount[r] : 0u;
+    const uint32_t base = n ? rstart[r] : 0u;
+    const uint32_t nmax = wave_max_u32(n);
+    float acc[kCPL][kV];
+#pragma unroll
+    for (int cc = 0; cc < kCPL; ++cc)
+#pragma unroll
+      for (int e = 0; e < kV; ++e) acc[cc][e] = 0.0f;
+    uint2 ent = fetch(c0, n, base);
+    for (uint32_t j = 0; j < nmax; j += lr) {
+      const bool ok = ent.x < nq_rows;
+      const float dlane = ok ? __uint_as_float(ent.y) : 0.0f;
+      const int qlane = ok ? (int)ent.x : 0;
+      ent = fetch(j + lr + c0, n, base);  // next batch
+      const uint32_t nb = std::min<uint32_t>(lr, nmax - j);
+      for (uint32_t i0 = 0; i0 < nb; i0 += kDdUnroll) {
+        uint4 raw[kDdUnroll][kCPL];
+        float dl[kDdUnroll];
+#pragma unroll
+        for (int i = 0; i < kDdUnroll; ++i) {
+          const int sl = gbase + (int)((i0 + i) & (uint32_t)(lr - 1));
+          dl[i] = (i0 + i < (uint32_t)lr) ? __shfl(dlane, sl) : 0.0f;
+          const char* qa = Qbase + (int64_t)__shfl(qlane, sl) * rb;
+#pragma unroll
+          for (int cc = 0; cc < kCPL; ++cc) {
+            const int ch = c0 + (cc << lg);
+            raw[i][cc] = (dl[i] != 0.0f && cc < geo.cpl && ch < geo.nch) ? load16(qa + ch * 16)
+                                                                        : make_uint4(0u, 0u, 0u, 0u);
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < kDdUnroll; ++i)
+#pragma unroll
+          for (int cc = 0; cc < kCPL; ++cc) {
+            float x[kV];
+            E::unpack(raw[i][cc], x);
+#pragma unroll
+            for (int e = 0; e < kV; ++e) acc[cc][e] += dl[i] * x[e];
+          }
+      }
+    }
+    if (rv) {
+#pragma unroll
+      for (int cc = 0; cc < kCPL; ++cc) {
+        const int ch = c0 + (cc << lg);
+        if (cc < geo.cpl && ch < geo.nch)
+          *reinterpret_cast<uint4*>(dD + r * rb + ch * 16) = E::pack(acc[cc]);
+      }
+    }
+  }
+}
+
+// ---- generic path (any row size) -----------------------------------------------------------
 
 // Sources of pair p: query tokens t < tq with qmask, a tape entry in 1..td,
 // and a nonzero delta (a zero delta adds nothing, backward_pair.jl:21).
@@ -225,6 +717,189 @@ void launch_rows_e(const L& lay, const PullbackArgs& a, const float* delta, cons
   else launch_rows<L, E, 32>(lay, a, delta, end, col, rb, st);
 }
 
+// ---- per-layout document views (host) ------------------------------------------------------
+
+// Candidates need the document order: make_docs runs the grouping into `gws`
+// (docs_workspace bytes) and reports its status in *e.
+DocsInBatch make_docs(const LayInBatch& l, const PullbackArgs& a, void*, hipStream_t, hipError_t*) {
+  DocsInBatch d;
+  d.ndocs = l.Bd;
+  d.Bd = (uint32_t)l.Bd;
+  d.Bq = (uint32_t)(a.npairs / l.Bd);
+  d.rows = a.rows;
+  d.Tq = l.Tq;
+  d.qm = l.qm;
+  d.qbytes = l.qbytes;
+  return d;
+}
+DocsPaired make_docs(const LayPaired& l, const PullbackArgs& a, void*, hipStream_t, hipError_t*) {
+  DocsPaired d;
+  d.ndocs = a.npairs;
+  d.rows = a.rows;
+  d.Tq = l.Tq;
+  d.qm = l.qm;
+  d.qbytes = l.qbytes;
+  return d;
+}
+DocsCand make_docs(const LayCand& l, const PullbackArgs& a, void* gws, hipStream_t st, hipError_t* e) {
+  DocsCand d;
+  d.ndocs = l.N;
+  d.C = (uint32_t)l.C;
+  d.rows = a.rows;
+  d.Tq = l.Tq;
+  d.qm = l.qm;
+  d.qbytes = l.qbytes;
+  *e = group_pairs_by_document(l.idx, l.idx64, a.npairs, l.N, gws, &d.order, &d.end, st);
+  return d;
+}
+DocsPacked make_docs(const LayPacked& l, const PullbackArgs& a, void*, hipStream_t, hipError_t*) {
+  DocsPacked d;
+  d.ndocs = a.npairs;
+  d.rows = a.rows;
+  d.qm = l.qm;
+  return d;
+}
+DocsVarlen make_docs(const LayVarlen& l, const PullbackArgs& a, void*, hipStream_t, hipError_t*) {
+  DocsVarlen d;
+  d.ndocs = a.npairs;
+  d.rows = a.rows;
+  d.cu_q = l.cu_q;
+  d.nq = l.nq;
+  d.rb = l.rowbytes;
+  return d;
+}
+template <class L> size_t docs_workspace(const L&, int64_t) { return 0; }
+template <> size_t docs_workspace<LayCand>(const LayCand& l, int64_t npairs) {
+  return al256(group_workspace_bytes(npairs, l.N));
+}
+
+// Vector-path geometry for rows of rb bytes, or false.
+bool vec_geometry(int64_t rb, int esz, RowGeo* g) {
+  if (rb % 16 != 0) return false;
+  const int64_t nch = rb / 16;
+  if (nch < 4 || nch > 128) return false;
+  int64_t pc = 1;
+  while (pc < nch) pc <<= 1;
+  const int lr = (int)std::min<int64_t>(64, pc);
+  g->lg_lr = 0;
+  while ((1 << g->lg_lr) < lr) ++g->lg_lr;
+  g->cpl = (int)(pc / lr);
+  g->nch = (int)nch;
+  const int slots = 64 / (16 / esz);
+  g->tpl = std::min(slots / g->cpl, lr);
+  g->tpw = g->tpl * (64 / lr);
+  return true;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+template <class L, class E>
+hipError_t launch_vec(const L& lay, const PullbackArgs& a, const RowGeo& geo, const float* delta,
+                      hipStream_t st) {
+  const int64_t rb = (int64_t)a.dim * E::kSz;
+  const int64_t ngroups = a.npairs / a.G;
+  const int ntb = (int)bcdiv(a.rows, geo.tpw);
+  const int64_t nitems = ngroups * ntb;
+  // dQ pair splits: aim at ~4096 workgroups, >= 16 pairs per split, a
+  // multiple of 8 splits (one share per XCD), partials within 512 MB.
+  int64_t nsplit = 1;
+  const bool wave_split = a.G >= 4;
+  if (a.G >= 16 && nitems < 4096) {
+    nsplit = std::min<int64_t>(4096 / nitems, a.G / 16);
+    if (nsplit >= 8) nsplit &= ~(int64_t)7;
+    while (nsplit > 1 && nsplit * a.nq_rows * a.dim * 4 > ((int64_t)512 << 20)) nsplit /= 2;
+    if (nsplit < 1) nsplit = 1;
+  }
+  // dD: document lists
+  const int64_t nsrc = a.npairs * a.rows;
+  const size_t b_part = nsplit > 1 ? al256((size_t)(nsplit * a.nq_rows * a.dim) * 4) : 0;
+  const size_t b_rows = al256((size_t)std::max<int64_t>(a.nd_rows, 1) * 4);
+  const size_t b_list = al256((size_t)std::max<int64_t>(nsrc, 1) * 8);
+  const size_t b_docs = docs_workspace(lay, a.npairs);
+  void* ws = nullptr;
+  hipError_t e = workspace_alloc(&ws, b_part + 2 * b_rows + b_list + b_docs, st);
+  if (e != hipSuccess) return e;
+  char* w = static_cast<char*>(ws);
+  float* part = reinterpret_cast<float*>(w);
+  uint32_t* rstart = reinterpret_cast<uint32_t*>(w + b_part);
+  uint32_t* rcount = reinterpret_cast<uint32_t*>(w + b_part + b_rows);
+  uint2* list = reinterpret_cast<uint2*>(w + b_part + 2 * b_rows);
+  void* gws = w + b_part + 2 * b_rows + b_list;
+
+  if (wave_split) {
+    const int64_t nblk = nitems * nsplit;
+    hipLaunchKernelGGL((bwd_dq_vec_kernel<L, E, true>), dim3((unsigned)nblk), dim3(kBwdThreads), 0, st,
+                       lay, delta, a.args, a.G, a.rows, ntb, (int)nsplit, nitems, geo, rb, a.dim,
+                       a.Qbase, a.dQ, part, a.nq_rows);
+  } else {
+    hipLaunchKernelGGL((bwd_dq_vec_kernel<L, E, false>), dim3((unsigned)bcdiv(nitems, 4)),
+                       dim3(kBwdThreads), 0, st, lay, delta, a.args, a.G, a.rows, ntb, 1, nitems,
+                       geo, rb, a.dim, a.Qbase, a.dQ, part, a.nq_rows);
+  }
+  if (nsplit > 1) {
+    const int64_t nchunks = a.nq_rows * rb / 16;
+    const unsigned blocks =
+        (unsigned)std::min<int64_t>(65536, std::max<int64_t>(1, bcdiv(nchunks, kBwdThreads)));
+    hipLaunchKernelGGL(bwd_dq_reduce_kernel<E>, dim3(blocks), dim3(kBwdThreads), 0, st, part,
+                       (int)nsplit, nchunks, a.nq_rows * a.dim, a.dQ);
+  }
+  if (a.nd_rows > 0) {
+    hipError_t eg = hipSuccess;
+    const auto docs = make_docs(lay, a, gws, st, &eg);
+    if (eg == hipSuccess) {
+      hipLaunchKernelGGL(bwd_zero_kernel, dim3(grid_for(bcdiv(a.nd_rows, 64))), dim3(kBwdThreads), 0,
+                         st, rcount, a.nd_rows);
+      const unsigned dblocks = (unsigned)std::min<int64_t>(std::max<int64_t>(docs.ndocs, 1), 65536);
+      hipLaunchKernelGGL((bwd_doc_csr_kernel<L, decltype(docs)>), dim3(dblocks), dim3(kDocThreads), 0,
+                         st, lay, docs, delta, a.args, a.rows, a.Dbase, rb, rstart, rcount, list);
+      const int64_t per_block = 4 * (int64_t)(64 >> geo.lg_lr);
+      const unsigned rblocks = (unsigned)std::min<int64_t>(1048576, bcdiv(a.nd_rows, per_block));
+      if (geo.cpl == 1)
+        hipLaunchKernelGGL((bwd_dd_vec_kernel<E, 1>), dim3(rblocks), dim3(kBwdThreads), 0, st, rstart,
+                           rcount, list, (uint32_t)nsrc, a.nd_rows, geo, rb, a.Qbase, a.nq_rows, a.dD);
+      else
+        hipLaunchKernelGGL((bwd_dd_vec_kernel<E, 2>), dim3(rblocks), dim3(kBwdThreads), 0, st, rstart,
+                           rcount, list, (uint32_t)nsrc, a.nd_rows, geo, rb, a.Qbase, a.nq_rows, a.dD);
+    }
+    e = eg;
+  }
+  if (e == hipSuccess) e = hipGetLastError();
+  const hipError_t ef = workspace_free(ws, st);
+  return e != hipSuccess ? e : ef;
+}
+
+template <class L>
+hipError_t launch_generic(const L& lay, const PullbackArgs& a, const float* delta, hipStream_t st) {
+  const int esz = a.dtype == 0 ? 4 : 2;
+  const int64_t rb = (int64_t)a.dim * esz;
+  // workspace: end offsets (nd_rows + 1), sources (npairs * rows), scan sums
+  const int64_t nsrc = a.npairs * a.rows;
+  const size_t b_end = al256((size_t)(a.nd_rows + 1) * 4);
+  const size_t b_col = al256((size_t)(nsrc > 0 ? nsrc : 1) * 4), b_sums = scan_workspace_bytes(a.nd_rows);
+  void* ws = nullptr;
+  hipError_t e = workspace_alloc(&ws, b_end + b_col + b_sums, st);
+  if (e != hipSuccess) return e;
+  char* w = static_cast<char*>(ws);
+  uint32_t* cnt = reinterpret_cast<uint32_t*>(w);
+  uint32_t* col = reinterpret_cast<uint32_t*>(w + b_end);
+  uint32_t* sums = reinterpret_cast<uint32_t*>(w + b_end + b_col);
+  hipLaunchKernelGGL(bwd_zero_kernel, dim3(grid_for(bcdiv(a.nd_rows + 1, 64))), dim3(kBwdThreads), 0, st,
+                     cnt, a.nd_rows + 1);
+  hipLaunchKernelGGL((bwd_csr_kernel<L, false>), dim3(grid_for(a.npairs)), dim3(kBwdThreads), 0, st, lay,
+                     a.args, delta, a.npairs, a.rows, a.Dbase, rb, cnt, col);
+  e = exclusive_scan_u32(cnt, a.nd_rows, sums, st);
+  if (e == hipSuccess) {
+    hipLaunchKernelGGL((bwd_csr_kernel<L, true>), dim3(grid_for(a.npairs)), dim3(kBwdThreads), 0, st, lay,
+                       a.args, delta, a.npairs, a.rows, a.Dbase, rb, cnt, col);
+    if (a.dtype == 0) launch_rows_e<L, EF32>(lay, a, delta, cnt, col, rb, st);
+    else if (a.dtype == 1) launch_rows_e<L, EF16>(lay, a, delta, cnt, col, rb, st);
+    else launch_rows_e<L, EBF16>(lay, a, delta, cnt, col, rb, st);
+    e = hipGetLastError();
+  }
+  const hipError_t ef = workspace_free(ws, st);
+  return e != hipSuccess ? e : ef;
+}
+
 }  // namespace
 
 template <class L>
@@ -244,19 +919,12 @@ hipError_t launch_pullback(const L& lay, const PullbackArgs& a, hipStream_t st) 
     clear(a.dD, a.nd_rows);
     return hipGetLastError();
   }
-  // workspace: delta (npairs f32), end offsets (nd_rows + 1), sources (npairs * rows), scan sums
-  const int64_t nsrc = a.npairs * a.rows;
-  const size_t b_delta = al256((size_t)a.npairs * 4), b_end = al256((size_t)(a.nd_rows + 1) * 4);
-  const size_t b_col = al256((size_t)(nsrc > 0 ? nsrc : 1) * 4), b_sums = scan_workspace_bytes(a.nd_rows);
   void* ws = nullptr;
-  hipError_t e = workspace_alloc(&ws, b_delta + b_end + b_col + b_sums, st);
+  hipError_t e = workspace_alloc(&ws, al256((size_t)a.npairs * 4), st);
   if (e != hipSuccess) return e;
-  char* w = static_cast<char*>(ws);
-  float* delta = reinterpret_cast<float*>(w);
-  uint32_t* cnt = reinterpret_cast<uint32_t*>(w + b_delta);
-  uint32_t* col = reinterpret_cast<uint32_t*>(w + b_delta + b_end);
-  uint32_t* sums = reinterpret_cast<uint32_t*>(w + b_delta + b_end + b_col);
-  const unsigned flat = (unsigned)std::min<int64_t>(65536, std::max<int64_t>(1, bcdiv(a.npairs, kBwdThreads)));
+  float* delta = static_cast<float*>(ws);
+  const unsigned flat =
+      (unsigned)std::min<int64_t>(65536, std::max<int64_t>(1, bcdiv(a.npairs, kBwdThreads)));
   const char* Dl = static_cast<const char*>(a.Delta);
   const char* Il = static_cast<const char*>(a.inv_n);
   if (a.dtype == 0)
@@ -266,19 +934,15 @@ hipError_t launch_pullback(const L& lay, const PullbackArgs& a, hipStream_t st) 
   else
     hipLaunchKernelGGL(bwd_delta_kernel<EBF16>, dim3(flat), dim3(kBwdThreads), 0, st, Dl, Il, a.npairs, a.G, delta);
   if (a.zero_dq) clear(a.dQ, a.nq_rows);
-  // destination CSR
-  hipLaunchKernelGGL(bwd_zero_kernel, dim3(grid_for(bcdiv(a.nd_rows + 1, 64))), dim3(kBwdThreads), 0, st,
-                     cnt, a.nd_rows + 1);
-  hipLaunchKernelGGL((bwd_csr_kernel<L, false>), dim3(grid_for(a.npairs)), dim3(kBwdThreads), 0, st, lay,
-                     a.args, delta, a.npairs, a.rows, a.Dbase, rb, cnt, col);
-  e = exclusive_scan_u32(cnt, a.nd_rows, sums, st);
-  if (e == hipSuccess) {
-    hipLaunchKernelGGL((bwd_csr_kernel<L, true>), dim3(grid_for(a.npairs)), dim3(kBwdThreads), 0, st, lay,
-                       a.args, delta, a.npairs, a.rows, a.Dbase, rb, cnt, col);
-    if (a.dtype == 0) launch_rows_e<L, EF32>(lay, a, delta, cnt, col, rb, st);
-    else if (a.dtype == 1) launch_rows_e<L, EF16>(lay, a, delta, cnt, col, rb, st);
-    else launch_rows_e<L, EBF16>(lay, a, delta, cnt, col, rb, st);
-    e = hipGetLastError();
+  RowGeo geo;
+  const bool vec = vec_geometry(rb, esz, &geo) && aligned16(a.dQ) && aligned16(a.dD) &&
+                   aligned16(a.Qbase) && aligned16(a.Dbase);
+  if (vec) {
+    if (a.dtype == 0) e = launch_vec<L, EF32>(lay, a, geo, delta, st);
+    else if (a.dtype == 1) e = launch_vec<L, EF16>(lay, a, geo, delta, st);
+    else e = launch_vec<L, EBF16>(lay, a, geo, delta, st);
+  } else {
+    e = launch_generic(lay, a, delta, st);
   }
   const hipError_t ef = workspace_free(ws, st);
   return e != hipSuccess ? e : ef;

@@ -174,6 +174,15 @@ hipError_t group_pairs_by_document(const void* idx, int idx64, int64_t npairs, i
   return hipGetLastError();
 }
 
+hipError_t group_pairs_by_document(const void* idx, int idx64, int64_t npairs, int64_t N,
+                                   void* workspace, const PairRef** order_out,
+                                   const uint32_t** doc_end, hipStream_t stream) {
+  // after the scatter, counter j holds the end of document j's run of pairs
+  *doc_end = reinterpret_cast<const uint32_t*>(static_cast<const char*>(workspace) +
+                                               align256((size_t)npairs * sizeof(PairRef)));
+  return group_pairs_by_document(idx, idx64, npairs, N, workspace, order_out, stream);
+}
+
 size_t scan_workspace_bytes(int64_t n) { return align256((size_t)cdiv(n > 0 ? n : 1, kScanTile) * 4); }
 
 hipError_t exclusive_scan_u32(uint32_t* counts, int64_t n, uint32_t* sums, hipStream_t stream) {

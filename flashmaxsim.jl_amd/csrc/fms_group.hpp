@@ -31,6 +31,11 @@ size_t group_workspace_bytes(int64_t npairs, int64_t N);
 // pair's result does not depend on it.  Requires npairs, N < 2^31.
 hipError_t group_pairs_by_document(const void* idx, int idx64, int64_t npairs, int64_t N,
                                    void* workspace, const PairRef** order, hipStream_t stream);
+// The same, also returning doc_end (N + 1 counters in `workspace`): the pairs of
+// document j are order[j > 0 ? doc_end[j-1] : 0 .. doc_end[j]).
+hipError_t group_pairs_by_document(const void* idx, int idx64, int64_t npairs, int64_t N,
+                                   void* workspace, const PairRef** order,
+                                   const uint32_t** doc_end, hipStream_t stream);
 
 // In-place exclusive prefix sum of n counters on `stream`; `sums` holds
 // scan_workspace_bytes(n) bytes.

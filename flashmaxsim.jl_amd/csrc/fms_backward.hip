@@ -30,6 +30,7 @@
 #include <algorithm>
 
 #include "fms_backward.hpp"
+#include "fms_device.hpp"
 #include "fms_group.hpp"
 
 namespace fms {
@@ -66,6 +67,13 @@ struct EF32 {
     return make_uint4(__float_as_uint(x[0]), __float_as_uint(x[1]), __float_as_uint(x[2]),
                       __float_as_uint(x[3]));
   }
+  // acc[e] += d * chunk element e, one fused multiply-add each
+  __device__ static void fma_chunk(const uint4& r, float d, float* acc) {
+    acc[0] = __builtin_fmaf(d, __uint_as_float(r.x), acc[0]);
+    acc[1] = __builtin_fmaf(d, __uint_as_float(r.y), acc[1]);
+    acc[2] = __builtin_fmaf(d, __uint_as_float(r.z), acc[2]);
+    acc[3] = __builtin_fmaf(d, __uint_as_float(r.w), acc[3]);
+  }
 };
 struct EF16 {
   static constexpr int kSz = 2, kV = 8;
@@ -85,6 +93,18 @@ struct EF16 {
   }
   __device__ static uint4 pack(const float* x) {
     return make_uint4(two(x[0], x[1]), two(x[2], x[3]), two(x[4], x[5]), two(x[6], x[7]));
+  }
+  // acc[e] += d * chunk element e; the half -> float widening folds into the
+  // fused multiply-add (v_fma_mix_f32 reads either half of a register)
+  __device__ static void fma_word(uint32_t w, float d, float& a0, float& a1) {
+    a0 = __builtin_fmaf(d, lo(w), a0);
+    a1 = __builtin_fmaf(d, hi(w), a1);
+  }
+  __device__ static void fma_chunk(const uint4& r, float d, float* acc) {
+    fma_word(r.x, d, acc[0], acc[1]);
+    fma_word(r.y, d, acc[2], acc[3]);
+    fma_word(r.z, d, acc[4], acc[5]);
+    fma_word(r.w, d, acc[6], acc[7]);
   }
 };
 struct EBF16 {
@@ -109,9 +129,20 @@ struct EBF16 {
   __device__ static uint4 pack(const float* x) {
     return make_uint4(two(x[0], x[1]), two(x[2], x[3]), two(x[4], x[5]), two(x[6], x[7]));
   }
+  __device__ static void fma_chunk(const uint4& r, float d, float* acc) {
+    acc[0] = __builtin_fmaf(d, lo(r.x), acc[0]);
+    acc[1] = __builtin_fmaf(d, hi(r.x), acc[1]);
+    acc[2] = __builtin_fmaf(d, lo(r.y), acc[2]);
+    acc[3] = __builtin_fmaf(d, hi(r.y), acc[3]);
+    acc[4] = __builtin_fmaf(d, lo(r.z), acc[4]);
+    acc[5] = __builtin_fmaf(d, hi(r.z), acc[5]);
+    acc[6] = __builtin_fmaf(d, lo(r.w), acc[6]);
+    acc[7] = __builtin_fmaf(d, hi(r.w), acc[7]);
+  }
 };
 
 __device__ __forceinline__ int64_t uni64(int64_t v) { return (int64_t)rfl64((uint64_t)v); }
+__device__ __forceinline__ float uniform_f(float v) { return __uint_as_float(rfl32(__float_as_uint(v))); }
 
 __device__ __forceinline__ uint4 load16(const char* p) { return *reinterpret_cast<const uint4*>(p); }
 
@@ -271,13 +302,37 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_dq_vec_kernel(
 #pragma unroll
     for (int e = 0; e < kV; ++e) acc[s][e] = 0.0f;
   const bool tlane = lane < geo.tpw && t0 + lane < tend;
-  // the tape block of pair p + 1 is loaded while pair p's rows are gathered
-  int tnext = (tlane && pa < pb) ? args[pa * rows + t0 + lane] : 0;
-  for (int64_t p = pa; p < pb; ++p) {
+  // Software pipeline: the view, delta and tape block of pair p + 1 are
+  // loaded while pair p's rows are gathered.
+  PairView vnext;
+  float dnext = 0.0f;
+  int tnext = 0;
+  // Items start at different pairs of their range (step k takes pair
+  // pa + (rot + k) mod len), so the waves that share documents do not
+  // request them in lockstep.
+  const int64_t len = pb - pa;
+  const int64_t rot = len > 0 ? (item * 2) % len : 0;
+  auto pair_at = [&](int64_t k) {
+    int64_t q = rot + k;
+    if (q >= len) q -= len;
+    return pa + q;
+  };
+  if (len > 0) {
+    const int64_t p0 = pair_at(0);
+    vnext = uniform_view(lay.get(p0));
+    dnext = sload(delta, p0);
+    tnext = tlane ? args[p0 * rows + t0 + lane] : 0;
+  }
+  for (int64_t k = 0; k < len; ++k) {
+    const PairView v = vnext;
+    const float dl = dnext;
     const int tv = tnext;
-    if (tlane && p + 1 < pb) tnext = args[(p + 1) * rows + t0 + lane];
-    const PairView v = uniform_view(lay.get(p));
-    const float dl = sload(delta, p);
+    if (k + 1 < len) {
+      const int64_t pn = pair_at(k + 1);
+      vnext = uniform_view(lay.get(pn));
+      dnext = sload(delta, pn);
+      if (tlane) tnext = args[pn * rows + t0 + lane];
+    }
     if (!v.valid || dl == 0.0f) continue;
     uint4 raw[kSL];
 #pragma unroll
@@ -289,10 +344,7 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_dq_vec_kernel(
     }
 #pragma unroll
     for (int s = 0; s < kSL; ++s) {
-      float x[kV];
-      E::unpack(raw[s], x);
-#pragma unroll
-      for (int e = 0; e < kV; ++e) acc[s][e] += dl * x[e];
+      E::fma_chunk(raw[s], dl, acc[s]);
     }
   }
   if constexpr (kWaveSplit) {  // (w0 + w2) + (w1 + w3), element-major LDS rows of 64 lanes
@@ -333,6 +385,192 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_dq_vec_kernel(
       *reinterpret_cast<uint4*>(dQ + (qrow0 + t) * rb + choff(s)) = E::pack(acc[s]);
     } else {
       float* dst = part + ((int64_t)split * nq_rows + qrow0 + t) * dim + (choff(s) / 16) * kV;
+#pragma unroll
+      for (int e = 0; e < kV; e += 4)
+        *reinterpret_cast<float4*>(dst + e) =
+            make_float4(acc[s][e], acc[s][e + 1], acc[s][e + 2], acc[s][e + 3]);
+    }
+  }
+}
+
+// In-batch dQ with the documents staged in LDS.  A workgroup of 16 waves owns
+// 16 work items (query i, token block) and document share s (documents
+// [s*ps, (s+1)*ps), split index = block index mod nsplit as above); every
+// document of the share is copied once into LDS by direct buffer-to-LDS
+// loads and the 16 queries gather their chosen rows from there, so a
+// document row leaves L2 once per workgroup instead of once per (query,
+// token) that chose it.  Three LDS buffers: documents j + 1 and j + 2 are in
+// flight while j is gathered (the copy latency is several gathers long).
+constexpr int kIbThreads = 1024;
+constexpr int kIbItems = kIbThreads / 64;
+constexpr int kIbStagePer = 3;                                // copies per wave per document
+constexpr int kIbStageChunks = kIbStagePer * kIbThreads;      // 48 KB per LDS buffer
+constexpr int kIbBufs = 3;
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// Wait until at most kVm of this wave's loads are outstanding (the
+// buffer-to-LDS copies among them; loads complete in issue order), then meet
+// the workgroup: every wave's finished copies are visible after.
+template <int kVm>
+__device__ __forceinline__ void dma_wait_barrier() {
+  static_assert(kVm >= 0 && kVm < 16, "vmcnt field");
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0x0070 | kVm);  // vmcnt(kVm) lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*)p);
+}
+
+// Four 16-byte LDS reads, complete on return.
+__device__ __forceinline__ void lds_read4(uint4 (&r)[4], const uint32_t (&a)[4]) {
+  asm volatile(
+      "ds_read_b128 %0, %4\n\t"
+      "ds_read_b128 %1, %5\n\t"
+      "ds_read_b128 %2, %6\n\t"
+      "ds_read_b128 %3, %7\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])
+      : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]));
+}
+
+template <class E, int kCPL>
+__global__ void __launch_bounds__(kIbThreads) bwd_dq_ib_kernel(
+    const LayInBatch lay, const float* delta, const int32_t* args, int rows, int ntb, int nsplit,
+    int64_t nitems, RowGeo geo, int64_t rb, int dim, char* dQ, float* part, int64_t nq_rows) {
+  constexpr int kV = E::kV, kSL = 64 / kV, kHalf = kSL / 2;
+  constexpr int kOps = kIbStagePer + 2;  // loads a wave issues per document
+  // Three separate arrays (not one indexed array): the compiler then sees that
+  // a copy into one buffer cannot alias reads of another and does not wait
+  // for the copy before each read.
+  __shared__ uint4 dbuf0[kIbStageChunks], dbuf1[kIbStageChunks], dbuf2[kIbStageChunks];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = uniform(tid >> 6);
+  const int split = (int)(blockIdx.x % (unsigned)nsplit);
+  const int64_t item = (int64_t)(blockIdx.x / (unsigned)nsplit) * kIbItems + w;
+  const bool live = item < nitems;  // (a dead wave still copies and meets the barriers)
+  const int64_t i = live ? item / ntb : 0;
+  const int tb = live ? (int)(item - i * ntb) : 0;
+  const int64_t Bd = lay.Bd;
+  const int td = lay.Td, nch = geo.nch;
+  const uint32_t stage_bytes = (uint32_t)(td * rb);
+  const int64_t ps = (Bd + nsplit - 1) / nsplit;
+  const int64_t ja = std::min<int64_t>(Bd, (int64_t)split * ps), jb = std::min<int64_t>(Bd, ja + ps);
+  const int lg = geo.lg_lr, rpi = 64 >> lg;
+  const int gid = lane >> lg, c0 = lane & ((1 << lg) - 1);
+  const int t0 = tb * geo.tpw;
+  const int tend = live ? std::min(lay.Tq, t0 + geo.tpw) : 0;
+  const uint8_t* qm = lay.qm ? lay.qm + i * lay.Tq : nullptr;
+  constexpr int cs = kCPL == 2 ? 1 : 0;
+  auto srcl = [&](int s) { return gid + rpi * (s >> cs); };
+  auto chunk = [&](int s) { return c0 + ((s & (kCPL - 1)) << lg); };
+  uint32_t actm = 0u, wrm = 0u;
+#pragma unroll
+  for (int s = 0; s < kSL; ++s) {
+    const int t = t0 + srcl(s);
+    const bool wr = (s >> cs) < geo.tpl && t < tend && chunk(s) < nch;
+    wrm |= (uint32_t)wr << s;
+    actm |= (uint32_t)(wr && (qm == nullptr || qm[t] != 0)) << s;
+  }
+  float acc[kSL][kV];
+#pragma unroll
+  for (int s = 0; s < kSL; ++s)
+#pragma unroll
+    for (int e = 0; e < kV; ++e) acc[s][e] = 0.0f;
+  const bool tlane = lane < geo.tpw && t0 + lane < tend;
+  const int tcol = std::min(t0 + lane, rows - 1);  // in bounds for every lane
+  // Document j -> LDS buffer b (wave w copies 16-byte chunks (k*16 + w)*64 +
+  // lane; a copy past the document reads 0 from the resource's range check),
+  // and the pair (i, j)'s delta and tape block.  Always exactly kOps loads.
+  // Workgroups of one share start at different documents (step k reads
+  // document ja + (rot + k) mod len), so the share's documents are requested
+  // from HBM by many workgroups at once rather than in lockstep.
+  const int64_t len = jb - ja;
+  const int64_t rot = len > 0 ? ((int64_t)(blockIdx.x / (unsigned)nsplit) * 2) % len : 0;
+  auto fetch = [&](int64_t k, uint4* buf, float& dl, int& tv) {
+    int64_t j = rot + k;
+    if (j >= len) j -= len;
+    j += ja;
+    const rsrc_t r = make_rsrc_u(lay.D + j * lay.dbytes, stage_bytes);
+#pragma unroll
+    for (int k = 0; k < kIbStagePer; ++k) {
+      const int base = (k * kIbItems + w) * 64;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)(buf + base), 16, (base + lane) * 16,
+                                               0, 0, 0);
+    }
+    const int64_t p = j + Bd * i;
+    dl = delta[p];
+    tv = args[p * rows + tcol];
+  };
+  // The LDS reads go through lds_read4: the compiler cannot tell which buffer
+  // a copy targets once the rotation wraps, and would otherwise wait for the
+  // copies in flight (the next two documents) before each read.  The step
+  // barrier already orders them: document j's copy completed before step j.
+  auto gather = [&](const uint4* rowbase, float dlv, int tvv) {
+    const float dl = live ? uniform_f(dlv) : 0.0f;
+    const int tv = tlane ? tvv : 0;
+    if (dl == 0.0f) return;
+    const uint32_t lbase = lds_addr(rowbase);
+#pragma unroll
+    for (int h = 0; h < kSL / 4; ++h) {
+      uint32_t addr[4];
+      bool ok[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int s = h * 4 + q;
+        const int u = __shfl(tv, srcl(s));
+        ok[q] = ((actm >> s) & 1u) && u >= 1 && u <= td;
+        addr[q] = lbase + (uint32_t)(((ok[q] ? u - 1 : 0) * nch + chunk(s)) * 16);
+      }
+      uint4 raw[4];
+      lds_read4(raw, addr);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        E::fma_chunk(raw[q], ok[q] ? dl : 0.0f, acc[h * 4 + q]);
+      }
+    }
+  };
+  // Steps 0, 1, 2, ... rotate through buffers 0, 1, 2 and register sets 0, 1,
+  // 2 (delta and tape block, loaded two steps ahead).  Every step issues the
+  // same loads (past the share's end it re-fetches the last step's document
+  // into the buffer just retired), so each wait is one count.
+  float d0 = 0.0f, d1 = 0.0f, d2 = 0.0f;
+  int v0r = 0, v1r = 0, v2r = 0;
+  if (len > 0) {
+    fetch(0, dbuf0, d0, v0r);
+    fetch(std::min<int64_t>(1, len - 1), dbuf1, d1, v1r);
+  }
+  dma_wait_barrier<kOps>();  // document ja ready
+  // step k: gather from `rd` with (dc, tc) (nothing past the share's end);
+  // fetch step k + 2's document into `wr` / (dn, tn).  The loop body is straight-line (the
+  // last round pads with empty steps) so the compiler's own load counting
+  // stays exact across the back edge.
+  auto step = [&](int64_t k, const uint4* rd, uint4* wr, float& dc, int& tc, float& dn, int& tn) {
+    const float dcur = k < len ? dc : 0.0f;
+    const int tcur = tc;
+    fetch(std::min(k + 2, len - 1), wr, dn, tn);  // `wr` was read at step k - 1
+    gather(rd, dcur, tcur);
+    dma_wait_barrier<kOps>();  // k + 1 ready; k + 2 may stay in flight
+  };
+  for (int64_t k = 0; k < len; k += 3) {
+    step(k, dbuf0, dbuf2, d0, v0r, d2, v2r);
+    step(k + 1, dbuf1, dbuf0, d1, v1r, d0, v0r);
+    step(k + 2, dbuf2, dbuf1, d2, v2r, d1, v1r);
+  }
+  dma_wait_barrier<0>();  // no copy may land after the workgroup's LDS is released
+  if (!live) return;
+  const int64_t qrow0 = i * lay.Tq;
+#pragma unroll
+  for (int s = 0; s < kSL; ++s) {
+    if (!((wrm >> s) & 1u)) continue;
+    const int t = t0 + srcl(s);
+    if (nsplit == 1) {
+      *reinterpret_cast<uint4*>(dQ + (qrow0 + t) * rb + chunk(s) * 16) = E::pack(acc[s]);
+    } else {
+      float* dst = part + ((int64_t)split * nq_rows + qrow0 + t) * dim + chunk(s) * kV;
 #pragma unroll
       for (int e = 0; e < kV; e += 4)
         *reinterpret_cast<float4*>(dst + e) =
@@ -542,10 +780,7 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_dd_vec_kernel(
         for (int i = 0; i < kDdUnroll; ++i)
 #pragma unroll
           for (int cc = 0; cc < kCPL; ++cc) {
-            float x[kV];
-            E::unpack(raw[i][cc], x);
-#pragma unroll
-            for (int e = 0; e < kV; ++e) acc[cc][e] += dl[i] * x[e];
+            E::fma_chunk(raw[i][cc], dl[i], acc[cc]);
           }
       }
     }
@@ -773,6 +1008,28 @@ template <> size_t docs_workspace<LayCand>(const LayCand& l, int64_t npairs) {
   return al256(group_workspace_bytes(npairs, l.N));
 }
 
+// Document rows the staged in-batch dQ kernel copies per document (-1: the
+// layout has no staged kernel).
+template <class L> int64_t staged_rows(const L&) { return -1; }
+template <> int64_t staged_rows<LayInBatch>(const LayInBatch& l) { return l.Td; }
+
+template <class E, class L>
+void launch_dq_staged(const L&, const PullbackArgs&, const RowGeo&, const float*, int, int, int64_t,
+                      int64_t, float*, hipStream_t) {}
+template <class E>
+void launch_dq_staged(const LayInBatch& lay, const PullbackArgs& a, const RowGeo& geo,
+                      const float* delta, int ntb, int nsplit, int64_t nitems, int64_t rb, float* part,
+                      hipStream_t st) {
+  const int64_t nblk = bcdiv(nitems, kIbItems) * nsplit;
+  if constexpr (E::kSz != 2) return;  // (16-bit features only, see launch_vec)
+  if (geo.cpl == 1)
+    hipLaunchKernelGGL((bwd_dq_ib_kernel<E, 1>), dim3((unsigned)nblk), dim3(kIbThreads), 0, st, lay,
+                       delta, a.args, a.rows, ntb, nsplit, nitems, geo, rb, a.dim, a.dQ, part, a.nq_rows);
+  else
+    hipLaunchKernelGGL((bwd_dq_ib_kernel<E, 2>), dim3((unsigned)nblk), dim3(kIbThreads), 0, st, lay,
+                       delta, a.args, a.rows, ntb, nsplit, nitems, geo, rb, a.dim, a.dQ, part, a.nq_rows);
+}
+
 // Vector-path geometry for rows of rb bytes, or false.
 bool vec_geometry(int64_t rb, int esz, RowGeo* g) {
   if (rb % 16 != 0) return false;
@@ -800,16 +1057,25 @@ hipError_t launch_vec(const L& lay, const PullbackArgs& a, const RowGeo& geo, co
   const int64_t ngroups = a.npairs / a.G;
   const int ntb = (int)bcdiv(a.rows, geo.tpw);
   const int64_t nitems = ngroups * ntb;
-  // dQ pair splits: aim at ~4096 workgroups, >= 16 pairs per split, a
-  // multiple of 8 splits (one share per XCD), partials within 512 MB.
+  // dQ pair splits: aim at ~4096 workgroups (the staged in-batch kernel: one
+  // 16-wave workgroup per CU), >= 16 pairs per split, a multiple of 8 splits
+  // (one share per XCD), partials within 512 MB.
+  // (16-bit features only: fp32 accumulators plus fp32 rows exceed the 128 registers
+  // a 16-wave workgroup leaves each lane)
+  const bool staged = E::kSz == 2 && staged_rows(lay) >= 0 &&
+                      staged_rows(lay) * geo.nch <= kIbStageChunks;
   int64_t nsplit = 1;
   const bool wave_split = a.G >= 4;
-  if (a.G >= 16 && nitems < 4096) {
+  if (staged) {
+    const int64_t nwg = bcdiv(nitems, kIbItems);
+    nsplit = std::min<int64_t>(a.G, std::max<int64_t>(1, bcdiv(256, nwg)));
+    if (nsplit >= 8) nsplit = std::min<int64_t>(a.G, (nsplit + 7) & ~(int64_t)7);
+  } else if (a.G >= 16 && nitems < 4096) {
     nsplit = std::min<int64_t>(4096 / nitems, a.G / 16);
     if (nsplit >= 8) nsplit &= ~(int64_t)7;
-    while (nsplit > 1 && nsplit * a.nq_rows * a.dim * 4 > ((int64_t)512 << 20)) nsplit /= 2;
-    if (nsplit < 1) nsplit = 1;
   }
+  while (nsplit > 1 && nsplit * a.nq_rows * a.dim * 4 > ((int64_t)512 << 20)) nsplit /= 2;
+  if (nsplit < 1) nsplit = 1;
   // dD: document lists
   const int64_t nsrc = a.npairs * a.rows;
   const size_t b_part = nsplit > 1 ? al256((size_t)(nsplit * a.nq_rows * a.dim) * 4) : 0;
@@ -826,7 +1092,9 @@ hipError_t launch_vec(const L& lay, const PullbackArgs& a, const RowGeo& geo, co
   uint2* list = reinterpret_cast<uint2*>(w + b_part + 2 * b_rows);
   void* gws = w + b_part + 2 * b_rows + b_list;
 
-  if (wave_split) {
+  if (staged) {
+    launch_dq_staged<E>(lay, a, geo, delta, ntb, (int)nsplit, nitems, rb, part, st);
+  } else if (wave_split) {
     const int64_t nblk = nitems * nsplit;
     hipLaunchKernelGGL((bwd_dq_vec_kernel<L, E, true>), dim3((unsigned)nblk), dim3(kBwdThreads), 0, st,
                        lay, delta, a.args, a.G, a.rows, ntb, (int)nsplit, nitems, geo, rb, a.dim,

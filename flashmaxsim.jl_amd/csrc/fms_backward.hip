@@ -42,6 +42,7 @@ constexpr int kBwdUnroll = 8;     // source rows in flight per wave (generic ker
 constexpr int kDocTile = 4096;    // destination rows per LDS tile of bwd_doc_csr
 constexpr int kDocThreads = 1024; // threads of bwd_doc_csr (16 waves)
 constexpr int kDocUnroll = 4;     // sources in flight per thread (bwd_doc_csr)
+constexpr int kDocKeep = 16;      // sources a thread keeps in registers (bwd_doc_csr, one tape read)
 constexpr int kDdUnroll = 8;      // sources in flight per row group (bwd_dd_vec)
 
 inline int64_t bcdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
@@ -158,32 +159,31 @@ struct RowGeo {
 // ---- documents as the dD kernels see them -----------------------------------------
 // A document owns a run of dD rows (found from the view of its first pair) and
 // the pairs that score it; its sources are (pair k, query token t), numbered
-// p * rows + t, with list slots from slot0(d) on.  npairs / first / slot0 take
-// a wave-uniform document; pair / qok / qoff take per-lane arguments.
+// p * rows + t, with list slots from slot0(d) on; qrow0(p) is the first dQ /
+// query row of p's query.  npairs / first / slot0 take a wave-uniform
+// document; pair / qok / qrow0 take per-lane arguments.
 struct DocsInBatch {  // document j: pairs p = j + Bd * i, i < Bq
   int64_t ndocs;
   uint32_t Bd, Bq;
   int rows, Tq;
   const uint8_t* qm;
-  int64_t qbytes;
   __device__ int64_t npairs(int64_t) const { return Bq; }
   __device__ int64_t first(int64_t d) const { return d; }
   __device__ int64_t pair(int64_t d, uint32_t k) const { return d + (int64_t)Bd * k; }
   __device__ int64_t slot0(int64_t d) const { return d * (int64_t)Bq * rows; }
   __device__ bool qok(uint32_t p, int t) const { return !qm || qm[(int64_t)(p / Bd) * Tq + t]; }
-  __device__ int64_t qoff(uint32_t p) const { return (int64_t)(p / Bd) * qbytes; }
+  __device__ int64_t qrow0(uint32_t p) const { return (int64_t)(p / Bd) * Tq; }
 };
 struct DocsPaired {  // document b: pair b
   int64_t ndocs;
   int rows, Tq;
   const uint8_t* qm;
-  int64_t qbytes;
   __device__ int64_t npairs(int64_t) const { return 1; }
   __device__ int64_t first(int64_t d) const { return d; }
   __device__ int64_t pair(int64_t d, uint32_t) const { return d; }
   __device__ int64_t slot0(int64_t d) const { return d * rows; }
   __device__ bool qok(uint32_t p, int t) const { return !qm || qm[(int64_t)p * Tq + t]; }
-  __device__ int64_t qoff(uint32_t p) const { return (int64_t)p * qbytes; }
+  __device__ int64_t qrow0(uint32_t p) const { return (int64_t)p * Tq; }
 };
 struct DocsCand {  // gallery document j: the pairs the document order lists for it
   int64_t ndocs;
@@ -192,14 +192,13 @@ struct DocsCand {  // gallery document j: the pairs the document order lists for
   uint32_t C;
   int rows, Tq;
   const uint8_t* qm;
-  int64_t qbytes;
   __device__ int64_t start(int64_t d) const { return d > 0 ? (int64_t)sload(end, d - 1) : 0; }
   __device__ int64_t npairs(int64_t d) const { return (int64_t)sload(end, d) - start(d); }
   __device__ int64_t first(int64_t d) const { return sload(&order[start(d)].p, 0); }
   __device__ int64_t pair(int64_t d, uint32_t k) const { return order[start(d) + k].p; }
   __device__ int64_t slot0(int64_t d) const { return start(d) * rows; }
   __device__ bool qok(uint32_t p, int t) const { return !qm || qm[(int64_t)(p / C) * Tq + t]; }
-  __device__ int64_t qoff(uint32_t p) const { return (int64_t)(p / C) * qbytes; }
+  __device__ int64_t qrow0(uint32_t p) const { return (int64_t)(p / C) * Tq; }
 };
 struct DocsPacked {  // document b: pair b; one shared query
   int64_t ndocs;
@@ -210,19 +209,19 @@ struct DocsPacked {  // document b: pair b; one shared query
   __device__ int64_t pair(int64_t d, uint32_t) const { return d; }
   __device__ int64_t slot0(int64_t d) const { return d * rows; }
   __device__ bool qok(uint32_t, int t) const { return !qm || qm[t]; }
-  __device__ int64_t qoff(uint32_t) const { return 0; }
+  __device__ int64_t qrow0(uint32_t) const { return 0; }
 };
 struct DocsVarlen {  // document segment n: pair n
   int64_t ndocs;
   int rows;
   const int32_t* cu_q;
-  int64_t nq, rb;
+  int64_t nq;
   __device__ int64_t npairs(int64_t) const { return 1; }
   __device__ int64_t first(int64_t d) const { return d; }
   __device__ int64_t pair(int64_t d, uint32_t) const { return d; }
   __device__ int64_t slot0(int64_t d) const { return d * rows; }
   __device__ bool qok(uint32_t, int) const { return true; }
-  __device__ int64_t qoff(uint32_t p) const { return clamp64((int64_t)cu_q[p] - 1, 0, nq) * rb; }
+  __device__ int64_t qrow0(uint32_t p) const { return clamp64((int64_t)cu_q[p] - 1, 0, nq); }
 };
 
 template <class E>
@@ -695,6 +694,42 @@ __global__ void __launch_bounds__(kDocThreads) bwd_doc_csr_kernel(const L lay, c
     const int td = v.td, tq = v.tq;
     const uint32_t nsrc = (uint32_t)(np * tq);
     int64_t slot = docs.slot0(d);
+    if (nsrc <= (uint32_t)(kDocKeep * kDocThreads) && td <= kDocTile) {
+      // One tape read: each thread keeps its sources (row, (query row, delta))
+      // in registers between the count and the fill.
+      uint32_t key[kDocKeep];
+      uint2 val[kDocKeep];
+#pragma unroll
+      for (int q = 0; q < kDocKeep; ++q) {
+        const uint32_t f = q * kDocThreads + tid;
+        const bool in = f < nsrc;
+        const uint32_t k = in ? f / (uint32_t)tq : 0u;
+        const int t = in ? (int)(f - k * (uint32_t)tq) : 0;
+        const int64_t p = docs.pair(d, k);
+        const int u = in ? args[p * rows + t] : 0;
+        const float dl = delta[p];
+        const bool ok = in && u >= 1 && u <= td && dl != 0.0f && docs.qok((uint32_t)p, t);
+        key[q] = ok ? (uint32_t)(u - 1) : 0xFFFFFFFFu;
+        val[q] = make_uint2((uint32_t)(docs.qrow0((uint32_t)p) + t), __float_as_uint(dl));
+      }
+      for (int i = tid; i < td; i += kDocThreads) cnt[i] = 0u;
+      __syncthreads();
+#pragma unroll
+      for (int q = 0; q < kDocKeep; ++q)
+        if (key[q] != 0xFFFFFFFFu) atomicAdd(&cnt[key[q]], 1u);
+      __syncthreads();
+      block_scan_tile(cnt, cur, td);
+      for (int i = tid; i < td; i += kDocThreads) {
+        rstart[r0 + i] = (uint32_t)slot + cur[i];
+        rcount[r0 + i] = cnt[i];
+      }
+      __syncthreads();  // every start read before the fill moves the cursors
+#pragma unroll
+      for (int q = 0; q < kDocKeep; ++q)
+        if (key[q] != 0xFFFFFFFFu) list[slot + atomicAdd(&cur[key[q]], 1u)] = val[q];
+      __syncthreads();
+      continue;
+    }
     for (int u0 = 0; u0 < td; u0 += kDocTile) {
       const int ut = std::min(kDocTile, td - u0);
       for (int i = tid; i < ut; i += kDocThreads) cnt[i] = 0u;
@@ -707,10 +742,10 @@ __global__ void __launch_bounds__(kDocThreads) bwd_doc_csr_kernel(const L lay, c
         rstart[r0 + u0 + i] = (uint32_t)slot + cur[i];
         rcount[r0 + u0 + i] = cnt[i];
       }
+      __syncthreads();  // every start read before the fill moves the cursors
       for_doc_sources(docs, d, nsrc, tq, delta, args, rows, u0, ut, [&](int64_t p, int t, int u) {
         const uint32_t pos = atomicAdd(&cur[u - 1 - u0], 1u);
-        list[slot + pos] = make_uint2((uint32_t)(docs.qoff((uint32_t)p) / rb + t),
-                                      __float_as_uint(delta[p]));
+        list[slot + pos] = make_uint2((uint32_t)(docs.qrow0((uint32_t)p) + t), __float_as_uint(delta[p]));
       });
       __syncthreads();
       slot += total;
@@ -964,7 +999,6 @@ DocsInBatch make_docs(const LayInBatch& l, const PullbackArgs& a, void*, hipStre
   d.rows = a.rows;
   d.Tq = l.Tq;
   d.qm = l.qm;
-  d.qbytes = l.qbytes;
   return d;
 }
 DocsPaired make_docs(const LayPaired& l, const PullbackArgs& a, void*, hipStream_t, hipError_t*) {
@@ -973,7 +1007,6 @@ DocsPaired make_docs(const LayPaired& l, const PullbackArgs& a, void*, hipStream
   d.rows = a.rows;
   d.Tq = l.Tq;
   d.qm = l.qm;
-  d.qbytes = l.qbytes;
   return d;
 }
 DocsCand make_docs(const LayCand& l, const PullbackArgs& a, void* gws, hipStream_t st, hipError_t* e) {
@@ -983,7 +1016,6 @@ DocsCand make_docs(const LayCand& l, const PullbackArgs& a, void* gws, hipStream
   d.rows = a.rows;
   d.Tq = l.Tq;
   d.qm = l.qm;
-  d.qbytes = l.qbytes;
   *e = group_pairs_by_document(l.idx, l.idx64, a.npairs, l.N, gws, &d.order, &d.end, st);
   return d;
 }
@@ -1000,7 +1032,6 @@ DocsVarlen make_docs(const LayVarlen& l, const PullbackArgs& a, void*, hipStream
   d.rows = a.rows;
   d.cu_q = l.cu_q;
   d.nq = l.nq;
-  d.rb = l.rowbytes;
   return d;
 }
 template <class L> size_t docs_workspace(const L&, int64_t) { return 0; }

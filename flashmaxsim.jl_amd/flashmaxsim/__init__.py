@@ -24,6 +24,7 @@ from .forward import (candidates_forward, inbatch_forward, int8_candidates_forwa
                       pair_forward, varlen_forward)
 from .packed import PackedSeq, nseq, pack_docs, pack_pairs
 from .quant import Int8Index, dequant_int8, quantize_int8_symmetric
+from .rrule import MaxSimFunction, rrule
 
 __all__ = [
     "maxsim", "MaxSim", "InBatch", "AtomicUnified", "InvGrid", "score_eltype", "dot_accum",
@@ -33,7 +34,7 @@ __all__ = [
     "packed_forward", "varlen_forward", "int8_pair_forward", "int8_paired_forward",
     "int8_candidates_forward",
     "pair_pullback", "paired_pullback", "inbatch_pullback", "candidates_pullback",
-    "packed_pullback", "varlen_pullback",
+    "packed_pullback", "varlen_pullback", "rrule", "MaxSimFunction",
     "launch_pair_scan", "launch_paired_scan", "launch_candidates_scan", "inbatch_device_scan",
     "launch_packed_scan", "launch_varlen_scan", "launch_int8_pair_scan",
     "launch_int8_paired_scan", "launch_int8_candidates_scan", "tensor_cores_active",

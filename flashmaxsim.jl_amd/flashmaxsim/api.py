@@ -15,7 +15,9 @@ Argument forms (Julia shapes in brackets; torch shapes are reversed):
 
 Keywords ``neg`` (fill for invalid candidate indices only, default
 T(-1f4)), ``normalize`` (divide by the number of valid query tokens) and
-``backward`` (∇D strategy, accepted for API compatibility; forward-only here).
+``backward`` (∇D strategy marker; the HIP pullback computes the same sums for
+either).  When a feature tensor requires grad, the call is recorded for torch
+autograd and back-propagates through the sparse pullbacks (``rrule``).
 Scores are Float32 for every feature type (score_eltype).
 """
 from __future__ import annotations
@@ -36,11 +38,12 @@ class InBatch:
 
 
 class AtomicUnified:
-    """∇D strategy marker (types.jl:10-11); forward results do not depend on it."""
+    """∇D strategy marker (types.jl:10-11).  The reference scatters dD with atomics; the
+    HIP pullback computes the same sums through a destination-sorted source list."""
 
 
 class InvGrid:
-    """∇D strategy marker (types.jl:13-14); forward results do not depend on it."""
+    """∇D strategy marker (types.jl:13-14): gather for dQ, destination CSR for dD."""
 
 
 def score_eltype(dtype):
@@ -113,6 +116,11 @@ def maxsim(*args, neg=None, normalize=None, backward=None):
             raise ArgumentError("pass either a MaxSim config or keywords, not both")
         if not isinstance(b, Int8Index) and cfg.dtype != T and not isinstance(a, PackedSeq):
             raise ArgumentError("MaxSim feature eltype must match the callable's parameter")
+
+    # ---- differentiable call: record the tape and the pullback (rrule.jl) ----
+    from .rrule import maxsim_autograd, needs_grad
+    if needs_grad(args):
+        return maxsim_autograd(cfg, args)
 
     # ---- varlen pairs ----
     if isinstance(a, PackedSeq):

@@ -13,6 +13,15 @@
 #   launch_int8_pair_scan!   src/quant.jl:139-154
 #   launch_int8_paired_scan! src/quant.jl:199-217
 #   tensor_cores_active      src/ka.jl:71
+# the device pullbacks on the argmax tape (both strategy markers; the library
+# runs the gather + destination-CSR form for either, overwriting the
+# zeros_like gradients it is handed):
+#   pair_apply_pullback!        src/backward_pair.jl:73-87
+#   paired_apply_pullback!      src/backward_layouts.jl:45-60
+#   inbatch_apply_pullback!     src/backward_layouts.jl:113-127
+#   candidates_apply_pullback!  src/backward_layouts.jl:187-202
+#   packed_apply_pullback!      src/packed.jl:384-390
+#   varlen_apply_pullback!      src/packed.jl:449-455
 # and additionally candidates_forward_ka (src/forward_layouts.jl:272-290), so
 # the candidate layout uses the library's fused Σ_t + `neg` epilogue instead
 # of the separate `sum(partial; dims=1)` and `ifelse.` kernels.
@@ -197,6 +206,104 @@ function FlashMaxSim.launch_int8_paired_scan!(::ROCBackend, args, partial,
                 dptr(qmask), dptr(dmask), dim, Tq, size(Dc, 2), B, C_NULL, stream_ptr()),
           "INT8 paired scan")
     nothing
+end
+
+
+# ---- pullbacks on the argmax tape ----------------------------------------------
+# Δ and inv_n arrive in the feature eltype (convert_scores in src/rrule.jl);
+# inv_n === nothing passes NULL (all ones).
+
+for M in (FlashMaxSim.AtomicUnified, FlashMaxSim.InvGrid)
+    @eval begin
+        function FlashMaxSim.pair_apply_pullback!(::$M, ::ROCBackend, dq, dd,
+                                                  q::ROCMatrix{T}, d::ROCMatrix{T}, qmask,
+                                                  argmax_u, δ, dim, Tq, Td) where {T<:FloatFeature}
+            check(ccall((:fms_pair_pullback, libfms), Int32,
+                        (Int32, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid},
+                         Ptr{Cvoid}, Ptr{Cvoid}, Int64, Int64, Int64, Ptr{Cvoid}),
+                        dtype_code(T), dptr(dq), dptr(dd), dptr(q), dptr(d), dptr(qmask),
+                        dptr(argmax_u), dptr(δ), dim, Tq, Td, stream_ptr()),
+                  "pair pullback")
+            nothing
+        end
+
+        function FlashMaxSim.paired_apply_pullback!(::$M, ::ROCBackend, dQ, dD,
+                                                    Q::ROCArray{T,3}, D::ROCArray{T,3}, qmask,
+                                                    args, Δ, inv_n, dim, Tq, B,
+                                                    Td) where {T<:FloatFeature}
+            check(ccall((:fms_paired_pullback, libfms), Int32,
+                        (Int32, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid},
+                         Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Int64, Int64, Int64, Int64, Ptr{Cvoid}),
+                        dtype_code(T), dptr(dQ), dptr(dD), dptr(Q), dptr(D), dptr(qmask),
+                        dptr(args), dptr(Δ), dptr(inv_n), dim, Tq, Td, B, stream_ptr()),
+                  "paired pullback")
+            nothing
+        end
+
+        function FlashMaxSim.inbatch_apply_pullback!(::$M, ::ROCBackend, dQ, dD,
+                                                     Q::ROCArray{T,3}, D::ROCArray{T,3}, qmask,
+                                                     args, Δ, inv_n, dim, Tq, Bq, Td,
+                                                     Bd) where {T<:FloatFeature}
+            check(ccall((:fms_inbatch_pullback, libfms), Int32,
+                        (Int32, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid},
+                         Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Int64, Int64, Int64, Int64, Int64,
+                         Ptr{Cvoid}),
+                        dtype_code(T), dptr(dQ), dptr(dD), dptr(Q), dptr(D), dptr(qmask),
+                        dptr(args), dptr(Δ), dptr(inv_n), dim, Tq, Td, Bq, Bd, stream_ptr()),
+                  "in-batch pullback")
+            nothing
+        end
+
+        function FlashMaxSim.candidates_apply_pullback!(::$M, ::ROCBackend, dQ, dG,
+                                                        Q::ROCArray{T,3}, gallery::ROCArray{T,3},
+                                                        idx, qmask, args, Δ, inv_n, dim, Tq, B,
+                                                        Td, C, N) where {T<:FloatFeature}
+            check(ccall((:fms_candidates_pullback, libfms), Int32,
+                        (Int32, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Int32,
+                         Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Int64, Int64, Int64,
+                         Int64, Int64, Int64, Ptr{Cvoid}),
+                        dtype_code(T), dptr(dQ), dptr(dG), dptr(Q), dptr(gallery), dptr(idx),
+                        Int32(sizeof(eltype(idx))), dptr(qmask), dptr(args), dptr(Δ),
+                        dptr(inv_n), dim, Tq, B, Td, N, C, stream_ptr()),
+                  "candidates pullback")
+            nothing
+        end
+
+        function FlashMaxSim.packed_apply_pullback!(::$M, ::ROCBackend, Δ, q::ROCMatrix{T},
+                                                    P::FlashMaxSim.PackedSeq, qmask, args,
+                                                    inv_n) where {T<:FloatFeature}
+            dq = similar(q)
+            dP = similar(P.tokens)
+            dim, Tq = size(q)
+            check(ccall((:fms_packed_pullback, libfms), Int32,
+                        (Int32, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid},
+                         Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Int64, Int64, Int64,
+                         Int64, Ptr{Cvoid}),
+                        dtype_code(T), dptr(dq), dptr(dP), dptr(q), dptr(P.tokens), dptr(P.cu),
+                        dptr(qmask), dptr(args), dptr(Δ), dptr(inv_n), dim, Tq,
+                        length(P.cu) - 1, size(P.tokens, 2), stream_ptr()),
+                  "packed pullback")
+            dq, dP
+        end
+
+        function FlashMaxSim.varlen_apply_pullback!(::$M, ::ROCBackend, Δ,
+                                                    Q::FlashMaxSim.PackedSeq,
+                                                    D::FlashMaxSim.PackedSeq, args, inv_n)
+            T = eltype(Q.tokens)
+            dQ = similar(Q.tokens)
+            dD = similar(D.tokens)
+            check(ccall((:fms_varlen_pullback, libfms), Int32,
+                        (Int32, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid},
+                         Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Int64, Int64, Int64,
+                         Int64, Int64, Ptr{Cvoid}),
+                        dtype_code(T), dptr(dQ), dptr(dD), dptr(Q.tokens), dptr(D.tokens),
+                        dptr(Q.cu), dptr(D.cu), dptr(args), dptr(Δ), dptr(inv_n),
+                        size(Q.tokens, 1), size(args, 1), size(args, 2), size(Q.tokens, 2),
+                        size(D.tokens, 2), stream_ptr()),
+                  "varlen pullback")
+            dQ, dD
+        end
+    end
 end
 
 end # module

@@ -103,3 +103,13 @@ def test_int8index_shape_checks():
         require_int8_index(fm.Int8Index(torch.zeros(2, 5, 8, dtype=torch.int8), torch.zeros(3, 5)))
     deq = fm.dequant_int8(fm.Int8Index(torch.tensor([[1, -2]], dtype=torch.int8), torch.tensor([0.5])))
     assert deq.tolist() == [[0.5, -1.0]]
+
+
+def test_rrule_refuses_host_arrays_and_bad_config():
+    """rrule mirrors the forward's colocation rule: host tensors never take a CPU path."""
+    import flashmaxsim as fm
+    Q = torch.zeros(2, 3, 8)
+    with pytest.raises(fm.ArgumentError):
+        fm.rrule(fm.MaxSim(torch.float32), Q, Q)
+    with pytest.raises(fm.ArgumentError):
+        fm.rrule("not a config", Q, Q)

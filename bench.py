@@ -10,7 +10,8 @@ resident in HBM, outputs preallocated.  Prints ONE JSON line.
 
 Other workloads (--workload c3 | c4 | c4d1024 | c5) measure the in-batch,
 packed and INT8 scans the same way (each prints its own JSON line); c3bwd
-measures the pullback of the c3 scores on their argmax tape (dQ and dD).
+measures the pullback of the c3 scores on their argmax tape (dQ and dD);
+c4mq scores the c4 workload with the multi-query packed scan (one launch).
 """
 from __future__ import annotations
 
@@ -40,7 +41,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="c2",
-                    choices=["c2", "c3", "c3bwd", "c4", "c4d1024", "c5", "read"])
+                    choices=["c2", "c3", "c3bwd", "c4", "c4d1024", "c4mq", "c5", "read"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="target duration of the bounded CPU baseline sample")
@@ -409,6 +410,51 @@ def run_c4(args, torch, fm, boundary, dev, dim=128):
     return res
 
 
+def run_c4mq(args, torch, fm, boundary, dev):
+    """The C4 workload (64 queries x 20,000 packed documents, bf16, d = 128) through the
+    multi-query packed scan: one launch scores every query, each document is read
+    once per block of 32 queries.  No reference counterpart (the reference's API
+    scores one query per call, which is --workload c4)."""
+    import numpy as np
+    dim, Lq, nd, nq = 128, 24, 20_000, 64
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(4)
+    lens = torch.randint(700, 1101, (nd,), generator=gen, device=dev)
+    cu = torch.zeros(nd + 1, dtype=torch.int32, device=dev)
+    cu[1:] = torch.cumsum(lens, 0).to(torch.int32)
+    cu += 1
+    ntok = int(lens.sum().item())
+    max_len = int(lens.max().item())
+    log(f"c4mq: packing {nd} docs, {ntok} tokens, d={dim} bf16 ...")
+    tok = normalized_randn(torch, (ntok, dim), gen, torch.bfloat16, dev, chunk_rows=1 << 20)
+    Qs = normalized_randn(torch, (nq, Lq, dim), gen, torch.bfloat16, dev)
+    S = torch.empty(nq, nd, dtype=torch.float32, device=dev)
+    args_t = torch.empty(nq, nd, Lq, dtype=torch.int32, device=dev)
+
+    def step():
+        boundary.launch_packed_multi_scan(args_t, S, Qs, tok, cu, None, max_len)
+
+    wall, launch_ms = timed_steps(torch, step, args.steps, args.warmup)
+    chunks = int(((lens + 31) // 32).sum().item())
+    res = dict(pairs_per_step=nq * nd, flops_per_launch=2 * dim * Lq * nq * ntok, wall=wall,
+               launch_ms=launch_ms, dtype="bf16", bound="mfma",
+               padded_flops=2 * dim * 32 * nq * chunks * 32,
+               config={"workload": "c4mq_packed_multi_bf16_d128", "dim": dim, "Lq": Lq,
+                       "docs": nd, "doc_len": "U[700,1100]", "tokens": ntok, "queries": nq,
+                       "call": "one multi-query packed scan for all queries"})
+    # spot check: 3 queries x 64 documents against the single-query scan
+    rng = np.random.default_rng(0)
+    worst = 0.0
+    for i in rng.choice(nq, 3, replace=False):
+        s1 = torch.empty(nd, dtype=torch.float32, device=dev)
+        boundary.launch_packed_scan(None, None, Qs[int(i)], tok, cu, None, s1)
+        sel = torch.from_numpy(rng.choice(nd, 64, replace=False)).to(dev)
+        a, b = S[int(i)][sel].double(), s1[sel].double()
+        worst = max(worst, float(((a - b).abs() / b.abs().clamp(min=1e-3)).max()))
+    res["check"] = {"vs": "single-query packed scan", "max_rel_err": worst, "ok": worst < 2e-3}
+    return res
+
+
 def run_read(args, torch, fm, boundary, dev):
     """Measured HBM read ceiling: fms_debug_read_bandwidth over an 8 GiB buffer (16-byte
     nontemporal loads, 8192 x 256 threads).  Also the known-size calibration of FETCH_SIZE."""
@@ -443,7 +489,7 @@ def main():
     torch.cuda.set_device(dev)
     boundary.candidates_grouping(args.grouping)
     runner = {"c2": run_c2, "c3": run_c3, "c3bwd": run_c3bwd, "c4": run_c4, "c5": run_c5,
-              "read": run_read,
+              "c4mq": run_c4mq, "read": run_read,
               "c4d1024": lambda *a: run_c4(*a, dim=1024)}[args.workload]
     r = runner(args, torch, fm, boundary, dev)
     steps = args.steps

@@ -325,6 +325,46 @@ fms_status fms_launch_packed_scan(int32_t dtype, int32_t* args, float* partial, 
                    vec_ok(esz, dim, {q, tokens}), as_stream(stream));
 }
 
+fms_status fms_launch_packed_multi_scan(int32_t dtype, int32_t* args, float* scores,
+                                        const void* Q, const void* tokens, const int32_t* cu,
+                                        const uint8_t* qmask, int64_t dim, int64_t Tq, int64_t nq,
+                                        int64_t B, int64_t ntokens, int64_t max_len,
+                                        void* stream) {
+  const int esz = elem_bytes(dtype);
+  if (esz == 0) return FMS_EUNSUPPORTED;
+  if (dim < 0 || Tq < 0 || nq < 0 || B < 0 || ntokens < 0 || max_len < 0) return FMS_EINVAL;
+  if (!seq_ok(Tq, dim, esz) || nq > kMaxTokens || B > kMaxTokens) return FMS_EUNSUPPORTED;
+  if (nq == 0 || B == 0) return FMS_OK;
+  if (!scores || !cu || (Tq * dim > 0 && !Q) || (ntokens * dim > 0 && !tokens)) return FMS_EINVAL;
+  const hipStream_t st = as_stream(stream);
+  if ((dtype == FMS_F16 || dtype == FMS_BF16) && inbatch_mfma_supported(dim, Tq, max_len, Q, tokens) &&
+      max_len >= 1 && ntokens <= kMaxTokens) {
+    InBatchArgs a;
+    a.Q = static_cast<const char*>(Q);
+    a.D = static_cast<const char*>(tokens);
+    a.qm = qmask;
+    a.dm = nullptr;
+    a.cu = cu;
+    a.ntok = ntokens;
+    a.S = scores;
+    a.args = args;
+    a.Bq = (int)nq;
+    a.Bd = (int)B;
+    a.Tq = (int)Tq;
+    a.Td = (int)max_len;
+    return from_hip(launch_inbatch_mfma(dtype == FMS_BF16, a, st));
+  }
+  // other shapes / fp32: one packed scan per query
+  for (int64_t i = 0; i < nq; ++i) {
+    const fms_status r = fms_launch_packed_scan(
+        dtype, args ? args + i * B * Tq : nullptr, nullptr,
+        static_cast<const char*>(Q) + i * Tq * dim * esz, tokens, cu,
+        qmask ? qmask + i * Tq : nullptr, dim, Tq, B, ntokens, scores + i * B, stream);
+    if (r != FMS_OK) return r;
+  }
+  return FMS_OK;
+}
+
 fms_status fms_launch_varlen_scan(int32_t dtype, int32_t* args, float* partial,
                                   const void* Qtokens, const void* Dtokens, const int32_t* cu_q,
                                   const int32_t* cu_d, int64_t dim, int64_t max_q, int64_t N,

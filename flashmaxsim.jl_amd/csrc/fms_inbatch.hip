@@ -153,6 +153,27 @@ __global__ void __launch_bounds__(256) inbatch_plan_kernel(const uint8_t* dm, in
   }
 }
 
+// The same plan for PackedSeq documents: document j is token rows
+// [cu[j]-1, cu[j+1]-1) (clamped into the token range and to Td = max_len
+// rows, as the packed scans clamp a malformed device cu); every row is valid.
+__global__ void __launch_bounds__(256) packed_plan_kernel(const int32_t* cu, int64_t ntok, int Bd,
+                                                          int Td, int nch, uint32_t* cmask,
+                                                          int32_t* dcount, int32_t* dfirst) {
+  const int lane = threadIdx.x & 63;
+  const int j = blockIdx.x * 4 + uniform(threadIdx.x >> 6);
+  if (j >= Bd) return;
+  const int64_t a = std::min<int64_t>(std::max<int64_t>((int64_t)cu[j] - 1, 0), ntok);
+  const int64_t z = std::min<int64_t>(std::max<int64_t>((int64_t)cu[j + 1] - 1, a), ntok);
+  const int len = (int)std::min<int64_t>(z - a, Td);
+  const int rows = len - lane * kTile;
+  const uint32_t m = rows >= kTile ? 0xffffffffu : (rows > 0 ? (1u << rows) - 1u : 0u);
+  if (lane < nch) cmask[(int64_t)j * nch + lane] = m;
+  if (lane == 0) {
+    dcount[j] = (len + kTile - 1) / kTile;
+    dfirst[j] = len > 0 ? 0 : -1;
+  }
+}
+
 // Exclusive scan over the 64 * kIbWaves threads of a block; every thread
 // must call it.  *total receives the block sum.
 __device__ int block_exclusive_scan_i32(int v, int* total) {
@@ -178,7 +199,8 @@ __device__ int block_exclusive_scan_i32(int v, int* total) {
   return before + x - v;
 }
 
-template <class Op>
+// kPacked: documents are PackedSeq token ranges (A.cu), not Td-row slabs.
+template <class Op, bool kPacked>
 __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(const InBatchArgs A) {
   typedef typename Op::Acc Acc;
   typedef typename Op::Frag Frag;
@@ -191,6 +213,8 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
   __shared__ int32_t doc_first[kIbMaxDocs];          // first valid token, -1 = none
   __shared__ uint32_t lst_mask[kIbMaxList];          // compacted chunk list
   __shared__ uint32_t lst_info[kIbMaxList];
+  __shared__ int32_t lst_row0[kPacked ? kIbMaxList : 1];  // packed: document's first row
+  __shared__ int32_t doc_row0[kPacked ? kIbMaxDocs + 1 : 1];
   __shared__ int lst_count;
   __shared__ int16_t res_tape[kIbWaves][kIbQpw][kIbMaxDocs][kTile];  // Td <= 2048
   __shared__ float res_score[kIbWaves][kIbQpw][kIbMaxDocs];
@@ -253,6 +277,20 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
   }
   const int ndoc = j1 - j0;
   const int Tq = A.Tq, Td = A.Td;
+  // Packed: the block's documents are token rows [row(j0), row(j1)); doc_row0
+  // holds each one's first row relative to row(j0) (cu clamped into the
+  // token range, as the packed scans clamp it).
+  int64_t prow0 = 0;
+  if constexpr (kPacked) {
+    if (tid <= ndoc) {
+      const int64_t a = std::min<int64_t>(std::max<int64_t>((int64_t)A.cu[j0 + tid] - 1, 0), A.ntok);
+      doc_row0[tid] = (int32_t)std::min<int64_t>(a, (int64_t)0x7fffffff);
+    }
+    __syncthreads();
+    prow0 = uniform(doc_row0[0]);
+    __syncthreads();
+    if (tid <= ndoc) doc_row0[tid] -= (int32_t)prow0;
+  }
   const int nch = Td > 0 ? (Td + kTile - 1) / kTile : 1;  // <= 64
   const int nall = ndoc * nch;
 
@@ -325,6 +363,7 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
         lst_mask[pos] = m;
         lst_info[pos] = (uint32_t)(ch | (jj << kInfoDocShift) |
                                    ((doc_first[jj] + 1) << kInfoFirstShift));
+        if constexpr (kPacked) lst_row0[pos] = doc_row0[jj];
       }
       base += __builtin_popcountll(bal);
     }
@@ -354,6 +393,7 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
   if (tid < nsteps_pad - nsteps) {
     lst_mask[nsteps + tid] = lst_mask[nsteps - 1];
     lst_info[nsteps + tid] = lst_info[nsteps - 1] & ~(1u << kInfoLastBit);
+    if constexpr (kPacked) lst_row0[nsteps + tid] = lst_row0[nsteps - 1];
   }
   __syncthreads();
 
@@ -365,14 +405,19 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
   // document's first valid token instead) into fragment slot kb*64 + l.
   // The stream position stops at the last (padded) entry, so loads issued
   // past the end re-read it.
-  const rsrc_t rd = make_rsrc(A.D + (int64_t)j0 * Td * kIbRowBytes, (uint32_t)(ndoc * Td * kIbRowBytes));
+  // (packed: the block's rows run to the end of the token array, at most
+  // 2^24 - 1 rows past row(j0) so the range fits the resource's 32 bits)
+  const rsrc_t rd = kPacked
+      ? make_rsrc_u(A.D + prow0 * kIbRowBytes,
+                    (uint32_t)std::min<int64_t>(A.ntok - prow0, 0xffffff) * kIbRowBytes)
+      : make_rsrc(A.D + (int64_t)j0 * Td * kIbRowBytes, (uint32_t)(ndoc * Td * kIbRowBytes));
   int ld_i = 0;  // next list entry to request
-  auto chunk_load = [&](u32x4* buf, uint32_t m, uint32_t info) {
+  auto chunk_load = [&](u32x4* buf, uint32_t m, uint32_t info, int row0) {
     const int ch = info & 63u, jj = (info >> kInfoDocShift) & kInfoDocMask;
     const int f = (int)(info >> kInfoFirstShift) - 1;
     const int fsrc = f < 0 ? 0 : f;  // (never: listed chunks have a valid row)
     const int src = ((m >> r32) & 1u) ? ch * kTile + r32 : fsrc;
-    const int voff = (jj * Td + src) * kIbRowBytes + h * 16;
+    const int voff = ((kPacked ? row0 : jj * Td) + src) * kIbRowBytes + h * 16;
 #pragma unroll
     for (int k = 0; k < kIbKbPerWave; ++k) {
       const int kb = kIbKbPerWave * wave + k;
@@ -434,6 +479,7 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
   // Every phase's VALU work is independent of its MFMAs, so the two overlap
   // within the wave, and only 4 accumulator tiles are ever live.
   uint32_t ld_m = 0u, ld_info = 0u;  // list entry ld_i, read one step ahead
+  int ld_r0 = 0;
   uint32_t cur_info = 0u;            // list entry i
   uint32_t prev_info = 0u;           // list entry i-1 (no close bit before step 0)
   Acc lag2, lag3;                    // tiles 2,3 of entry i-1
@@ -442,11 +488,12 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
   // Step i multiplies buffer `cur` (entry i) and requests entry
   // i + kIbBufs - 1 into buffer `ahead` (the one entry i-1 used).
   auto step = [&](int i, const u32x4* cur, u32x4* ahead) {
-    chunk_load(ahead, (uint32_t)uniform((int)ld_m), (uint32_t)uniform((int)ld_info));
+    chunk_load(ahead, (uint32_t)uniform((int)ld_m), (uint32_t)uniform((int)ld_info), uniform(ld_r0));
     // List entries for the next step, read now so the LDS latency hides
     // behind this step's MFMAs instead of stalling before the barrier.
     ld_m = lst_mask[ld_i];
     ld_info = lst_info[ld_i];
+    if constexpr (kPacked) ld_r0 = lst_row0[ld_i];
     const uint32_t next_info = lst_info[i + 1 < nsteps_pad ? i + 1 : i];
     const uint32_t info = (uint32_t)uniform((int)cur_info);
     const uint32_t pinfo = (uint32_t)uniform((int)prev_info);
@@ -481,12 +528,14 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
   };
 
   if (nsteps_pad > 0) {
-    chunk_load(cbuf0, lst_mask[0], lst_info[0]);         // entry 0
-    chunk_load(cbuf1, lst_mask[ld_i], lst_info[ld_i]);   // entry 1
+    auto row0_at = [&](int i) { return kPacked ? uniform(lst_row0[i]) : 0; };
+    chunk_load(cbuf0, lst_mask[0], lst_info[0], row0_at(0));                // entry 0
+    chunk_load(cbuf1, lst_mask[ld_i], lst_info[ld_i], row0_at(ld_i));       // entry 1
     if constexpr (kIbBufs == 4)
-      chunk_load(cbuf2, lst_mask[ld_i], lst_info[ld_i]); // entry 2
+      chunk_load(cbuf2, lst_mask[ld_i], lst_info[ld_i], row0_at(ld_i));     // entry 2
     ld_m = lst_mask[ld_i];
     ld_info = lst_info[ld_i];
+    if constexpr (kPacked) ld_r0 = lst_row0[ld_i];
     cur_info = lst_info[0];
     dma_barrier<(kIbBufs - 2) * kIbKbPerWave>();  // entry 0 in LDS
     // Every load is unconditional and the buffers rotate statically.
@@ -576,15 +625,26 @@ hipError_t launch_inbatch_mfma(int dtype_bf16, const InBatchArgs& args_in, hipSt
   A.cmask = cmask;
   A.dcount = dcount;
   A.dfirst = dfirst;
-  hipLaunchKernelGGL(inbatch_plan_kernel, dim3((unsigned)((A.Bd + 3) / 4)), dim3(256), 0, stream,
-                     A.dm, A.Bd, A.Td, nch, cmask, dcount, dfirst);
+  if (A.cu)
+    hipLaunchKernelGGL(packed_plan_kernel, dim3((unsigned)((A.Bd + 3) / 4)), dim3(256), 0, stream,
+                       A.cu, A.ntok, A.Bd, A.Td, nch, cmask, dcount, dfirst);
+  else
+    hipLaunchKernelGGL(inbatch_plan_kernel, dim3((unsigned)((A.Bd + 3) / 4)), dim3(256), 0, stream,
+                       A.dm, A.Bd, A.Td, nch, cmask, dcount, dfirst);
   e = hipGetLastError();
   if (e == hipSuccess) {
     const dim3 grid((unsigned)(A.nqb * A.ndb)), block(64 * kIbWaves);
-    if (dtype_bf16)
-      hipLaunchKernelGGL((inbatch_mfma<OpBF16>), grid, block, 0, stream, A);
-    else
-      hipLaunchKernelGGL((inbatch_mfma<OpF16>), grid, block, 0, stream, A);
+    if (A.cu) {
+      if (dtype_bf16)
+        hipLaunchKernelGGL((inbatch_mfma<OpBF16, true>), grid, block, 0, stream, A);
+      else
+        hipLaunchKernelGGL((inbatch_mfma<OpF16, true>), grid, block, 0, stream, A);
+    } else {
+      if (dtype_bf16)
+        hipLaunchKernelGGL((inbatch_mfma<OpBF16, false>), grid, block, 0, stream, A);
+      else
+        hipLaunchKernelGGL((inbatch_mfma<OpF16, false>), grid, block, 0, stream, A);
+    }
     e = hipGetLastError();
   }
   const hipError_t ef = workspace_free(ws, stream);

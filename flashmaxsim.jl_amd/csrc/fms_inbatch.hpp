@@ -10,7 +10,10 @@ struct InBatchArgs {
   const char* Q;       // (Bq, Tq, dim) 16-bit features
   const char* D;       // (Bd, Td, dim)
   const uint8_t* qm;   // (Bq, Tq) nullable
-  const uint8_t* dm;   // (Bd, Td) nullable
+  const uint8_t* dm;   // (Bd, Td) nullable (in-batch only)
+  const int32_t* cu = nullptr;  // packed documents: (Bd + 1,) 1-based CSR over D (ntok
+                                // rows); nullptr = the in-batch layout.  Td is then max_len.
+  int64_t ntok = 0;
   float* S;            // (Bq, Bd): S[i*Bd + j] = MaxSim(Q_i, D_j)
   int32_t* args;       // (Bq, Bd, Tq) nullable
   int Bq, Bd, Tq, Td;
@@ -27,7 +30,9 @@ struct InBatchArgs {
 // dim == 128, 1 <= Tq <= 32, 16-byte aligned features.
 bool inbatch_mfma_supported(int64_t dim, int64_t Tq, int64_t Td, const void* Q, const void* D);
 // Runs the plan kernel (per-document chunk masks, in a workspace from the
-// library pool) and the in-batch kernel on `stream`.
+// library pool) and the in-batch kernel on `stream`.  With args.cu set the
+// documents are PackedSeq token ranges (every row valid, no dmask): the
+// multi-query packed scan.
 hipError_t launch_inbatch_mfma(int dtype_bf16, const InBatchArgs& args, hipStream_t stream);
 
 }  // namespace fms

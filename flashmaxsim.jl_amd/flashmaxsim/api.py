@@ -8,6 +8,8 @@ Argument forms (Julia shapes in brackets; torch shapes are reversed):
     maxsim(Q, D[, qmask, dmask], InBatch())      in-batch      -> (Bq, Bd)  [Julia (Bd, Bq)]
     maxsim(Q, gallery, idxs[, qmask, dmask])     candidates    -> (B, C)    [Julia (C, B)]
     maxsim(q, P::PackedSeq[, qmask])             packed        -> (B,)
+    maxsim(Q, P::PackedSeq[, qmask])             packed, nq queries in one pass (extension)
+                                                               -> (nq, B)   [Julia (B, nq)]
     maxsim(Qp::PackedSeq, Dp::PackedSeq)         varlen        -> (N,)
     maxsim(q, d::Int8Index[, qmask, dmask])      INT8 pair     -> (1,)
     maxsim(Q, D::Int8Index[, qmask, dmask])      INT8 paired   -> (B,)
@@ -132,6 +134,9 @@ def maxsim(*args, neg=None, normalize=None, backward=None):
     # ---- packed ----
     if isinstance(b, PackedSeq):
         qmask = rest[0] if rest else None
+        if a.dim() == 3:  # several queries in one pass (extension): (nq, B) scores
+            S, _ = F.packed_multi_forward(a, b, qmask, cfg.neg)
+            return F.length_normalize(S, qmask, a.shape[1]) if cfg.normalize else S
         scores, _ = F.packed_forward(a, b, qmask, cfg.neg)
         return F.packed_finalize(scores, qmask, a.shape[0], cfg.normalize)
 

@@ -16,6 +16,7 @@ package (Julia ``(dim, T, B)`` == torch ``(B, T, dim)``).
 | launch_int8_pair_scan     | launch_int8_pair_scan!   (quant.jl:139-154)          |
 | launch_int8_paired_scan   | launch_int8_paired_scan! (quant.jl:199-217)          |
 | launch_int8_candidates_scan | (no reference method; candidate conventions)    |
+| launch_packed_multi_scan  | (no reference method; nq packed scans in one pass) |
 | tensor_cores_active       | tensor_cores_active      (ka.jl:71)                  |
 | pair_apply_pullback       | pair_apply_pullback!     (backward_pair.jl:73-87)    |
 | paired_apply_pullback     | paired_apply_pullback!   (backward_layouts.jl:45-60) |
@@ -165,6 +166,21 @@ def launch_packed_scan(args, partial, q, tokens, cu, qmask, scores=None):
         dtype_code(q), ptr(args), ptr(partial), ptr(q), ptr(tokens), ptr(cu), ptr(_mask(qmask)),
         dim, Tq, B, tokens.shape[0], ptr(scores), stream_handle(dev))
     _lib.check(st, "launch_packed_scan")
+
+
+def launch_packed_multi_scan(args, scores, Q, tokens, cu, qmask, max_len):
+    """nq queries Q (nq, Tq, dim) against one PackedSeq in one pass (no reference
+    method: the reference scores one query per call).  scores (nq, B) [Julia (B, nq)],
+    args (nq, B, Tq) nullable."""
+    dev = require_device(args, scores, Q, tokens, cu, qmask)
+    nq, Tq, dim = Q.shape
+    B = cu.shape[0] - 1
+    if cu.dtype != torch.int32:
+        raise ArgumentError("PackedSeq cu must be Int32 on device")
+    st = _lib.lib().fms_launch_packed_multi_scan(
+        dtype_code(Q), ptr(args), ptr(scores), ptr(Q), ptr(tokens), ptr(cu), ptr(_mask(qmask)),
+        dim, Tq, nq, B, tokens.shape[0], int(max_len), stream_handle(dev))
+    _lib.check(st, "launch_packed_multi_scan")
 
 
 def launch_varlen_scan(args, partial, Qp, Dp, cu_q, cu_d, scores=None):

@@ -159,6 +159,30 @@ def packed_forward(q, P: PackedSeq, qmask=None, neg=None):
     return scores, args
 
 
+def packed_multi_forward(Q, P: PackedSeq, qmask=None, neg=None):
+    """nq queries against one PackedSeq in one pass: (S (nq,B), args (nq,B,Tq)).
+
+    No reference counterpart (the reference's packed_forward takes one query,
+    packed.jl:191-202); row i equals packed_forward(Q[i], P, qmask[i]) within
+    the score tolerance.  Each document is read once per block of 32 queries
+    (the in-batch MFMA kernel over CSR documents)."""
+    boundary.require_device(Q, P.tokens, P.cu, qmask)
+    if Q.dim() != 3:
+        raise DimensionMismatch("multi-query packed scan takes Q (nq, Tq, dim)")
+    nq, Tq, dim = Q.shape
+    if P.tokens.shape[1] != dim:
+        raise DimensionMismatch("feature dim")
+    if qmask is not None and tuple(qmask.shape) != (nq, Tq):
+        raise DimensionMismatch("qmask")
+    B = P.nseq()
+    S = _zeros(Q, SCORE_DTYPE, nq, B)
+    args = _zeros(Q, torch.int32, nq, B, Tq)
+    if nq == 0 or B == 0:
+        return S, args
+    boundary.launch_packed_multi_scan(args, S, Q, P.tokens, P.cu, qmask, P.max_len)
+    return S, args
+
+
 def varlen_forward(Qp: PackedSeq, Dp: PackedSeq, neg=None):
     """varlen_forward_ka (packed.jl:274-284): (scores (N,), args (N,max_q))."""
     boundary.require_device(Qp.tokens, Dp.tokens, Qp.cu, Dp.cu)

@@ -101,6 +101,29 @@ def rrule(cfg, *args):
             return _pad((dQ, dD), nargs)
         return y, pullback
 
+    # ---- several queries against one PackedSeq (extension): per-query pullbacks ----
+    if isinstance(b, PackedSeq) and a.dim() == 3:
+        qmask = rest[0] if rest else None
+        S, tape = F.packed_multi_forward(a, b, qmask, cfg.neg)
+        nq, Tq = a.shape[0], a.shape[1]
+        inv = _inv_counts(qmask, nq, Tq, a.device) if norm else None
+        y = S * inv[:, None] if norm else S
+        T = a.dtype
+
+        def pullback(delta):
+            dh = _cotangent(delta, y).to(T)
+            dQ = torch.empty_like(a)
+            dP = None
+            for i in range(nq):
+                qi = None if qmask is None else qmask[i].contiguous()
+                iv = None if inv is None else inv[i:i + 1].to(T)
+                dq, dp = BW.packed_pullback(dh[i].contiguous(), a[i], b, qi, tape[i].contiguous(),
+                                            iv, mode)
+                dQ[i] = dq
+                dP = dp if dP is None else dP + dp
+            return _pad((dQ, dP), nargs)
+        return y, pullback
+
     # ---- packed (rrule.jl:119-130) ----
     if isinstance(b, PackedSeq):
         qmask = rest[0] if rest else None

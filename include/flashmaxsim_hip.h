@@ -157,6 +157,26 @@ fms_status fms_launch_packed_scan(int32_t dtype, int32_t* args, float* partial,
                                   float* scores, void* stream);
 
 /*
+ * Multi-query packed scan (no reference counterpart: the reference scores one
+ * query per `maxsim(q, P::PackedSeq)` call, packed.jl:178-210).  Scores nq
+ * queries against every document of one PackedSeq in a single pass, reading
+ * each document once for a block of 32 queries instead of once per query.
+ * Q (dim,Tq,nq), tokens (dim,ntokens), cu (B+1,) 1-based, qmask (Tq,nq)
+ * nullable; scores (B,nq) receives S[b, i] = Sigma_t of query i against
+ * document b (required); args (Tq,B,nq) nullable, tapes as in
+ * fms_launch_packed_scan.  max_len >= every document's length (PackedSeq's
+ * max_len; longer documents are clamped to it).  f16/bf16 with dim = 128,
+ * Tq <= 32 and max_len <= 2048 run on MFMA; other shapes make one packed
+ * scan per query.  Row i of the result equals fms_launch_packed_scan of
+ * query i within the score tolerance (tapes equal except at near-ties).
+ */
+fms_status fms_launch_packed_multi_scan(int32_t dtype, int32_t* args, float* scores,
+                                        const void* Q, const void* tokens, const int32_t* cu,
+                                        const uint8_t* qmask, int64_t dim, int64_t Tq, int64_t nq,
+                                        int64_t B, int64_t ntokens, int64_t max_len,
+                                        void* stream);
+
+/*
  * Varlen scan: N ragged (query, document) pairs.  Replaces
  * launch_varlen_scan!(backend, args, partial, Qp, Dp, cu_q, cu_d)
  * (src/packed.jl:298-314; CUDA override ext/FlashMaxSimCUDAExt.jl:98-110).

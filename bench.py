@@ -452,6 +452,15 @@ def run_c4mq(args, torch, fm, boundary, dev):
         a, b = S[int(i)][sel].double(), s1[sel].double()
         worst = max(worst, float(((a - b).abs() / b.abs().clamp(min=1e-3)).max()))
     res["check"] = {"vs": "single-query packed scan", "max_rel_err": worst, "ok": worst < 2e-3}
+    # retrieval's last step: the best 100 documents of every query (fms_topk), timed apart
+    k = 100
+    _, tk_ms = timed_steps(torch, lambda: fm.topk(S, k), max(args.steps, 10), 3)
+    v, i = fm.topk(S, k)
+    best = S.gather(1, (i[:, :1] - 1).long())[:, 0]
+    tk_avg = sum(tk_ms) / len(tk_ms)
+    res["topk"] = {"k": k, "ms_per_call": round(tk_avg, 4),
+                   "score_bytes_GBps": round(S.numel() * 4 / (tk_avg / 1e3) / 1e9, 1),
+                   "ok": bool(torch.equal(v[:, 0], S.max(1).values) and torch.equal(best, v[:, 0]))}
     return res
 
 
@@ -531,6 +540,8 @@ def main():
     }
     if "check" in r:
         out["parity_check"] = r["check"]
+    if "topk" in r:
+        out["topk"] = r["topk"]
     if "gather_bytes" in r:
         out["roofline"]["gather_bytes"] = r["gather_bytes"]
         out["roofline"]["gather_GBps"] = round(r["gather_bytes"] / avg_launch_s / 1e9, 1)

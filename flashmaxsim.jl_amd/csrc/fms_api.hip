@@ -16,6 +16,7 @@
 #include "fms_group.hpp"
 #include "fms_inbatch.hpp"
 #include "fms_misc.hpp"
+#include "fms_topk.hpp"
 #include "fms_scan_decl.hpp"
 
 #define FMS_VERSION_STRING "flashmaxsim-hip 0.1.0 (gfx950)"
@@ -504,6 +505,15 @@ fms_status fms_varlen_normalize(float* scores, const int32_t* cu_q, int64_t N, v
   if (N == 0) return FMS_OK;
   if (!scores || !cu_q) return FMS_EINVAL;
   return from_hip(varlen_normalize(scores, cu_q, N, as_stream(stream)));
+}
+
+fms_status fms_topk(const float* scores, int64_t nrows, int64_t ncols, int64_t k, float* vals,
+                    int32_t* idx, void* stream) {
+  if (nrows < 0 || ncols < 0 || k < 0 || k > ncols) return FMS_EINVAL;
+  if (ncols > INT32_MAX || nrows > (int64_t)UINT32_MAX || k > kTopkMaxK) return FMS_EUNSUPPORTED;
+  if (nrows == 0 || k == 0) return FMS_OK;
+  if (!scores || !vals || !idx) return FMS_EINVAL;
+  return from_hip(topk_rows(scores, nrows, ncols, (int)k, vals, idx, as_stream(stream)));
 }
 
 fms_status fms_debug_mfma_layout(float* out, int32_t dtype_or_int8, void* stream) {

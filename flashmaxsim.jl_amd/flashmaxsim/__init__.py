@@ -21,7 +21,7 @@ from .boundary import (inbatch_device_scan, launch_candidates_scan, launch_int8_
 from .errors import ArgumentError, DimensionMismatch, HIPError, UnsupportedError
 from .forward import (candidates_forward, inbatch_forward, int8_candidates_forward,
                       int8_pair_forward, int8_paired_forward, packed_forward,
-                      packed_multi_forward, paired_forward, pair_forward, varlen_forward)
+                      packed_multi_forward, paired_forward, pair_forward, topk, varlen_forward)
 from .packed import PackedSeq, nseq, pack_docs, pack_pairs
 from .quant import Int8Index, dequant_int8, quantize_int8_symmetric
 from .rrule import MaxSimFunction, rrule
@@ -32,7 +32,7 @@ __all__ = [
     "Int8Index", "quantize_int8_symmetric", "dequant_int8",
     "pair_forward", "paired_forward", "inbatch_forward", "candidates_forward",
     "packed_forward", "packed_multi_forward", "varlen_forward", "int8_pair_forward", "int8_paired_forward",
-    "int8_candidates_forward",
+    "int8_candidates_forward", "topk",
     "pair_pullback", "paired_pullback", "inbatch_pullback", "candidates_pullback",
     "packed_pullback", "varlen_pullback", "rrule", "MaxSimFunction",
     "launch_pair_scan", "launch_paired_scan", "launch_candidates_scan", "inbatch_device_scan",

@@ -17,6 +17,7 @@ package (Julia ``(dim, T, B)`` == torch ``(B, T, dim)``).
 | launch_int8_paired_scan   | launch_int8_paired_scan! (quant.jl:199-217)          |
 | launch_int8_candidates_scan | (no reference method; candidate conventions)    |
 | launch_packed_multi_scan  | (no reference method; nq packed scans in one pass) |
+| topk_rows                 | (no reference method; the caller's partialsortperm) |
 | tensor_cores_active       | tensor_cores_active      (ka.jl:71)                  |
 | pair_apply_pullback       | pair_apply_pullback!     (backward_pair.jl:73-87)    |
 | paired_apply_pullback     | paired_apply_pullback!   (backward_layouts.jl:45-60) |
@@ -181,6 +182,17 @@ def launch_packed_multi_scan(args, scores, Q, tokens, cu, qmask, max_len):
         dtype_code(Q), ptr(args), ptr(scores), ptr(Q), ptr(tokens), ptr(cu), ptr(_mask(qmask)),
         dim, Tq, nq, B, tokens.shape[0], int(max_len), stream_handle(dev))
     _lib.check(st, "launch_packed_multi_scan")
+
+
+def topk_rows(vals, idx, scores, k):
+    """k best entries of every row of scores (nrows, ncols) fp32 [Julia (ncols, nrows),
+    one column per query]: vals (nrows, k) descending, idx (nrows, k) 1-based int32.
+    No reference method (ranking is the caller's partialsortperm)."""
+    dev = require_device(vals, idx, scores)
+    nrows, ncols = scores.shape
+    st = _lib.lib().fms_topk(ptr(scores), nrows, ncols, int(k), ptr(vals), ptr(idx),
+                             stream_handle(dev))
+    _lib.check(st, "topk")
 
 
 def launch_varlen_scan(args, partial, Qp, Dp, cu_q, cu_d, scores=None):

@@ -16,7 +16,7 @@ from __future__ import annotations
 import torch
 
 from . import boundary
-from .errors import DimensionMismatch
+from .errors import ArgumentError, DimensionMismatch
 from .packed import PackedSeq
 from .quant import Int8Index, quantize_int8_symmetric, require_int8_index
 
@@ -181,6 +181,36 @@ def packed_multi_forward(Q, P: PackedSeq, qmask=None, neg=None):
         return S, args
     boundary.launch_packed_multi_scan(args, S, Q, P.tokens, P.cu, qmask, P.max_len)
     return S, args
+
+
+def topk(scores: torch.Tensor, k: int):
+    """The k best scores of every row: (vals, idx), each (..., k), idx 1-based.
+
+    No reference counterpart: it is what a retrieval caller does with the
+    score matrix (``partialsortperm(S[:, i], 1:k; rev = true)`` per query in
+    the reference's column-major terms, README.md:132).  ``scores`` is fp32
+    of shape (ncols,) or (nrows, ncols) -- one row per query, as
+    ``packed_multi_forward`` and ``inbatch_forward`` return them.  Rows are
+    ranked descending by Julia's isless (NaN first, +0.0 before -0.0), equal
+    scores by smaller index.  1 <= k <= 1024 and k <= ncols.
+    """
+    boundary.require_device(scores)
+    if scores.dtype != SCORE_DTYPE:
+        raise ArgumentError("topk takes fp32 scores")
+    if scores.dim() not in (1, 2):
+        raise DimensionMismatch("topk takes a score vector or a (rows, columns) matrix")
+    S2 = scores.reshape(1, -1) if scores.dim() == 1 else scores
+    S2 = S2.contiguous()
+    nrows, ncols = S2.shape
+    if k < 0 or k > ncols:
+        raise ArgumentError(f"topk: k = {k} outside 0..{ncols}")
+    vals = torch.empty(nrows, k, dtype=SCORE_DTYPE, device=S2.device)
+    idx = torch.empty(nrows, k, dtype=torch.int32, device=S2.device)
+    if nrows and k:
+        boundary.topk_rows(vals, idx, S2, k)
+    if scores.dim() == 1:
+        return vals[0], idx[0]
+    return vals, idx
 
 
 def varlen_forward(Qp: PackedSeq, Dp: PackedSeq, neg=None):

@@ -25,6 +25,9 @@
 # and additionally candidates_forward_ka (src/forward_layouts.jl:272-290), so
 # the candidate layout uses the library's fused Σ_t + `neg` epilogue instead
 # of the separate `sum(partial; dims=1)` and `ifelse.` kernels.
+# Two functions have no reference method and are called through the
+# extension module: packed_multi_scan (nq queries against one PackedSeq in
+# one pass) and topk (the k best scores of every query column).
 #
 # Arrays are passed as raw device pointers in Julia's own column-major
 # layout, which is the layout the C ABI documents; nothing is copied or
@@ -304,6 +307,53 @@ for M in (FlashMaxSim.AtomicUnified, FlashMaxSim.InvGrid)
             dQ, dD
         end
     end
+end
+
+# ---- extensions without a reference method -------------------------------------
+# Called as FlashMaxSimHIPExt.packed_multi_scan(Q, P) and
+# FlashMaxSimHIPExt.topk(S, k) (Base.get_extension(FlashMaxSim, :FlashMaxSimHIPExt)).
+
+"""
+    packed_multi_scan(Q::ROCArray{T,3}, P::PackedSeq; qmask = nothing) -> (S, args)
+
+nq queries `Q (dim, Tq, nq)` against every document of `P` in one pass: `S (B, nq)`
+Float32 and the 1-based document-local tape `args (Tq, B, nq)`.  Column i equals
+`maxsim(Q[:, :, i], P, qmask[:, i])` unnormalised (src/packed.jl:178-210) within the
+score tolerance.
+"""
+function packed_multi_scan(Q::ROCArray{T,3}, P::FlashMaxSim.PackedSeq;
+                           qmask = nothing) where {T<:FloatFeature}
+    dim, Tq, nq = size(Q)
+    B = length(P.cu) - 1
+    S = AMDGPU.zeros(Float32, B, nq)
+    args = AMDGPU.zeros(Int32, Tq, B, nq)
+    (nq == 0 || B == 0) && return S, args
+    check(ccall((:fms_launch_packed_multi_scan, libfms), Int32,
+                (Int32, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid},
+                 Int64, Int64, Int64, Int64, Int64, Int64, Ptr{Cvoid}),
+                dtype_code(T), dptr(args), dptr(S), dptr(Q), dptr(P.tokens), dptr(P.cu),
+                qmask === nothing ? C_NULL : dptr(qmask), dim, Tq, nq, B,
+                size(P.tokens, 2), P.max_len, stream_ptr()),
+          "multi-query packed scan")
+    S, args
+end
+
+"""
+    topk(S::ROCMatrix{Float32}, k) -> (vals, idx)
+
+The k best scores of every column of `S` (one column per query): `vals (k, ncols)`
+descending, `idx (k, ncols)` 1-based row indices -- `partialsortperm(S[:, i], 1:k;
+rev = true)` with a stable sort, for every column in one launch.  1 <= k <= 1024.
+"""
+function topk(S::ROCMatrix{Float32}, k::Integer)
+    n, ncol = size(S)
+    vals = AMDGPU.zeros(Float32, k, ncol)
+    idx = AMDGPU.zeros(Int32, k, ncol)
+    check(ccall((:fms_topk, libfms), Int32,
+                (Ptr{Cvoid}, Int64, Int64, Int64, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}),
+                dptr(S), ncol, n, k, dptr(vals), dptr(idx), stream_ptr()),
+          "topk")
+    vals, idx
 end
 
 end # module

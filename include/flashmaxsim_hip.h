@@ -157,6 +157,21 @@ fms_status fms_launch_packed_scan(int32_t dtype, int32_t* args, float* partial,
                                   float* scores, void* stream);
 
 /*
+ * Per-row top-k of an fp32 score matrix (no reference counterpart: ranking is
+ * the caller's job in the reference, README.md:132, e.g.
+ * partialsortperm(scores[:, i], 1:k; rev = true)).  scores is (ncols, nrows)
+ * column-major -- one column per query, as fms_launch_packed_multi_scan and
+ * fms_inbatch_device_scan write them; vals (k, nrows) receives each column's
+ * k largest scores in descending order, idx (k, nrows) their 1-based row
+ * indices.  Order: Julia's isless reversed (NaN first, +0.0 before -0.0),
+ * equal scores by smaller index -- a stable reverse sort.  1 <= k <= 1024
+ * (larger k: FMS_EUNSUPPORTED); k > ncols is FMS_EINVAL (a BoundsError in
+ * partialsortperm).  One 1024-thread workgroup per column, no workspace.
+ */
+fms_status fms_topk(const float* scores, int64_t nrows, int64_t ncols, int64_t k, float* vals,
+                    int32_t* idx, void* stream);
+
+/*
  * Multi-query packed scan (no reference counterpart: the reference scores one
  * query per `maxsim(q, P::PackedSeq)` call, packed.jl:178-210).  Scores nq
  * queries against every document of one PackedSeq in a single pass, reading

@@ -110,6 +110,8 @@ def _declare(L):
     L.fmso_varlen_backward.restype = None
     L.fmso_varlen_backward.argtypes = [_int, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64,
                                        _i64, _p, _p]
+    L.fmso_topk.restype = None
+    L.fmso_topk.argtypes = [_p, _i64, _i64, _i64, _p, _p]
 
 
 def max_threads() -> int:
@@ -446,3 +448,17 @@ def varlen_backward(Qt, Dt, cu_q, cu_d, args, Delta, inv_n=None, bf16=False):
     lib().fmso_varlen_backward(code, _ptr(Qt), _ptr(Dt), _ptr(cu_q), _ptr(cu_d), _ptr(args),
                                _ptr(De), _ptr(iv), dim, max_q, N, nq, nd, _ptr(dQ), _ptr(dD))
     return dQ, dD
+
+
+def topk(scores, k):
+    """Per-row top-k (no reference counterpart; the caller's stable
+    partialsortperm(rev = true) in the reference, README.md:132).  scores
+    (nrows, ncols) fp32 -> (vals (nrows, k) fp32, idx (nrows, k) int32 1-based)."""
+    S = _c(scores, np.float32)
+    if S.ndim == 1:
+        S = S.reshape(1, -1)
+    nrows, ncols = S.shape
+    vals = np.zeros((nrows, k), np.float32)
+    idx = np.zeros((nrows, k), np.int32)
+    lib().fmso_topk(_ptr(S), nrows, ncols, k, _ptr(vals), _ptr(idx))
+    return vals, idx

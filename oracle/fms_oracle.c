@@ -730,3 +730,47 @@ void fmso_varlen_backward(int dtype, const void* Qt, const void* Dt, const int32
                           dz - da, dQ + qa * dim, dD + da * dim);
     }
 }
+
+/* ---- per-row top-k (no reference counterpart) ------------------------------
+ *
+ * What a retrieval caller does with a score column in the reference
+ * (README.md:132: ranking is the caller's job), i.e.
+ * partialsortperm(scores[:, i], 1:k; rev = true) with a stable sort: the order
+ * is Base.isless reversed, equal scores by smaller index.  isless on floats:
+ * NaN is above everything (every NaN equal), -0.0 below +0.0, otherwise <.
+ * Restated with a comparison sort (qsort on (value, index)), not with the
+ * device kernel's radix keys.
+ */
+typedef struct { float v; int64_t i; } fmso_scored;
+
+static int julia_isless_f32(float a, float b) {
+    if (isnan(a)) return 0;
+    if (isnan(b)) return 1;
+    if (a < b) return 1;
+    if (a > b) return 0;
+    return signbit(a) && !signbit(b); /* -0.0 < +0.0 */
+}
+
+static int topk_cmp(const void* pa, const void* pb) {
+    const fmso_scored* a = (const fmso_scored*)pa;
+    const fmso_scored* b = (const fmso_scored*)pb;
+    if (julia_isless_f32(b->v, a->v)) return -1; /* a ranks first */
+    if (julia_isless_f32(a->v, b->v)) return 1;
+    return a->i < b->i ? -1 : (a->i > b->i ? 1 : 0);
+}
+
+/* scores (nrows, ncols) row-major; vals/idx (nrows, k), idx 1-based. 0 <= k <= ncols. */
+void fmso_topk(const float* scores, int64_t nrows, int64_t ncols, int64_t k, float* vals,
+               int32_t* idx) {
+    int64_t r, j;
+    fmso_scored* buf = (fmso_scored*)malloc(sizeof(fmso_scored) * (size_t)(ncols > 0 ? ncols : 1));
+    for (r = 0; r < nrows; ++r) {
+        for (j = 0; j < ncols; ++j) { buf[j].v = scores[r * ncols + j]; buf[j].i = j; }
+        qsort(buf, (size_t)ncols, sizeof(fmso_scored), topk_cmp);
+        for (j = 0; j < k; ++j) {
+            vals[r * k + j] = buf[j].v;
+            idx[r * k + j] = (int32_t)(buf[j].i + 1);
+        }
+    }
+    free(buf);
+}

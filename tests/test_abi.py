@@ -89,6 +89,13 @@ EINVAL, EUNSUP, OK = _lib.FMS_EINVAL, _lib.FMS_EUNSUPPORTED, _lib.FMS_OK
     (lambda L: L.fms_packed_pullback(0, None, None, None, None, None, None, None, None, None, -1, 4, 3, 10, None), EINVAL),
     (lambda L: L.fms_varlen_pullback(0, 1, 1, 1, 1, None, None, 1, 1, None, 8, 4, 3, 10, 10, None), EINVAL),
     (lambda L: L.fms_varlen_pullback(0, None, None, None, None, None, None, None, None, None, 8, 4, 3, 0, 0, None), OK),
+    # top-k: k beyond the row, k beyond the LDS sort, empty, NULL buffers
+    (lambda L: L.fms_topk(None, 2, 5, 6, None, None, None), EINVAL),
+    (lambda L: L.fms_topk(None, 2, 5000, 1025, None, None, None), EUNSUP),
+    (lambda L: L.fms_topk(None, 0, 5, 3, None, None, None), OK),
+    (lambda L: L.fms_topk(None, 2, 5, 0, None, None, None), OK),
+    (lambda L: L.fms_topk(None, 2, 5, 3, None, None, None), EINVAL),
+    (lambda L: L.fms_topk(None, -1, 5, 3, None, None, None), EINVAL),
 ])
 def test_validation_status_codes(call, expect):
     assert call(_lib.lib()) == expect

@@ -63,24 +63,28 @@ bool vec_ok(int esz, int64_t dim, std::initializer_list<const void*> ptrs) {
 // Launches the scan for a float feature type (dtype already validated).
 template <class L>
 hipError_t launch_float(int32_t dtype, const L& lay, int dim, int rows, int64_t npairs,
-                        int32_t* args, float* partial, float* scores, float neg, bool vec,
-                        hipStream_t st) {
+                        int32_t* args, float* partial, float* scores, float neg, bool norm,
+                        bool vec, hipStream_t st) {
   switch (dtype) {
     case FMS_F16:
-      return launch_scan<OpF16, L>(lay, dim, rows, npairs, args, partial, scores, neg, vec, false, st);
+      return launch_scan<OpF16, L>(lay, dim, rows, npairs, args, partial, scores, neg, norm, vec,
+                                   false, st);
     case FMS_BF16:
-      return launch_scan<OpBF16, L>(lay, dim, rows, npairs, args, partial, scores, neg, vec, false, st);
+      return launch_scan<OpBF16, L>(lay, dim, rows, npairs, args, partial, scores, neg, norm, vec,
+                                    false, st);
     default:
-      return launch_scan<OpF32, L>(lay, dim, rows, npairs, args, partial, scores, neg, vec, false, st);
+      return launch_scan<OpF32, L>(lay, dim, rows, npairs, args, partial, scores, neg, norm, vec,
+                                   false, st);
   }
 }
 
 template <class L>
 fms_status run_float(int32_t dtype, const L& lay, int dim, int rows, int64_t npairs,
-                     int32_t* args, float* partial, float* scores, float neg, bool vec,
+                     int32_t* args, float* partial, float* scores, float neg, bool norm, bool vec,
                      hipStream_t st) {
   if (elem_bytes(dtype) == 0) return FMS_EUNSUPPORTED;
-  return from_hip(launch_float(dtype, lay, dim, rows, npairs, args, partial, scores, neg, vec, st));
+  return from_hip(
+      launch_float(dtype, lay, dim, rows, npairs, args, partial, scores, neg, norm, vec, st));
 }
 
 // Candidate pair grouping (fms_candidates_grouping): 0 auto, 1 always, 2 never.
@@ -198,10 +202,10 @@ int fms_arch_supported(void) {
 fms_status fms_launch_paired_scan(int32_t dtype, int32_t* args, float* partial, const void* Q,
                                   const void* D, const uint8_t* qmask, const uint8_t* dmask,
                                   int64_t dim, int64_t Tq, int64_t Td, int64_t B, float* scores,
-                                  void* stream) {
+                                  int32_t normalize, void* stream) {
   const int esz = elem_bytes(dtype);
   if (esz == 0) return FMS_EUNSUPPORTED;
-  if (dim < 0 || Tq < 0 || Td < 0 || B < 0) return FMS_EINVAL;
+  if (dim < 0 || Tq < 0 || Td < 0 || B < 0 || (normalize & ~1)) return FMS_EINVAL;
   if (!seq_ok(Tq, dim, esz) || !seq_ok(Td, dim, esz)) return FMS_EUNSUPPORTED;
   if (B == 0 || (Tq == 0 && !scores)) return FMS_OK;
   if ((Tq * dim > 0 && !Q) || (Td * dim > 0 && !D)) return FMS_EINVAL;
@@ -216,15 +220,16 @@ fms_status fms_launch_paired_scan(int32_t dtype, int32_t* args, float* partial, 
   lay.dbytes = Td * dim * esz;
   lay.Tq = (int)Tq;
   lay.Td = (int)Td;
-  return run_float(dtype, lay, (int)dim, (int)Tq, B, args, partial, scores, 0.0f,
+  return run_float(dtype, lay, (int)dim, (int)Tq, B, args, partial, scores, 0.0f, normalize != 0,
                    vec_ok(esz, dim, {Q, D}), as_stream(stream));
 }
 
 fms_status fms_launch_pair_scan(int32_t dtype, int32_t* argmax_u, float* partial, const void* q,
                                 const void* d, const uint8_t* qmask, const uint8_t* dmask,
-                                int64_t dim, int64_t Tq, int64_t Td, float* score, void* stream) {
+                                int64_t dim, int64_t Tq, int64_t Td, float* score,
+                                int32_t normalize, void* stream) {
   return fms_launch_paired_scan(dtype, argmax_u, partial, q, d, qmask, dmask, dim, Tq, Td, 1,
-                                score, stream);
+                                score, normalize, stream);
 }
 
 fms_status fms_launch_candidates_scan(int32_t dtype, int32_t* args, float* partial,
@@ -232,10 +237,11 @@ fms_status fms_launch_candidates_scan(int32_t dtype, int32_t* args, float* parti
                                       int32_t idx_bytes, const uint8_t* qmask,
                                       const uint8_t* dmask, int64_t dim, int64_t Tq, int64_t B,
                                       int64_t Td, int64_t N, int64_t C, float* scores, float neg,
-                                      void* stream) {
+                                      int32_t normalize, void* stream) {
   const int esz = elem_bytes(dtype);
   if (esz == 0) return FMS_EUNSUPPORTED;
-  if (dim < 0 || Tq < 0 || Td < 0 || B < 0 || N < 0 || C < 0) return FMS_EINVAL;
+  if (dim < 0 || Tq < 0 || Td < 0 || B < 0 || N < 0 || C < 0 || (normalize & ~1))
+    return FMS_EINVAL;
   if (idx_bytes != 4 && idx_bytes != 8) return FMS_EINVAL;
   if (!seq_ok(Tq, dim, esz) || !seq_ok(Td, dim, esz)) return FMS_EUNSUPPORTED;
   if (C == 0 || B == 0 || (Tq == 0 && !scores)) return FMS_OK;
@@ -258,17 +264,18 @@ fms_status fms_launch_candidates_scan(int32_t dtype, int32_t* args, float* parti
   const bool vec = vec_ok(esz, dim, {Q, gallery});
   const hipStream_t st = as_stream(stream);
   return run_candidates(lay, C * B, st, [&](const auto& L) -> hipError_t {
-    return launch_float(dtype, L, (int)dim, (int)Tq, C * B, args, partial, scores, neg, vec, st);
+    return launch_float(dtype, L, (int)dim, (int)Tq, C * B, args, partial, scores, neg,
+                        normalize != 0, vec, st);
   });
 }
 
 fms_status fms_inbatch_device_scan(int32_t dtype, float* S, int32_t* args, const void* Q,
                                    const void* D, const uint8_t* qmask, const uint8_t* dmask,
                                    int64_t dim, int64_t Tq, int64_t Bq, int64_t Td, int64_t Bd,
-                                   void* stream) {
+                                   int32_t normalize, void* stream) {
   const int esz = elem_bytes(dtype);
   if (esz == 0) return FMS_EUNSUPPORTED;
-  if (dim < 0 || Tq < 0 || Td < 0 || Bq < 0 || Bd < 0) return FMS_EINVAL;
+  if (dim < 0 || Tq < 0 || Td < 0 || Bq < 0 || Bd < 0 || (normalize & ~1)) return FMS_EINVAL;
   if (!seq_ok(Tq, dim, esz) || !seq_ok(Td, dim, esz)) return FMS_EUNSUPPORTED;
   if (Bq == 0 || Bd == 0) return FMS_OK;
   if (!S || (Tq * dim > 0 && !Q) || (Td * dim > 0 && !D)) return FMS_EINVAL;
@@ -285,6 +292,7 @@ fms_status fms_inbatch_device_scan(int32_t dtype, float* S, int32_t* args, const
     a.Bd = (int)Bd;
     a.Tq = (int)Tq;
     a.Td = (int)Td;
+    a.norm = normalize;
     return from_hip(launch_inbatch_mfma(dtype == FMS_BF16, a, as_stream(stream)));
   }
   // other shapes / fp32: the per-pair scan over p = j + Bd*i
@@ -299,16 +307,16 @@ fms_status fms_inbatch_device_scan(int32_t dtype, float* S, int32_t* args, const
   lay.Tq = (int)Tq;
   lay.Td = (int)Td;
   return run_float(dtype, lay, (int)dim, (int)Tq, Bq * Bd, args, nullptr, S, 0.0f,
-                   vec_ok(esz, dim, {Q, D}), as_stream(stream));
+                   normalize != 0, vec_ok(esz, dim, {Q, D}), as_stream(stream));
 }
 
 fms_status fms_launch_packed_scan(int32_t dtype, int32_t* args, float* partial, const void* q,
                                   const void* tokens, const int32_t* cu, const uint8_t* qmask,
                                   int64_t dim, int64_t Tq, int64_t B, int64_t ntokens,
-                                  float* scores, void* stream) {
+                                  float* scores, int32_t normalize, void* stream) {
   const int esz = elem_bytes(dtype);
   if (esz == 0) return FMS_EUNSUPPORTED;
-  if (dim < 0 || Tq < 0 || B < 0 || ntokens < 0) return FMS_EINVAL;
+  if (dim < 0 || Tq < 0 || B < 0 || ntokens < 0 || (normalize & ~1)) return FMS_EINVAL;
   // Each document gets its own buffer resource; one longer than 2^31 bytes
   // is truncated to that size on device (LayPacked::get).
   if (!seq_ok(Tq, dim, esz)) return FMS_EUNSUPPORTED;
@@ -322,7 +330,7 @@ fms_status fms_launch_packed_scan(int32_t dtype, int32_t* args, float* partial, 
   lay.ntok = ntokens;
   lay.rowbytes = dim * esz;
   lay.Tq = (int)Tq;
-  return run_float(dtype, lay, (int)dim, (int)Tq, B, args, partial, scores, 0.0f,
+  return run_float(dtype, lay, (int)dim, (int)Tq, B, args, partial, scores, 0.0f, normalize != 0,
                    vec_ok(esz, dim, {q, tokens}), as_stream(stream));
 }
 
@@ -330,10 +338,11 @@ fms_status fms_launch_packed_multi_scan(int32_t dtype, int32_t* args, float* sco
                                         const void* Q, const void* tokens, const int32_t* cu,
                                         const uint8_t* qmask, int64_t dim, int64_t Tq, int64_t nq,
                                         int64_t B, int64_t ntokens, int64_t max_len,
-                                        void* stream) {
+                                        int32_t normalize, void* stream) {
   const int esz = elem_bytes(dtype);
   if (esz == 0) return FMS_EUNSUPPORTED;
-  if (dim < 0 || Tq < 0 || nq < 0 || B < 0 || ntokens < 0 || max_len < 0) return FMS_EINVAL;
+  if (dim < 0 || Tq < 0 || nq < 0 || B < 0 || ntokens < 0 || max_len < 0 || (normalize & ~1))
+    return FMS_EINVAL;
   if (!seq_ok(Tq, dim, esz) || nq > kMaxTokens || B > kMaxTokens) return FMS_EUNSUPPORTED;
   if (nq == 0 || B == 0) return FMS_OK;
   if (!scores || !cu || (Tq * dim > 0 && !Q) || (ntokens * dim > 0 && !tokens)) return FMS_EINVAL;
@@ -353,6 +362,7 @@ fms_status fms_launch_packed_multi_scan(int32_t dtype, int32_t* args, float* sco
     a.Bd = (int)B;
     a.Tq = (int)Tq;
     a.Td = (int)max_len;
+    a.norm = normalize;
     return from_hip(launch_inbatch_mfma(dtype == FMS_BF16, a, st));
   }
   // other shapes / fp32: one packed scan per query
@@ -360,7 +370,7 @@ fms_status fms_launch_packed_multi_scan(int32_t dtype, int32_t* args, float* sco
     const fms_status r = fms_launch_packed_scan(
         dtype, args ? args + i * B * Tq : nullptr, nullptr,
         static_cast<const char*>(Q) + i * Tq * dim * esz, tokens, cu,
-        qmask ? qmask + i * Tq : nullptr, dim, Tq, B, ntokens, scores + i * B, stream);
+        qmask ? qmask + i * Tq : nullptr, dim, Tq, B, ntokens, scores + i * B, normalize, stream);
     if (r != FMS_OK) return r;
   }
   return FMS_OK;
@@ -370,10 +380,11 @@ fms_status fms_launch_varlen_scan(int32_t dtype, int32_t* args, float* partial,
                                   const void* Qtokens, const void* Dtokens, const int32_t* cu_q,
                                   const int32_t* cu_d, int64_t dim, int64_t max_q, int64_t N,
                                   int64_t nq_tokens, int64_t nd_tokens, float* scores,
-                                  void* stream) {
+                                  int32_t normalize, void* stream) {
   const int esz = elem_bytes(dtype);
   if (esz == 0) return FMS_EUNSUPPORTED;
-  if (dim < 0 || max_q < 0 || N < 0 || nq_tokens < 0 || nd_tokens < 0) return FMS_EINVAL;
+  if (dim < 0 || max_q < 0 || N < 0 || nq_tokens < 0 || nd_tokens < 0 || (normalize & ~1))
+    return FMS_EINVAL;
   if (!seq_ok(max_q, dim, esz)) return FMS_EUNSUPPORTED;
   if (N == 0 || (max_q == 0 && !scores)) return FMS_OK;
   if (!cu_q || !cu_d || (nq_tokens * dim > 0 && !Qtokens) || (nd_tokens * dim > 0 && !Dtokens))
@@ -388,7 +399,7 @@ fms_status fms_launch_varlen_scan(int32_t dtype, int32_t* args, float* partial,
   lay.rowbytes = dim * esz;
   lay.max_q = (int)max_q;
   return run_float(dtype, lay, (int)dim, (int)max_q, N, args, partial, scores, 0.0f,
-                   vec_ok(esz, dim, {Qtokens, Dtokens}), as_stream(stream));
+                   normalize != 0, vec_ok(esz, dim, {Qtokens, Dtokens}), as_stream(stream));
 }
 
 fms_status fms_int8_quantize(const float* X, int8_t* codes, float* scales, int64_t dim,
@@ -403,8 +414,8 @@ fms_status fms_launch_int8_paired_scan(int32_t* args, float* partial, const int8
                                        const float* Qs, const int8_t* Dc, const float* Ds,
                                        const uint8_t* qmask, const uint8_t* dmask, int64_t dim,
                                        int64_t Tq, int64_t Td, int64_t B, float* scores,
-                                       void* stream) {
-  if (dim < 0 || Tq < 0 || Td < 0 || B < 0) return FMS_EINVAL;
+                                       int32_t normalize, void* stream) {
+  if (dim < 0 || Tq < 0 || Td < 0 || B < 0 || (normalize & ~1)) return FMS_EINVAL;
   if (!seq_ok(Tq, dim, 4) || !seq_ok(Td, dim, 4)) return FMS_EUNSUPPORTED;
   if (B == 0 || (Tq == 0 && !scores)) return FMS_OK;
   if ((Tq > 0 && (!Qs || (dim > 0 && !Qc))) || (Td > 0 && (!Ds || (dim > 0 && !Dc))))
@@ -423,15 +434,17 @@ fms_status fms_launch_int8_paired_scan(int32_t* args, float* partial, const int8
   const bool vec = vec_ok(1, dim, {Qc, Dc});
   const bool ds_vec = (Td % 4 == 0) && aligned16(Ds);
   return from_hip(launch_scan<OpI8, LayPaired>(lay, (int)dim, (int)Tq, B, args, partial, scores,
-                                               0.0f, vec, ds_vec, as_stream(stream)));
+                                               0.0f, normalize != 0, vec, ds_vec,
+                                               as_stream(stream)));
 }
 
 fms_status fms_launch_int8_pair_scan(int32_t* args, float* partial, const int8_t* qc,
                                      const float* qs, const int8_t* dc, const float* ds,
                                      const uint8_t* qmask, const uint8_t* dmask, int64_t dim,
-                                     int64_t Tq, int64_t Td, float* score, void* stream) {
+                                     int64_t Tq, int64_t Td, float* score, int32_t normalize,
+                                     void* stream) {
   return fms_launch_int8_paired_scan(args, partial, qc, qs, dc, ds, qmask, dmask, dim, Tq, Td, 1,
-                                     score, stream);
+                                     score, normalize, stream);
 }
 
 fms_status fms_launch_int8_candidates_scan(int32_t* args, float* partial, const int8_t* Qc,
@@ -440,8 +453,9 @@ fms_status fms_launch_int8_candidates_scan(int32_t* args, float* partial, const 
                                            const uint8_t* qmask, const uint8_t* dmask,
                                            int64_t dim, int64_t Tq, int64_t B, int64_t Td,
                                            int64_t N, int64_t C, float* scores, float neg,
-                                           void* stream) {
-  if (dim < 0 || Tq < 0 || Td < 0 || B < 0 || N < 0 || C < 0) return FMS_EINVAL;
+                                           int32_t normalize, void* stream) {
+  if (dim < 0 || Tq < 0 || Td < 0 || B < 0 || N < 0 || C < 0 || (normalize & ~1))
+    return FMS_EINVAL;
   if (idx_bytes != 4 && idx_bytes != 8) return FMS_EINVAL;
   if (!seq_ok(Tq, dim, 4) || !seq_ok(Td, dim, 4)) return FMS_EUNSUPPORTED;
   if (C == 0 || B == 0 || (Tq == 0 && !scores)) return FMS_OK;
@@ -468,8 +482,8 @@ fms_status fms_launch_int8_candidates_scan(int32_t* args, float* partial, const 
   const hipStream_t st = as_stream(stream);
   return run_candidates(lay, C * B, st, [&](const auto& L) -> hipError_t {
     typedef typename std::decay<decltype(L)>::type Lay;
-    return launch_scan<OpI8, Lay>(L, (int)dim, (int)Tq, C * B, args, partial, scores, neg, vec,
-                                  ds_vec, st);
+    return launch_scan<OpI8, Lay>(L, (int)dim, (int)Tq, C * B, args, partial, scores, neg,
+                                  normalize != 0, vec, ds_vec, st);
   });
 }
 

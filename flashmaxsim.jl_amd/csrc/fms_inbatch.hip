@@ -577,7 +577,16 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
         out[e] = res_tape[wave][q][jj][t];
       }
     }
-    if (lane < ndoc) A.S[p0 + lane] = res_score[wave][q][lane];
+    // normalize epilogue: 1 / max(valid query tokens, 1) in fp32 (normalize.jl:4-10)
+    float inv = 1.0f;
+    if (A.norm) {
+      const float nf = (float)__builtin_popcountll(__ballot(h == 0 && token_valid(q)));
+      inv = 1.0f / (nf > 1.0f ? nf : 1.0f);
+    }
+    if (lane < ndoc) {
+      const float sc = res_score[wave][q][lane];
+      A.S[p0 + lane] = A.norm ? sc * inv : sc;
+    }
   }
 }
 

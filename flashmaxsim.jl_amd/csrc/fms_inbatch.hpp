@@ -17,6 +17,7 @@ struct InBatchArgs {
   float* S;            // (Bq, Bd): S[i*Bd + j] = MaxSim(Q_i, D_j)
   int32_t* args;       // (Bq, Bd, Tq) nullable
   int Bq, Bd, Tq, Td;
+  int norm = 0;        // S *= 1 / max(valid tokens of query i, 1)
   // filled by the launcher
   int nqb, ndb;        // query blocks, document blocks
   int db;              // documents per block of the uniform partition

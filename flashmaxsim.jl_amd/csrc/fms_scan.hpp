@@ -58,6 +58,7 @@ struct ScanArgs {
   float* partial;   // (rows, npairs) nullable
   float* scores;    // (npairs,) nullable
   float neg;
+  int norm;         // scores *= 1 / max(valid query tokens, 1) (valid pairs only)
 };
 
 template <class Op, int NKB>
@@ -175,10 +176,29 @@ __device__ __forceinline__ float finish_tile(const ScanArgs<L>& A, int64_t out, 
   return half_sum(part);
 }
 
+// 1 / max(n, 1) in fp32, n = the pair's valid query tokens (its qmask count,
+// or all tq tokens without a mask): inv_token_counts (normalize.jl:4-10) and
+// varlen_inv_n_kernel! (kernels_packed.jl:277-282).  Wave-uniform control.
+__device__ __forceinline__ float pair_inv_count(const PairView& v, int lane) {
+  int n = 0;
+  for (int t0 = 0; t0 < v.tq; t0 += 64) {
+    const int t = t0 + lane;
+    const bool ok = t < v.tq && (v.qm == nullptr || v.qm[t] != 0);
+    n += __builtin_popcountll(__ballot(ok));
+  }
+  const float nf = (float)n;
+  return 1.0f / (nf > 1.0f ? nf : 1.0f);
+}
+
+// The pair's score: Σ_t, then the normalize epilogue (length_normalize,
+// normalize.jl:23-25) on valid pairs; an invalid candidate keeps neg
+// (length_normalize_candidates, normalize.jl:37-46).
 template <class L>
-__device__ __forceinline__ void write_score(const ScanArgs<L>& A, int64_t out, bool valid,
-                                            float score, int lane) {
-  if (A.scores && lane == 0) A.scores[out] = valid ? score : A.neg;
+__device__ __forceinline__ void write_score(const ScanArgs<L>& A, const PairView& v, float score,
+                                            int lane) {
+  if (!A.scores) return;
+  if (A.norm && v.valid) score *= pair_inv_count(v, lane);
+  if (lane == 0) A.scores[v.out] = v.valid ? score : A.neg;
 }
 
 // ---- fast kernel ------------------------------------------------------------------
@@ -306,7 +326,7 @@ __global__ void __launch_bounds__(64 * kWaves) scan_fast(const ScanArgs<L> A) {
       mx = -INFINITY;
       slot = -1;
       if (qt == A.nqt - 1) {
-        write_score(A, v.out, v.valid, score, lane);
+        write_score(A, v, score, lane);
         score = 0.0f;
       }
     }
@@ -394,7 +414,7 @@ __global__ void __launch_bounds__(64 * kWaves) scan_generic(const ScanArgs<L> A)
       }
       score += finish_tile(A, v.out, qt, r32, h, tvalid, mx, slot);
     }
-    write_score(A, v.out, v.valid, score, lane);
+    write_score(A, v, score, lane);
   }
 }
 
@@ -422,8 +442,8 @@ inline int pairs_per_wave(int64_t npairs) {
 
 template <class Op, class L>
 hipError_t launch_scan(const L& lay, int dim, int rows, int64_t npairs, int32_t* args,
-                       float* partial, float* scores, float neg, bool vec, bool ds_vec,
-                       hipStream_t stream) {
+                       float* partial, float* scores, float neg, bool norm, bool vec,
+                       bool ds_vec, hipStream_t stream) {
   ScanArgs<L> A;
   A.lay = lay;
   A.dim = dim;
@@ -437,6 +457,7 @@ hipError_t launch_scan(const L& lay, int dim, int rows, int64_t npairs, int32_t*
   A.partial = partial;
   A.scores = scores;
   A.neg = neg;
+  A.norm = norm ? 1 : 0;
   const int64_t waves = (npairs + A.ppw - 1) / A.ppw;
   const dim3 grid((unsigned)((waves + kWaves - 1) / kWaves));
   const dim3 block(64 * kWaves);

@@ -3,11 +3,11 @@
 #include "fms_scan.hpp"
 
 namespace fms {
-template hipError_t launch_scan<OpI8, LayPaired>(const LayPaired&, int, int, int64_t, int32_t*,
-                                                 float*, float*, float, bool, bool, hipStream_t);
-template hipError_t launch_scan<OpI8, LayCand>(const LayCand&, int, int, int64_t, int32_t*,
-                                               float*, float*, float, bool, bool, hipStream_t);
-template hipError_t launch_scan<OpI8, LayCandSorted>(const LayCandSorted&, int, int, int64_t,
-                                                     int32_t*, float*, float*, float, bool, bool,
-                                                     hipStream_t);
+#define FMS_INST(L)                                                                    \
+  template hipError_t launch_scan<OpI8, L>(const L&, int, int, int64_t, int32_t*, float*, \
+                                           float*, float, bool, bool, bool, hipStream_t);
+FMS_INST(LayPaired)
+FMS_INST(LayCand)
+FMS_INST(LayCandSorted)
+#undef FMS_INST
 }  // namespace fms

@@ -175,7 +175,7 @@ __global__ void __launch_bounds__(64 * kWaves) scan_split(const ScanArgs<L> A) {
         mx = -INFINITY;
         slot = -1;
         if (qt == A.nqt - 1) {
-          write_score(A, v.out, v.valid, score, lane);
+          write_score(A, v, score, lane);
           score = 0.0f;
         }
       }

@@ -23,13 +23,14 @@ from .forward import (candidates_forward, inbatch_forward, int8_candidates_forwa
                       int8_pair_forward, int8_paired_forward, packed_forward,
                       packed_multi_forward, paired_forward, pair_forward, topk, varlen_forward)
 from .packed import PackedSeq, nseq, pack_docs, pack_pairs
-from .quant import Int8Index, dequant_int8, quantize_int8_symmetric
+from .quant import (Int8Index, dequant_int8, load_int8_index, quantize_int8_symmetric,
+                    save_int8_index)
 from .rrule import MaxSimFunction, rrule
 
 __all__ = [
     "maxsim", "MaxSim", "InBatch", "AtomicUnified", "InvGrid", "score_eltype", "dot_accum",
     "PackedSeq", "nseq", "pack_docs", "pack_pairs",
-    "Int8Index", "quantize_int8_symmetric", "dequant_int8",
+    "Int8Index", "quantize_int8_symmetric", "dequant_int8", "save_int8_index", "load_int8_index",
     "pair_forward", "paired_forward", "inbatch_forward", "candidates_forward",
     "packed_forward", "packed_multi_forward", "varlen_forward", "int8_pair_forward", "int8_paired_forward",
     "int8_candidates_forward", "topk",

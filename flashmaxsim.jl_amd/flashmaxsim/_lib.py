@@ -32,18 +32,18 @@ SIGNATURES = {
     "fms_status_string": [_i32],
     "fms_arch_supported": [],
     "fms_version": [],
-    "fms_launch_pair_scan": [_i32, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _p],
-    "fms_launch_paired_scan": [_i32, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _p],
+    "fms_launch_pair_scan": [_i32, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _i32, _p],
+    "fms_launch_paired_scan": [_i32, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _i32, _p],
     "fms_launch_candidates_scan": [_i32, _p, _p, _p, _p, _p, _i32, _p, _p, _i64, _i64, _i64,
-                                   _i64, _i64, _i64, _p, _f, _p],
-    "fms_inbatch_device_scan": [_i32, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p],
-    "fms_launch_packed_scan": [_i32, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _p],
-    "fms_launch_varlen_scan": [_i32, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _p],
+                                   _i64, _i64, _i64, _p, _f, _i32, _p],
+    "fms_inbatch_device_scan": [_i32, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _p],
+    "fms_launch_packed_scan": [_i32, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _i32, _p],
+    "fms_launch_varlen_scan": [_i32, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _i32, _p],
     "fms_int8_quantize": [_p, _p, _p, _i64, _i64, _p],
-    "fms_launch_int8_pair_scan": [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _p],
-    "fms_launch_int8_paired_scan": [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _p],
+    "fms_launch_int8_pair_scan": [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _i32, _p],
+    "fms_launch_int8_paired_scan": [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _i32, _p],
     "fms_launch_int8_candidates_scan": [_p, _p, _p, _p, _p, _p, _p, _i32, _p, _p, _i64, _i64,
-                                        _i64, _i64, _i64, _i64, _p, _f, _p],
+                                        _i64, _i64, _i64, _i64, _p, _f, _i32, _p],
     "fms_int8_dots": [_p, _p, _p, _i64, _i64, _i64, _p],
     "fms_length_normalize": [_p, _p, _i64, _i64, _i64, _p, _i32, _i64, _f, _p],
     "fms_varlen_normalize": [_p, _p, _i64, _p],
@@ -53,7 +53,7 @@ SIGNATURES = {
     "fms_debug_cross_lane": [_p, _p],
     "fms_topk": [_p, _i64, _i64, _i64, _p, _p, _p],
     "fms_launch_packed_multi_scan": [_i32, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64,
-                                     _i64, _p],
+                                     _i64, _i32, _p],
     "fms_pair_pullback": [_i32, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p],
     "fms_paired_pullback": [_i32, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p],
     "fms_inbatch_pullback": [_i32, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64,

@@ -128,49 +128,44 @@ def maxsim(*args, neg=None, normalize=None, backward=None):
     if isinstance(a, PackedSeq):
         if not isinstance(b, PackedSeq) or rest:
             raise ArgumentError("varlen maxsim takes two PackedSeq")
-        scores, _ = F.varlen_forward(a, b, cfg.neg)
-        return F.varlen_finalize(scores, a, cfg.normalize)
+        scores, _ = F.varlen_forward(a, b, cfg.neg, cfg.normalize)
+        return scores
 
     # ---- packed ----
     if isinstance(b, PackedSeq):
         qmask = rest[0] if rest else None
         if a.dim() == 3:  # several queries in one pass (extension): (nq, B) scores
-            S, _ = F.packed_multi_forward(a, b, qmask, cfg.neg)
-            return F.length_normalize(S, qmask, a.shape[1]) if cfg.normalize else S
-        scores, _ = F.packed_forward(a, b, qmask, cfg.neg)
-        return F.packed_finalize(scores, qmask, a.shape[0], cfg.normalize)
+            S, _ = F.packed_multi_forward(a, b, qmask, cfg.neg, cfg.normalize)
+            return S
+        scores, _ = F.packed_forward(a, b, qmask, cfg.neg, cfg.normalize)
+        return scores
 
     # ---- INT8 index ----
     if isinstance(b, Int8Index):
         if rest and _is_index(rest[0]):
             idxs, masks = rest[0], rest[1:]
             qmask, dmask = (masks + [None, None])[:2]
-            S, _ = F.int8_candidates_forward(a, b, idxs, qmask, dmask, cfg.neg)
-            if cfg.normalize:
-                return F.length_normalize_candidates(S, qmask, a.shape[1], idxs,
-                                                     b.codes.shape[0], cfg.neg)
+            S, _ = F.int8_candidates_forward(a, b, idxs, qmask, dmask, cfg.neg, cfg.normalize)
             return S
         qmask, dmask = (rest + [None, None])[:2]
         if a.dim() == 2:
-            score, _ = F.int8_pair_forward(a, b, qmask, dmask)
-            return F.length_normalize(score, qmask, a.shape[0]) if cfg.normalize else score
-        scores, _ = F.int8_paired_forward(a, b, qmask, dmask)
-        return F.length_normalize(scores, qmask, a.shape[1]) if cfg.normalize else scores
+            score, _ = F.int8_pair_forward(a, b, qmask, dmask, cfg.normalize)
+            return score
+        scores, _ = F.int8_paired_forward(a, b, qmask, dmask, cfg.normalize)
+        return scores
 
     # ---- dense features ----
     if rest and _is_index(rest[0]) and not inbatch:
         idxs, masks = rest[0], rest[1:]
         qmask, dmask = (masks + [None, None])[:2]
-        S, _ = F.candidates_forward(a, b, idxs, qmask, dmask, cfg.neg)
-        if cfg.normalize:
-            return F.length_normalize_candidates(S, qmask, a.shape[1], idxs, b.shape[0], cfg.neg)
+        S, _ = F.candidates_forward(a, b, idxs, qmask, dmask, cfg.neg, cfg.normalize)
         return S
     qmask, dmask = (rest + [None, None])[:2]
     if inbatch:
-        S, _ = F.inbatch_forward(a, b, qmask, dmask, cfg.neg)
-        return F.length_normalize(S, qmask, a.shape[1]) if cfg.normalize else S
+        S, _ = F.inbatch_forward(a, b, qmask, dmask, cfg.neg, cfg.normalize)
+        return S
     if a.dim() == 2:
-        score, _ = F.pair_forward(a, b, qmask, dmask, cfg.neg)
-        return F.length_normalize(score, qmask, a.shape[0]) if cfg.normalize else score
-    scores, _ = F.paired_forward(a, b, qmask, dmask, cfg.neg)
-    return F.length_normalize(scores, qmask, a.shape[1]) if cfg.normalize else scores
+        score, _ = F.pair_forward(a, b, qmask, dmask, cfg.neg, cfg.normalize)
+        return score
+    scores, _ = F.paired_forward(a, b, qmask, dmask, cfg.neg, cfg.normalize)
+    return scores

@@ -100,28 +100,33 @@ def _idx_bytes(idx: torch.Tensor) -> int:
     raise ArgumentError("candidate indices must be Int32 or Int64")
 
 
-def launch_pair_scan(argmax_u, partial, q, d, qmask, dmask, score=None):
+def _norm(normalize) -> int:
+    """The scans' fused normalize=true epilogue flag (0 or 1)."""
+    return 1 if normalize else 0
+
+
+def launch_pair_scan(argmax_u, partial, q, d, qmask, dmask, score=None, normalize=False):
     dev = require_device(argmax_u, partial, q, d, qmask, dmask, score)
     Tq, dim = q.shape
     Td = d.shape[0]
     st = _lib.lib().fms_launch_pair_scan(
         dtype_code(q), ptr(argmax_u), ptr(partial), ptr(q), ptr(d), ptr(_mask(qmask)),
-        ptr(_mask(dmask)), dim, Tq, Td, ptr(score), stream_handle(dev))
+        ptr(_mask(dmask)), dim, Tq, Td, ptr(score), _norm(normalize), stream_handle(dev))
     _lib.check(st, "launch_pair_scan")
 
 
-def launch_paired_scan(args, partial, Q, D, qmask, dmask, scores=None):
+def launch_paired_scan(args, partial, Q, D, qmask, dmask, scores=None, normalize=False):
     dev = require_device(args, partial, Q, D, qmask, dmask, scores)
     B, Tq, dim = Q.shape
     Td = D.shape[1]
     st = _lib.lib().fms_launch_paired_scan(
         dtype_code(Q), ptr(args), ptr(partial), ptr(Q), ptr(D), ptr(_mask(qmask)),
-        ptr(_mask(dmask)), dim, Tq, Td, B, ptr(scores), stream_handle(dev))
+        ptr(_mask(dmask)), dim, Tq, Td, B, ptr(scores), _norm(normalize), stream_handle(dev))
     _lib.check(st, "launch_paired_scan")
 
 
 def launch_candidates_scan(args, partial, Q, gallery, idx, qmask, dmask, N, scores=None,
-                           neg=-1.0e4):
+                           neg=-1.0e4, normalize=False):
     dev = require_device(args, partial, Q, gallery, idx, qmask, dmask, scores)
     B, Tq, dim = Q.shape
     Td = gallery.shape[1]
@@ -129,7 +134,7 @@ def launch_candidates_scan(args, partial, Q, gallery, idx, qmask, dmask, N, scor
     st = _lib.lib().fms_launch_candidates_scan(
         dtype_code(Q), ptr(args), ptr(partial), ptr(Q), ptr(gallery), ptr(idx), _idx_bytes(idx),
         ptr(_mask(qmask)), ptr(_mask(dmask)), dim, Tq, B, Td, N, C, ptr(scores), float(neg),
-        stream_handle(dev))
+        _norm(normalize), stream_handle(dev))
     _lib.check(st, "launch_candidates_scan")
 
 
@@ -147,17 +152,17 @@ def candidates_grouping(mode: str) -> str:
     return {v: k for k, v in GROUPING_MODES.items()}[prev]
 
 
-def inbatch_device_scan(S, args, Q, D, qmask, dmask):
+def inbatch_device_scan(S, args, Q, D, qmask, dmask, normalize=False):
     dev = require_device(S, args, Q, D, qmask, dmask)
     Bq, Tq, dim = Q.shape
     Bd, Td = D.shape[0], D.shape[1]
     st = _lib.lib().fms_inbatch_device_scan(
         dtype_code(Q), ptr(S), ptr(args), ptr(Q), ptr(D), ptr(_mask(qmask)), ptr(_mask(dmask)),
-        dim, Tq, Bq, Td, Bd, stream_handle(dev))
+        dim, Tq, Bq, Td, Bd, _norm(normalize), stream_handle(dev))
     _lib.check(st, "inbatch_device_scan")
 
 
-def launch_packed_scan(args, partial, q, tokens, cu, qmask, scores=None):
+def launch_packed_scan(args, partial, q, tokens, cu, qmask, scores=None, normalize=False):
     dev = require_device(args, partial, q, tokens, cu, qmask, scores)
     Tq, dim = q.shape
     B = cu.shape[0] - 1
@@ -165,11 +170,11 @@ def launch_packed_scan(args, partial, q, tokens, cu, qmask, scores=None):
         raise ArgumentError("PackedSeq cu must be Int32 on device")
     st = _lib.lib().fms_launch_packed_scan(
         dtype_code(q), ptr(args), ptr(partial), ptr(q), ptr(tokens), ptr(cu), ptr(_mask(qmask)),
-        dim, Tq, B, tokens.shape[0], ptr(scores), stream_handle(dev))
+        dim, Tq, B, tokens.shape[0], ptr(scores), _norm(normalize), stream_handle(dev))
     _lib.check(st, "launch_packed_scan")
 
 
-def launch_packed_multi_scan(args, scores, Q, tokens, cu, qmask, max_len):
+def launch_packed_multi_scan(args, scores, Q, tokens, cu, qmask, max_len, normalize=False):
     """nq queries Q (nq, Tq, dim) against one PackedSeq in one pass (no reference
     method: the reference scores one query per call).  scores (nq, B) [Julia (B, nq)],
     args (nq, B, Tq) nullable."""
@@ -180,7 +185,7 @@ def launch_packed_multi_scan(args, scores, Q, tokens, cu, qmask, max_len):
         raise ArgumentError("PackedSeq cu must be Int32 on device")
     st = _lib.lib().fms_launch_packed_multi_scan(
         dtype_code(Q), ptr(args), ptr(scores), ptr(Q), ptr(tokens), ptr(cu), ptr(_mask(qmask)),
-        dim, Tq, nq, B, tokens.shape[0], int(max_len), stream_handle(dev))
+        dim, Tq, nq, B, tokens.shape[0], int(max_len), _norm(normalize), stream_handle(dev))
     _lib.check(st, "launch_packed_multi_scan")
 
 
@@ -195,7 +200,7 @@ def topk_rows(vals, idx, scores, k):
     _lib.check(st, "topk")
 
 
-def launch_varlen_scan(args, partial, Qp, Dp, cu_q, cu_d, scores=None):
+def launch_varlen_scan(args, partial, Qp, Dp, cu_q, cu_d, scores=None, normalize=False):
     dev = require_device(args, partial, Qp, Dp, cu_q, cu_d, scores)
     N, max_q = args.shape
     dim = Qp.shape[1]
@@ -203,7 +208,7 @@ def launch_varlen_scan(args, partial, Qp, Dp, cu_q, cu_d, scores=None):
         raise ArgumentError("PackedSeq cu must be Int32 on device")
     st = _lib.lib().fms_launch_varlen_scan(
         dtype_code(Qp), ptr(args), ptr(partial), ptr(Qp), ptr(Dp), ptr(cu_q), ptr(cu_d), dim,
-        max_q, N, Qp.shape[0], Dp.shape[0], ptr(scores), stream_handle(dev))
+        max_q, N, Qp.shape[0], Dp.shape[0], ptr(scores), _norm(normalize), stream_handle(dev))
     _lib.check(st, "launch_varlen_scan")
 
 
@@ -219,30 +224,32 @@ def _f32(t, what):
     return t
 
 
-def launch_int8_pair_scan(args, partial, qc, qs, dc, ds, qmask, dmask, score=None):
+def launch_int8_pair_scan(args, partial, qc, qs, dc, ds, qmask, dmask, score=None,
+                          normalize=False):
     dev = require_device(args, partial, qc, qs, dc, ds, qmask, dmask, score)
     Tq, dim = qc.shape
     Td = dc.shape[0]
     st = _lib.lib().fms_launch_int8_pair_scan(
         ptr(args), ptr(partial), ptr(_int8(qc, "qc")), ptr(_f32(qs, "qs")), ptr(_int8(dc, "dc")),
         ptr(_f32(ds, "ds")), ptr(_mask(qmask)), ptr(_mask(dmask)), dim, Tq, Td, ptr(score),
-        stream_handle(dev))
+        _norm(normalize), stream_handle(dev))
     _lib.check(st, "launch_int8_pair_scan")
 
 
-def launch_int8_paired_scan(args, partial, Qc, Qs, Dc, Ds, qmask, dmask, scores=None):
+def launch_int8_paired_scan(args, partial, Qc, Qs, Dc, Ds, qmask, dmask, scores=None,
+                            normalize=False):
     dev = require_device(args, partial, Qc, Qs, Dc, Ds, qmask, dmask, scores)
     B, Tq, dim = Qc.shape
     Td = Dc.shape[1]
     st = _lib.lib().fms_launch_int8_paired_scan(
         ptr(args), ptr(partial), ptr(_int8(Qc, "Qc")), ptr(_f32(Qs, "Qs")), ptr(_int8(Dc, "Dc")),
         ptr(_f32(Ds, "Ds")), ptr(_mask(qmask)), ptr(_mask(dmask)), dim, Tq, Td, B, ptr(scores),
-        stream_handle(dev))
+        _norm(normalize), stream_handle(dev))
     _lib.check(st, "launch_int8_paired_scan")
 
 
 def launch_int8_candidates_scan(args, partial, Qc, Qs, Gc, Gs, idx, qmask, dmask, N,
-                                scores=None, neg=-1.0e4):
+                                scores=None, neg=-1.0e4, normalize=False):
     dev = require_device(args, partial, Qc, Qs, Gc, Gs, idx, qmask, dmask, scores)
     B, Tq, dim = Qc.shape
     Td = Gc.shape[1]
@@ -250,7 +257,7 @@ def launch_int8_candidates_scan(args, partial, Qc, Qs, Gc, Gs, idx, qmask, dmask
     st = _lib.lib().fms_launch_int8_candidates_scan(
         ptr(args), ptr(partial), ptr(_int8(Qc, "Qc")), ptr(_f32(Qs, "Qs")), ptr(_int8(Gc, "Gc")),
         ptr(_f32(Gs, "Gs")), ptr(idx), _idx_bytes(idx), ptr(_mask(qmask)), ptr(_mask(dmask)), dim,
-        Tq, B, Td, N, C, ptr(scores), float(neg), stream_handle(dev))
+        Tq, B, Td, N, C, ptr(scores), float(neg), _norm(normalize), stream_handle(dev))
     _lib.check(st, "launch_int8_candidates_scan")
 
 

@@ -2,9 +2,11 @@
 
 Each ``*_forward`` mirrors the reference's device driver ``*_forward_ka``
 (outputs allocated with zeros_like, one scan launch, scores kept on device)
-and returns ``(scores, argmax_tape)``.  Σ_t and the candidate ``neg`` fill
-are fused into the scan kernel (the reference runs ``sum(partial; dims=1)``
-and ``ifelse.(valid, S, neg)`` as separate device kernels).
+and returns ``(scores, argmax_tape)``.  Σ_t, the candidate ``neg`` fill and,
+with ``normalize=True``, the length normalisation are fused into the scan
+kernel's score write (the reference runs ``sum(partial; dims=1)``,
+``ifelse.(valid, S, neg)`` and ``scores .* inv_n`` as separate device
+kernels; normalize.jl, packed.jl:316-354).  The tape is the same either way.
 
 Shapes follow the package convention (Julia ``(a, b, c)`` is torch
 ``(c, b, a)``): a paired tape Julia ``(Tq, B)`` is ``(B, Tq)``, a candidate
@@ -99,28 +101,28 @@ def indices_on(prototype: torch.Tensor, idxs: torch.Tensor) -> torch.Tensor:
 
 # ---- forward drivers ---------------------------------------------------------------------
 
-def pair_forward(q, d, qmask=None, dmask=None, neg=None):
+def pair_forward(q, d, qmask=None, dmask=None, neg=None, normalize=False):
     """pair_forward_ka (forward_pair.jl:104-116): (score (1,), argmax_u (Tq,))."""
     boundary.require_device(q, d, qmask, dmask)
     _, Tq, _ = require_pair_shapes(q, d, qmask, dmask)
     argmax_u = _zeros(q, torch.int32, Tq)
     partial = _zeros(q, SCORE_DTYPE, Tq)
     score = _zeros(q, SCORE_DTYPE, 1)
-    boundary.launch_pair_scan(argmax_u, partial, q, d, qmask, dmask, score)
+    boundary.launch_pair_scan(argmax_u, partial, q, d, qmask, dmask, score, normalize)
     return score, argmax_u
 
 
-def paired_forward(Q, D, qmask=None, dmask=None, neg=None):
+def paired_forward(Q, D, qmask=None, dmask=None, neg=None, normalize=False):
     """paired_forward_ka (forward_layouts.jl:112-124): (scores (B,), args (B,Tq))."""
     boundary.require_device(Q, D, qmask, dmask)
     _, Tq, _, B = require_paired_shapes(Q, D, qmask, dmask)
     args = _zeros(Q, torch.int32, B, Tq)
     scores = _zeros(Q, SCORE_DTYPE, B)
-    boundary.launch_paired_scan(args, None, Q, D, qmask, dmask, scores)
+    boundary.launch_paired_scan(args, None, Q, D, qmask, dmask, scores, normalize)
     return scores, args
 
 
-def inbatch_forward(Q, D, qmask=None, dmask=None, neg=None):
+def inbatch_forward(Q, D, qmask=None, dmask=None, neg=None, normalize=False):
     """inbatch_forward_ka (forward_layouts.jl:188-200): (S (Bq,Bd), args (Bq,Bd,Tq))."""
     boundary.require_device(Q, D, qmask, dmask)
     _, Tq, Bq, Td, Bd = require_inbatch_shapes(Q, D, qmask, dmask)
@@ -128,11 +130,11 @@ def inbatch_forward(Q, D, qmask=None, dmask=None, neg=None):
     args = _zeros(Q, torch.int32, Bq, Bd, Tq)
     if Bd == 0 or Bq == 0 or Tq == 0 or Td == 0:
         return S, args
-    boundary.inbatch_device_scan(S, args, Q, D, qmask, dmask)
+    boundary.inbatch_device_scan(S, args, Q, D, qmask, dmask, normalize)
     return S, args
 
 
-def candidates_forward(Q, gallery, idxs, qmask=None, dmask=None, neg=-1.0e4):
+def candidates_forward(Q, gallery, idxs, qmask=None, dmask=None, neg=-1.0e4, normalize=False):
     """candidates_forward_ka (forward_layouts.jl:272-290): (S (B,C), args (B,C,Tq))."""
     boundary.require_device(Q, gallery, qmask, dmask)
     _, Tq, B, _, N = require_candidates_shapes(Q, gallery, idxs, qmask, dmask)
@@ -140,11 +142,12 @@ def candidates_forward(Q, gallery, idxs, qmask=None, dmask=None, neg=-1.0e4):
     C = idx.shape[1]
     args = _zeros(Q, torch.int32, B, C, Tq)
     S = _zeros(Q, SCORE_DTYPE, B, C)
-    boundary.launch_candidates_scan(args, None, Q, gallery, idx, qmask, dmask, N, S, neg)
+    boundary.launch_candidates_scan(args, None, Q, gallery, idx, qmask, dmask, N, S, neg,
+                                    normalize)
     return S, args
 
 
-def packed_forward(q, P: PackedSeq, qmask=None, neg=None):
+def packed_forward(q, P: PackedSeq, qmask=None, neg=None, normalize=False):
     """packed_forward_ka (packed.jl:191-202): (scores (B,), args (B,Tq))."""
     boundary.require_device(q, P.tokens, P.cu, qmask)
     Tq = q.shape[0]
@@ -155,11 +158,11 @@ def packed_forward(q, P: PackedSeq, qmask=None, neg=None):
     B = P.nseq()
     args = _zeros(q, torch.int32, B, Tq)
     scores = _zeros(q, SCORE_DTYPE, B)
-    boundary.launch_packed_scan(args, None, q, P.tokens, P.cu, qmask, scores)
+    boundary.launch_packed_scan(args, None, q, P.tokens, P.cu, qmask, scores, normalize)
     return scores, args
 
 
-def packed_multi_forward(Q, P: PackedSeq, qmask=None, neg=None):
+def packed_multi_forward(Q, P: PackedSeq, qmask=None, neg=None, normalize=False):
     """nq queries against one PackedSeq in one pass: (S (nq,B), args (nq,B,Tq)).
 
     No reference counterpart (the reference's packed_forward takes one query,
@@ -179,7 +182,7 @@ def packed_multi_forward(Q, P: PackedSeq, qmask=None, neg=None):
     args = _zeros(Q, torch.int32, nq, B, Tq)
     if nq == 0 or B == 0:
         return S, args
-    boundary.launch_packed_multi_scan(args, S, Q, P.tokens, P.cu, qmask, P.max_len)
+    boundary.launch_packed_multi_scan(args, S, Q, P.tokens, P.cu, qmask, P.max_len, normalize)
     return S, args
 
 
@@ -213,7 +216,7 @@ def topk(scores: torch.Tensor, k: int):
     return vals, idx
 
 
-def varlen_forward(Qp: PackedSeq, Dp: PackedSeq, neg=None):
+def varlen_forward(Qp: PackedSeq, Dp: PackedSeq, neg=None, normalize=False):
     """varlen_forward_ka (packed.jl:274-284): (scores (N,), args (N,max_q))."""
     boundary.require_device(Qp.tokens, Dp.tokens, Qp.cu, Dp.cu)
     N = Qp.nseq()
@@ -224,11 +227,11 @@ def varlen_forward(Qp: PackedSeq, Dp: PackedSeq, neg=None):
     max_q = Qp.max_len
     args = _zeros(Qp.tokens, torch.int32, N, max_q)
     scores = _zeros(Qp.tokens, SCORE_DTYPE, N)
-    boundary.launch_varlen_scan(args, None, Qp.tokens, Dp.tokens, Qp.cu, Dp.cu, scores)
+    boundary.launch_varlen_scan(args, None, Qp.tokens, Dp.tokens, Qp.cu, Dp.cu, scores, normalize)
     return scores, args
 
 
-def int8_pair_forward(q, d: Int8Index, qmask=None, dmask=None):
+def int8_pair_forward(q, d: Int8Index, qmask=None, dmask=None, normalize=False):
     """int8_pair_forward (quant.jl:156-170): quantise q on device, then the INT8 scan."""
     qq = quantize_int8_symmetric(q)
     require_int8_index(d)
@@ -246,11 +249,11 @@ def int8_pair_forward(q, d: Int8Index, qmask=None, dmask=None):
     args = _zeros(q, torch.int32, Tq)
     score = _zeros(q, SCORE_DTYPE, 1)
     boundary.launch_int8_pair_scan(args, None, qq.codes, qq.scales, d.codes, d.scales, qmask,
-                                   dmask, score)
+                                   dmask, score, normalize)
     return score, args
 
 
-def int8_paired_forward(Q, D: Int8Index, qmask=None, dmask=None):
+def int8_paired_forward(Q, D: Int8Index, qmask=None, dmask=None, normalize=False):
     """int8_paired_forward (quant.jl:219-226)."""
     QQ = quantize_int8_symmetric(Q)
     require_int8_index(D)
@@ -270,11 +273,12 @@ def int8_paired_forward(Q, D: Int8Index, qmask=None, dmask=None):
     args = _zeros(Q, torch.int32, B, Tq)
     scores = _zeros(Q, SCORE_DTYPE, B)
     boundary.launch_int8_paired_scan(args, None, QQ.codes, QQ.scales, D.codes, D.scales, qmask,
-                                     dmask, scores)
+                                     dmask, scores, normalize)
     return scores, args
 
 
-def int8_candidates_forward(Q, G: Int8Index, idxs, qmask=None, dmask=None, neg=-1.0e4):
+def int8_candidates_forward(Q, G: Int8Index, idxs, qmask=None, dmask=None, neg=-1.0e4,
+                            normalize=False):
     """INT8 candidate layout (no reference method): quantised Q_b vs gallery[idxs[c,b]]."""
     QQ = quantize_int8_symmetric(Q)
     boundary.require_device(Q, QQ.codes, QQ.scales, G.codes, G.scales, qmask, dmask)
@@ -295,7 +299,7 @@ def int8_candidates_forward(Q, G: Int8Index, idxs, qmask=None, dmask=None, neg=-
     args = _zeros(Q, torch.int32, B, C, Tq)
     S = _zeros(Q, SCORE_DTYPE, B, C)
     boundary.launch_int8_candidates_scan(args, None, QQ.codes, QQ.scales, G.codes, G.scales, idx,
-                                         qmask, dmask, N, S, neg)
+                                         qmask, dmask, N, S, neg, normalize)
     return S, args
 
 

@@ -65,6 +65,28 @@ class PackedSeq:
         self.cu = cu
         self.max_len = int(max_len)
 
+    @classmethod
+    def from_cu_seqlens(cls, tokens: torch.Tensor, cu_seqlens,
+                        max_len: int | None = None) -> "PackedSeq":
+        """From a 0-based ``cu_seqlens`` (length B+1, starting at 0, the
+        flash-attention varlen convention): ``cu = cu_seqlens + 1`` as Int32 on
+        the same device (packed.jl:5-6).  A host ``cu_seqlens`` is validated
+        like a host ``cu``; a device one is converted on the device without a
+        host round trip (pass ``max_len`` to avoid the one read it costs)."""
+        if not isinstance(cu_seqlens, torch.Tensor):
+            cu_seqlens = torch.as_tensor(np.asarray(cu_seqlens))
+        if cu_seqlens.dim() != 1 or cu_seqlens.numel() < 1:
+            raise ArgumentError("cu_seqlens must be a vector of length B+1")
+        if cu_seqlens.is_floating_point() or cu_seqlens.dtype == torch.bool:
+            raise ArgumentError("cu_seqlens must hold integers")
+        if cu_seqlens.device.type == "cpu" and cu_seqlens.numel() and int(cu_seqlens[-1]) >= 2**31 - 1:
+            raise ArgumentError("cu_seqlens exceeds the Int32 range of cu")
+        return cls(tokens, (cu_seqlens.to(torch.int64) + 1).to(torch.int32), max_len)
+
+    def cu_seqlens(self) -> torch.Tensor:
+        """The 0-based Int32 ``cu_seqlens`` of this sequence set (``cu - 1``)."""
+        return self.cu - 1
+
     def nseq(self) -> int:
         return self.cu.numel() - 1
 

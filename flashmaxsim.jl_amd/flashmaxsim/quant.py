@@ -3,13 +3,22 @@
 ``Int8Index.codes`` has the feature shape ((T, dim) or (B, T, dim)) as Int8;
 ``scales`` is (T,) or (B, T) Float32.  Quantisation runs on the device
 (``fms_int8_quantize``) and is bit-exact with quantize_int8_symmetric.
+
+At rest (``save_int8_index`` / ``load_int8_index``) an index is one
+safetensors file with two tensors, ``codes`` and ``scales``, in exactly the
+in-memory layout above -- Julia's column-major ``codes (dim, Td, N)`` and
+``scales (Td, N)`` byte for byte (quant.jl:11-14) -- plus the format name in
+the metadata.  Loading reads the bytes without executing anything from the
+file and moves them to the requested device.
 """
 from __future__ import annotations
 
 import torch
 
 from . import boundary
-from .errors import DimensionMismatch, UnsupportedError
+from .errors import ArgumentError, DimensionMismatch, UnsupportedError
+
+INT8_INDEX_FORMAT = "flashmaxsim-int8-index-v1"
 
 
 class Int8Index:
@@ -53,3 +62,31 @@ def require_int8_index(d: Int8Index) -> None:
             raise DimensionMismatch("Int8Index token count")
         if d.codes.shape[0] != d.scales.shape[0]:
             raise DimensionMismatch("Int8Index batch")
+
+
+def save_int8_index(idx: Int8Index, path: str) -> None:
+    """Write an Int8Index to ``path`` as safetensors (codes int8, scales fp32)."""
+    from safetensors.torch import save_file
+    require_int8_index(idx)
+    if idx.codes.dtype != torch.int8 or idx.scales.dtype != torch.float32:
+        raise ArgumentError("Int8Index at rest holds Int8 codes and Float32 scales")
+    save_file({"codes": idx.codes.detach().contiguous().cpu(),
+               "scales": idx.scales.detach().contiguous().cpu()}, path,
+              metadata={"format": INT8_INDEX_FORMAT,
+                        "layout": "codes (N, Td, dim) row-major = Julia (dim, Td, N); "
+                                  "scales (N, Td) = Julia (Td, N)"})
+
+
+def load_int8_index(path: str, device="cpu") -> Int8Index:
+    """Read an Int8Index written by ``save_int8_index`` onto ``device``."""
+    from safetensors import safe_open
+    with safe_open(path, framework="pt", device="cpu") as f:
+        meta = f.metadata() or {}
+        if meta.get("format") != INT8_INDEX_FORMAT:
+            raise ArgumentError(f"{path}: not a {INT8_INDEX_FORMAT} file")
+        codes, scales = f.get_tensor("codes"), f.get_tensor("scales")
+    if codes.dtype != torch.int8 or scales.dtype != torch.float32:
+        raise ArgumentError(f"{path}: codes must be Int8 and scales Float32")
+    idx = Int8Index(codes, scales)
+    require_int8_index(idx)
+    return idx.to(device)

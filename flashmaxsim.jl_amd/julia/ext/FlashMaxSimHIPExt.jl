@@ -85,9 +85,9 @@ function FlashMaxSim.launch_pair_scan!(::ROCBackend, argmax_u, partial,
     dim, Tq = size(q)
     check(ccall((:fms_launch_pair_scan, libfms), Int32,
                 (Int32, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid},
-                 Int64, Int64, Int64, Ptr{Cvoid}, Ptr{Cvoid}),
+                 Int64, Int64, Int64, Ptr{Cvoid}, Int32, Ptr{Cvoid}),
                 dtype_code(T), dptr(argmax_u), dptr(partial), dptr(q), dptr(d),
-                dptr(qmask), dptr(dmask), dim, Tq, size(d, 2), C_NULL, stream_ptr()),
+                dptr(qmask), dptr(dmask), dim, Tq, size(d, 2), C_NULL, Int32(0), stream_ptr()),
           "pair scan")
     nothing
 end
@@ -98,9 +98,9 @@ function FlashMaxSim.launch_paired_scan!(::ROCBackend, args, partial,
     dim, Tq, B = size(Q)
     check(ccall((:fms_launch_paired_scan, libfms), Int32,
                 (Int32, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid},
-                 Int64, Int64, Int64, Int64, Ptr{Cvoid}, Ptr{Cvoid}),
+                 Int64, Int64, Int64, Int64, Ptr{Cvoid}, Int32, Ptr{Cvoid}),
                 dtype_code(T), dptr(args), dptr(partial), dptr(Q), dptr(D),
-                dptr(qmask), dptr(dmask), dim, Tq, size(D, 2), B, C_NULL, stream_ptr()),
+                dptr(qmask), dptr(dmask), dim, Tq, size(D, 2), B, C_NULL, Int32(0), stream_ptr()),
           "paired scan")
     nothing
 end
@@ -111,11 +111,11 @@ function candidates_call(args, partial, scores, Q::ROCArray{T,3}, gallery, idx,
     check(ccall((:fms_launch_candidates_scan, libfms), Int32,
                 (Int32, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Int32,
                  Ptr{Cvoid}, Ptr{Cvoid}, Int64, Int64, Int64, Int64, Int64, Int64,
-                 Ptr{Cvoid}, Float32, Ptr{Cvoid}),
+                 Ptr{Cvoid}, Float32, Int32, Ptr{Cvoid}),
                 dtype_code(T), dptr(args), dptr(partial), dptr(Q), dptr(gallery),
                 dptr(idx), Int32(sizeof(eltype(idx))), dptr(qmask), dptr(dmask),
                 dim, Tq, B, size(gallery, 2), N, size(idx, 1),
-                dptr(scores), Float32(neg), stream_ptr()),
+                dptr(scores), Float32(neg), Int32(0), stream_ptr()),
           "candidate scan")
     nothing
 end
@@ -149,9 +149,10 @@ function FlashMaxSim.inbatch_device_scan!(::ROCBackend, S, args,
     dim, Tq, Bq = size(Q)
     check(ccall((:fms_inbatch_device_scan, libfms), Int32,
                 (Int32, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid},
-                 Int64, Int64, Int64, Int64, Int64, Ptr{Cvoid}),
+                 Int64, Int64, Int64, Int64, Int64, Int32, Ptr{Cvoid}),
                 dtype_code(T), dptr(S), dptr(args), dptr(Q), dptr(D),
-                dptr(qmask), dptr(dmask), dim, Tq, Bq, size(D, 2), size(D, 3), stream_ptr()),
+                dptr(qmask), dptr(dmask), dim, Tq, Bq, size(D, 2), size(D, 3), Int32(0),
+                stream_ptr()),
           "in-batch scan")
     nothing
 end
@@ -162,9 +163,10 @@ function FlashMaxSim.launch_packed_scan!(::ROCBackend, args, partial, q::ROCMatr
     dim, Tq = size(q)
     check(ccall((:fms_launch_packed_scan, libfms), Int32,
                 (Int32, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid},
-                 Int64, Int64, Int64, Int64, Ptr{Cvoid}, Ptr{Cvoid}),
+                 Int64, Int64, Int64, Int64, Ptr{Cvoid}, Int32, Ptr{Cvoid}),
                 dtype_code(T), dptr(args), dptr(partial), dptr(q), dptr(packed), dptr(cu),
-                dptr(qmask), dim, Tq, length(cu) - 1, size(packed, 2), C_NULL, stream_ptr()),
+                dptr(qmask), dim, Tq, length(cu) - 1, size(packed, 2), C_NULL, Int32(0),
+                stream_ptr()),
           "packed scan")
     nothing
 end
@@ -174,10 +176,10 @@ function FlashMaxSim.launch_varlen_scan!(::ROCBackend, args, partial, Qp::ROCMat
                                          cu_d::ROCVector{Int32}) where {T<:FloatFeature}
     check(ccall((:fms_launch_varlen_scan, libfms), Int32,
                 (Int32, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid},
-                 Int64, Int64, Int64, Int64, Int64, Ptr{Cvoid}, Ptr{Cvoid}),
+                 Int64, Int64, Int64, Int64, Int64, Ptr{Cvoid}, Int32, Ptr{Cvoid}),
                 dtype_code(T), dptr(args), dptr(partial), dptr(Qp), dptr(Dp),
                 dptr(cu_q), dptr(cu_d), size(Qp, 1), size(args, 1), size(args, 2),
-                size(Qp, 2), size(Dp, 2), C_NULL, stream_ptr()),
+                size(Qp, 2), size(Dp, 2), C_NULL, Int32(0), stream_ptr()),
           "varlen scan")
     nothing
 end
@@ -190,9 +192,9 @@ function FlashMaxSim.launch_int8_pair_scan!(::ROCBackend, args, partial, qc::ROC
     dim, Tq = size(qc)
     check(ccall((:fms_launch_int8_pair_scan, libfms), Int32,
                 (Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid},
-                 Ptr{Cvoid}, Ptr{Cvoid}, Int64, Int64, Int64, Ptr{Cvoid}, Ptr{Cvoid}),
+                 Ptr{Cvoid}, Ptr{Cvoid}, Int64, Int64, Int64, Ptr{Cvoid}, Int32, Ptr{Cvoid}),
                 dptr(args), dptr(partial), dptr(qc), dptr(qs), dptr(dc), dptr(ds),
-                dptr(qmask), dptr(dmask), dim, Tq, size(dc, 2), C_NULL, stream_ptr()),
+                dptr(qmask), dptr(dmask), dim, Tq, size(dc, 2), C_NULL, Int32(0), stream_ptr()),
           "INT8 pair scan")
     nothing
 end
@@ -204,9 +206,9 @@ function FlashMaxSim.launch_int8_paired_scan!(::ROCBackend, args, partial,
     dim, Tq, B = size(Qc)
     check(ccall((:fms_launch_int8_paired_scan, libfms), Int32,
                 (Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid},
-                 Ptr{Cvoid}, Ptr{Cvoid}, Int64, Int64, Int64, Int64, Ptr{Cvoid}, Ptr{Cvoid}),
+                 Ptr{Cvoid}, Ptr{Cvoid}, Int64, Int64, Int64, Int64, Ptr{Cvoid}, Int32, Ptr{Cvoid}),
                 dptr(args), dptr(partial), dptr(Qc), dptr(Qs), dptr(Dc), dptr(Ds),
-                dptr(qmask), dptr(dmask), dim, Tq, size(Dc, 2), B, C_NULL, stream_ptr()),
+                dptr(qmask), dptr(dmask), dim, Tq, size(Dc, 2), B, C_NULL, Int32(0), stream_ptr()),
           "INT8 paired scan")
     nothing
 end
@@ -318,11 +320,11 @@ end
 
 nq queries `Q (dim, Tq, nq)` against every document of `P` in one pass: `S (B, nq)`
 Float32 and the 1-based document-local tape `args (Tq, B, nq)`.  Column i equals
-`maxsim(Q[:, :, i], P, qmask[:, i])` unnormalised (src/packed.jl:178-210) within the
-score tolerance.
+`maxsim(Q[:, :, i], P, qmask[:, i]; normalize)` (src/packed.jl:178-210) within the
+score tolerance; `normalize` is fused into the scan's score write.
 """
 function packed_multi_scan(Q::ROCArray{T,3}, P::FlashMaxSim.PackedSeq;
-                           qmask = nothing) where {T<:FloatFeature}
+                           qmask = nothing, normalize::Bool = false) where {T<:FloatFeature}
     dim, Tq, nq = size(Q)
     B = length(P.cu) - 1
     S = AMDGPU.zeros(Float32, B, nq)
@@ -330,10 +332,10 @@ function packed_multi_scan(Q::ROCArray{T,3}, P::FlashMaxSim.PackedSeq;
     (nq == 0 || B == 0) && return S, args
     check(ccall((:fms_launch_packed_multi_scan, libfms), Int32,
                 (Int32, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid},
-                 Int64, Int64, Int64, Int64, Int64, Int64, Ptr{Cvoid}),
+                 Int64, Int64, Int64, Int64, Int64, Int64, Int32, Ptr{Cvoid}),
                 dtype_code(T), dptr(args), dptr(S), dptr(Q), dptr(P.tokens), dptr(P.cu),
                 qmask === nothing ? C_NULL : dptr(qmask), dim, Tq, nq, B,
-                size(P.tokens, 2), P.max_len, stream_ptr()),
+                size(P.tokens, 2), P.max_len, Int32(normalize), stream_ptr()),
           "multi-query packed scan")
     S, args
 end

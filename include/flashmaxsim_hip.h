@@ -30,6 +30,12 @@
  *     the candidate layouts an invalid index writes `neg` there, fusing
  *     forward_layouts.jl:285-287.  `partial` and `args` may be NULL when not
  *     wanted.
+ *   - `normalize` (0 or 1; extension) fuses the normalize=true epilogue into
+ *     the same write: every valid pair's score is multiplied by the fp32
+ *     1 / max(n, 1), n = its query's valid tokens (qmask count; the pair's
+ *     query length for varlen) -- length_normalize / packed_finalize /
+ *     varlen_finalize (normalize.jl:4-25, packed.jl:316-354); invalid
+ *     candidates keep `neg` (normalize.jl:37-46).  Partials stay unscaled.
  *   - Zero-size inputs return FMS_OK without launching (ka.jl:12); an empty
  *     document (Td = 0 or cu[b+1] = cu[b]) still writes zeros.
  *   - Kernels never trap: an out-of-range candidate index yields tape 0 /
@@ -85,7 +91,7 @@ fms_status fms_launch_pair_scan(int32_t dtype, int32_t* argmax_u, float* partial
                                 const void* q, const void* d,
                                 const uint8_t* qmask, const uint8_t* dmask,
                                 int64_t dim, int64_t Tq, int64_t Td,
-                                float* score, void* stream);
+                                float* score, int32_t normalize, void* stream);
 
 /*
  * Paired-batch scan.  Replaces launch_paired_scan!(backend, args, partial, Q,
@@ -97,7 +103,7 @@ fms_status fms_launch_paired_scan(int32_t dtype, int32_t* args, float* partial,
                                   const void* Q, const void* D,
                                   const uint8_t* qmask, const uint8_t* dmask,
                                   int64_t dim, int64_t Tq, int64_t Td, int64_t B,
-                                  float* scores, void* stream);
+                                  float* scores, int32_t normalize, void* stream);
 
 /*
  * Candidate scan.  Replaces launch_candidates_scan!(backend, args, partial,
@@ -113,7 +119,7 @@ fms_status fms_launch_candidates_scan(int32_t dtype, int32_t* args, float* parti
                                       const uint8_t* qmask, const uint8_t* dmask,
                                       int64_t dim, int64_t Tq, int64_t B,
                                       int64_t Td, int64_t N, int64_t C,
-                                      float* scores, float neg, void* stream);
+                                      float* scores, float neg, int32_t normalize, void* stream);
 
 /*
  * Document-order grouping of the candidate scans (float and INT8).  No
@@ -140,7 +146,7 @@ fms_status fms_inbatch_device_scan(int32_t dtype, float* S, int32_t* args,
                                    const void* Q, const void* D,
                                    const uint8_t* qmask, const uint8_t* dmask,
                                    int64_t dim, int64_t Tq, int64_t Bq,
-                                   int64_t Td, int64_t Bd, void* stream);
+                                   int64_t Td, int64_t Bd, int32_t normalize, void* stream);
 
 /*
  * Packed scan: one query against B ragged documents.  Replaces
@@ -154,7 +160,7 @@ fms_status fms_launch_packed_scan(int32_t dtype, int32_t* args, float* partial,
                                   const void* q, const void* tokens, const int32_t* cu,
                                   const uint8_t* qmask,
                                   int64_t dim, int64_t Tq, int64_t B, int64_t ntokens,
-                                  float* scores, void* stream);
+                                  float* scores, int32_t normalize, void* stream);
 
 /*
  * Per-row top-k of an fp32 score matrix (no reference counterpart: ranking is
@@ -189,7 +195,7 @@ fms_status fms_launch_packed_multi_scan(int32_t dtype, int32_t* args, float* sco
                                         const void* Q, const void* tokens, const int32_t* cu,
                                         const uint8_t* qmask, int64_t dim, int64_t Tq, int64_t nq,
                                         int64_t B, int64_t ntokens, int64_t max_len,
-                                        void* stream);
+                                        int32_t normalize, void* stream);
 
 /*
  * Varlen scan: N ragged (query, document) pairs.  Replaces
@@ -202,7 +208,7 @@ fms_status fms_launch_varlen_scan(int32_t dtype, int32_t* args, float* partial,
                                   const int32_t* cu_q, const int32_t* cu_d,
                                   int64_t dim, int64_t max_q, int64_t N,
                                   int64_t nq_tokens, int64_t nd_tokens,
-                                  float* scores, void* stream);
+                                  float* scores, int32_t normalize, void* stream);
 
 /*
  * Per-token symmetric INT8 quantisation of fp32 features, bit-exact with
@@ -225,7 +231,7 @@ fms_status fms_launch_int8_pair_scan(int32_t* args, float* partial,
                                      const int8_t* dc, const float* ds,
                                      const uint8_t* qmask, const uint8_t* dmask,
                                      int64_t dim, int64_t Tq, int64_t Td,
-                                     float* score, void* stream);
+                                     float* score, int32_t normalize, void* stream);
 
 /*
  * INT8 paired scan.  Replaces launch_int8_paired_scan!(backend, args,
@@ -237,7 +243,7 @@ fms_status fms_launch_int8_paired_scan(int32_t* args, float* partial,
                                        const int8_t* Dc, const float* Ds,
                                        const uint8_t* qmask, const uint8_t* dmask,
                                        int64_t dim, int64_t Tq, int64_t Td, int64_t B,
-                                       float* scores, void* stream);
+                                       float* scores, int32_t normalize, void* stream);
 
 /*
  * INT8 candidate scan.  No reference counterpart: Int8Index has only pair
@@ -252,7 +258,8 @@ fms_status fms_launch_int8_candidates_scan(int32_t* args, float* partial,
                                            const uint8_t* qmask, const uint8_t* dmask,
                                            int64_t dim, int64_t Tq, int64_t B,
                                            int64_t Td, int64_t N, int64_t C,
-                                           float* scores, float neg, void* stream);
+                                           float* scores, float neg, int32_t normalize,
+                                           void* stream);
 
 /*
  * Test-only: raw int32 dots out (Td,Tq) with out[u + Td*t] = <qc_t, dc_u>,

@@ -50,28 +50,31 @@ EINVAL, EUNSUP, OK = _lib.FMS_EINVAL, _lib.FMS_EUNSUPPORTED, _lib.FMS_OK
 
 @pytest.mark.parametrize("call,expect", [
     # unsupported feature type
-    (lambda L: L.fms_launch_paired_scan(9, None, None, None, None, None, None, 8, 4, 5, 2, None, None), EUNSUP),
+    (lambda L: L.fms_launch_paired_scan(9, None, None, None, None, None, None, 8, 4, 5, 2, None, 0, None), EUNSUP),
     # negative extents
-    (lambda L: L.fms_launch_paired_scan(1, None, None, None, None, None, None, -1, 4, 5, 2, None, None), EINVAL),
+    (lambda L: L.fms_launch_paired_scan(1, None, None, None, None, None, None, -1, 4, 5, 2, None, 0, None), EINVAL),
     # zero batch: nothing to do (ka.jl:12)
-    (lambda L: L.fms_launch_paired_scan(1, None, None, None, None, None, None, 8, 4, 5, 0, None, None), OK),
+    (lambda L: L.fms_launch_paired_scan(1, None, None, None, None, None, None, 8, 4, 5, 0, None, 0, None), OK),
     # work but NULL features
-    (lambda L: L.fms_launch_paired_scan(1, None, None, None, None, None, None, 8, 4, 5, 2, None, None), EINVAL),
+    (lambda L: L.fms_launch_paired_scan(1, None, None, None, None, None, None, 8, 4, 5, 2, None, 0, None), EINVAL),
+    # normalize must be 0 or 1
+    (lambda L: L.fms_launch_paired_scan(1, None, None, None, None, None, None, 8, 4, 5, 2, None, 2, None), EINVAL),
+    (lambda L: L.fms_inbatch_device_scan(1, None, None, None, None, None, None, 8, 4, 2, 5, 3, -1, None), EINVAL),
     # bad index width
-    (lambda L: L.fms_launch_candidates_scan(1, None, None, 1, 1, 1, 3, None, None, 8, 4, 2, 5, 7, 3, None, 0.0, None), EINVAL),
+    (lambda L: L.fms_launch_candidates_scan(1, None, None, 1, 1, 1, 3, None, None, 8, 4, 2, 5, 7, 3, None, 0.0, 0, None), EINVAL),
     # zero candidates
-    (lambda L: L.fms_launch_candidates_scan(1, None, None, None, None, None, 8, None, None, 8, 4, 2, 5, 7, 0, None, 0.0, None), OK),
+    (lambda L: L.fms_launch_candidates_scan(1, None, None, None, None, None, 8, None, None, 8, 4, 2, 5, 7, 0, None, 0.0, 0, None), OK),
     # NULL idx with work
-    (lambda L: L.fms_launch_candidates_scan(1, None, None, 1, 1, None, 8, None, None, 8, 4, 2, 5, 7, 3, None, 0.0, None), EINVAL),
+    (lambda L: L.fms_launch_candidates_scan(1, None, None, 1, 1, None, 8, None, None, 8, 4, 2, 5, 7, 3, None, 0.0, 0, None), EINVAL),
     # a single sequence too large for one buffer resource
-    (lambda L: L.fms_launch_paired_scan(0, None, None, 1, 1, None, None, 1 << 20, 1 << 10, 5, 2, None, None), EUNSUP),
-    (lambda L: L.fms_inbatch_device_scan(1, None, None, 1, 1, None, None, 8, 4, 2, 5, 3, None), EINVAL),
-    (lambda L: L.fms_launch_packed_scan(1, None, None, 1, 1, None, None, 8, 4, 3, 10, None, None), EINVAL),
-    (lambda L: L.fms_launch_varlen_scan(2, None, None, 1, 1, None, 1, 8, 4, 3, 10, 10, None, None), EINVAL),
+    (lambda L: L.fms_launch_paired_scan(0, None, None, 1, 1, None, None, 1 << 20, 1 << 10, 5, 2, None, 0, None), EUNSUP),
+    (lambda L: L.fms_inbatch_device_scan(1, None, None, 1, 1, None, None, 8, 4, 2, 5, 3, 0, None), EINVAL),
+    (lambda L: L.fms_launch_packed_scan(1, None, None, 1, 1, None, None, 8, 4, 3, 10, None, 0, None), EINVAL),
+    (lambda L: L.fms_launch_varlen_scan(2, None, None, 1, 1, None, 1, 8, 4, 3, 10, 10, None, 0, None), EINVAL),
     (lambda L: L.fms_int8_quantize(None, None, None, 8, 4, None), EINVAL),
     (lambda L: L.fms_int8_quantize(None, None, None, 8, 0, None), OK),
-    (lambda L: L.fms_launch_int8_paired_scan(None, None, 1, None, 1, 1, None, None, 8, 4, 5, 2, None, None), EINVAL),
-    (lambda L: L.fms_launch_int8_candidates_scan(None, None, 1, 1, 1, 1, 1, 2, None, None, 8, 4, 2, 5, 7, 3, None, 0.0, None), EINVAL),
+    (lambda L: L.fms_launch_int8_paired_scan(None, None, 1, None, 1, 1, None, None, 8, 4, 5, 2, None, 0, None), EINVAL),
+    (lambda L: L.fms_launch_int8_candidates_scan(None, None, 1, 1, 1, 1, 1, 2, None, None, 8, 4, 2, 5, 7, 3, None, 0.0, 0, None), EINVAL),
     (lambda L: L.fms_int8_dots(None, 1, 1, 8, 4, 5, None), EINVAL),
     (lambda L: L.fms_length_normalize(None, None, 4, 3, 2, None, 0, 0, 0.0, None), EINVAL),
     (lambda L: L.fms_length_normalize(None, None, 4, 0, 2, None, 0, 0, 0.0, None), OK),

@@ -120,3 +120,20 @@ def test_int8_matches_dequantised_fp(device):
     s_hat = fm.maxsim(fm.dequant_int8(q_idx), fm.dequant_int8(d_idx))
     assert abs(s8.item() - s_hat.item()) <= 1e-5 * (1 + abs(s_hat.item()))
     assert abs(fm.maxsim(q, d_idx, normalize=True).item() - s_hat.item() / 8) <= 1e-5 * (1 + abs(s_hat.item()))
+
+
+def test_int8_index_at_rest_scans_identically(device, tmp_path):
+    """A gallery quantised on the device, saved (save_int8_index) and loaded
+    back onto the device, scores bit-identically to the in-memory index."""
+    rng = np.random.default_rng(21)
+    B, Tq, Td, dim = 3, 8, 21, 64
+    Q = torch.from_numpy(tokens(rng, (B, Tq, dim))).to(device)
+    D = torch.from_numpy(tokens(rng, (B, Td, dim))).to(device)
+    idx8 = fm.quantize_int8_symmetric(D)
+    path = str(tmp_path / "g.safetensors")
+    fm.save_int8_index(idx8, path)
+    back = fm.load_int8_index(path, device)
+    assert back.codes.device.type == "cuda"
+    s0 = fm.maxsim(Q, idx8)
+    s1 = fm.maxsim(Q, back)
+    assert torch.equal(s0, s1)

@@ -113,3 +113,48 @@ def test_rrule_refuses_host_arrays_and_bad_config():
         fm.rrule(fm.MaxSim(torch.float32), Q, Q)
     with pytest.raises(fm.ArgumentError):
         fm.rrule("not a config", Q, Q)
+
+
+def test_cu_seqlens_interop():
+    """0-based cu_seqlens <-> 1-based cu (packed.jl:5-6: `cu = cu_seqlens .+ 1`)."""
+    dim = 4
+    tok = torch.randn(9, dim)
+    P = fm.PackedSeq.from_cu_seqlens(tok, [0, 5, 5, 9])
+    assert P.cu.dtype == torch.int32 and P.cu.tolist() == [1, 6, 6, 10]
+    assert P.max_len == 5 and P.nseq() == 3
+    assert P.cu_seqlens().tolist() == [0, 5, 5, 9]
+    P64 = fm.PackedSeq.from_cu_seqlens(tok, torch.tensor([0, 2, 9], dtype=torch.int64))
+    assert P64.cu.tolist() == [1, 3, 10] and P64.max_len == 7
+    # the same validation as a 1-based cu (packed.jl:47-57)
+    with pytest.raises(fm.ArgumentError):
+        fm.PackedSeq.from_cu_seqlens(tok, [1, 5, 9])  # does not start at 0
+    with pytest.raises(fm.ArgumentError):
+        fm.PackedSeq.from_cu_seqlens(tok, [0, 5, 8])  # does not cover the tokens
+    with pytest.raises(fm.ArgumentError):
+        fm.PackedSeq.from_cu_seqlens(tok, [0, 6, 5, 9])  # decreasing
+    with pytest.raises(fm.ArgumentError):
+        fm.PackedSeq.from_cu_seqlens(tok, torch.tensor([0.0, 9.0]))  # not integers
+
+
+def test_int8_index_at_rest_round_trip(tmp_path):
+    """save_int8_index / load_int8_index keep the codes and scales bytes."""
+    g = torch.Generator().manual_seed(0)
+    codes = torch.randint(-127, 128, (6, 11, 32), generator=g, dtype=torch.int8)
+    scales = torch.rand(6, 11, generator=g) * 0.01
+    idx = fm.Int8Index(codes, scales)
+    path = str(tmp_path / "gallery.safetensors")
+    fm.save_int8_index(idx, path)
+    back = fm.load_int8_index(path)
+    assert torch.equal(back.codes, codes) and torch.equal(back.scales, scales)
+    assert back.codes.dtype == torch.int8 and back.scales.dtype == torch.float32
+    # the file's tensors are the in-memory layout, byte for byte
+    from safetensors import safe_open
+    with safe_open(path, framework="pt") as f:
+        assert f.metadata()["format"] == "flashmaxsim-int8-index-v1"
+        assert f.get_tensor("codes").numpy().tobytes() == codes.numpy().tobytes()
+    with pytest.raises(fm.DimensionMismatch):
+        fm.save_int8_index(fm.Int8Index(codes, scales[:, :10]), str(tmp_path / "bad.safetensors"))
+    from safetensors.torch import save_file
+    save_file({"codes": codes, "scales": scales}, str(tmp_path / "plain.safetensors"))
+    with pytest.raises(fm.ArgumentError):
+        fm.load_int8_index(str(tmp_path / "plain.safetensors"))

@@ -68,13 +68,13 @@ hipError_t launch_float(int32_t dtype, const L& lay, int dim, int rows, int64_t 
   switch (dtype) {
     case FMS_F16:
       return launch_scan<OpF16, L>(lay, dim, rows, npairs, args, partial, scores, neg, norm, vec,
-                                   false, st);
+                                   st);
     case FMS_BF16:
-      return launch_scan<OpBF16, L>(lay, dim, rows, npairs, args, partial, scores, neg, norm, vec,
-                                    false, st);
+      return launch_scan<OpBF16, L>(lay, dim, rows, npairs, args, partial, scores, neg, norm,
+                                    vec, st);
     default:
       return launch_scan<OpF32, L>(lay, dim, rows, npairs, args, partial, scores, neg, norm, vec,
-                                   false, st);
+                                   st);
   }
 }
 
@@ -432,10 +432,8 @@ fms_status fms_launch_int8_paired_scan(int32_t* args, float* partial, const int8
   lay.Tq = (int)Tq;
   lay.Td = (int)Td;
   const bool vec = vec_ok(1, dim, {Qc, Dc});
-  const bool ds_vec = (Td % 4 == 0) && aligned16(Ds);
   return from_hip(launch_scan<OpI8, LayPaired>(lay, (int)dim, (int)Tq, B, args, partial, scores,
-                                               0.0f, normalize != 0, vec, ds_vec,
-                                               as_stream(stream)));
+                                               0.0f, normalize != 0, vec, as_stream(stream)));
 }
 
 fms_status fms_launch_int8_pair_scan(int32_t* args, float* partial, const int8_t* qc,
@@ -478,12 +476,11 @@ fms_status fms_launch_int8_candidates_scan(int32_t* args, float* partial, const 
   lay.Tq = (int)Tq;
   lay.Td = (int)Td;
   const bool vec = vec_ok(1, dim, {Qc, Gc});
-  const bool ds_vec = (Td % 4 == 0) && aligned16(Gs);
   const hipStream_t st = as_stream(stream);
   return run_candidates(lay, C * B, st, [&](const auto& L) -> hipError_t {
     typedef typename std::decay<decltype(L)>::type Lay;
     return launch_scan<OpI8, Lay>(L, (int)dim, (int)Tq, C * B, args, partial, scores, neg,
-                                  normalize != 0, vec, ds_vec, st);
+                                  normalize != 0, vec, st);
   });
 }
 

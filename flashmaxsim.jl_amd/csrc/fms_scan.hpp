@@ -52,7 +52,6 @@ struct ScanArgs {
   int rows;       // tape rows per pair (Tq, or max_q for varlen)
   int nqt;        // query tiles per pair = max(1, ceil(rows / 32))
   int ppw;        // pairs per wave
-  int ds_vec;     // int8: document scale rows are 16-byte aligned (Td % 4 == 0)
   int64_t npairs;
   int32_t* args;    // (rows, npairs) nullable
   float* partial;   // (rows, npairs) nullable
@@ -66,7 +65,7 @@ struct Chunk {
   typename Op::Frag a[NKB];
   uint32_t mbyte;                 // document mask byte of row lane%32 (0 when the
                                   // pair has no mask: test with mask_ok)
-  float ds[Op::kInt ? 16 : 1];    // int8: document scale of each accumulator row
+  float ds[1];                    // int8: document scale of chunk row lane%32
 };
 
 // Per-lane query state for one (pair, query tile).
@@ -113,23 +112,15 @@ __device__ __forceinline__ uint32_t chunk_rows_valid(const PairView& v, int ch, 
   return (uint32_t)__ballot(ok);
 }
 
+// int8: each lane loads the document scale of chunk row lane%32 (rows past the
+// document read 0 and are masked).  acc_to_scores fetches the 16 scales of its
+// accumulator rows from the lanes that hold them, so a chunk buffer carries
+// one scale register instead of sixteen.
 template <class Op>
-__device__ __forceinline__ void load_ds(float (&ds)[Op::kInt ? 16 : 1], const PairView& v, int ch,
-                                        int h, bool vec) {
+__device__ __forceinline__ void load_ds(float (&ds)[1], const PairView& v, int ch, int r32) {
   if constexpr (Op::kInt) {
     const rsrc_t rs = make_rsrc_u(v.ds, (uint32_t)v.td * 4u);
-    if (vec) {
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const f32x4 w = buf_load16f(rs, (ch * kTile + 8 * g + 4 * h) * 4);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) ds[4 * g + i] = w[i];
-      }
-    } else {
-#pragma unroll
-      for (int r = 0; r < 16; ++r)
-        ds[r] = __builtin_bit_cast(float, buf_load4(rs, (ch * kTile + acc_row(r, h)) * 4));
-    }
+    ds[0] = __builtin_bit_cast(float, buf_load4(rs, (ch * kTile + r32) * 4));
   }
 }
 
@@ -137,12 +128,11 @@ __device__ __forceinline__ void load_ds(float (&ds)[Op::kInt ? 16 : 1], const Pa
 // evaluated left to right (quant.jl:113, kernels_int8.jl:25).
 template <class Op>
 __device__ __forceinline__ void acc_to_scores(const typename Op::Acc& acc, float qscale,
-                                              const float (&ds)[Op::kInt ? 16 : 1],
-                                              float (&s)[16]) {
+                                              const float (&ds)[1], int h, float (&s)[16]) {
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     if constexpr (Op::kInt) {
-      const float sc = qscale * ds[r];
+      const float sc = qscale * __shfl(ds[0], acc_row(r, h), 64);
       s[r] = sc * (float)acc[r];
     } else {
       s[r] = acc[r];
@@ -205,8 +195,7 @@ __device__ __forceinline__ void write_score(const ScanArgs<L>& A, const PairView
 
 template <class Op, int NKB>
 __device__ __forceinline__ void load_chunk(Chunk<Op, NKB>& c, const PairView& v, int ch, int nkb,
-                                           int rowbytes, int lane_off, int r32, int h,
-                                           bool ds_vec) {
+                                           int rowbytes, int lane_off, int r32) {
   const rsrc_t rd = make_rsrc_u(v.d, (uint32_t)v.td * (uint32_t)rowbytes);
   const int base = ch * kTile * rowbytes + lane_off;
 #pragma unroll
@@ -219,7 +208,7 @@ __device__ __forceinline__ void load_chunk(Chunk<Op, NKB>& c, const PairView& v,
                                               has_m ? (uint32_t)v.td : 0u),
                                   ch * kTile + r32);
   c.mbyte = mraw;
-  load_ds<Op>(c.ds, v, ch, h, ds_vec);
+  load_ds<Op>(c.ds, v, ch, r32);
 }
 
 template <class Op, int NKB>
@@ -250,7 +239,6 @@ __global__ void __launch_bounds__(64 * kWaves) scan_fast(const ScanArgs<L> A) {
   const int rowbytes = A.dim * Op::kEsz;
   const int lane_off = r32 * rowbytes + h * Op::kEpl * Op::kEsz;
   const int nkb = A.nkb;
-  const bool ds_vec = A.ds_vec != 0;
 
   // wave cursor: position index pi (pair view v), query tile qt, chunk ch of nch
   int pi = 0;
@@ -265,7 +253,7 @@ __global__ void __launch_bounds__(64 * kWaves) scan_fast(const ScanArgs<L> A) {
   float mx = -INFINITY, score = 0.0f;
   int slot = -1;
 
-  load_chunk<Op, NKB>(bufA, v, 0, nkb, rowbytes, lane_off, r32, h, ds_vec);
+  load_chunk<Op, NKB>(bufA, v, 0, nkb, rowbytes, lane_off, r32);
 
   // One step: make sure the query tile is resident, prefetch the next chunk
   // into `nxt`, multiply `cur`, fold it into the running max, and close the
@@ -303,8 +291,7 @@ __global__ void __launch_bounds__(64 * kWaves) scan_fast(const ScanArgs<L> A) {
     // Unconditional: after the wave's last chunk it re-reads the current one
     // (an L2 hit), so every step issues the same loads and the MFMAs below
     // wait only for the chunk they multiply.
-    load_chunk<Op, NKB>(nxt, more ? nv : v, more ? nch_i : ch, nkb, rowbytes, lane_off, r32, h,
-                        ds_vec);
+    load_chunk<Op, NKB>(nxt, more ? nv : v, more ? nch_i : ch, nkb, rowbytes, lane_off, r32);
     // Keep the prefetch ahead of the MFMAs: the scheduler would otherwise
     // sink the independent loads below them and nothing would overlap.
     __builtin_amdgcn_sched_barrier(0);
@@ -313,7 +300,7 @@ __global__ void __launch_bounds__(64 * kWaves) scan_fast(const ScanArgs<L> A) {
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) acc = Op::mma(cur.a[kb], q.f[kb], acc);
     float s[16];
-    acc_to_scores<Op>(acc, q.qscale, cur.ds, s);
+    acc_to_scores<Op>(acc, q.qscale, cur.ds, h, s);
     update_chunk(s, m32, h, ch, mx, slot);
 
     if (ch == nch - 1) {
@@ -406,10 +393,10 @@ __global__ void __launch_bounds__(64 * kWaves) scan_generic(const ScanArgs<L> A)
         }
         uint32_t mbyte = 1u;
         if (v.dm) mbyte = buf_load1(make_rsrc_u(v.dm, (uint32_t)v.td), row);
-        float ds[Op::kInt ? 16 : 1];
-        load_ds<Op>(ds, v, ch, h, false);
+        float ds[1];
+        load_ds<Op>(ds, v, ch, r32);
         float s[16];
-        acc_to_scores<Op>(acc, qscale, ds, s);
+        acc_to_scores<Op>(acc, qscale, ds, h, s);
         update_chunk(s, chunk_rows_valid(v, ch, r32, mbyte), h, ch, mx, slot);
       }
       score += finish_tile(A, v.out, qt, r32, h, tvalid, mx, slot);
@@ -443,7 +430,7 @@ inline int pairs_per_wave(int64_t npairs) {
 template <class Op, class L>
 hipError_t launch_scan(const L& lay, int dim, int rows, int64_t npairs, int32_t* args,
                        float* partial, float* scores, float neg, bool norm, bool vec,
-                       bool ds_vec, hipStream_t stream) {
+                       hipStream_t stream) {
   ScanArgs<L> A;
   A.lay = lay;
   A.dim = dim;
@@ -451,7 +438,6 @@ hipError_t launch_scan(const L& lay, int dim, int rows, int64_t npairs, int32_t*
   A.rows = rows;
   A.nqt = rows > 0 ? (rows + kTile - 1) / kTile : 1;
   A.ppw = pairs_per_wave(npairs);
-  A.ds_vec = ds_vec ? 1 : 0;
   A.npairs = npairs;
   A.args = args;
   A.partial = partial;

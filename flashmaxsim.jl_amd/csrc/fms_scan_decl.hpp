@@ -14,6 +14,6 @@ namespace fms {
 template <class Op, class L>
 hipError_t launch_scan(const L& lay, int dim, int rows, int64_t npairs, int32_t* args,
                        float* partial, float* scores, float neg, bool norm, bool vec,
-                       bool ds_vec, hipStream_t stream);
+                       hipStream_t stream);
 
 }  // namespace fms

@@ -5,7 +5,7 @@
 namespace fms {
 #define FMS_INST(L)                                                                    \
   template hipError_t launch_scan<OpI8, L>(const L&, int, int, int64_t, int32_t*, float*, \
-                                           float*, float, bool, bool, bool, hipStream_t);
+                                           float*, float, bool, bool, hipStream_t);
 FMS_INST(LayPaired)
 FMS_INST(LayCand)
 FMS_INST(LayCandSorted)

@@ -38,13 +38,13 @@ struct SplitBatch {
   uint32_t mbyte;                // raw document mask byte of row lane%32
   uint32_t qmbyte;               // raw query mask byte of token lane%32
   float qscale;                  // int8 query scale of token lane%32
-  float ds[Op::kInt ? 16 : 1];   // int8 document scales of the accumulator rows
+  float ds[1];                   // int8 document scale of chunk row lane%32
 };
 
 template <class Op, int KBAT, bool kLdsQ>
 __device__ __forceinline__ void load_split(SplitBatch<Op, KBAT>& c, const PairView& v, int qt,
                                            int ch, int bi, int rowbytes, int h, int r32,
-                                           bool ds_vec, const u32x4* qlds, int nkb) {
+                                           const u32x4* qlds, int nkb) {
   const int kofs = (bi * KBAT * Op::kKb + h * Op::kEpl) * Op::kEsz;
   const rsrc_t rd = make_rsrc_u(v.d, (uint32_t)v.td * (uint32_t)rowbytes);
   const rsrc_t rq = make_rsrc_u(v.q, (uint32_t)v.tq * (uint32_t)rowbytes);
@@ -70,7 +70,7 @@ __device__ __forceinline__ void load_split(SplitBatch<Op, KBAT>& c, const PairVi
   if constexpr (Op::kInt)
     c.qscale = __builtin_bit_cast(float, buf_load4(make_rsrc_u(v.qs, (uint32_t)v.tq * 4u),
                                                    (qt * kTile + r32) * 4));
-  load_ds<Op>(c.ds, v, ch, h, ds_vec);
+  load_ds<Op>(c.ds, v, ch, r32);
 }
 
 template <class Op, class L, int KBAT, bool kLdsQ>
@@ -108,7 +108,6 @@ __global__ void __launch_bounds__(64 * kWaves) scan_split(const ScanArgs<L> A) {
   if (cnt <= 0) return;
   const int rowbytes = A.dim * Op::kEsz;
   const int nbat = A.nkb / KBAT;
-  const bool ds_vec = A.ds_vec != 0;
 
   // wave cursor: position index pi (view v), query tile qt, chunk ch of
   // nch, batch bi of nbat
@@ -121,7 +120,7 @@ __global__ void __launch_bounds__(64 * kWaves) scan_split(const ScanArgs<L> A) {
   float mx = -INFINITY, score = 0.0f;
   int slot = -1;
 
-  load_split<Op, KBAT, kLdsQ>(bufA, v, 0, 0, 0, rowbytes, h, r32, ds_vec, qlds, A.nkb);
+  load_split<Op, KBAT, kLdsQ>(bufA, v, 0, 0, 0, rowbytes, h, r32, qlds, A.nkb);
 
   auto step = [&](SplitBatch<Op, KBAT>& cur, SplitBatch<Op, KBAT>& nxt) -> bool {
     // advance a copy of the cursor and prefetch its batch
@@ -147,7 +146,7 @@ __global__ void __launch_bounds__(64 * kWaves) scan_split(const ScanArgs<L> A) {
     // the current one): two calls under `if (more)` get merged with their
     // arguments as divergent phis, and the loads become waterfall loops.
     load_split<Op, KBAT, kLdsQ>(nxt, more ? nv : v, more ? nqt_i : qt, more ? nch_i : ch,
-                                more ? nbi : bi, rowbytes, h, r32, ds_vec, qlds, A.nkb);
+                                more ? nbi : bi, rowbytes, h, r32, qlds, A.nkb);
     __builtin_amdgcn_sched_barrier(0);
 
 #pragma unroll
@@ -165,7 +164,7 @@ __global__ void __launch_bounds__(64 * kWaves) scan_split(const ScanArgs<L> A) {
       acc0 = Acc{};
       acc1 = Acc{};
       float s[16];
-      acc_to_scores<Op>(acc, cur.qscale, cur.ds, s);
+      acc_to_scores<Op>(acc, cur.qscale, cur.ds, h, s);
       update_chunk(s, chunk_rows_valid(v, ch, r32, cur.mbyte), h, ch, mx, slot);
       if (ch == nch - 1) {
         uint32_t qmb = cur.qmbyte;

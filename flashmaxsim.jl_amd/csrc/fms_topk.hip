@@ -22,6 +22,10 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
+#include <cmath>
+
+#include "fms_group.hpp"
 #include "fms_topk.hpp"
 
 namespace fms {
@@ -31,6 +35,9 @@ namespace {
 constexpr int kTkThreads = 1024;
 constexpr int kTkWaves = kTkThreads / 64;
 constexpr int kTkBins = 256;
+constexpr int64_t kTkMinSlice = 512;    // entries per slice of the two-stage split, at least
+constexpr int64_t kTkMaxBlocks = 512;   // workgroups of the first stage (one round), at most
+constexpr int64_t kTkSplitCols = 16384; // rows shorter than this are ranked in one stage
 
 // Order-preserving key: unsigned order of keys = isless order of floats.
 __device__ __forceinline__ uint32_t order_key(float f) {
@@ -53,8 +60,15 @@ __device__ __forceinline__ uint32_t wave_inclusive_sum(uint32_t v, int lane) {
   return v;
 }
 
+// Block b ranks slice b % nslices of row b / nslices: entries [c0, c1) of the
+// row (ld apart), c0 = slice * ncols / nslices.  An entry's index is its
+// column, or (kIdx) the 1-based index stored beside it in SI; ties go to the
+// smaller index either way.  Out: k entries at vals/idx[b * k ...], 1-based.
+template <bool kIdx>
 __global__ void __launch_bounds__(kTkThreads) topk_rows_kernel(const float* __restrict__ S,
-                                                               int64_t ncols, int k, int kpow2,
+                                                               const int32_t* __restrict__ SI,
+                                                               int64_t ld, int64_t ncols,
+                                                               int nslices, int k, int kpow2,
                                                                float* __restrict__ vals,
                                                                int32_t* __restrict__ idx) {
   __shared__ uint32_t hist[kTkBins];
@@ -63,8 +77,16 @@ __global__ void __launch_bounds__(kTkThreads) topk_rows_kernel(const float* __re
   __shared__ uint64_t pick[kTopkMaxK];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t row = blockIdx.x;
-  const float* const s = S + row * ncols;
+  const int64_t row = blockIdx.x / nslices, slice = blockIdx.x % nslices;
+  const int64_t c0 = slice * ncols / nslices, n = (slice + 1) * ncols / nslices - c0;
+  const float* const s = S + row * ld + c0;
+  // 0-based index of entry i (i < n)
+  auto index_of = [&](int64_t i) -> uint32_t {
+    if constexpr (kIdx)
+      return (uint32_t)SI[row * ld + c0 + i] - 1u;
+    else
+      return (uint32_t)(c0 + i);
+  };
 
   // ---- 1. radix select: T = the k-th largest key ---------------------------------
   // Invariant: 1 <= need <= (entries whose key matches prefix under pmask); the
@@ -75,7 +97,7 @@ __global__ void __launch_bounds__(kTkThreads) topk_rows_kernel(const float* __re
     for (int b = tid; b < kTkBins; b += kTkThreads) hist[b] = 0u;
     __syncthreads();
 #pragma unroll 4
-    for (int64_t i = tid; i < ncols; i += kTkThreads) {
+    for (int64_t i = tid; i < n; i += kTkThreads) {
       const uint32_t key = order_key(s[i]);
       if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 0xffu], 1u);
     }
@@ -115,11 +137,11 @@ __global__ void __launch_bounds__(kTkThreads) topk_rows_kernel(const float* __re
   // ---- 2. ordered collection -------------------------------------------------------
   // pick = (key << 32) | ~index: descending order of pick is the output order.
   uint32_t base_gt = 0u, base_eq = 0u;
-  for (int64_t t0 = 0; t0 < ncols; t0 += kTkThreads) {
+  for (int64_t t0 = 0; t0 < n; t0 += kTkThreads) {
     const int64_t i = t0 + tid;
-    const uint32_t key = i < ncols ? order_key(s[i]) : 0u;
-    const uint32_t gt = (i < ncols && key > T) ? 1u : 0u;
-    const uint32_t eq = (i < ncols && key == T) ? 1u : 0u;
+    const uint32_t key = i < n ? order_key(s[i]) : 0u;
+    const uint32_t gt = (i < n && key > T) ? 1u : 0u;
+    const uint32_t eq = (i < n && key == T) ? 1u : 0u;
     const uint32_t v = gt | (eq << 16);  // (at most 1024 of each per tile)
     const uint32_t inc = wave_inclusive_sum(v, lane);
     if (lane == 63) wsum[wave] = inc;
@@ -132,7 +154,8 @@ __global__ void __launch_bounds__(kTkThreads) topk_rows_kernel(const float* __re
       tot += x;
     }
     const uint32_t ex = off + inc - v;
-    const uint64_t p = ((uint64_t)key << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
+    const uint64_t p =
+        ((uint64_t)key << 32) | (uint64_t)(0xffffffffu - (i < n ? index_of(i) : 0u));
     if (gt) {  // exactly ngt entries lie above T (the guard holds for a row read unchanged)
       const uint32_t r = base_gt + (ex & 0xffffu);
       if (r < ngt) pick[r] = p;
@@ -169,8 +192,8 @@ __global__ void __launch_bounds__(kTkThreads) topk_rows_kernel(const float* __re
   __syncthreads();
   for (int e = tid; e < k; e += kTkThreads) {
     const uint64_t p = pick[e];
-    vals[row * k + e] = key_value((uint32_t)(p >> 32));
-    idx[row * k + e] = (int32_t)(0xffffffffu - (uint32_t)p) + 1;
+    vals[(int64_t)blockIdx.x * k + e] = key_value((uint32_t)(p >> 32));
+    idx[(int64_t)blockIdx.x * k + e] = (int32_t)(0xffffffffu - (uint32_t)p) + 1;
   }
 }
 
@@ -180,9 +203,39 @@ hipError_t topk_rows(const float* S, int64_t nrows, int64_t ncols, int k, float*
                      int32_t* idx, hipStream_t stream) {
   int kpow2 = 1;
   while (kpow2 < k) kpow2 <<= 1;
-  hipLaunchKernelGGL(topk_rows_kernel, dim3((unsigned)nrows), dim3(kTkThreads), 0, stream, S,
-                     ncols, k, kpow2, vals, idx);
-  return hipGetLastError();
+  // One workgroup ranks a row in time proportional to its length (LDS
+  // histogram atomics), so rows of kTkSplitCols entries or more are first cut
+  // into G slices, each ranked by its own workgroup (G ~ sqrt(ncols / k),
+  // every slice at least max(k, kTkMinSlice) entries, one round of at most
+  // kTkMaxBlocks workgroups; a second launch costs more than it saves on
+  // shorter rows), and the
+  // G * k survivors of a row -- slice-major, so equal scores stay in index
+  // order -- are ranked again.  The global top-k lies within the union of the
+  // slice top-ks under the same (score, index) order, so the result is exact.
+  int64_t G = (int64_t)std::sqrt((double)ncols / (double)k);
+  G = std::min<int64_t>(G, ncols / std::max<int64_t>(k, kTkMinSlice));
+  G = std::min<int64_t>(G, std::max<int64_t>(1, kTkMaxBlocks / nrows));
+  if (ncols < kTkSplitCols || G < 2) {
+    hipLaunchKernelGGL(topk_rows_kernel<false>, dim3((unsigned)nrows), dim3(kTkThreads), 0,
+                       stream, S, nullptr, ncols, ncols, 1, k, kpow2, vals, idx);
+    return hipGetLastError();
+  }
+  void* ws = nullptr;
+  const size_t nsurv = (size_t)(nrows * G * k);
+  hipError_t e = workspace_alloc(&ws, nsurv * 8, stream);
+  if (e != hipSuccess) return e;
+  float* sv = static_cast<float*>(ws);
+  int32_t* si = reinterpret_cast<int32_t*>(sv + nsurv);
+  hipLaunchKernelGGL(topk_rows_kernel<false>, dim3((unsigned)(nrows * G)), dim3(kTkThreads), 0,
+                     stream, S, nullptr, ncols, ncols, (int)G, k, kpow2, sv, si);
+  e = hipGetLastError();
+  if (e == hipSuccess) {
+    hipLaunchKernelGGL(topk_rows_kernel<true>, dim3((unsigned)nrows), dim3(kTkThreads), 0,
+                       stream, sv, si, G * k, G * k, 1, k, kpow2, vals, idx);
+    e = hipGetLastError();
+  }
+  const hipError_t ef = workspace_free(ws, stream);
+  return e != hipSuccess ? e : ef;
 }
 
 }  // namespace fms

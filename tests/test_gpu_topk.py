@@ -4,8 +4,10 @@ stable partialsortperm(rev = true), README.md:132) against the CPU oracle.
 Bit-exact: the same values (NaN where the oracle has a NaN; the kernel writes
 one canonical NaN) and the same 1-based indices, at row widths that are not
 multiples of the 1024-entry tile, k from 1 to the 1024 maximum and k = ncols,
-heavy ties (three levels, all equal), NaN / +-Inf / signed zeros, and the
-score matrices the multi-query packed and in-batch scans write.
+heavy ties (three levels, all equal), NaN / +-Inf / signed zeros -- in rows
+short enough for one workgroup and long enough for the two-stage split, where
+ties cross slice boundaries -- and the score matrices the multi-query packed
+and in-batch scans write.
 """
 import numpy as np
 import pytest
@@ -39,10 +41,11 @@ def test_topk_random_rows(device, nrows, ncols, k):
     _check(fm.topk(torch.from_numpy(S).to(device), k), S, k)
 
 
+@pytest.mark.parametrize("ncols", [4099, 40000])  # one stage; two stages (ties across slices)
 @pytest.mark.parametrize("kind", ["three_levels", "all_equal", "special"])
-def test_topk_ties_and_special_values(device, kind):
+def test_topk_ties_and_special_values(device, kind, ncols):
     rng = np.random.default_rng(5)
-    nrows, ncols, k = 4, 4099, 300
+    nrows, k = 4, 300
     if kind == "three_levels":
         S = rng.integers(0, 3, size=(nrows, ncols)).astype(np.float32)
     elif kind == "all_equal":
@@ -53,7 +56,7 @@ def test_topk_ties_and_special_values(device, kind):
         vals = np.array([np.nan, -np.nan, np.inf, -np.inf, 0.0, -0.0], np.float32)
         for r in range(nrows):
             S[r, picks[r]] = vals[rng.integers(0, len(vals), 60)]
-    print(f"topk {kind}", flush=True)
+    print(f"topk {kind} ncols={ncols}", flush=True)
     _check(fm.topk(torch.from_numpy(S).to(device), k), S, k)
 
 

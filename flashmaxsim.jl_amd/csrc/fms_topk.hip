@@ -9,7 +9,7 @@
 // NaN above +Inf, -0.0 below +0.0), equal scores by smaller index -- what a
 // stable reverse sort returns.
 //
-// One 1024-thread workgroup per row, three phases, no workspace:
+// One 1024-thread workgroup ranks a row (or a slice of one) in three phases:
 //   1. radix select over the 32-bit order keys, 8 bits per pass from the top
 //      (4 passes; LDS histogram of the entries still matching the prefix):
 //      the k-th largest key T and how many entries lie strictly above it;

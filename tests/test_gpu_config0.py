@@ -1,4 +1,4 @@
-"""GPU: BASELINE configs[0] at its exact shape -- paired-batch MaxSim in Float32,
+"""GPU: the benchmark's CPU-runnable configuration at its exact shape -- paired-batch MaxSim in Float32,
 Q (128, 32, 64) and D (128, 180, 64) in Julia terms (torch (64, 32, 128) and
 (64, 180, 128)), randn token columns L2-normalised, all-true masks; outputs the
 64 scores and the 32 x 64 Int32 argmax tape.  This is the reference's own

@@ -521,7 +521,8 @@ fms_status fms_varlen_normalize(float* scores, const int32_t* cu_q, int64_t N, v
 fms_status fms_topk(const float* scores, int64_t nrows, int64_t ncols, int64_t k, float* vals,
                     int32_t* idx, void* stream) {
   if (nrows < 0 || ncols < 0 || k < 0 || k > ncols) return FMS_EINVAL;
-  if (ncols > INT32_MAX || nrows > (int64_t)UINT32_MAX || k > kTopkMaxK) return FMS_EUNSUPPORTED;
+  // (one 1024-thread workgroup per row: the grid's work-items must fit 32 bits)
+  if (ncols > INT32_MAX || nrows > kTopkMaxRows || k > kTopkMaxK) return FMS_EUNSUPPORTED;
   if (nrows == 0 || k == 0) return FMS_OK;
   if (!scores || !vals || !idx) return FMS_EINVAL;
   return from_hip(topk_rows(scores, nrows, ncols, (int)k, vals, idx, as_stream(stream)));

@@ -170,11 +170,12 @@ fms_status fms_launch_packed_scan(int32_t dtype, int32_t* args, float* partial,
  * fms_inbatch_device_scan write them; vals (k, nrows) receives each column's
  * k largest scores in descending order, idx (k, nrows) their 1-based row
  * indices.  Order: Julia's isless reversed (NaN first, +0.0 before -0.0),
- * equal scores by smaller index -- a stable reverse sort.  1 <= k <= 1024
- * (larger k: FMS_EUNSUPPORTED); k > ncols is FMS_EINVAL (a BoundsError in
- * partialsortperm).  One 1024-thread workgroup per column; columns of 16,384
- * rows or more are first ranked in slices (a workspace of 8 * k bytes per
- * slice from the library pool) and the slices' survivors ranked again.
+ * equal scores by smaller index -- a stable reverse sort.  1 <= k <= 1024 and
+ * at most 2^22 - 1 columns of scores, else FMS_EUNSUPPORTED; k > ncols is
+ * FMS_EINVAL (a BoundsError in partialsortperm).  One 1024-thread workgroup
+ * per column; columns of 16,384 rows or more are first ranked in slices (a
+ * workspace of 8 * k bytes per slice from the library pool) and the slices'
+ * survivors ranked again.
  */
 fms_status fms_topk(const float* scores, int64_t nrows, int64_t ncols, int64_t k, float* vals,
                     int32_t* idx, void* stream);

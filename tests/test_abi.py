@@ -95,6 +95,7 @@ EINVAL, EUNSUP, OK = _lib.FMS_EINVAL, _lib.FMS_EUNSUPPORTED, _lib.FMS_OK
     # top-k: k beyond the row, k beyond the LDS sort, empty, NULL buffers
     (lambda L: L.fms_topk(None, 2, 5, 6, None, None, None), EINVAL),
     (lambda L: L.fms_topk(None, 2, 5000, 1025, None, None, None), EUNSUP),
+    (lambda L: L.fms_topk(None, 1 << 22, 5, 3, None, None, None), EUNSUP),
     (lambda L: L.fms_topk(None, 0, 5, 3, None, None, None), OK),
     (lambda L: L.fms_topk(None, 2, 5, 0, None, None, None), OK),
     (lambda L: L.fms_topk(None, 2, 5, 3, None, None, None), EINVAL),

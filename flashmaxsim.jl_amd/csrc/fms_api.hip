@@ -83,6 +83,7 @@ fms_status run_float(int32_t dtype, const L& lay, int dim, int rows, int64_t npa
                      int32_t* args, float* partial, float* scores, float neg, bool norm, bool vec,
                      hipStream_t st) {
   if (elem_bytes(dtype) == 0) return FMS_EUNSUPPORTED;
+  if (!scan_grid_fits(npairs)) return FMS_EUNSUPPORTED;  // 32-bit work-item count
   return from_hip(
       launch_float(dtype, lay, dim, rows, npairs, args, partial, scores, neg, norm, vec, st));
 }
@@ -118,6 +119,7 @@ bool group_candidates(int64_t P, int64_t N, int64_t dbytes) {
 // back to output order: the results are identical either way.
 template <class Launch>
 fms_status run_candidates(const LayCand& lay, int64_t npairs, hipStream_t st, Launch&& launch) {
+  if (!scan_grid_fits(npairs)) return FMS_EUNSUPPORTED;  // 32-bit work-item count
   if (group_candidates(npairs, lay.N, lay.dbytes)) {
     void* ws = nullptr;
     if (workspace_alloc(&ws, group_workspace_bytes(npairs, lay.N), st) == hipSuccess) {
@@ -131,6 +133,21 @@ fms_status run_candidates(const LayCand& lay, int64_t npairs, hipStream_t st, La
     (void)hipGetLastError();  // clear the failed allocation; scan in output order
   }
   return from_hip(launch(lay));
+}
+
+// Byte width of an INT8 scale type (fp32 or fp16); 0 = not a scale type.
+int scale_bytes(int32_t dtype) {
+  return dtype == FMS_F32 ? 4 : (dtype == FMS_F16 ? 2 : 0);
+}
+
+// The INT8 scan for the document-scale width (fp32: OpI8, fp16: OpI8H).
+template <class L>
+hipError_t launch_int8(int ds_esz, const L& lay, int dim, int rows, int64_t npairs, int32_t* args,
+                       float* partial, float* scores, float neg, bool norm, bool vec,
+                       hipStream_t st) {
+  if (ds_esz == 2)
+    return launch_scan<OpI8H, L>(lay, dim, rows, npairs, args, partial, scores, neg, norm, vec, st);
+  return launch_scan<OpI8, L>(lay, dim, rows, npairs, args, partial, scores, neg, norm, vec, st);
 }
 
 }  // namespace
@@ -245,6 +262,7 @@ fms_status fms_launch_candidates_scan(int32_t dtype, int32_t* args, float* parti
   if (idx_bytes != 4 && idx_bytes != 8) return FMS_EINVAL;
   if (!seq_ok(Tq, dim, esz) || !seq_ok(Td, dim, esz)) return FMS_EUNSUPPORTED;
   if (C == 0 || B == 0 || (Tq == 0 && !scores)) return FMS_OK;
+  if (B > INT64_MAX / C) return FMS_EUNSUPPORTED;
   if (!idx || (Tq * dim > 0 && !Q) || (N * Td * dim > 0 && !gallery)) return FMS_EINVAL;
   LayCand lay;
   lay.Q = static_cast<const char*>(Q);
@@ -402,19 +420,24 @@ fms_status fms_launch_varlen_scan(int32_t dtype, int32_t* args, float* partial,
                    normalize != 0, vec_ok(esz, dim, {Qtokens, Dtokens}), as_stream(stream));
 }
 
-fms_status fms_int8_quantize(const float* X, int8_t* codes, float* scales, int64_t dim,
-                             int64_t ntok, void* stream) {
+fms_status fms_int8_quantize(int32_t dtype, const void* X, int8_t* codes, void* scales,
+                             int64_t dim, int64_t ntok, void* stream) {
+  if (dtype != FMS_F32 && dtype != FMS_F16) return FMS_EUNSUPPORTED;
   if (dim < 0 || ntok < 0 || dim > kMaxTokens) return FMS_EINVAL;
   if (ntok == 0) return FMS_OK;
   if (!scales || (dim > 0 && (!X || !codes))) return FMS_EINVAL;
-  return from_hip(quantize_int8(X, codes, scales, (int)dim, ntok, as_stream(stream)));
+  return from_hip(quantize_int8(dtype == FMS_F16, X, codes, scales, (int)dim, ntok,
+                                as_stream(stream)));
 }
 
 fms_status fms_launch_int8_paired_scan(int32_t* args, float* partial, const int8_t* Qc,
-                                       const float* Qs, const int8_t* Dc, const float* Ds,
-                                       const uint8_t* qmask, const uint8_t* dmask, int64_t dim,
-                                       int64_t Tq, int64_t Td, int64_t B, float* scores,
-                                       int32_t normalize, void* stream) {
+                                       const void* Qs, int32_t qs_dtype, const int8_t* Dc,
+                                       const void* Ds, int32_t ds_dtype, const uint8_t* qmask,
+                                       const uint8_t* dmask, int64_t dim, int64_t Tq, int64_t Td,
+                                       int64_t B, float* scores, int32_t normalize,
+                                       void* stream) {
+  const int qs_esz = scale_bytes(qs_dtype), ds_esz = scale_bytes(ds_dtype);
+  if (qs_esz == 0 || ds_esz == 0) return FMS_EUNSUPPORTED;
   if (dim < 0 || Tq < 0 || Td < 0 || B < 0 || (normalize & ~1)) return FMS_EINVAL;
   if (!seq_ok(Tq, dim, 4) || !seq_ok(Td, dim, 4)) return FMS_EUNSUPPORTED;
   if (B == 0 || (Tq == 0 && !scores)) return FMS_OK;
@@ -425,33 +448,39 @@ fms_status fms_launch_int8_paired_scan(int32_t* args, float* partial, const int8
   lay.D = reinterpret_cast<const char*>(Dc);
   lay.qm = qmask;
   lay.dm = dmask;
-  lay.Qs = Qs;
-  lay.Ds = Ds;
+  lay.Qs = static_cast<const char*>(Qs);
+  lay.Ds = static_cast<const char*>(Ds);
   lay.qbytes = Tq * dim;
   lay.dbytes = Td * dim;
   lay.Tq = (int)Tq;
   lay.Td = (int)Td;
+  lay.qs_esz = qs_esz;
+  lay.ds_esz = ds_esz;
   const bool vec = vec_ok(1, dim, {Qc, Dc});
-  return from_hip(launch_scan<OpI8, LayPaired>(lay, (int)dim, (int)Tq, B, args, partial, scores,
-                                               0.0f, normalize != 0, vec, as_stream(stream)));
+  if (!scan_grid_fits(B)) return FMS_EUNSUPPORTED;
+  return from_hip(launch_int8(ds_esz, lay, (int)dim, (int)Tq, B, args, partial, scores, 0.0f,
+                              normalize != 0, vec, as_stream(stream)));
 }
 
 fms_status fms_launch_int8_pair_scan(int32_t* args, float* partial, const int8_t* qc,
-                                     const float* qs, const int8_t* dc, const float* ds,
-                                     const uint8_t* qmask, const uint8_t* dmask, int64_t dim,
-                                     int64_t Tq, int64_t Td, float* score, int32_t normalize,
-                                     void* stream) {
-  return fms_launch_int8_paired_scan(args, partial, qc, qs, dc, ds, qmask, dmask, dim, Tq, Td, 1,
-                                     score, normalize, stream);
+                                     const void* qs, int32_t qs_dtype, const int8_t* dc,
+                                     const void* ds, int32_t ds_dtype, const uint8_t* qmask,
+                                     const uint8_t* dmask, int64_t dim, int64_t Tq, int64_t Td,
+                                     float* score, int32_t normalize, void* stream) {
+  return fms_launch_int8_paired_scan(args, partial, qc, qs, qs_dtype, dc, ds, ds_dtype, qmask,
+                                     dmask, dim, Tq, Td, 1, score, normalize, stream);
 }
 
 fms_status fms_launch_int8_candidates_scan(int32_t* args, float* partial, const int8_t* Qc,
-                                           const float* Qs, const int8_t* Gc, const float* Gs,
-                                           const void* idx, int32_t idx_bytes,
-                                           const uint8_t* qmask, const uint8_t* dmask,
-                                           int64_t dim, int64_t Tq, int64_t B, int64_t Td,
-                                           int64_t N, int64_t C, float* scores, float neg,
-                                           int32_t normalize, void* stream) {
+                                           const void* Qs, int32_t qs_dtype, const int8_t* Gc,
+                                           const void* Gs, int32_t ds_dtype, const void* idx,
+                                           int32_t idx_bytes, const uint8_t* qmask,
+                                           const uint8_t* dmask, int64_t dim, int64_t Tq,
+                                           int64_t B, int64_t Td, int64_t N, int64_t C,
+                                           float* scores, float neg, int32_t normalize,
+                                           void* stream) {
+  const int qs_esz = scale_bytes(qs_dtype), ds_esz = scale_bytes(ds_dtype);
+  if (qs_esz == 0 || ds_esz == 0) return FMS_EUNSUPPORTED;
   if (dim < 0 || Tq < 0 || Td < 0 || B < 0 || N < 0 || C < 0 || (normalize & ~1))
     return FMS_EINVAL;
   if (idx_bytes != 4 && idx_bytes != 8) return FMS_EINVAL;
@@ -467,20 +496,21 @@ fms_status fms_launch_int8_candidates_scan(int32_t* args, float* partial, const 
   lay.idx64 = idx_bytes == 8;
   lay.qm = qmask;
   lay.dm = dmask;
-  lay.Qs = Qs;
-  lay.Gs = Gs;
+  lay.Qs = static_cast<const char*>(Qs);
+  lay.Gs = static_cast<const char*>(Gs);
   lay.qbytes = Tq * dim;
   lay.dbytes = Td * dim;
   lay.N = N;
   lay.C = C;
   lay.Tq = (int)Tq;
   lay.Td = (int)Td;
+  lay.qs_esz = qs_esz;
+  lay.ds_esz = ds_esz;
   const bool vec = vec_ok(1, dim, {Qc, Gc});
   const hipStream_t st = as_stream(stream);
   return run_candidates(lay, C * B, st, [&](const auto& L) -> hipError_t {
-    typedef typename std::decay<decltype(L)>::type Lay;
-    return launch_scan<OpI8, Lay>(L, (int)dim, (int)Tq, C * B, args, partial, scores, neg,
-                                  normalize != 0, vec, st);
+    return launch_int8(ds_esz, L, (int)dim, (int)Tq, C * B, args, partial, scores, neg,
+                       normalize != 0, vec, st);
   });
 }
 

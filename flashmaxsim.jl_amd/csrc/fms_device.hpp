@@ -119,9 +119,14 @@ struct OpBF16 : OpF16 {
   }
 };
 
-struct OpI8 {
+// INT8 codes; kDsHalf: the document scales are stored as fp16 (an
+// Int8Index quantised from Float16 features keeps Float16 scales) rather
+// than fp32.  Both widen exactly to fp32 before the dequant.
+template <bool kDsHalf_>
+struct OpI8T {
   static constexpr int kEsz = 1, kEpl = 16, kKb = 32;
   static constexpr bool kInt = true;
+  static constexpr bool kDsHalf = kDsHalf_;
   typedef u32x4 Frag;
   typedef i32x16 Acc;
   __device__ static Frag zero() { return u32x4{0u, 0u, 0u, 0u}; }
@@ -145,6 +150,8 @@ struct OpI8 {
     return u32x4{w[0], w[1], w[2], w[3]};
   }
 };
+typedef OpI8T<false> OpI8;   // fp32 document scales
+typedef OpI8T<true> OpI8H;   // fp16 document scales
 
 struct OpF32 {
   static constexpr int kEsz = 4, kEpl = 1, kKb = 2;
@@ -179,15 +186,27 @@ __device__ __forceinline__ constexpr int acc_row(int r, int h) {
 // fold_tree: a v_max3 tree gives the chunk maximum, a reverse scan the first
 // register equal to it -- short dependency chains, ~2.6 VALU ops per score.
 // Every row must hold a valid token (callers substitute masked rows).
+//
+// The maxima are v_max3_f32 written out: in the IEEE mode compute kernels
+// run in, a quiet NaN operand is ignored (the hardware's maxNum), so NaN
+// scores never become the chunk maximum -- as NaN never compares greater in
+// the reference's `s > mx`.  Written through the compiler's fmax it would
+// insert an input canonicalisation per tree unless told NaNs cannot occur.
+__device__ __forceinline__ float max3_ieee(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
 __device__ __forceinline__ void fold_tree(const float (&s)[16], int slot0, float& mx, int& slot) {
-  const float m0 = __builtin_fmaxf(__builtin_fmaxf(s[0], s[1]), s[2]);
-  const float m1 = __builtin_fmaxf(__builtin_fmaxf(s[3], s[4]), s[5]);
-  const float m2 = __builtin_fmaxf(__builtin_fmaxf(s[6], s[7]), s[8]);
-  const float m3 = __builtin_fmaxf(__builtin_fmaxf(s[9], s[10]), s[11]);
-  const float m4 = __builtin_fmaxf(__builtin_fmaxf(s[12], s[13]), s[14]);
-  const float m5 = __builtin_fmaxf(__builtin_fmaxf(s[15], m0), m1);
-  const float m6 = __builtin_fmaxf(__builtin_fmaxf(m2, m3), m4);
-  const float cm = __builtin_fmaxf(m5, m6);
+  const float m0 = max3_ieee(s[0], s[1], s[2]);
+  const float m1 = max3_ieee(s[3], s[4], s[5]);
+  const float m2 = max3_ieee(s[6], s[7], s[8]);
+  const float m3 = max3_ieee(s[9], s[10], s[11]);
+  const float m4 = max3_ieee(s[12], s[13], s[14]);
+  const float m5 = max3_ieee(s[15], m0, m1);
+  const float m6 = max3_ieee(m2, m3, m4);
+  const float cm = max3_ieee(m5, m6, m6);
   int ci = 15;
 #pragma unroll
   for (int r = 14; r >= 0; --r) ci = (s[r] == cm) ? r : ci;
@@ -249,6 +268,54 @@ __device__ __forceinline__ void merge_halves(float& mx, int& tok, int h) {
   const bool take = (otok != 0) & ((tok == 0) | (omx > mx) | ((omx == mx) & (otok < tok)));
   mx = take ? omx : mx;
   tok = take ? otok : tok;
+}
+
+// The reference's running max starts empty, `arg == 0 || s > mx`
+// (kernels_forward.jl:49-52, forward_pair.jl:82-85): the first valid
+// document token u0 is always taken, whatever its score.  The scans start
+// from -Inf and take only s > mx instead, which agrees for every finite
+// score.  They differ in two cases only: score(u0) is NaN (the reference
+// then keeps (NaN, u0) for good, since nothing compares greater than NaN),
+// or no valid score exceeds -Inf (the reference keeps (score(u0), u0), the
+// scan would keep nothing).  FirstTok holds score(u0) from the chunk that
+// contains u0, and first_token_fix applies the reference's outcome at the
+// close of the (pair, query tile).
+struct FirstTok {
+  float s0;  // score of the first valid row (meaningful on lanes of half h0)
+  int h0;    // wave half whose accumulators hold that row
+  int u0;    // its 1-based document token; 0 = no valid row seen yet (uniform)
+};
+
+// NaN test on the bit pattern (no floating-point compare for the compiler
+// to rewrite).
+__device__ __forceinline__ bool is_nan_bits(float x) {
+  return (__builtin_bit_cast(uint32_t, x) & 0x7fffffffu) > 0x7f800000u;
+}
+
+// Record the first valid row of chunk ch (m32: its row validity, uniform)
+// unless an earlier chunk held one.  Uniform control flow.
+__device__ __forceinline__ void capture_first(FirstTok& f, const float (&s)[16], uint32_t m32,
+                                              int ch) {
+  if (f.u0 == 0 && m32 != 0u) {
+    const int row = __builtin_ctz(m32);
+    const int reg = ((row >> 3) << 2) | (row & 3);  // acc_row(reg, (row >> 2) & 1) == row
+    float v = s[0];
+#pragma unroll
+    for (int r = 1; r < 16; ++r) v = (reg == r) ? s[r] : v;
+    f.s0 = v;
+    f.h0 = (row >> 2) & 1;
+    f.u0 = ch * kTile + row + 1;
+  }
+}
+
+// Apply the first-token rule to a merged (mx, tok) (after merge_halves).
+__device__ __forceinline__ void first_token_fix(const FirstTok& f, int h, float& mx, int& tok) {
+  const float other =
+      __builtin_bit_cast(float, lane_xor32(__builtin_bit_cast(uint32_t, f.s0), h));
+  const float s0 = (h == f.h0) ? f.s0 : other;
+  const bool fix = (f.u0 != 0) & ((tok == 0) | is_nan_bits(s0));
+  mx = fix ? s0 : mx;
+  tok = fix ? f.u0 : tok;
 }
 
 // Sum over lanes 0-31, returned in every lane (wave-uniform).  After

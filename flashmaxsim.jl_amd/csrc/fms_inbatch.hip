@@ -55,6 +55,7 @@
 
 #include <algorithm>
 #include <stdint.h>
+#include <type_traits>
 
 #include "fms_device.hpp"
 #include "fms_group.hpp"
@@ -84,7 +85,11 @@ constexpr int kIbBalanceMaxDocs = 6144;          // partition weights fit the re
 // List entry: chunk (6 bits) | document in block (6) | last chunk of its
 // document (1) | first valid token + 1 (19).
 constexpr int kInfoDocShift = 6, kInfoLastBit = 12, kInfoFirstShift = 13;
-constexpr uint32_t kInfoDocMask = 63u;
+constexpr uint32_t kInfoDocMask = 63u, kInfoFirstMask = 0x7ffffu;
+// Plan value of a document's first valid token: the token (-1 = none), with
+// kPlanNfBit set when its feature row holds an Inf or NaN.
+constexpr int kPlanNfBit = 30;
+constexpr int kPlanTooLong = -2;  // packed document longer than max_len
 static_assert(kIbMaxDocs <= (int)kInfoDocMask + 1, "document index fits its field");
 
 }  // namespace
@@ -116,14 +121,36 @@ __device__ __forceinline__ void dma_barrier() {
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
+// Whether any 16-bit element of a fragment word pair is Inf or NaN.
+template <class Op>
+__device__ __forceinline__ bool frag_nonfinite(const u32x4& w) {
+  constexpr uint32_t e = std::is_same<Op, OpBF16>::value ? 0x7f80u : 0x7c00u;
+  bool nf = false;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) nf |= ((w[i] & e) == e) | ((w[i] & (e << 16)) == (e << 16));
+  return nf;
+}
+
+
+// Whether the 256-byte feature row at `row` (16-bit elements, bf16 or fp16)
+// holds an Inf or NaN: one dword per lane, wave ballot.  Uniform result.
+__device__ __forceinline__ bool row_nonfinite(const char* row, int bf16) {
+  const int lane = threadIdx.x & 63;
+  const uint32_t w = *reinterpret_cast<const uint32_t*>(row + lane * 4);
+  const uint32_t e = bf16 ? 0x7f807f80u : 0x7c007c00u;
+  const bool nf = ((w & (e & 0xffffu)) == (e & 0xffffu)) | ((w & (e & 0xffff0000u)) == (e & 0xffff0000u));
+  return __ballot(nf) != 0ull;
+}
+
 // Per-document chunk plan, computed once per call rather than once per query
 // block: one wave per document, lane = chunk (nch <= 64).  cmask[j*nch + ch]
 // holds the valid rows of chunk ch of document j (rows past Td clear),
 // dcount[j] the chunks with a valid row, dfirst[j] the first valid token
-// (-1 = none).
-__global__ void __launch_bounds__(256) inbatch_plan_kernel(const uint8_t* dm, int Bd, int Td,
-                                                           int nch, uint32_t* cmask,
-                                                           int32_t* dcount, int32_t* dfirst) {
+// (-1 = none) with kPlanNfBit set when that token's row is not finite.
+__global__ void __launch_bounds__(256) inbatch_plan_kernel(const uint8_t* dm, const char* D,
+                                                           int bf16, int Bd, int Td, int nch,
+                                                           uint32_t* cmask, int32_t* dcount,
+                                                           int32_t* dfirst) {
   const int lane = threadIdx.x & 63;
   const int j = blockIdx.x * 4 + uniform(threadIdx.x >> 6);
   if (j >= Bd) return;
@@ -142,35 +169,43 @@ __global__ void __launch_bounds__(256) inbatch_plan_kernel(const uint8_t* dm, in
   }
   if (lane < nch) cmask[(int64_t)j * nch + lane] = m;
   const uint64_t nz = __ballot(m != 0u);
+  int f = -1;
+  if (nz != 0u) {
+    const int k = __builtin_ctzll(nz);
+    f = k * kTile + __builtin_ctz((uint32_t)__builtin_amdgcn_readlane((int)m, k));
+    if (row_nonfinite(D + ((int64_t)j * Td + f) * kIbRowBytes, bf16)) f |= 1 << kPlanNfBit;
+  }
   if (lane == 0) {
     dcount[j] = __builtin_popcountll(nz);
-    int f = -1;
-    if (nz != 0u) {
-      const int k = __builtin_ctzll(nz);
-      f = k * kTile + __builtin_ctz((uint32_t)__builtin_amdgcn_readlane((int)m, k));
-    }
     dfirst[j] = f;
   }
 }
 
 // The same plan for PackedSeq documents: document j is token rows
-// [cu[j]-1, cu[j+1]-1) (clamped into the token range and to Td = max_len
-// rows, as the packed scans clamp a malformed device cu); every row is valid.
-__global__ void __launch_bounds__(256) packed_plan_kernel(const int32_t* cu, int64_t ntok, int Bd,
-                                                          int Td, int nch, uint32_t* cmask,
+// [cu[j]-1, cu[j+1]-1) (clamped into the token range, as the packed scans
+// clamp a malformed device cu); every row is valid.  A document longer than
+// Td = max_len rows does not fit the plan: it gets no chunks and the plan
+// value kPlanTooLong, and the scan writes NaN scores for it rather than
+// scoring a truncated document.
+__global__ void __launch_bounds__(256) packed_plan_kernel(const int32_t* cu, const char* tokens,
+                                                          int bf16, int64_t ntok, int Bd, int Td,
+                                                          int nch, uint32_t* cmask,
                                                           int32_t* dcount, int32_t* dfirst) {
   const int lane = threadIdx.x & 63;
   const int j = blockIdx.x * 4 + uniform(threadIdx.x >> 6);
   if (j >= Bd) return;
   const int64_t a = std::min<int64_t>(std::max<int64_t>((int64_t)cu[j] - 1, 0), ntok);
   const int64_t z = std::min<int64_t>(std::max<int64_t>((int64_t)cu[j + 1] - 1, a), ntok);
-  const int len = (int)std::min<int64_t>(z - a, Td);
+  const bool too_long = z - a > Td;
+  const int len = too_long ? 0 : (int)(z - a);
   const int rows = len - lane * kTile;
   const uint32_t m = rows >= kTile ? 0xffffffffu : (rows > 0 ? (1u << rows) - 1u : 0u);
   if (lane < nch) cmask[(int64_t)j * nch + lane] = m;
+  int f = too_long ? kPlanTooLong : -1;
+  if (len > 0) f = row_nonfinite(tokens + a * kIbRowBytes, bf16) ? (1 << kPlanNfBit) : 0;
   if (lane == 0) {
     dcount[j] = (len + kTile - 1) / kTile;
-    dfirst[j] = len > 0 ? 0 : -1;
+    dfirst[j] = f;
   }
 }
 
@@ -210,12 +245,13 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
   __shared__ u32x4 cbuf0[kIbFrags], cbuf1[kIbFrags], cbuf2[kIbFrags];
   __shared__ u32x4 cbuf3[kIbBufs == 4 ? kIbFrags : 1];
   __shared__ uint32_t chunk_mask[kIbMaxChunkMasks];  // valid rows per (doc, chunk)
-  __shared__ int32_t doc_first[kIbMaxDocs];          // first valid token, -1 = none
+  __shared__ int32_t doc_first[kIbMaxDocs];          // plan value: first valid token | flag
   __shared__ uint32_t lst_mask[kIbMaxList];          // compacted chunk list
   __shared__ uint32_t lst_info[kIbMaxList];
   __shared__ int32_t lst_row0[kPacked ? kIbMaxList : 1];  // packed: document's first row
   __shared__ int32_t doc_row0[kPacked ? kIbMaxDocs + 1 : 1];
   __shared__ int lst_count;
+  __shared__ int any_nf;  // some document's first valid row is not finite
   __shared__ int16_t res_tape[kIbWaves][kIbQpw][kIbMaxDocs][kTile];  // Td <= 2048
   __shared__ float res_score[kIbWaves][kIbQpw][kIbMaxDocs];
 
@@ -335,6 +371,7 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
     if (c < nall) chunk_mask[c] = cm[k];
   }
   if (tid < ndoc) doc_first[tid] = dfv;
+  if (tid == 0) any_nf = 0;
 
   // ---- defaults of the results --------------------------------------------------
   // A document without a valid token never closes: score 0, tape 0.
@@ -345,6 +382,12 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
   for (int e = tid; e < kIbWaves * kIbQpw * kIbMaxDocs; e += 64 * kIbWaves)
     (&res_score[0][0][0])[e] = 0.0f;
   __syncthreads();  // chunk_mask, doc_first complete
+  if (tid < ndoc && dfv >= 0 && ((dfv >> kPlanNfBit) & 1)) any_nf = 1;
+  if (tid < ndoc && dfv == kPlanTooLong) {  // packed document longer than max_len: NaN
+    for (int w = 0; w < kIbWaves; ++w)
+      for (int q = 0; q < kIbQpw; ++q)
+        res_score[w][q][tid] = __builtin_bit_cast(float, 0x7fc00000u);
+  }
 
   // ---- compacted chunk list ------------------------------------------------------
   // Only chunks with at least one valid row are streamed and multiplied (a
@@ -361,8 +404,9 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
         const int pos = base + __builtin_popcountll(bal & ((1ull << lane) - 1ull));
         const int jj = c / nch, ch = c - jj * nch;
         lst_mask[pos] = m;
-        lst_info[pos] = (uint32_t)(ch | (jj << kInfoDocShift) |
-                                   ((doc_first[jj] + 1) << kInfoFirstShift));
+        const int df = doc_first[jj];
+        const uint32_t f1 = df < 0 ? 0u : (uint32_t)(df & ~(1 << kPlanNfBit)) + 1u;
+        lst_info[pos] = (uint32_t)ch | ((uint32_t)jj << kInfoDocShift) | (f1 << kInfoFirstShift);
         if constexpr (kPacked) lst_row0[pos] = doc_row0[jj];
       }
       base += __builtin_popcountll(bal);
@@ -414,7 +458,7 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
   int ld_i = 0;  // next list entry to request
   auto chunk_load = [&](u32x4* buf, uint32_t m, uint32_t info, int row0) {
     const int ch = info & 63u, jj = (info >> kInfoDocShift) & kInfoDocMask;
-    const int f = (int)(info >> kInfoFirstShift) - 1;
+    const int f = (int)((info >> kInfoFirstShift) & kInfoFirstMask) - 1;
     const int fsrc = f < 0 ? 0 : f;  // (never: listed chunks have a valid row)
     const int src = ((m >> r32) & 1u) ? ch * kTile + r32 : fsrc;
     const int voff = ((kPacked ? row0 : jj * Td) + src) * kIbRowBytes + h * 16;
@@ -434,7 +478,9 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
 
   // Close query q's document jj: merge the wave halves, map a winning
   // substituted row back to the first valid token f, reduce the score,
-  // stage tape and score in LDS, reset the running max.
+  // stage tape and score in LDS, reset the running max.  (A document whose
+  // scores are all -Inf closes on f with -Inf, as the reference's first-token
+  // rule gives; the NaN case of that rule is settled after the loop.)
   auto close = [&](int q, int jj, int f) {
     int tok = slot_to_token(slot[q], h);
     float m = mx[q];
@@ -465,7 +511,7 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
   auto close_if_last = [&](int q0, int q1, uint32_t inf) {
     if (inf & (1u << kInfoLastBit)) {
       const int jj = (inf >> kInfoDocShift) & kInfoDocMask;
-      const int f = (int)(inf >> kInfoFirstShift) - 1;
+      const int f = (int)((inf >> kInfoFirstShift) & kInfoFirstMask) - 1;
       close(q0, jj, f);
       close(q1, jj, f);
     }
@@ -559,6 +605,51 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
     fold_close(3, lag3, pinfo);
     close_if_last(2, 3, pinfo);
   }
+
+  // ---- first-token rule for NaN scores -------------------------------------------
+  // The reference keeps (NaN, f) when the first valid token f of a document
+  // scores NaN (`arg == 0 || s > mx`, kernels_forward.jl:49-52); the fold
+  // skipped that NaN like any other.  score(f) can be NaN only when the query
+  // token or f's feature row holds an Inf or NaN (plan flag kPlanNfBit), so
+  // only those (query, document) pairs are examined, after the loop, on the
+  // staged results: score(f) is recomputed by the same MFMAs (row f as every
+  // row of the A operand), and where it is NaN the token's tape becomes f
+  // and the document's score NaN.  Finite features never enter this branch.
+  {
+    uint32_t qnf = 0u;  // bit q: some valid token of query q is not finite
+#pragma unroll
+    for (int q = 0; q < kIbQpw; ++q) {
+      bool nf = false;
+#pragma unroll
+      for (int kb = 0; kb < kIbNkb; ++kb) nf |= frag_nonfinite<Op>(qf[q][kb]);
+      nf = ((uint32_t)nf | lane_xor32((uint32_t)nf, h)) != 0u;
+      qnf |= __ballot(nf & token_valid(q)) != 0ull ? (1u << q) : 0u;
+    }
+    if (qnf != 0u || uniform(any_nf) != 0) {
+      for (int jj = 0; jj < ndoc; ++jj) {
+        const int df = uniform(doc_first[jj]);
+        if (df < 0) continue;  // no valid token: the document never closed
+        const int f = df & ~(1 << kPlanNfBit);
+        const bool dnf = ((df >> kPlanNfBit) & 1) != 0;
+        const int rowoff = ((kPacked ? doc_row0[jj] : jj * Td) + f) * kIbRowBytes;
+        Frag a[kIbNkb];
+#pragma unroll
+        for (int kb = 0; kb < kIbNkb; ++kb) a[kb] = Op::load(rd, rowoff + kb * 32 + h * 16);
+#pragma unroll
+        for (int q = 0; q < kIbQpw; ++q) {
+          if (!dnf && !((qnf >> q) & 1u)) continue;
+          Acc acc = Acc{};
+#pragma unroll
+          for (int kb = 0; kb < kIbNkb; ++kb) acc = Op::mma(a[kb], qf[q][kb], acc);
+          const float s0 = acc[0];  // every row is f: <f, q token lane%32>
+          const bool fix = token_valid(q) && is_nan_bits(s0);
+          if (__ballot(fix) == 0ull) continue;
+          if (fix & (h == 0)) res_tape[wave][q][jj][r32] = (int16_t)(f + 1);
+          if (lane == 0) res_score[wave][q][jj] = __builtin_bit_cast(float, 0x7fc00000u);
+        }
+      }
+    }
+  }
   __syncthreads();  // results of every wave staged
 
   // ---- write the block's tape and scores (coalesced) ------------------------------
@@ -636,10 +727,10 @@ hipError_t launch_inbatch_mfma(int dtype_bf16, const InBatchArgs& args_in, hipSt
   A.dfirst = dfirst;
   if (A.cu)
     hipLaunchKernelGGL(packed_plan_kernel, dim3((unsigned)((A.Bd + 3) / 4)), dim3(256), 0, stream,
-                       A.cu, A.ntok, A.Bd, A.Td, nch, cmask, dcount, dfirst);
+                       A.cu, A.D, dtype_bf16, A.ntok, A.Bd, A.Td, nch, cmask, dcount, dfirst);
   else
     hipLaunchKernelGGL(inbatch_plan_kernel, dim3((unsigned)((A.Bd + 3) / 4)), dim3(256), 0, stream,
-                       A.dm, A.Bd, A.Td, nch, cmask, dcount, dfirst);
+                       A.dm, A.D, dtype_bf16, A.Bd, A.Td, nch, cmask, dcount, dfirst);
   e = hipGetLastError();
   if (e == hipSuccess) {
     const dim3 grid((unsigned)(A.nqb * A.ndb)), block(64 * kIbWaves);

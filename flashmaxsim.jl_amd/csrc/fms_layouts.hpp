@@ -17,11 +17,12 @@ namespace fms {
 struct PairView {
   const char* q;      // first query token (features or int8 codes)
   const uint8_t* qm;  // query mask of that query (nullable = all true)
-  const float* qs;    // int8 query scales (nullable for float features)
+  const char* qs;     // int8 query scales (nullable for float features)
+  int qs_half;        // 1: the query scales are fp16, 0: fp32
   int tq;             // query tokens that exist for this pair
   const char* d;      // first document token
   const uint8_t* dm;  // document mask (nullable = all true)
-  const float* ds;    // int8 document scales
+  const char* ds;     // int8 document scales (fp16 / fp32 per the scan's Op)
   int td;             // document tokens (0 = empty / invalid)
   bool valid;         // false only for an out-of-range candidate index
   int64_t out;        // output slot (pair id) of this pair
@@ -51,6 +52,7 @@ __device__ __forceinline__ PairView uniform_view(const PairView& v) {
   u.q = uniform_ptr(v.q);
   u.qm = uniform_ptr(v.qm);
   u.qs = uniform_ptr(v.qs);
+  u.qs_half = (int)rfl32((uint32_t)v.qs_half);
   u.tq = (int)rfl32((uint32_t)v.tq);
   u.d = uniform_ptr(v.d);
   u.dm = uniform_ptr(v.dm);
@@ -72,17 +74,21 @@ __device__ __forceinline__ int64_t max_seq_tokens(int64_t rowbytes) {
 
 // paired_tile_kernel! (kernels_forward.jl:195-269): pair b = (Q_b, D_b).
 // The single pair layout is B = 1.
+// INT8 scales are addressed in bytes: qs_esz / ds_esz are 2 (fp16) or 4 (fp32).
 struct LayPaired {
   const char* Q; const char* D;
   const uint8_t* qm; const uint8_t* dm;
-  const float* Qs; const float* Ds;
+  const char* Qs; const char* Ds;
   int64_t qbytes, dbytes;  // bytes of one query / one document
   int Tq, Td;
+  int qs_esz = 4, ds_esz = 4;
   __device__ PairView get(int64_t b) const {
     PairView v;
-    v.q = Q + b * qbytes; v.qm = qm ? qm + b * Tq : nullptr; v.qs = Qs ? Qs + b * Tq : nullptr;
+    v.q = Q + b * qbytes; v.qm = qm ? qm + b * Tq : nullptr;
+    v.qs = Qs ? Qs + b * Tq * qs_esz : nullptr; v.qs_half = qs_esz == 2;
     v.tq = Tq;
-    v.d = D + b * dbytes; v.dm = dm ? dm + b * Td : nullptr; v.ds = Ds ? Ds + b * Td : nullptr;
+    v.d = D + b * dbytes; v.dm = dm ? dm + b * Td : nullptr;
+    v.ds = Ds ? Ds + b * Td * ds_esz : nullptr;
     v.td = Td; v.valid = true; v.out = b;
     return v;
   }
@@ -93,19 +99,22 @@ struct LayPaired {
 struct LayCand {
   const char* Q; const char* G; const void* idx;
   const uint8_t* qm; const uint8_t* dm;
-  const float* Qs; const float* Gs;
+  const char* Qs; const char* Gs;
   int64_t qbytes, dbytes, N, C;
   int Tq, Td, idx64;
+  int qs_esz = 4, ds_esz = 4;
   __device__ PairView get(int64_t p) const {
     const int64_t b = p / C;
     const int64_t j = idx64 ? sload(static_cast<const int64_t*>(idx), p)
                             : (int64_t)sload(static_cast<const int32_t*>(idx), p);
     PairView v;
-    v.q = Q + b * qbytes; v.qm = qm ? qm + b * Tq : nullptr; v.qs = Qs ? Qs + b * Tq : nullptr;
+    v.q = Q + b * qbytes; v.qm = qm ? qm + b * Tq : nullptr;
+    v.qs = Qs ? Qs + b * Tq * qs_esz : nullptr; v.qs_half = qs_esz == 2;
     v.tq = Tq;
     v.valid = (j >= 1 && j <= N);
     const int64_t jj = v.valid ? j - 1 : 0;
-    v.d = G + jj * dbytes; v.dm = dm ? dm + jj * Td : nullptr; v.ds = Gs ? Gs + jj * Td : nullptr;
+    v.d = G + jj * dbytes; v.dm = dm ? dm + jj * Td : nullptr;
+    v.ds = Gs ? Gs + jj * Td * ds_esz : nullptr;
     v.td = v.valid ? Td : 0;
     v.out = p;
     return v;
@@ -125,12 +134,12 @@ struct LayCandSorted {
     const int64_t p = r.p, b = p / c.C;
     PairView v;
     v.q = c.Q + b * c.qbytes; v.qm = c.qm ? c.qm + b * c.Tq : nullptr;
-    v.qs = c.Qs ? c.Qs + b * c.Tq : nullptr;
+    v.qs = c.Qs ? c.Qs + b * c.Tq * c.qs_esz : nullptr; v.qs_half = c.qs_esz == 2;
     v.tq = c.Tq;
     v.valid = r.j >= 0;
     const int64_t jj = v.valid ? r.j : 0;
     v.d = c.G + jj * c.dbytes; v.dm = c.dm ? c.dm + jj * c.Td : nullptr;
-    v.ds = c.Gs ? c.Gs + jj * c.Td : nullptr;
+    v.ds = c.Gs ? c.Gs + jj * c.Td * c.ds_esz : nullptr;
     v.td = v.valid ? c.Td : 0;
     v.out = p;
     return v;
@@ -146,7 +155,8 @@ struct LayInBatch {
   __device__ PairView get(int64_t p) const {
     const int64_t j = p % Bd, i = p / Bd;
     PairView v;
-    v.q = Q + i * qbytes; v.qm = qm ? qm + i * Tq : nullptr; v.qs = nullptr; v.tq = Tq;
+    v.q = Q + i * qbytes; v.qm = qm ? qm + i * Tq : nullptr; v.qs = nullptr; v.qs_half = 0;
+    v.tq = Tq;
     v.d = D + j * dbytes; v.dm = dm ? dm + j * Td : nullptr; v.ds = nullptr; v.td = Td;
     v.valid = true; v.out = p;
     return v;
@@ -165,7 +175,7 @@ struct LayPacked {
     const int64_t z = clamp64(clamp64((int64_t)sload(cu, b + 1) - 1, a, ntok), a,
                               a + max_seq_tokens(rowbytes));
     PairView v;
-    v.q = q; v.qm = qm; v.qs = nullptr; v.tq = Tq;
+    v.q = q; v.qm = qm; v.qs = nullptr; v.qs_half = 0; v.tq = Tq;
     v.d = tok + a * rowbytes; v.dm = nullptr; v.ds = nullptr; v.td = (int)(z - a);
     v.valid = true; v.out = b;
     return v;
@@ -184,7 +194,7 @@ struct LayVarlen {
     const int64_t da = clamp64((int64_t)sload(cu_d, n) - 1, 0, nd);
     const int64_t dz = clamp64(clamp64((int64_t)sload(cu_d, n + 1) - 1, da, nd), da, da + max_seq_tokens(rowbytes));
     PairView v;
-    v.q = Qt + qa * rowbytes; v.qm = nullptr; v.qs = nullptr;
+    v.q = Qt + qa * rowbytes; v.qm = nullptr; v.qs = nullptr; v.qs_half = 0;
     v.tq = (int)((qz - qa) < max_q ? (qz - qa) : max_q);
     v.d = Dt + da * rowbytes; v.dm = nullptr; v.ds = nullptr; v.td = (int)(dz - da);
     v.valid = true; v.out = n;

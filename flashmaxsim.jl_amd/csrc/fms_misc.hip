@@ -12,41 +12,73 @@
 
 namespace fms {
 
-// quantize_int8_symmetric for Float32 (src/quant.jl:21-49), one wave per
-// token.  `/` is IEEE-correctly rounded (built without fast-math and with
-// -fhip-fp32-correctly-rounded-divide-sqrt); rintf rounds half to even,
-// which is Julia's RoundNearest used by round(Int8, x).
-__global__ void __launch_bounds__(256) quantize_int8_kernel(const float* __restrict__ X,
+// quantize_int8_symmetric (src/quant.jl:21-49), one wave per token, in the
+// feature type T (Float32, or Float16 via kHalf):
+//   am    = max_k |x[k]|                                  (exact in either type)
+//   raw   = T(max(am, T(1f-8)) / T(127))                   (quant.jl:44)
+//   scale = max(raw, floatmin(T))                          (quant.jl:45)
+//   code  = round(Int8, clamp(T(x / scale), -127, 127))    (quant.jl:46-47)
+// Julia evaluates a Float16 `/` as the fp32 quotient rounded to Float16; an
+// fp32 quotient rounded once more to 11 bits equals the correctly rounded
+// Float16 quotient (24 >= 2*11 + 2 bits), so both steps below are exact
+// restatements.  T(1f-8) is 0 in Float16 (below half the least subnormal).
+// `/` is IEEE-correctly rounded (built without fast-math and with
+// -fhip-fp32-correctly-rounded-divide-sqrt); (_Float16) conversions and
+// rintf round half to even, which is Julia's RoundNearest.
+template <bool kHalf>
+__global__ void __launch_bounds__(256) quantize_int8_kernel(const void* __restrict__ Xv,
                                                             int8_t* __restrict__ codes,
-                                                            float* __restrict__ scales, int dim,
+                                                            void* __restrict__ scales_v, int dim,
                                                             int64_t ntok) {
   const int lane = threadIdx.x & 63;
   const int64_t nwaves = (int64_t)gridDim.x * (blockDim.x >> 6);
+  auto elem = [&](int64_t tok, int k) -> float {
+    if constexpr (kHalf)
+      return (float)static_cast<const _Float16*>(Xv)[tok * dim + k];
+    else
+      return static_cast<const float*>(Xv)[tok * dim + k];
+  };
+  auto to_t = [](float v) -> float {  // round to T
+    if constexpr (kHalf)
+      return (float)(_Float16)v;
+    else
+      return v;
+  };
+  const float eps = to_t(1.0e-8f);
+  const float tmin = kHalf ? 6.103515625e-05f : FLT_MIN;  // floatmin(T)
   for (int64_t tok = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6); tok < ntok;
        tok += nwaves) {
-    const float* x = X + tok * dim;
     float am = 0.0f;
-    for (int k = lane; k < dim; k += 64) am = fmaxf(am, fabsf(x[k]));
+    for (int k = lane; k < dim; k += 64) am = fmaxf(am, fabsf(elem(tok, k)));
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) am = fmaxf(am, __shfl_xor(am, o));
-    const float raw = fmaxf(am, 1.0e-8f) / 127.0f;  // quant.jl:44
-    const float sc = fmaxf(raw, FLT_MIN);           // quant.jl:45
+    const float raw = to_t(fmaxf(am, eps) / 127.0f);  // quant.jl:44
+    const float sc = fmaxf(raw, tmin);                // quant.jl:45
     int8_t* c = codes + tok * dim;
     for (int k = lane; k < dim; k += 64) {
-      float v = x[k] / sc;                          // quant.jl:46
+      float v = to_t(elem(tok, k) / sc);              // quant.jl:46
       v = v > 127.0f ? 127.0f : (v < -127.0f ? -127.0f : v);
       c[k] = (int8_t)__builtin_rintf(v);
     }
-    if (lane == 0) scales[tok] = sc;
+    if (lane == 0) {
+      if constexpr (kHalf)
+        static_cast<_Float16*>(scales_v)[tok] = (_Float16)sc;
+      else
+        static_cast<float*>(scales_v)[tok] = sc;
+    }
   }
 }
 
-hipError_t quantize_int8(const float* X, int8_t* codes, float* scales, int dim, int64_t ntok,
-                         hipStream_t stream) {
+hipError_t quantize_int8(bool half, const void* X, int8_t* codes, void* scales, int dim,
+                         int64_t ntok, hipStream_t stream) {
   int64_t blocks = (ntok + 3) / 4;
   if (blocks > 65536) blocks = 65536;
-  hipLaunchKernelGGL(quantize_int8_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, X, codes,
-                     scales, dim, ntok);
+  if (half)
+    hipLaunchKernelGGL(quantize_int8_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, stream, X,
+                       codes, scales, dim, ntok);
+  else
+    hipLaunchKernelGGL(quantize_int8_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, stream,
+                       X, codes, scales, dim, ntok);
   return hipGetLastError();
 }
 

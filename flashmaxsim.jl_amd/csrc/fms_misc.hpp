@@ -6,8 +6,9 @@
 
 namespace fms {
 
-hipError_t quantize_int8(const float* X, int8_t* codes, float* scales, int dim, int64_t ntok,
-                         hipStream_t stream);
+// X (ntok, dim) of fp32, or of fp16 when `half`; scales of the same type.
+hipError_t quantize_int8(bool half, const void* X, int8_t* codes, void* scales, int dim,
+                         int64_t ntok, hipStream_t stream);
 hipError_t int8_dots(int32_t* out, const int8_t* qc, const int8_t* dc, int dim, int Tq, int Td,
                      bool vec, hipStream_t stream);
 hipError_t length_normalize(float* scores, const uint8_t* qmask, int64_t Tq, int64_t nrows,

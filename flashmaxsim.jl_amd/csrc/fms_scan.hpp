@@ -35,6 +35,7 @@
 
 #include "fms_device.hpp"
 #include "fms_layouts.hpp"
+#include "fms_scan_decl.hpp"
 
 namespace fms {
 
@@ -116,12 +117,33 @@ __device__ __forceinline__ uint32_t chunk_rows_valid(const PairView& v, int ch, 
 // document read 0 and are masked).  acc_to_scores fetches the 16 scales of its
 // accumulator rows from the lanes that hold them, so a chunk buffer carries
 // one scale register instead of sixteen.
+// fp16 document scales (Op::kDsHalf) widen exactly to fp32.
 template <class Op>
 __device__ __forceinline__ void load_ds(float (&ds)[1], const PairView& v, int ch, int r32) {
   if constexpr (Op::kInt) {
-    const rsrc_t rs = make_rsrc_u(v.ds, (uint32_t)v.td * 4u);
-    ds[0] = __builtin_bit_cast(float, buf_load4(rs, (ch * kTile + r32) * 4));
+    const int row = ch * kTile + r32;
+    if constexpr (Op::kDsHalf) {
+      const rsrc_t rs = make_rsrc_u(v.ds, (uint32_t)v.td * 2u);
+      ds[0] = (float)__builtin_bit_cast(_Float16, (uint16_t)buf_load2(rs, row * 2));
+    } else {
+      const rsrc_t rs = make_rsrc_u(v.ds, (uint32_t)v.td * 4u);
+      ds[0] = __builtin_bit_cast(float, buf_load4(rs, row * 4));
+    }
   }
+}
+
+// int8 query scale of token t, fp32 or fp16 (v.qs_half, uniform) widened to
+// fp32.  Both halves of the 4-byte word are read unconditionally (a
+// conditional load would make the compiler drain the chunk prefetch); for
+// fp16 scales the second read is the next token's scale or 0 past the end.
+__device__ __forceinline__ float load_qscale(const PairView& v, int t) {
+  const uint32_t esz = v.qs_half ? 2u : 4u;
+  const rsrc_t r = make_rsrc_u(v.qs, (uint32_t)v.tq * esz);
+  const uint32_t lo = buf_load2(r, t * (int)esz) & 0xffffu;
+  const uint32_t hi = buf_load2(r, t * (int)esz + 2) & 0xffffu;
+  const float h16 = (float)__builtin_bit_cast(_Float16, (uint16_t)lo);
+  const float f32 = __builtin_bit_cast(float, lo | (hi << 16));
+  return v.qs_half ? h16 : f32;
 }
 
 // Accumulator -> fp32 scores.  int8: s = (qs[t] * ds[u]) * Float32(acc)
@@ -152,9 +174,11 @@ __device__ __forceinline__ void update_chunk(const float (&s)[16], uint32_t m32,
 // this tile's contribution to the pair score (same value in every lane).
 template <class L>
 __device__ __forceinline__ float finish_tile(const ScanArgs<L>& A, int64_t out, int qt, int r32,
-                                             int h, bool tvalid, float mx, int slot) {
+                                             int h, bool tvalid, float mx, int slot,
+                                             const FirstTok& first) {
   int tok = slot_to_token(slot, h);
   merge_halves(mx, tok, h);
+  first_token_fix(first, h, mx, tok);
   const float part = (tvalid && tok != 0) ? mx : 0.0f;
   const int arg = tvalid ? tok : 0;
   const int t = qt * kTile + r32;
@@ -225,7 +249,7 @@ __device__ __forceinline__ void load_qtile(QTile<Op, NKB>& q, const PairView& v,
                                   q.t);
   q.mbyte = mraw;
   q.qscale = 0.0f;
-  if constexpr (Op::kInt) q.qscale = __builtin_bit_cast(float, buf_load4(make_rsrc_u(v.qs, (uint32_t)v.tq * 4u), q.t * 4));
+  if constexpr (Op::kInt) q.qscale = load_qscale(v, q.t);
 }
 
 template <class Op, class L, int NKB>
@@ -252,6 +276,7 @@ __global__ void __launch_bounds__(64 * kWaves) scan_fast(const ScanArgs<L> A) {
   int q_qt = -1;
   float mx = -INFINITY, score = 0.0f;
   int slot = -1;
+  FirstTok ftok = {0.0f, 0, 0};
 
   load_chunk<Op, NKB>(bufA, v, 0, nkb, rowbytes, lane_off, r32);
 
@@ -302,6 +327,7 @@ __global__ void __launch_bounds__(64 * kWaves) scan_fast(const ScanArgs<L> A) {
     float s[16];
     acc_to_scores<Op>(acc, q.qscale, cur.ds, h, s);
     update_chunk(s, m32, h, ch, mx, slot);
+    capture_first(ftok, s, m32, ch);
 
     if (ch == nch - 1) {
       // The empty asm pins the query-mask test here: hoisted next to its
@@ -309,9 +335,10 @@ __global__ void __launch_bounds__(64 * kWaves) scan_fast(const ScanArgs<L> A) {
       uint32_t qmb = q.mbyte;
       asm volatile("" : "+v"(qmb));
       const bool tvalid = q.t < v.tq && mask_ok(v.qm, qmb);
-      score += finish_tile(A, v.out, qt, r32, h, tvalid, mx, slot);
+      score += finish_tile(A, v.out, qt, r32, h, tvalid, mx, slot, ftok);
       mx = -INFINITY;
       slot = -1;
+      ftok.u0 = 0;
       if (qt == A.nqt - 1) {
         write_score(A, v, score, lane);
         score = 0.0f;
@@ -372,9 +399,10 @@ __global__ void __launch_bounds__(64 * kWaves) scan_generic(const ScanArgs<L> A)
       if (v.qm) mb = buf_load1(make_rsrc_u(v.qm, (uint32_t)v.tq), t);
       const bool tvalid = (t < v.tq) && (mb != 0u);
       float qscale = 0.0f;
-      if constexpr (Op::kInt) qscale = __builtin_bit_cast(float, buf_load4(make_rsrc_u(v.qs, (uint32_t)v.tq * 4u), t * 4));
+      if constexpr (Op::kInt) qscale = load_qscale(v, t);
       float mx = -INFINITY;
       int slot = -1;
+      FirstTok ftok = {0.0f, 0, 0};
       for (int ch = 0; ch < nch; ++ch) {
         Acc acc = {};
         const int row = ch * kTile + r32;
@@ -397,9 +425,11 @@ __global__ void __launch_bounds__(64 * kWaves) scan_generic(const ScanArgs<L> A)
         load_ds<Op>(ds, v, ch, r32);
         float s[16];
         acc_to_scores<Op>(acc, qscale, ds, h, s);
-        update_chunk(s, chunk_rows_valid(v, ch, r32, mbyte), h, ch, mx, slot);
+        const uint32_t m32 = chunk_rows_valid(v, ch, r32, mbyte);
+        update_chunk(s, m32, h, ch, mx, slot);
+        capture_first(ftok, s, m32, ch);
       }
-      score += finish_tile(A, v.out, qt, r32, h, tvalid, mx, slot);
+      score += finish_tile(A, v.out, qt, r32, h, tvalid, mx, slot, ftok);
     }
     write_score(A, v, score, lane);
   }
@@ -418,14 +448,6 @@ constexpr int fast_nkb(int nkb) {
 }
 
 
-inline int pairs_per_wave(int64_t npairs) {
-  // Aim for ~32k waves (8 resident per SIMD over 1024 SIMDs, several rounds)
-  // so that each wave keeps its query tile across a handful of pairs.
-  int64_t ppw = npairs / 32768;
-  if (ppw < 1) ppw = 1;
-  if (ppw > 32) ppw = 32;
-  return (int)ppw;
-}
 
 template <class Op, class L>
 hipError_t launch_scan(const L& lay, int dim, int rows, int64_t npairs, int32_t* args,

@@ -67,9 +67,7 @@ __device__ __forceinline__ void load_split(SplitBatch<Op, KBAT>& c, const PairVi
                                    has_qm ? (uint32_t)v.tq : 0u),
                        qt * kTile + r32);
   c.qscale = 0.0f;
-  if constexpr (Op::kInt)
-    c.qscale = __builtin_bit_cast(float, buf_load4(make_rsrc_u(v.qs, (uint32_t)v.tq * 4u),
-                                                   (qt * kTile + r32) * 4));
+  if constexpr (Op::kInt) c.qscale = load_qscale(v, qt * kTile + r32);
   load_ds<Op>(c.ds, v, ch, r32);
 }
 
@@ -119,6 +117,7 @@ __global__ void __launch_bounds__(64 * kWaves) scan_split(const ScanArgs<L> A) {
   Acc acc0 = {}, acc1 = {};
   float mx = -INFINITY, score = 0.0f;
   int slot = -1;
+  FirstTok ftok = {0.0f, 0, 0};
 
   load_split<Op, KBAT, kLdsQ>(bufA, v, 0, 0, 0, rowbytes, h, r32, qlds, A.nkb);
 
@@ -165,14 +164,17 @@ __global__ void __launch_bounds__(64 * kWaves) scan_split(const ScanArgs<L> A) {
       acc1 = Acc{};
       float s[16];
       acc_to_scores<Op>(acc, cur.qscale, cur.ds, h, s);
-      update_chunk(s, chunk_rows_valid(v, ch, r32, cur.mbyte), h, ch, mx, slot);
+      const uint32_t m32 = chunk_rows_valid(v, ch, r32, cur.mbyte);
+      update_chunk(s, m32, h, ch, mx, slot);
+      capture_first(ftok, s, m32, ch);
       if (ch == nch - 1) {
         uint32_t qmb = cur.qmbyte;
         asm volatile("" : "+v"(qmb));
         const bool tvalid = (qt * kTile + r32) < v.tq && mask_ok(v.qm, qmb);
-        score += finish_tile(A, v.out, qt, r32, h, tvalid, mx, slot);
+        score += finish_tile(A, v.out, qt, r32, h, tvalid, mx, slot, ftok);
         mx = -INFINITY;
         slot = -1;
+        ftok.u0 = 0;
         if (qt == A.nqt - 1) {
           write_score(A, v, score, lane);
           score = 0.0f;

@@ -39,11 +39,13 @@ SIGNATURES = {
     "fms_inbatch_device_scan": [_i32, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _p],
     "fms_launch_packed_scan": [_i32, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _i32, _p],
     "fms_launch_varlen_scan": [_i32, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _i32, _p],
-    "fms_int8_quantize": [_p, _p, _p, _i64, _i64, _p],
-    "fms_launch_int8_pair_scan": [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _i32, _p],
-    "fms_launch_int8_paired_scan": [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _i32, _p],
-    "fms_launch_int8_candidates_scan": [_p, _p, _p, _p, _p, _p, _p, _i32, _p, _p, _i64, _i64,
-                                        _i64, _i64, _i64, _i64, _p, _f, _i32, _p],
+    "fms_int8_quantize": [_i32, _p, _p, _p, _i64, _i64, _p],
+    "fms_launch_int8_pair_scan": [_p, _p, _p, _p, _i32, _p, _p, _i32, _p, _p, _i64, _i64, _i64, _p,
+                                  _i32, _p],
+    "fms_launch_int8_paired_scan": [_p, _p, _p, _p, _i32, _p, _p, _i32, _p, _p, _i64, _i64, _i64,
+                                    _i64, _p, _i32, _p],
+    "fms_launch_int8_candidates_scan": [_p, _p, _p, _p, _i32, _p, _p, _i32, _p, _i32, _p, _p, _i64,
+                                        _i64, _i64, _i64, _i64, _i64, _p, _f, _i32, _p],
     "fms_int8_dots": [_p, _p, _p, _i64, _i64, _i64, _p],
     "fms_length_normalize": [_p, _p, _i64, _i64, _i64, _p, _i32, _i64, _f, _p],
     "fms_varlen_normalize": [_p, _p, _i64, _p],

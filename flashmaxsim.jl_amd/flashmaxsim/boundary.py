@@ -36,7 +36,7 @@ from __future__ import annotations
 import torch
 
 from . import _lib
-from .errors import ArgumentError, UnsupportedError
+from .errors import ArgumentError, DimensionMismatch, UnsupportedError
 
 _DTYPES = {torch.float32: _lib.FMS_F32, torch.float16: _lib.FMS_F16, torch.bfloat16: _lib.FMS_BF16}
 
@@ -105,36 +105,105 @@ def _norm(normalize) -> int:
     return 1 if normalize else 0
 
 
+# ---- argument checks ---------------------------------------------------------------
+# The library writes fp32 partials / scores and int32 tapes and reads features of the
+# declared type and dim; a buffer of another type or size would be read or written
+# out of bounds on the device.  So every tensor is checked here, before the call:
+# wrong element types raise ArgumentError, wrong sizes DimensionMismatch (the
+# reference's pre-launch checks, forward_layouts.jl:20-47, forward_pair.jl:14-21,
+# packed.jl:138-151, quant.jl:62-94).
+
+def _buf(t, what, dtype, numel):
+    """An optional output / index buffer: exact dtype and element count."""
+    if t is None:
+        return None
+    if t.dtype != dtype:
+        raise ArgumentError(f"{what} must be {dtype}, got {t.dtype}")
+    if t.numel() != numel:
+        raise DimensionMismatch(f"{what}: {t.numel()} elements, expected {numel}")
+    return t
+
+
+def _maskn(m, what, numel):
+    m = _mask(m)
+    if m is not None and m.numel() != numel:
+        raise DimensionMismatch(f"{what}: {m.numel()} elements, expected {numel}")
+    return m
+
+
+def _feat(t, what, ndim, proto=None):
+    """A feature array of `ndim` dimensions; with `proto`, the same eltype and dim."""
+    if t.dim() != ndim:
+        raise DimensionMismatch(f"{what} must have {ndim} dimensions, got {t.dim()}")
+    if proto is not None:
+        if t.dtype != proto.dtype:
+            raise ArgumentError(f"{what} must have the feature eltype {proto.dtype}, got {t.dtype}")
+        if t.shape[-1] != proto.shape[-1]:
+            raise DimensionMismatch(f"feature dim: {what} has {t.shape[-1]}, expected {proto.shape[-1]}")
+    return t
+
+
+def _cu(cu, what, n):
+    if cu.dtype != torch.int32:
+        raise ArgumentError("PackedSeq cu must be Int32 on device")
+    if cu.dim() != 1 or cu.numel() != n:
+        raise DimensionMismatch(f"{what}: {cu.numel()} entries, expected {n}")
+    return cu
+
+
 def launch_pair_scan(argmax_u, partial, q, d, qmask, dmask, score=None, normalize=False):
-    dev = require_device(argmax_u, partial, q, d, qmask, dmask, score)
+    _feat(q, "q", 2)
+    _feat(d, "d", 2, q)
     Tq, dim = q.shape
     Td = d.shape[0]
+    _buf(argmax_u, "argmax_u", torch.int32, Tq)
+    _buf(partial, "partial", torch.float32, Tq)
+    _buf(score, "score", torch.float32, 1)
+    dev = require_device(argmax_u, partial, q, d, qmask, dmask, score)
     st = _lib.lib().fms_launch_pair_scan(
-        dtype_code(q), ptr(argmax_u), ptr(partial), ptr(q), ptr(d), ptr(_mask(qmask)),
-        ptr(_mask(dmask)), dim, Tq, Td, ptr(score), _norm(normalize), stream_handle(dev))
+        dtype_code(q), ptr(argmax_u), ptr(partial), ptr(q), ptr(d), ptr(_maskn(qmask, "qmask", Tq)),
+        ptr(_maskn(dmask, "dmask", Td)), dim, Tq, Td, ptr(score), _norm(normalize),
+        stream_handle(dev))
     _lib.check(st, "launch_pair_scan")
 
 
 def launch_paired_scan(args, partial, Q, D, qmask, dmask, scores=None, normalize=False):
-    dev = require_device(args, partial, Q, D, qmask, dmask, scores)
+    _feat(Q, "Q", 3)
+    _feat(D, "D", 3, Q)
     B, Tq, dim = Q.shape
     Td = D.shape[1]
+    if D.shape[0] != B:
+        raise DimensionMismatch("batch")
+    _buf(args, "args", torch.int32, B * Tq)
+    _buf(partial, "partial", torch.float32, B * Tq)
+    _buf(scores, "scores", torch.float32, B)
+    dev = require_device(args, partial, Q, D, qmask, dmask, scores)
     st = _lib.lib().fms_launch_paired_scan(
-        dtype_code(Q), ptr(args), ptr(partial), ptr(Q), ptr(D), ptr(_mask(qmask)),
-        ptr(_mask(dmask)), dim, Tq, Td, B, ptr(scores), _norm(normalize), stream_handle(dev))
+        dtype_code(Q), ptr(args), ptr(partial), ptr(Q), ptr(D), ptr(_maskn(qmask, "qmask", B * Tq)),
+        ptr(_maskn(dmask, "dmask", B * Td)), dim, Tq, Td, B, ptr(scores), _norm(normalize),
+        stream_handle(dev))
     _lib.check(st, "launch_paired_scan")
 
 
 def launch_candidates_scan(args, partial, Q, gallery, idx, qmask, dmask, N, scores=None,
                            neg=-1.0e4, normalize=False):
-    dev = require_device(args, partial, Q, gallery, idx, qmask, dmask, scores)
+    _feat(Q, "Q", 3)
+    _feat(gallery, "gallery", 3, Q)
     B, Tq, dim = Q.shape
     Td = gallery.shape[1]
+    if N != gallery.shape[0]:
+        raise DimensionMismatch(f"N = {N} but the gallery holds {gallery.shape[0]} documents")
+    if idx.dim() != 2 or idx.shape[0] != B:
+        raise DimensionMismatch("idxs")
     C = idx.shape[1]
+    _buf(args, "args", torch.int32, B * C * Tq)
+    _buf(partial, "partial", torch.float32, B * C * Tq)
+    _buf(scores, "scores", torch.float32, B * C)
+    dev = require_device(args, partial, Q, gallery, idx, qmask, dmask, scores)
     st = _lib.lib().fms_launch_candidates_scan(
         dtype_code(Q), ptr(args), ptr(partial), ptr(Q), ptr(gallery), ptr(idx), _idx_bytes(idx),
-        ptr(_mask(qmask)), ptr(_mask(dmask)), dim, Tq, B, Td, N, C, ptr(scores), float(neg),
-        _norm(normalize), stream_handle(dev))
+        ptr(_maskn(qmask, "qmask", B * Tq)), ptr(_maskn(dmask, "dmask", N * Td)), dim, Tq, B, Td, N,
+        C, ptr(scores), float(neg), _norm(normalize), stream_handle(dev))
     _lib.check(st, "launch_candidates_scan")
 
 
@@ -153,39 +222,59 @@ def candidates_grouping(mode: str) -> str:
 
 
 def inbatch_device_scan(S, args, Q, D, qmask, dmask, normalize=False):
-    dev = require_device(S, args, Q, D, qmask, dmask)
+    _feat(Q, "Q", 3)
+    _feat(D, "D", 3, Q)
     Bq, Tq, dim = Q.shape
     Bd, Td = D.shape[0], D.shape[1]
+    if S is None:
+        raise ArgumentError("inbatch_device_scan needs the score matrix S")
+    _buf(S, "S", torch.float32, Bq * Bd)
+    _buf(args, "args", torch.int32, Bq * Bd * Tq)
+    dev = require_device(S, args, Q, D, qmask, dmask)
     st = _lib.lib().fms_inbatch_device_scan(
-        dtype_code(Q), ptr(S), ptr(args), ptr(Q), ptr(D), ptr(_mask(qmask)), ptr(_mask(dmask)),
-        dim, Tq, Bq, Td, Bd, _norm(normalize), stream_handle(dev))
+        dtype_code(Q), ptr(S), ptr(args), ptr(Q), ptr(D), ptr(_maskn(qmask, "qmask", Bq * Tq)),
+        ptr(_maskn(dmask, "dmask", Bd * Td)), dim, Tq, Bq, Td, Bd, _norm(normalize),
+        stream_handle(dev))
     _lib.check(st, "inbatch_device_scan")
 
 
 def launch_packed_scan(args, partial, q, tokens, cu, qmask, scores=None, normalize=False):
-    dev = require_device(args, partial, q, tokens, cu, qmask, scores)
+    _feat(q, "q", 2)
+    _feat(tokens, "tokens", 2, q)
     Tq, dim = q.shape
     B = cu.shape[0] - 1
-    if cu.dtype != torch.int32:
-        raise ArgumentError("PackedSeq cu must be Int32 on device")
+    _cu(cu, "cu", B + 1)
+    _buf(args, "args", torch.int32, B * Tq)
+    _buf(partial, "partial", torch.float32, B * Tq)
+    _buf(scores, "scores", torch.float32, B)
+    dev = require_device(args, partial, q, tokens, cu, qmask, scores)
     st = _lib.lib().fms_launch_packed_scan(
-        dtype_code(q), ptr(args), ptr(partial), ptr(q), ptr(tokens), ptr(cu), ptr(_mask(qmask)),
-        dim, Tq, B, tokens.shape[0], ptr(scores), _norm(normalize), stream_handle(dev))
+        dtype_code(q), ptr(args), ptr(partial), ptr(q), ptr(tokens), ptr(cu),
+        ptr(_maskn(qmask, "qmask", Tq)), dim, Tq, B, tokens.shape[0], ptr(scores),
+        _norm(normalize), stream_handle(dev))
     _lib.check(st, "launch_packed_scan")
 
 
 def launch_packed_multi_scan(args, scores, Q, tokens, cu, qmask, max_len, normalize=False):
     """nq queries Q (nq, Tq, dim) against one PackedSeq in one pass (no reference
     method: the reference scores one query per call).  scores (nq, B) [Julia (B, nq)],
-    args (nq, B, Tq) nullable."""
-    dev = require_device(args, scores, Q, tokens, cu, qmask)
+    args (nq, B, Tq) nullable.  Every document must be at most max_len tokens (the
+    PackedSeq's max_len); the library checks that on the device and flags a
+    violation through a NaN score row (see fms_launch_packed_multi_scan)."""
+    _feat(Q, "Q", 3)
+    _feat(tokens, "tokens", 2, Q)
     nq, Tq, dim = Q.shape
     B = cu.shape[0] - 1
-    if cu.dtype != torch.int32:
-        raise ArgumentError("PackedSeq cu must be Int32 on device")
+    _cu(cu, "cu", B + 1)
+    if scores is None:
+        raise ArgumentError("launch_packed_multi_scan needs the score matrix")
+    _buf(scores, "scores", torch.float32, nq * B)
+    _buf(args, "args", torch.int32, nq * B * Tq)
+    dev = require_device(args, scores, Q, tokens, cu, qmask)
     st = _lib.lib().fms_launch_packed_multi_scan(
-        dtype_code(Q), ptr(args), ptr(scores), ptr(Q), ptr(tokens), ptr(cu), ptr(_mask(qmask)),
-        dim, Tq, nq, B, tokens.shape[0], int(max_len), _norm(normalize), stream_handle(dev))
+        dtype_code(Q), ptr(args), ptr(scores), ptr(Q), ptr(tokens), ptr(cu),
+        ptr(_maskn(qmask, "qmask", nq * Tq)), dim, Tq, nq, B, tokens.shape[0], int(max_len),
+        _norm(normalize), stream_handle(dev))
     _lib.check(st, "launch_packed_multi_scan")
 
 
@@ -193,23 +282,39 @@ def topk_rows(vals, idx, scores, k):
     """k best entries of every row of scores (nrows, ncols) fp32 [Julia (ncols, nrows),
     one column per query]: vals (nrows, k) descending, idx (nrows, k) 1-based int32.
     No reference method (ranking is the caller's partialsortperm)."""
-    dev = require_device(vals, idx, scores)
+    if scores.dim() != 2:
+        raise DimensionMismatch("top-k scores must be a matrix")
     nrows, ncols = scores.shape
+    _buf(scores, "scores", torch.float32, nrows * ncols)
+    if 0 <= k <= ncols:
+        _buf(vals, "vals", torch.float32, nrows * k)
+        _buf(idx, "idx", torch.int32, nrows * k)
+    dev = require_device(vals, idx, scores)
     st = _lib.lib().fms_topk(ptr(scores), nrows, ncols, int(k), ptr(vals), ptr(idx),
                              stream_handle(dev))
     _lib.check(st, "topk")
 
 
 def launch_varlen_scan(args, partial, Qp, Dp, cu_q, cu_d, scores=None, normalize=False):
-    dev = require_device(args, partial, Qp, Dp, cu_q, cu_d, scores)
+    if args is None or args.dim() != 2:
+        raise DimensionMismatch("varlen args must be (N, max_q)")
     N, max_q = args.shape
+    _feat(Qp, "Q tokens", 2)
+    _feat(Dp, "D tokens", 2, Qp)
     dim = Qp.shape[1]
-    if cu_q.dtype != torch.int32 or cu_d.dtype != torch.int32:
-        raise ArgumentError("PackedSeq cu must be Int32 on device")
+    _cu(cu_q, "cu_q", N + 1)
+    _cu(cu_d, "cu_d", N + 1)
+    _buf(args, "args", torch.int32, N * max_q)
+    _buf(partial, "partial", torch.float32, N * max_q)
+    _buf(scores, "scores", torch.float32, N)
+    dev = require_device(args, partial, Qp, Dp, cu_q, cu_d, scores)
     st = _lib.lib().fms_launch_varlen_scan(
         dtype_code(Qp), ptr(args), ptr(partial), ptr(Qp), ptr(Dp), ptr(cu_q), ptr(cu_d), dim,
         max_q, N, Qp.shape[0], Dp.shape[0], ptr(scores), _norm(normalize), stream_handle(dev))
     _lib.check(st, "launch_varlen_scan")
+
+
+_SCALE_CODES = {torch.float32: _lib.FMS_F32, torch.float16: _lib.FMS_F16}
 
 
 def _int8(t, what):
@@ -218,65 +323,101 @@ def _int8(t, what):
     return t
 
 
-def _f32(t, what):
-    if t is not None and t.dtype != torch.float32:
-        raise UnsupportedError(f"{what} must be Float32 scales")
-    return t
+def _scales(t, what, numel):
+    """INT8 scales: Float32 or Float16 (an Int8Index keeps its features' eltype)."""
+    if t.dtype not in _SCALE_CODES:
+        raise UnsupportedError(f"{what} must be Float32 or Float16 scales, got {t.dtype}")
+    if t.numel() != numel:
+        raise DimensionMismatch(f"{what}: {t.numel()} scales, expected {numel}")
+    return _SCALE_CODES[t.dtype]
 
 
 def launch_int8_pair_scan(args, partial, qc, qs, dc, ds, qmask, dmask, score=None,
                           normalize=False):
-    dev = require_device(args, partial, qc, qs, dc, ds, qmask, dmask, score)
+    _feat(_int8(qc, "qc"), "qc", 2)
+    _feat(_int8(dc, "dc"), "dc", 2, qc)
     Tq, dim = qc.shape
     Td = dc.shape[0]
+    qsc, dsc = _scales(qs, "qs", Tq), _scales(ds, "ds", Td)
+    _buf(args, "args", torch.int32, Tq)
+    _buf(partial, "partial", torch.float32, Tq)
+    _buf(score, "score", torch.float32, 1)
+    dev = require_device(args, partial, qc, qs, dc, ds, qmask, dmask, score)
     st = _lib.lib().fms_launch_int8_pair_scan(
-        ptr(args), ptr(partial), ptr(_int8(qc, "qc")), ptr(_f32(qs, "qs")), ptr(_int8(dc, "dc")),
-        ptr(_f32(ds, "ds")), ptr(_mask(qmask)), ptr(_mask(dmask)), dim, Tq, Td, ptr(score),
+        ptr(args), ptr(partial), ptr(qc), ptr(qs), qsc, ptr(dc), ptr(ds), dsc,
+        ptr(_maskn(qmask, "qmask", Tq)), ptr(_maskn(dmask, "dmask", Td)), dim, Tq, Td, ptr(score),
         _norm(normalize), stream_handle(dev))
     _lib.check(st, "launch_int8_pair_scan")
 
 
 def launch_int8_paired_scan(args, partial, Qc, Qs, Dc, Ds, qmask, dmask, scores=None,
                             normalize=False):
-    dev = require_device(args, partial, Qc, Qs, Dc, Ds, qmask, dmask, scores)
+    _feat(_int8(Qc, "Qc"), "Qc", 3)
+    _feat(_int8(Dc, "Dc"), "Dc", 3, Qc)
     B, Tq, dim = Qc.shape
     Td = Dc.shape[1]
+    if Dc.shape[0] != B:
+        raise DimensionMismatch("batch")
+    qsc, dsc = _scales(Qs, "Qs", B * Tq), _scales(Ds, "Ds", B * Td)
+    _buf(args, "args", torch.int32, B * Tq)
+    _buf(partial, "partial", torch.float32, B * Tq)
+    _buf(scores, "scores", torch.float32, B)
+    dev = require_device(args, partial, Qc, Qs, Dc, Ds, qmask, dmask, scores)
     st = _lib.lib().fms_launch_int8_paired_scan(
-        ptr(args), ptr(partial), ptr(_int8(Qc, "Qc")), ptr(_f32(Qs, "Qs")), ptr(_int8(Dc, "Dc")),
-        ptr(_f32(Ds, "Ds")), ptr(_mask(qmask)), ptr(_mask(dmask)), dim, Tq, Td, B, ptr(scores),
-        _norm(normalize), stream_handle(dev))
+        ptr(args), ptr(partial), ptr(Qc), ptr(Qs), qsc, ptr(Dc), ptr(Ds), dsc,
+        ptr(_maskn(qmask, "qmask", B * Tq)), ptr(_maskn(dmask, "dmask", B * Td)), dim, Tq, Td, B,
+        ptr(scores), _norm(normalize), stream_handle(dev))
     _lib.check(st, "launch_int8_paired_scan")
 
 
 def launch_int8_candidates_scan(args, partial, Qc, Qs, Gc, Gs, idx, qmask, dmask, N,
                                 scores=None, neg=-1.0e4, normalize=False):
-    dev = require_device(args, partial, Qc, Qs, Gc, Gs, idx, qmask, dmask, scores)
+    _feat(_int8(Qc, "Qc"), "Qc", 3)
+    _feat(_int8(Gc, "Gc"), "Gc", 3, Qc)
     B, Tq, dim = Qc.shape
     Td = Gc.shape[1]
+    if N != Gc.shape[0]:
+        raise DimensionMismatch(f"N = {N} but the gallery holds {Gc.shape[0]} documents")
+    if idx.dim() != 2 or idx.shape[0] != B:
+        raise DimensionMismatch("idxs")
     C = idx.shape[1]
+    qsc, dsc = _scales(Qs, "Qs", B * Tq), _scales(Gs, "Gs", N * Td)
+    _buf(args, "args", torch.int32, B * C * Tq)
+    _buf(partial, "partial", torch.float32, B * C * Tq)
+    _buf(scores, "scores", torch.float32, B * C)
+    dev = require_device(args, partial, Qc, Qs, Gc, Gs, idx, qmask, dmask, scores)
     st = _lib.lib().fms_launch_int8_candidates_scan(
-        ptr(args), ptr(partial), ptr(_int8(Qc, "Qc")), ptr(_f32(Qs, "Qs")), ptr(_int8(Gc, "Gc")),
-        ptr(_f32(Gs, "Gs")), ptr(idx), _idx_bytes(idx), ptr(_mask(qmask)), ptr(_mask(dmask)), dim,
-        Tq, B, Td, N, C, ptr(scores), float(neg), _norm(normalize), stream_handle(dev))
+        ptr(args), ptr(partial), ptr(Qc), ptr(Qs), qsc, ptr(Gc), ptr(Gs), dsc, ptr(idx),
+        _idx_bytes(idx), ptr(_maskn(qmask, "qmask", B * Tq)), ptr(_maskn(dmask, "dmask", N * Td)),
+        dim, Tq, B, Td, N, C, ptr(scores), float(neg), _norm(normalize), stream_handle(dev))
     _lib.check(st, "launch_int8_candidates_scan")
 
 
 def int8_quantize(X, codes, scales):
+    """quantize_int8_symmetric (quant.jl:42-49) of Float32 or Float16 features X
+    (..., dim): codes int8 of X's shape, scales (...) of X's eltype."""
+    if X.dtype not in _SCALE_CODES:
+        raise UnsupportedError("quantize_int8_symmetric on device takes Float32 or Float16 features")
+    if X.dim() < 1:
+        raise DimensionMismatch("features need a feature dimension")
+    dim = X.shape[-1]
+    ntok = X.numel() // dim if dim > 0 else scales.numel()
+    _buf(_int8(codes, "codes"), "codes", torch.int8, X.numel())
+    _buf(scales, "scales", X.dtype, ntok)
     dev = require_device(X, codes, scales)
-    if X.dtype != torch.float32:
-        raise UnsupportedError("quantize_int8_symmetric on device takes Float32 features")
-    dim = X.shape[-1] if X.dim() > 0 else 0
-    ntok = scales.numel()
-    st = _lib.lib().fms_int8_quantize(ptr(X), ptr(codes), ptr(scales), dim, ntok,
-                                      stream_handle(dev))
+    st = _lib.lib().fms_int8_quantize(_SCALE_CODES[X.dtype], ptr(X), ptr(codes), ptr(scales), dim,
+                                      ntok, stream_handle(dev))
     _lib.check(st, "int8_quantize")
 
 
 def int8_dots(out, qc, dc):
     """Test-only raw int32 dots: out (Tq, Td) with out[t, u] = <qc_t, dc_u>."""
-    dev = require_device(out, qc, dc)
+    _feat(_int8(qc, "qc"), "qc", 2)
+    _feat(_int8(dc, "dc"), "dc", 2, qc)
     Tq, dim = qc.shape
     Td = dc.shape[0]
+    _buf(out, "out", torch.int32, Tq * Td)
+    dev = require_device(out, qc, dc)
     st = _lib.lib().fms_int8_dots(ptr(out), ptr(qc), ptr(dc), dim, Tq, Td, stream_handle(dev))
     _lib.check(st, "int8_dots")
 
@@ -284,9 +425,11 @@ def int8_dots(out, qc, dc):
 def length_normalize_(scores, qmask, Tq, nrows, ncols, idx=None, N=0, neg=0.0):
     """In place on the Julia-(nrows, ncols) score matrix (torch (ncols, nrows)):
     column c is multiplied by 1/max(count(qmask[:, c]), 1); invalid idx -> neg."""
+    _buf(scores, "scores", torch.float32, nrows * ncols)
+    _maskn(qmask, "qmask", Tq * ncols)
+    if idx is not None and idx.numel() != nrows * ncols:
+        raise DimensionMismatch("length_normalize: idx shape")
     dev = require_device(scores, qmask, idx)
-    if scores.numel() != nrows * ncols:
-        raise ArgumentError("length_normalize: score shape")
     st = _lib.lib().fms_length_normalize(
         ptr(scores), ptr(_mask(qmask)), Tq, nrows, ncols, ptr(idx),
         0 if idx is None else _idx_bytes(idx), N, float(neg), stream_handle(dev))
@@ -294,6 +437,8 @@ def length_normalize_(scores, qmask, Tq, nrows, ncols, idx=None, N=0, neg=0.0):
 
 
 def varlen_normalize_(scores, cu_q):
+    _buf(scores, "scores", torch.float32, scores.numel())
+    _cu(cu_q, "cu_q", scores.numel() + 1)
     dev = require_device(scores, cu_q)
     st = _lib.lib().fms_varlen_normalize(ptr(scores), ptr(cu_q), scores.numel(),
                                          stream_handle(dev))

@@ -1,15 +1,21 @@
 """Per-token symmetric INT8 index (src/quant.jl:1-60).
 
 ``Int8Index.codes`` has the feature shape ((T, dim) or (B, T, dim)) as Int8;
-``scales`` is (T,) or (B, T) Float32.  Quantisation runs on the device
+``scales`` is (T,) or (B, T) in the features' eltype, Float32 or Float16
+(quant.jl:42-49 computes them in T).  Quantisation runs on the device
 (``fms_int8_quantize``) and is bit-exact with quantize_int8_symmetric.
 
 At rest (``save_int8_index`` / ``load_int8_index``) an index is one
 safetensors file with two tensors, ``codes`` and ``scales``, in exactly the
 in-memory layout above -- Julia's column-major ``codes (dim, Td, N)`` and
 ``scales (Td, N)`` byte for byte (quant.jl:11-14) -- plus the format name in
-the metadata.  Loading reads the bytes without executing anything from the
-file and moves them to the requested device.
+the metadata.  Byte layout: a little-endian uint64 header length n, n bytes of
+JSON naming each tensor's dtype ("I8", "F32" / "F16"), shape (row-major, i.e.
+Julia's reversed) and data_offsets [begin, end) after the header, then the
+tensor bytes.  The Julia extension reads the same file with
+``FlashMaxSimHIPExt.load_int8_index`` (plain ``read!``, no JSON package).
+Loading reads the bytes without executing anything from the file and moves
+them to the requested device.
 """
 from __future__ import annotations
 
@@ -37,12 +43,13 @@ class Int8Index:
 
 
 def quantize_int8_symmetric(x: torch.Tensor) -> Int8Index:
-    """quantize_int8_symmetric (quant.jl:42-49) for Float32 device features."""
-    if x.dtype != torch.float32:
-        raise UnsupportedError("quantize_int8_symmetric on device takes Float32 features")
+    """quantize_int8_symmetric (quant.jl:42-49) for Float32 or Float16 device
+    features, computed in the features' type; the scales keep that type."""
+    if x.dtype not in (torch.float32, torch.float16):
+        raise UnsupportedError("quantize_int8_symmetric on device takes Float32 or Float16 features")
     x = x.contiguous()
     codes = torch.empty(x.shape, dtype=torch.int8, device=x.device)
-    scales = torch.empty(x.shape[:-1], dtype=torch.float32, device=x.device)
+    scales = torch.empty(x.shape[:-1], dtype=x.dtype, device=x.device)
     boundary.int8_quantize(x, codes, scales)
     return Int8Index(codes, scales)
 
@@ -65,11 +72,11 @@ def require_int8_index(d: Int8Index) -> None:
 
 
 def save_int8_index(idx: Int8Index, path: str) -> None:
-    """Write an Int8Index to ``path`` as safetensors (codes int8, scales fp32)."""
+    """Write an Int8Index to ``path`` as safetensors (codes int8, scales fp32 / fp16)."""
     from safetensors.torch import save_file
     require_int8_index(idx)
-    if idx.codes.dtype != torch.int8 or idx.scales.dtype != torch.float32:
-        raise ArgumentError("Int8Index at rest holds Int8 codes and Float32 scales")
+    if idx.codes.dtype != torch.int8 or idx.scales.dtype not in (torch.float32, torch.float16):
+        raise ArgumentError("Int8Index at rest holds Int8 codes and Float32 or Float16 scales")
     save_file({"codes": idx.codes.detach().contiguous().cpu(),
                "scales": idx.scales.detach().contiguous().cpu()}, path,
               metadata={"format": INT8_INDEX_FORMAT,
@@ -85,8 +92,8 @@ def load_int8_index(path: str, device="cpu") -> Int8Index:
         if meta.get("format") != INT8_INDEX_FORMAT:
             raise ArgumentError(f"{path}: not a {INT8_INDEX_FORMAT} file")
         codes, scales = f.get_tensor("codes"), f.get_tensor("scales")
-    if codes.dtype != torch.int8 or scales.dtype != torch.float32:
-        raise ArgumentError(f"{path}: codes must be Int8 and scales Float32")
+    if codes.dtype != torch.int8 or scales.dtype not in (torch.float32, torch.float16):
+        raise ArgumentError(f"{path}: codes must be Int8 and scales Float32 or Float16")
     idx = Int8Index(codes, scales)
     require_int8_index(idx)
     return idx.to(device)

@@ -2,7 +2,7 @@
 # routes the fused MaxSim forward on AMDGPU.jl arrays (MI355X / gfx950) to
 # libflashmaxsim_hip.so through `ccall`.
 #
-# It specialises exactly the device plugin boundary that the CUDA extension
+# It specialises the device plugin boundary that the CUDA extension
 # specialises (ext/FlashMaxSimCUDAExt.jl:57-167 in FlashMaxSim.jl):
 #   launch_pair_scan!        src/forward_pair.jl:118-132
 #   launch_paired_scan!      src/forward_layouts.jl:126-143
@@ -13,21 +13,40 @@
 #   launch_int8_pair_scan!   src/quant.jl:139-154
 #   launch_int8_paired_scan! src/quant.jl:199-217
 #   tensor_cores_active      src/ka.jl:71
-# the device pullbacks on the argmax tape (both strategy markers; the library
-# runs the gather + destination-CSR form for either, overwriting the
-# zeros_like gradients it is handed):
+# the layout drivers that allocate the boundary's buffers, so that every
+# float layout uses the library's fused Σ_t / `neg` / tape epilogue:
+#   pair_forward_ka          src/forward_pair.jl:104-116
+#   paired_forward_ka        src/forward_layouts.jl:112-124
+#   inbatch_forward_ka       src/forward_layouts.jl:188-200
+#   candidates_forward_ka    src/forward_layouts.jl:272-290
+#   packed_forward_ka        src/packed.jl:178-202
+#   varlen_forward_ka        src/packed.jl:262-284
+# the device quantiser (quantize_int8_symmetric, src/quant.jl:42-49), and the
+# device pullbacks on the argmax tape (both strategy markers; the library runs
+# the gather + destination-CSR form for either, overwriting the zeros_like
+# gradients it is handed):
 #   pair_apply_pullback!        src/backward_pair.jl:73-87
 #   paired_apply_pullback!      src/backward_layouts.jl:45-60
 #   inbatch_apply_pullback!     src/backward_layouts.jl:113-127
 #   candidates_apply_pullback!  src/backward_layouts.jl:187-202
 #   packed_apply_pullback!      src/packed.jl:384-390
 #   varlen_apply_pullback!      src/packed.jl:449-455
-# and additionally candidates_forward_ka (src/forward_layouts.jl:272-290), so
-# the candidate layout uses the library's fused Σ_t + `neg` epilogue instead
-# of the separate `sum(partial; dims=1)` and `ifelse.` kernels.
-# Two functions have no reference method and are called through the
+# Three functions have no reference method and are called through the
 # extension module: packed_multi_scan (nq queries against one PackedSeq in
-# one pass) and topk (the k best scores of every query column).
+# one pass), topk (the k best scores of every query column) and
+# load_int8_index (an Int8Index read from its at-rest file).
+#
+# Score buffers.  Every scan entry point writes Float32 partials and scores.
+# The reference allocates them as dot_accum(T) / score_eltype(T)
+# (src/kernels_forward.jl:16-21): Float32 for Float16 and Float32 features,
+# but BFloat16 for BFloat16 features.  So the buffer-taking launch_*! and
+# inbatch_device_scan! methods below require Float32 buffers in their
+# signatures (a BFloat16 buffer matches none of them and keeps the
+# reference's own KA path), and BFloat16 features reach the library only
+# through the *_forward_ka drivers, which allocate Float32 outputs
+# themselves.  BFloat16 scores therefore come back Float32: the library
+# accumulates in fp32 for every 16-bit type, where the reference would
+# accumulate BFloat16 in BFloat16.
 #
 # Arrays are passed as raw device pointers in Julia's own column-major
 # layout, which is the layout the C ABI documents; nothing is copied or
@@ -36,13 +55,15 @@
 # an ArgumentError, like the reference's pre-launch checks.
 #
 # Julia is not installed in the build container, so this file is written to
-# the AMDGPU.jl 1.x API and is not exercised by the repository's tests; the
-# Python host mirror (flashmaxsim.jl_amd/flashmaxsim) drives the same C ABI
-# in the test suite.
+# the AMDGPU.jl 1.x API and its `ccall`s are checked against the C header by
+# a parser in the repository's CPU tests (symbol, arity, argument types and
+# argument order); the Python host mirror (flashmaxsim.jl_amd/flashmaxsim)
+# drives the same C ABI on the GPU.
 module FlashMaxSimHIPExt
 
 using AMDGPU
 using FlashMaxSim
+using FlashMaxSim: PackedSeq, Int8Index
 
 const libfms = get(ENV, "FLASHMAXSIM_HIP_LIB",
                    joinpath(@__DIR__, "..", "..", "lib", "libflashmaxsim_hip.so"))
@@ -53,11 +74,16 @@ const FMS_BF16 = Int32(2)
 
 const ROCBackend = AMDGPU.ROCBackend
 
+# Feature types whose reference-allocated partial / score buffers are Float32.
+const ScanFeature = Union{Float16, Float32}
+# Scale types of an Int8Index whose dot_accum is Float32.
+const ScaleType = Union{Float16, Float32}
+
 @static if isdefined(Core, :BFloat16)
-    const FloatFeature = Union{Float16, Float32, Core.BFloat16}
+    const AnyFeature = Union{Float16, Float32, Core.BFloat16}
     dtype_code(::Type{Core.BFloat16}) = FMS_BF16
 else
-    const FloatFeature = Union{Float16, Float32}
+    const AnyFeature = ScanFeature
 end
 dtype_code(::Type{Float32}) = FMS_F32
 dtype_code(::Type{Float16}) = FMS_F16
@@ -74,237 +100,413 @@ end
 
 gfx950() = ccall((:fms_arch_supported, libfms), Cint, ()) == 1
 
-FlashMaxSim.tensor_cores_active(::ROCBackend, ::Type{T}) where {T<:FloatFeature} = gfx950()
+FlashMaxSim.tensor_cores_active(::ROCBackend, ::Type{T}) where {T<:AnyFeature} = gfx950()
 FlashMaxSim.tensor_cores_active(::ROCBackend, ::Type{Int8}) = gfx950()
 
-# ---- float scans -------------------------------------------------------------
+# ---- C entry points (one Julia function per ccall) ------------------------------
+# `partial` / `scores` may be `nothing` (NULL): the fused drivers pass scores
+# only, the boundary methods partials only.
 
-function FlashMaxSim.launch_pair_scan!(::ROCBackend, argmax_u, partial,
-                                       q::ROCMatrix{T}, d::ROCMatrix{T},
-                                       qmask, dmask) where {T<:FloatFeature}
-    dim, Tq = size(q)
+function c_pair_scan(dtype, argmax_u, partial, q, d, qmask, dmask, dim, Tq, Td, score)
     check(ccall((:fms_launch_pair_scan, libfms), Int32,
                 (Int32, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid},
                  Int64, Int64, Int64, Ptr{Cvoid}, Int32, Ptr{Cvoid}),
-                dtype_code(T), dptr(argmax_u), dptr(partial), dptr(q), dptr(d),
-                dptr(qmask), dptr(dmask), dim, Tq, size(d, 2), C_NULL, Int32(0), stream_ptr()),
+                dtype, dptr(argmax_u), dptr(partial), dptr(q), dptr(d), dptr(qmask),
+                dptr(dmask), dim, Tq, Td, dptr(score), Int32(0), stream_ptr()),
           "pair scan")
-    nothing
 end
 
-function FlashMaxSim.launch_paired_scan!(::ROCBackend, args, partial,
-                                         Q::ROCArray{T,3}, D::ROCArray{T,3},
-                                         qmask, dmask) where {T<:FloatFeature}
-    dim, Tq, B = size(Q)
+function c_paired_scan(dtype, args, partial, Q, D, qmask, dmask, dim, Tq, Td, B, scores)
     check(ccall((:fms_launch_paired_scan, libfms), Int32,
                 (Int32, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid},
                  Int64, Int64, Int64, Int64, Ptr{Cvoid}, Int32, Ptr{Cvoid}),
-                dtype_code(T), dptr(args), dptr(partial), dptr(Q), dptr(D),
-                dptr(qmask), dptr(dmask), dim, Tq, size(D, 2), B, C_NULL, Int32(0), stream_ptr()),
+                dtype, dptr(args), dptr(partial), dptr(Q), dptr(D), dptr(qmask), dptr(dmask),
+                dim, Tq, Td, B, dptr(scores), Int32(0), stream_ptr()),
           "paired scan")
-    nothing
 end
 
-function candidates_call(args, partial, scores, Q::ROCArray{T,3}, gallery, idx,
-                         qmask, dmask, N, neg) where {T<:FloatFeature}
-    dim, Tq, B = size(Q)
+function c_candidates_scan(dtype, args, partial, Q, gallery, idx, qmask, dmask,
+                           dim, Tq, B, Td, N, C, scores, neg)
     check(ccall((:fms_launch_candidates_scan, libfms), Int32,
                 (Int32, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Int32,
                  Ptr{Cvoid}, Ptr{Cvoid}, Int64, Int64, Int64, Int64, Int64, Int64,
                  Ptr{Cvoid}, Float32, Int32, Ptr{Cvoid}),
-                dtype_code(T), dptr(args), dptr(partial), dptr(Q), dptr(gallery),
-                dptr(idx), Int32(sizeof(eltype(idx))), dptr(qmask), dptr(dmask),
-                dim, Tq, B, size(gallery, 2), N, size(idx, 1),
+                dtype, dptr(args), dptr(partial), dptr(Q), dptr(gallery), dptr(idx),
+                Int32(sizeof(eltype(idx))), dptr(qmask), dptr(dmask), dim, Tq, B, Td, N, C,
                 dptr(scores), Float32(neg), Int32(0), stream_ptr()),
           "candidate scan")
+end
+
+function c_inbatch_scan(dtype, S, args, Q, D, qmask, dmask, dim, Tq, Bq, Td, Bd)
+    check(ccall((:fms_inbatch_device_scan, libfms), Int32,
+                (Int32, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid},
+                 Int64, Int64, Int64, Int64, Int64, Int32, Ptr{Cvoid}),
+                dtype, dptr(S), dptr(args), dptr(Q), dptr(D), dptr(qmask), dptr(dmask),
+                dim, Tq, Bq, Td, Bd, Int32(0), stream_ptr()),
+          "in-batch scan")
+end
+
+function c_packed_scan(dtype, args, partial, q, tokens, cu, qmask, dim, Tq, B, ntokens, scores)
+    check(ccall((:fms_launch_packed_scan, libfms), Int32,
+                (Int32, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid},
+                 Int64, Int64, Int64, Int64, Ptr{Cvoid}, Int32, Ptr{Cvoid}),
+                dtype, dptr(args), dptr(partial), dptr(q), dptr(tokens), dptr(cu), dptr(qmask),
+                dim, Tq, B, ntokens, dptr(scores), Int32(0), stream_ptr()),
+          "packed scan")
+end
+
+function c_varlen_scan(dtype, args, partial, Qtokens, Dtokens, cu_q, cu_d, dim, max_q, N,
+                       nq_tokens, nd_tokens, scores)
+    check(ccall((:fms_launch_varlen_scan, libfms), Int32,
+                (Int32, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid},
+                 Int64, Int64, Int64, Int64, Int64, Ptr{Cvoid}, Int32, Ptr{Cvoid}),
+                dtype, dptr(args), dptr(partial), dptr(Qtokens), dptr(Dtokens), dptr(cu_q),
+                dptr(cu_d), dim, max_q, N, nq_tokens, nd_tokens, dptr(scores), Int32(0),
+                stream_ptr()),
+          "varlen scan")
+end
+
+# ---- float scans: the boundary methods (reference-allocated Float32 buffers) ------
+
+function FlashMaxSim.launch_pair_scan!(::ROCBackend, argmax_u::ROCVector{Int32},
+                                       partial::ROCVector{Float32},
+                                       q::ROCMatrix{T}, d::ROCMatrix{T},
+                                       qmask, dmask) where {T<:ScanFeature}
+    dim, Tq = size(q)
+    c_pair_scan(dtype_code(T), argmax_u, partial, q, d, qmask, dmask, dim, Tq, size(d, 2),
+                nothing)
     nothing
 end
 
-FlashMaxSim.launch_candidates_scan!(::ROCBackend, args, partial, Q::ROCArray{T,3},
-                                    gallery::ROCArray{T,3}, idx, qmask, dmask,
-                                    N) where {T<:FloatFeature} =
-    candidates_call(args, partial, nothing, Q, gallery, idx, qmask, dmask, N, 0)
+function FlashMaxSim.launch_paired_scan!(::ROCBackend, args::ROCMatrix{Int32},
+                                         partial::ROCMatrix{Float32},
+                                         Q::ROCArray{T,3}, D::ROCArray{T,3},
+                                         qmask, dmask) where {T<:ScanFeature}
+    dim, Tq, B = size(Q)
+    c_paired_scan(dtype_code(T), args, partial, Q, D, qmask, dmask, dim, Tq, size(D, 2), B,
+                  nothing)
+    nothing
+end
 
-# Fused driver: Σ_t and the `neg` fill happen inside the scan kernel
-# (replaces src/forward_layouts.jl:285-287).  Same outputs as the reference
-# driver: (scores (C,B) in score_eltype(T), args (Tq,C,B)).
-function FlashMaxSim.candidates_forward_ka(backend::ROCBackend, Q::ROCArray{T,3},
+function FlashMaxSim.launch_candidates_scan!(::ROCBackend, args::ROCArray{Int32,3},
+                                             partial::ROCArray{Float32,3},
+                                             Q::ROCArray{T,3}, gallery::ROCArray{T,3}, idx,
+                                             qmask, dmask, N) where {T<:ScanFeature}
+    dim, Tq, B = size(Q)
+    c_candidates_scan(dtype_code(T), args, partial, Q, gallery, idx, qmask, dmask,
+                      dim, Tq, B, size(gallery, 2), N, size(idx, 1), nothing, 0)
+    nothing
+end
+
+function FlashMaxSim.inbatch_device_scan!(::ROCBackend, S::ROCMatrix{Float32},
+                                          args::ROCArray{Int32,3},
+                                          Q::ROCArray{T,3}, D::ROCArray{T,3},
+                                          qmask, dmask) where {T<:ScanFeature}
+    dim, Tq, Bq = size(Q)
+    c_inbatch_scan(dtype_code(T), S, args, Q, D, qmask, dmask, dim, Tq, Bq, size(D, 2),
+                   size(D, 3))
+    nothing
+end
+
+function FlashMaxSim.launch_packed_scan!(::ROCBackend, args::ROCMatrix{Int32},
+                                         partial::ROCMatrix{Float32}, q::ROCMatrix{T},
+                                         tokens::ROCMatrix{T}, cu::ROCVector{Int32},
+                                         qmask) where {T<:ScanFeature}
+    dim, Tq = size(q)
+    c_packed_scan(dtype_code(T), args, partial, q, tokens, cu, qmask, dim, Tq,
+                  length(cu) - 1, size(tokens, 2), nothing)
+    nothing
+end
+
+function FlashMaxSim.launch_varlen_scan!(::ROCBackend, args::ROCMatrix{Int32},
+                                         partial::ROCMatrix{Float32}, Qtokens::ROCMatrix{T},
+                                         Dtokens::ROCMatrix{T}, cu_q::ROCVector{Int32},
+                                         cu_d::ROCVector{Int32}) where {T<:ScanFeature}
+    c_varlen_scan(dtype_code(T), args, partial, Qtokens, Dtokens, cu_q, cu_d,
+                  size(Qtokens, 1), size(args, 1), size(args, 2), size(Qtokens, 2),
+                  size(Dtokens, 2), nothing)
+    nothing
+end
+
+# ---- float scans: the layout drivers (Float32 outputs allocated here) -----------
+# Same results as the reference drivers: (scores, args) with scores in Float32
+# (score_eltype(T) for Float16 / Float32 features; Float32 in place of BFloat16
+# for BFloat16 features, see the header).  Σ_t and the `neg` fill run inside
+# the scan kernel instead of the separate `sum(partial; dims = 1)` and
+# `ifelse.` kernels.
+
+function FlashMaxSim.pair_forward_ka(::ROCBackend, q::ROCMatrix{T}, d::ROCMatrix{T},
+                                     qmask::AbstractVector{Bool}, dmask::AbstractVector{Bool},
+                                     ::T) where {T<:AnyFeature}
+    dim, Tq, Td = FlashMaxSim.require_pair_shapes(q, d, qmask, dmask)
+    argmax_u = AMDGPU.zeros(Int32, Tq)
+    score = AMDGPU.zeros(Float32, 1)     # length-1, stays on the device
+    c_pair_scan(dtype_code(T), argmax_u, nothing, q, d, qmask, dmask, dim, Tq, Td, score)
+    score, argmax_u
+end
+
+function FlashMaxSim.paired_forward_ka(::ROCBackend, Q::ROCArray{T,3}, D::ROCArray{T,3},
+                                       qmask::AbstractMatrix{Bool},
+                                       dmask::AbstractMatrix{Bool},
+                                       ::T) where {T<:AnyFeature}
+    dim, Tq, Td, B = FlashMaxSim.require_paired_shapes(Q, D, qmask, dmask)
+    args = AMDGPU.zeros(Int32, Tq, B)
+    scores = AMDGPU.zeros(Float32, B)
+    c_paired_scan(dtype_code(T), args, nothing, Q, D, qmask, dmask, dim, Tq, Td, B, scores)
+    scores, args
+end
+
+function FlashMaxSim.inbatch_forward_ka(::ROCBackend, Q::ROCArray{T,3}, D::ROCArray{T,3},
+                                        qmask::AbstractMatrix{Bool},
+                                        dmask::AbstractMatrix{Bool},
+                                        ::T) where {T<:AnyFeature}
+    dim, Tq, Bq, Td, Bd = FlashMaxSim.require_inbatch_shapes(Q, D, qmask, dmask)
+    S = AMDGPU.zeros(Float32, Bd, Bq)
+    args = AMDGPU.zeros(Int32, Tq, Bd, Bq)
+    (Bd == 0 || Bq == 0 || Tq == 0 || Td == 0) && return S, args
+    c_inbatch_scan(dtype_code(T), S, args, Q, D, qmask, dmask, dim, Tq, Bq, Td, Bd)
+    S, args
+end
+
+function FlashMaxSim.candidates_forward_ka(::ROCBackend, Q::ROCArray{T,3},
                                            gallery::ROCArray{T,3},
                                            idxs::AbstractMatrix{<:Integer},
                                            qmask::AbstractMatrix{Bool},
                                            dmask::AbstractMatrix{Bool},
-                                           neg::T) where {T<:FloatFeature}
-    _, Tq, B, _, N = FlashMaxSim.require_candidates_shapes(Q, gallery, idxs, qmask, dmask)
+                                           neg::T) where {T<:AnyFeature}
+    dim, Tq, B, Td, N = FlashMaxSim.require_candidates_shapes(Q, gallery, idxs, qmask, dmask)
     idx = FlashMaxSim.indices_on(Q, idxs)
     C = size(idx, 1)
-    args = FlashMaxSim.zeros_like(Q, Int32, Tq, C, B)
-    S = similar(Q, FlashMaxSim.score_eltype(T), C, B)
-    candidates_call(args, nothing, S, Q, gallery, idx, qmask, dmask, N, neg)
-    S, args
+    args = AMDGPU.zeros(Int32, Tq, C, B)
+    scores = AMDGPU.zeros(Float32, C, B)
+    c_candidates_scan(dtype_code(T), args, nothing, Q, gallery, idx, qmask, dmask,
+                      dim, Tq, B, Td, N, C, scores, neg)
+    scores, args
 end
 
-function FlashMaxSim.inbatch_device_scan!(::ROCBackend, S, args,
-                                          Q::ROCArray{T,3}, D::ROCArray{T,3},
-                                          qmask, dmask) where {T<:FloatFeature}
-    dim, Tq, Bq = size(Q)
-    check(ccall((:fms_inbatch_device_scan, libfms), Int32,
-                (Int32, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid},
-                 Int64, Int64, Int64, Int64, Int64, Int32, Ptr{Cvoid}),
-                dtype_code(T), dptr(S), dptr(args), dptr(Q), dptr(D),
-                dptr(qmask), dptr(dmask), dim, Tq, Bq, size(D, 2), size(D, 3), Int32(0),
-                stream_ptr()),
-          "in-batch scan")
-    nothing
+function FlashMaxSim.packed_forward_ka(::ROCBackend, q::ROCMatrix{T}, P::PackedSeq,
+                                       qmask::AbstractVector{Bool}, ::T) where {T<:AnyFeature}
+    Tq, B = FlashMaxSim.require_packed_shapes(q, P, qmask)
+    tokens, cu = P.tokens, P.cu
+    eltype(tokens) === T || throw(ArgumentError("PackedSeq tokens must have the query eltype"))
+    eltype(cu) === Int32 || throw(ArgumentError("PackedSeq cu must be Int32 on the device"))
+    args = AMDGPU.zeros(Int32, Tq, B)
+    scores = AMDGPU.zeros(Float32, B)
+    c_packed_scan(dtype_code(T), args, nothing, q, tokens, cu, qmask, size(q, 1), Tq, B,
+                  size(tokens, 2), scores)
+    scores, args
 end
 
-function FlashMaxSim.launch_packed_scan!(::ROCBackend, args, partial, q::ROCMatrix{T},
-                                         packed::ROCMatrix{T}, cu::ROCVector{Int32},
-                                         qmask) where {T<:FloatFeature}
-    dim, Tq = size(q)
-    check(ccall((:fms_launch_packed_scan, libfms), Int32,
-                (Int32, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid},
-                 Int64, Int64, Int64, Int64, Ptr{Cvoid}, Int32, Ptr{Cvoid}),
-                dtype_code(T), dptr(args), dptr(partial), dptr(q), dptr(packed), dptr(cu),
-                dptr(qmask), dim, Tq, length(cu) - 1, size(packed, 2), C_NULL, Int32(0),
-                stream_ptr()),
-          "packed scan")
-    nothing
+function FlashMaxSim.varlen_forward_ka(::ROCBackend, Q::PackedSeq{<:ROCMatrix{T}},
+                                       D::PackedSeq{<:ROCMatrix{T}}, ::T) where {T<:AnyFeature}
+    N, max_q = FlashMaxSim.require_varlen_shapes(Q, D)
+    Qtokens, Dtokens, cu_q, cu_d = Q.tokens, D.tokens, Q.cu, D.cu
+    (eltype(cu_q) === Int32 && eltype(cu_d) === Int32) ||
+        throw(ArgumentError("PackedSeq cu must be Int32 on the device"))
+    args = AMDGPU.zeros(Int32, max_q, N)
+    scores = AMDGPU.zeros(Float32, N)
+    c_varlen_scan(dtype_code(T), args, nothing, Qtokens, Dtokens, cu_q, cu_d, size(Qtokens, 1),
+                  max_q, N, size(Qtokens, 2), size(Dtokens, 2), scores)
+    scores, args
 end
 
-function FlashMaxSim.launch_varlen_scan!(::ROCBackend, args, partial, Qp::ROCMatrix{T},
-                                         Dp::ROCMatrix{T}, cu_q::ROCVector{Int32},
-                                         cu_d::ROCVector{Int32}) where {T<:FloatFeature}
-    check(ccall((:fms_launch_varlen_scan, libfms), Int32,
-                (Int32, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid},
-                 Int64, Int64, Int64, Int64, Int64, Ptr{Cvoid}, Int32, Ptr{Cvoid}),
-                dtype_code(T), dptr(args), dptr(partial), dptr(Qp), dptr(Dp),
-                dptr(cu_q), dptr(cu_d), size(Qp, 1), size(args, 1), size(args, 2),
-                size(Qp, 2), size(Dp, 2), C_NULL, Int32(0), stream_ptr()),
-          "varlen scan")
-    nothing
+# ---- INT8 --------------------------------------------------------------------------
+# Scales may be Float16 or Float32 (an Int8Index keeps the eltype of the features it
+# was quantised from, src/quant.jl:42-49); the scans widen them to Float32 and
+# evaluate (qs * ds) * Float32(acc) (src/kernels_int8.jl:17-25).  Partials are
+# dot_accum(eltype(qs)) = Float32 for both.
+
+scale_code(::Type{Float32}) = FMS_F32
+scale_code(::Type{Float16}) = FMS_F16
+
+function FlashMaxSim.quantize_int8_symmetric(X::ROCArray{T}) where {T<:ScaleType}
+    ndims(X) in (2, 3) || throw(ArgumentError("quantize_int8_symmetric takes (dim, T[, B]) features"))
+    dim = size(X, 1)
+    codes = similar(X, Int8)
+    scales = similar(X, T, size(X)[2:end]...)
+    ntok = length(scales)
+    ntok == 0 || check(ccall((:fms_int8_quantize, libfms), Int32,
+                             (Int32, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Int64, Int64, Ptr{Cvoid}),
+                             dtype_code(T), dptr(X), dptr(codes), dptr(scales), dim, ntok,
+                             stream_ptr()),
+                       "INT8 quantiser")
+    Int8Index(codes, scales)
 end
 
-# ---- INT8 scans ----------------------------------------------------------------
-
-function FlashMaxSim.launch_int8_pair_scan!(::ROCBackend, args, partial, qc::ROCMatrix{Int8},
-                                            qs::ROCVector{Float32}, dc::ROCMatrix{Int8},
-                                            ds::ROCVector{Float32}, qmask, dmask)
+function FlashMaxSim.launch_int8_pair_scan!(::ROCBackend, args::ROCVector{Int32},
+                                            partial::ROCVector{Float32}, qc::ROCMatrix{Int8},
+                                            qs::ROCVector{S1}, dc::ROCMatrix{Int8},
+                                            ds::ROCVector{S2}, qmask,
+                                            dmask) where {S1<:ScaleType, S2<:ScaleType}
     dim, Tq = size(qc)
     check(ccall((:fms_launch_int8_pair_scan, libfms), Int32,
-                (Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid},
-                 Ptr{Cvoid}, Ptr{Cvoid}, Int64, Int64, Int64, Ptr{Cvoid}, Int32, Ptr{Cvoid}),
-                dptr(args), dptr(partial), dptr(qc), dptr(qs), dptr(dc), dptr(ds),
-                dptr(qmask), dptr(dmask), dim, Tq, size(dc, 2), C_NULL, Int32(0), stream_ptr()),
+                (Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Int32, Ptr{Cvoid}, Ptr{Cvoid},
+                 Int32, Ptr{Cvoid}, Ptr{Cvoid}, Int64, Int64, Int64, Ptr{Cvoid}, Int32,
+                 Ptr{Cvoid}),
+                dptr(args), dptr(partial), dptr(qc), dptr(qs), scale_code(S1), dptr(dc),
+                dptr(ds), scale_code(S2), dptr(qmask), dptr(dmask), dim, Tq, size(dc, 2),
+                C_NULL, Int32(0), stream_ptr()),
           "INT8 pair scan")
     nothing
 end
 
-function FlashMaxSim.launch_int8_paired_scan!(::ROCBackend, args, partial,
-                                              Qc::ROCArray{Int8,3}, Qs::ROCMatrix{Float32},
-                                              Dc::ROCArray{Int8,3}, Ds::ROCMatrix{Float32},
-                                              qmask, dmask)
+function FlashMaxSim.launch_int8_paired_scan!(::ROCBackend, args::ROCMatrix{Int32},
+                                              partial::ROCMatrix{Float32},
+                                              Qc::ROCArray{Int8,3}, Qs::ROCMatrix{S1},
+                                              Dc::ROCArray{Int8,3}, Ds::ROCMatrix{S2},
+                                              qmask, dmask) where {S1<:ScaleType, S2<:ScaleType}
     dim, Tq, B = size(Qc)
     check(ccall((:fms_launch_int8_paired_scan, libfms), Int32,
-                (Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid},
-                 Ptr{Cvoid}, Ptr{Cvoid}, Int64, Int64, Int64, Int64, Ptr{Cvoid}, Int32, Ptr{Cvoid}),
-                dptr(args), dptr(partial), dptr(Qc), dptr(Qs), dptr(Dc), dptr(Ds),
-                dptr(qmask), dptr(dmask), dim, Tq, size(Dc, 2), B, C_NULL, Int32(0), stream_ptr()),
+                (Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Int32, Ptr{Cvoid}, Ptr{Cvoid},
+                 Int32, Ptr{Cvoid}, Ptr{Cvoid}, Int64, Int64, Int64, Int64, Ptr{Cvoid}, Int32,
+                 Ptr{Cvoid}),
+                dptr(args), dptr(partial), dptr(Qc), dptr(Qs), scale_code(S1), dptr(Dc),
+                dptr(Ds), scale_code(S2), dptr(qmask), dptr(dmask), dim, Tq, size(Dc, 2), B,
+                C_NULL, Int32(0), stream_ptr()),
           "INT8 paired scan")
     nothing
 end
 
+"""
+    int8_candidates_scan(Q::ROCArray{T,3}, D::Int8Index, idxs; qmask, dmask, neg) -> (S, args)
+
+The INT8 candidate layout (no reference method: the candidate conventions of
+`maxsim(Q, gallery, idxs)`, src/forward_layouts.jl:272-290, applied to an Int8Index
+gallery).  Q is quantised on the fly; `S (C, B)` Float32 with `neg` at invalid
+indices, `args (Tq, C, B)`.
+"""
+function int8_candidates_scan(Q::ROCArray{T,3}, D::Int8Index, idxs::ROCMatrix{<:Integer};
+                              qmask = nothing, dmask = nothing,
+                              neg::Real = -1.0f4) where {T<:ScaleType}
+    QQ = FlashMaxSim.quantize_int8_symmetric(Q)
+    Qc, Qs, Gc, Gs = QQ.codes, QQ.scales, D.codes, D.scales
+    dim, Tq, B = size(Qc)
+    Td, N = size(Gc, 2), size(Gc, 3)
+    size(Gc, 1) == dim || throw(DimensionMismatch("feature dim"))
+    size(idxs, 2) == B || throw(DimensionMismatch("idxs"))
+    eltype(Gs) <: ScaleType || throw(ArgumentError("Int8Index scales must be Float16 or Float32"))
+    idx = FlashMaxSim.indices_on(Qc, idxs)
+    C = size(idx, 1)
+    args = AMDGPU.zeros(Int32, Tq, C, B)
+    scores = AMDGPU.zeros(Float32, C, B)
+    check(ccall((:fms_launch_int8_candidates_scan, libfms), Int32,
+                (Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Int32, Ptr{Cvoid}, Ptr{Cvoid},
+                 Int32, Ptr{Cvoid}, Int32, Ptr{Cvoid}, Ptr{Cvoid}, Int64, Int64, Int64, Int64,
+                 Int64, Int64, Ptr{Cvoid}, Float32, Int32, Ptr{Cvoid}),
+                dptr(args), C_NULL, dptr(Qc), dptr(Qs), scale_code(eltype(Qs)), dptr(Gc),
+                dptr(Gs), scale_code(eltype(Gs)), dptr(idx), Int32(sizeof(eltype(idx))),
+                dptr(qmask), dptr(dmask), dim, Tq, B, Td, N, C, dptr(scores), Float32(neg),
+                Int32(0), stream_ptr()),
+          "INT8 candidate scan")
+    scores, args
+end
 
 # ---- pullbacks on the argmax tape ----------------------------------------------
-# Δ and inv_n arrive in the feature eltype (convert_scores in src/rrule.jl);
-# inv_n === nothing passes NULL (all ones).
+# Δ and inv_n arrive in the feature eltype (convert_scores in src/rrule.jl), and the
+# gradients are feature-eltype buffers, which is what the library reads and writes
+# for every feature type; inv_n === nothing passes NULL (all ones).
 
 for M in (FlashMaxSim.AtomicUnified, FlashMaxSim.InvGrid)
     @eval begin
-        function FlashMaxSim.pair_apply_pullback!(::$M, ::ROCBackend, dq, dd,
-                                                  q::ROCMatrix{T}, d::ROCMatrix{T}, qmask,
-                                                  argmax_u, δ, dim, Tq, Td) where {T<:FloatFeature}
+        function FlashMaxSim.pair_apply_pullback!(::$M, ::ROCBackend, dq::ROCMatrix{T},
+                                                  dd::ROCMatrix{T}, q::ROCMatrix{T},
+                                                  d::ROCMatrix{T}, qmask,
+                                                  argmax_u::ROCVector{Int32},
+                                                  delta::ROCVector{T}, dim, Tq,
+                                                  Td) where {T<:AnyFeature}
             check(ccall((:fms_pair_pullback, libfms), Int32,
                         (Int32, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid},
                          Ptr{Cvoid}, Ptr{Cvoid}, Int64, Int64, Int64, Ptr{Cvoid}),
                         dtype_code(T), dptr(dq), dptr(dd), dptr(q), dptr(d), dptr(qmask),
-                        dptr(argmax_u), dptr(δ), dim, Tq, Td, stream_ptr()),
+                        dptr(argmax_u), dptr(delta), dim, Tq, Td, stream_ptr()),
                   "pair pullback")
             nothing
         end
 
-        function FlashMaxSim.paired_apply_pullback!(::$M, ::ROCBackend, dQ, dD,
-                                                    Q::ROCArray{T,3}, D::ROCArray{T,3}, qmask,
-                                                    args, Δ, inv_n, dim, Tq, B,
-                                                    Td) where {T<:FloatFeature}
+        function FlashMaxSim.paired_apply_pullback!(::$M, ::ROCBackend, dQ::ROCArray{T,3},
+                                                    dD::ROCArray{T,3}, Q::ROCArray{T,3},
+                                                    D::ROCArray{T,3}, qmask,
+                                                    args::ROCMatrix{Int32}, Delta::ROCVector{T},
+                                                    inv_n, dim, Tq, B,
+                                                    Td) where {T<:AnyFeature}
             check(ccall((:fms_paired_pullback, libfms), Int32,
                         (Int32, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid},
                          Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Int64, Int64, Int64, Int64, Ptr{Cvoid}),
                         dtype_code(T), dptr(dQ), dptr(dD), dptr(Q), dptr(D), dptr(qmask),
-                        dptr(args), dptr(Δ), dptr(inv_n), dim, Tq, Td, B, stream_ptr()),
+                        dptr(args), dptr(Delta), dptr(inv_n), dim, Tq, Td, B, stream_ptr()),
                   "paired pullback")
             nothing
         end
 
-        function FlashMaxSim.inbatch_apply_pullback!(::$M, ::ROCBackend, dQ, dD,
-                                                     Q::ROCArray{T,3}, D::ROCArray{T,3}, qmask,
-                                                     args, Δ, inv_n, dim, Tq, Bq, Td,
-                                                     Bd) where {T<:FloatFeature}
+        function FlashMaxSim.inbatch_apply_pullback!(::$M, ::ROCBackend, dQ::ROCArray{T,3},
+                                                     dD::ROCArray{T,3}, Q::ROCArray{T,3},
+                                                     D::ROCArray{T,3}, qmask,
+                                                     args::ROCArray{Int32,3},
+                                                     Delta::ROCMatrix{T}, inv_n, dim, Tq, Bq,
+                                                     Td, Bd) where {T<:AnyFeature}
             check(ccall((:fms_inbatch_pullback, libfms), Int32,
                         (Int32, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid},
                          Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Int64, Int64, Int64, Int64, Int64,
                          Ptr{Cvoid}),
                         dtype_code(T), dptr(dQ), dptr(dD), dptr(Q), dptr(D), dptr(qmask),
-                        dptr(args), dptr(Δ), dptr(inv_n), dim, Tq, Td, Bq, Bd, stream_ptr()),
+                        dptr(args), dptr(Delta), dptr(inv_n), dim, Tq, Td, Bq, Bd, stream_ptr()),
                   "in-batch pullback")
             nothing
         end
 
-        function FlashMaxSim.candidates_apply_pullback!(::$M, ::ROCBackend, dQ, dG,
-                                                        Q::ROCArray{T,3}, gallery::ROCArray{T,3},
-                                                        idx, qmask, args, Δ, inv_n, dim, Tq, B,
-                                                        Td, C, N) where {T<:FloatFeature}
+        function FlashMaxSim.candidates_apply_pullback!(::$M, ::ROCBackend, dQ::ROCArray{T,3},
+                                                        dG::ROCArray{T,3}, Q::ROCArray{T,3},
+                                                        gallery::ROCArray{T,3}, idx, qmask,
+                                                        args::ROCArray{Int32,3},
+                                                        Delta::ROCMatrix{T}, inv_n, dim, Tq, B,
+                                                        Td, C, N) where {T<:AnyFeature}
             check(ccall((:fms_candidates_pullback, libfms), Int32,
                         (Int32, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Int32,
                          Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Int64, Int64, Int64,
                          Int64, Int64, Int64, Ptr{Cvoid}),
                         dtype_code(T), dptr(dQ), dptr(dG), dptr(Q), dptr(gallery), dptr(idx),
-                        Int32(sizeof(eltype(idx))), dptr(qmask), dptr(args), dptr(Δ),
+                        Int32(sizeof(eltype(idx))), dptr(qmask), dptr(args), dptr(Delta),
                         dptr(inv_n), dim, Tq, B, Td, N, C, stream_ptr()),
                   "candidates pullback")
             nothing
         end
 
-        function FlashMaxSim.packed_apply_pullback!(::$M, ::ROCBackend, Δ, q::ROCMatrix{T},
-                                                    P::FlashMaxSim.PackedSeq, qmask, args,
-                                                    inv_n) where {T<:FloatFeature}
+        function FlashMaxSim.packed_apply_pullback!(::$M, ::ROCBackend, Delta::ROCVector{T},
+                                                    q::ROCMatrix{T}, P::PackedSeq, qmask,
+                                                    args::ROCMatrix{Int32},
+                                                    inv_n) where {T<:AnyFeature}
+            tokens, cu = P.tokens, P.cu
+            eltype(tokens) === T || throw(ArgumentError("PackedSeq tokens must have the query eltype"))
             dq = similar(q)
-            dP = similar(P.tokens)
+            dP = similar(tokens)
             dim, Tq = size(q)
             check(ccall((:fms_packed_pullback, libfms), Int32,
                         (Int32, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid},
                          Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Int64, Int64, Int64,
                          Int64, Ptr{Cvoid}),
-                        dtype_code(T), dptr(dq), dptr(dP), dptr(q), dptr(P.tokens), dptr(P.cu),
-                        dptr(qmask), dptr(args), dptr(Δ), dptr(inv_n), dim, Tq,
-                        length(P.cu) - 1, size(P.tokens, 2), stream_ptr()),
+                        dtype_code(T), dptr(dq), dptr(dP), dptr(q), dptr(tokens), dptr(cu),
+                        dptr(qmask), dptr(args), dptr(Delta), dptr(inv_n), dim, Tq,
+                        length(cu) - 1, size(tokens, 2), stream_ptr()),
                   "packed pullback")
             dq, dP
         end
 
-        function FlashMaxSim.varlen_apply_pullback!(::$M, ::ROCBackend, Δ,
-                                                    Q::FlashMaxSim.PackedSeq,
-                                                    D::FlashMaxSim.PackedSeq, args, inv_n)
-            T = eltype(Q.tokens)
-            dQ = similar(Q.tokens)
-            dD = similar(D.tokens)
+        function FlashMaxSim.varlen_apply_pullback!(::$M, ::ROCBackend, Delta::ROCVector{T},
+                                                    Q::PackedSeq{<:ROCMatrix{T}},
+                                                    D::PackedSeq{<:ROCMatrix{T}},
+                                                    args::ROCMatrix{Int32},
+                                                    inv_n) where {T<:AnyFeature}
+            Qtokens, Dtokens, cu_q, cu_d = Q.tokens, D.tokens, Q.cu, D.cu
+            dQ = similar(Qtokens)
+            dD = similar(Dtokens)
             check(ccall((:fms_varlen_pullback, libfms), Int32,
                         (Int32, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid},
                          Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Int64, Int64, Int64,
                          Int64, Int64, Ptr{Cvoid}),
-                        dtype_code(T), dptr(dQ), dptr(dD), dptr(Q.tokens), dptr(D.tokens),
-                        dptr(Q.cu), dptr(D.cu), dptr(args), dptr(Δ), dptr(inv_n),
-                        size(Q.tokens, 1), size(args, 1), size(args, 2), size(Q.tokens, 2),
-                        size(D.tokens, 2), stream_ptr()),
+                        dtype_code(T), dptr(dQ), dptr(dD), dptr(Qtokens), dptr(Dtokens),
+                        dptr(cu_q), dptr(cu_d), dptr(args), dptr(Delta), dptr(inv_n),
+                        size(Qtokens, 1), size(args, 1), size(args, 2), size(Qtokens, 2),
+                        size(Dtokens, 2), stream_ptr()),
                   "varlen pullback")
             dQ, dD
         end
@@ -312,8 +514,9 @@ for M in (FlashMaxSim.AtomicUnified, FlashMaxSim.InvGrid)
 end
 
 # ---- extensions without a reference method -------------------------------------
-# Called as FlashMaxSimHIPExt.packed_multi_scan(Q, P) and
-# FlashMaxSimHIPExt.topk(S, k) (Base.get_extension(FlashMaxSim, :FlashMaxSimHIPExt)).
+# Called as FlashMaxSimHIPExt.packed_multi_scan(Q, P), FlashMaxSimHIPExt.topk(S, k) and
+# FlashMaxSimHIPExt.load_int8_index(path)
+# (Base.get_extension(FlashMaxSim, :FlashMaxSimHIPExt)).
 
 """
     packed_multi_scan(Q::ROCArray{T,3}, P::PackedSeq; qmask = nothing) -> (S, args)
@@ -323,21 +526,23 @@ Float32 and the 1-based document-local tape `args (Tq, B, nq)`.  Column i equals
 `maxsim(Q[:, :, i], P, qmask[:, i]; normalize)` (src/packed.jl:178-210) within the
 score tolerance; `normalize` is fused into the scan's score write.
 """
-function packed_multi_scan(Q::ROCArray{T,3}, P::FlashMaxSim.PackedSeq;
-                           qmask = nothing, normalize::Bool = false) where {T<:FloatFeature}
+function packed_multi_scan(Q::ROCArray{T,3}, P::PackedSeq;
+                           qmask = nothing, normalize::Bool = false) where {T<:AnyFeature}
     dim, Tq, nq = size(Q)
-    B = length(P.cu) - 1
-    S = AMDGPU.zeros(Float32, B, nq)
+    tokens, cu, max_len = P.tokens, P.cu, P.max_len
+    eltype(tokens) === T || throw(ArgumentError("PackedSeq tokens must have the query eltype"))
+    B = length(cu) - 1
+    scores = AMDGPU.zeros(Float32, B, nq)
     args = AMDGPU.zeros(Int32, Tq, B, nq)
-    (nq == 0 || B == 0) && return S, args
+    (nq == 0 || B == 0) && return scores, args
     check(ccall((:fms_launch_packed_multi_scan, libfms), Int32,
                 (Int32, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid},
                  Int64, Int64, Int64, Int64, Int64, Int64, Int32, Ptr{Cvoid}),
-                dtype_code(T), dptr(args), dptr(S), dptr(Q), dptr(P.tokens), dptr(P.cu),
-                qmask === nothing ? C_NULL : dptr(qmask), dim, Tq, nq, B,
-                size(P.tokens, 2), P.max_len, Int32(normalize), stream_ptr()),
+                dtype_code(T), dptr(args), dptr(scores), dptr(Q), dptr(tokens), dptr(cu),
+                dptr(qmask), dim, Tq, nq, B, size(tokens, 2), max_len, Int32(normalize),
+                stream_ptr()),
           "multi-query packed scan")
-    S, args
+    scores, args
 end
 
 """
@@ -347,15 +552,76 @@ The k best scores of every column of `S` (one column per query): `vals (k, ncols
 descending, `idx (k, ncols)` 1-based row indices -- `partialsortperm(S[:, i], 1:k;
 rev = true)` with a stable sort, for every column in one launch.  1 <= k <= 1024.
 """
-function topk(S::ROCMatrix{Float32}, k::Integer)
-    n, ncol = size(S)
-    vals = AMDGPU.zeros(Float32, k, ncol)
-    idx = AMDGPU.zeros(Int32, k, ncol)
+function topk(scores::ROCMatrix{Float32}, k::Integer)
+    ncols, nrows = size(scores)   # C rows: one score row per query column
+    vals = AMDGPU.zeros(Float32, k, nrows)
+    idx = AMDGPU.zeros(Int32, k, nrows)
     check(ccall((:fms_topk, libfms), Int32,
                 (Ptr{Cvoid}, Int64, Int64, Int64, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}),
-                dptr(S), ncol, n, k, dptr(vals), dptr(idx), stream_ptr()),
+                dptr(scores), nrows, ncols, k, dptr(vals), dptr(idx), stream_ptr()),
           "topk")
     vals, idx
+end
+
+# ---- Int8Index at rest -------------------------------------------------------------
+# The file is safetensors: a little-endian UInt64 header length n, n bytes of JSON,
+# then the tensor bytes.  The JSON names two tensors, "codes" (dtype "I8", shape
+# [N, Td, dim], i.e. Julia's column-major (dim, Td, N)) and "scales" ("F32" or
+# "F16", shape [N, Td] = Julia (Td, N)), each with "data_offsets" [begin, end)
+# relative to the end of the header, and "__metadata__" with
+# "format": "flashmaxsim-int8-index-v1".  The index is read with `read!` into
+# host arrays of the reversed shape, byte for byte, with no JSON package: the
+# patterns below pick the fields out of the header.
+
+const ST_FORMAT = r"\"format\"\s*:\s*\"flashmaxsim-int8-index-v1\""
+const ST_ENTRY_CODES = r"\"codes\"\s*:\s*\{([^}]*)\}"
+const ST_ENTRY_SCALES = r"\"scales\"\s*:\s*\{([^}]*)\}"
+const ST_DTYPE = r"\"dtype\"\s*:\s*\"([A-Z0-9]+)\""
+const ST_SHAPE = r"\"shape\"\s*:\s*\[([0-9,\s]*)\]"
+const ST_OFFSETS = r"\"data_offsets\"\s*:\s*\[\s*([0-9]+)\s*,\s*([0-9]+)\s*\]"
+
+const ST_TYPES = Dict("I8" => Int8, "F32" => Float32, "F16" => Float16)
+
+function st_tensor(io::IO, header::AbstractString, data0::Integer, entry::Regex)
+    m = match(entry, header)
+    m === nothing && throw(ArgumentError("Int8Index file: tensor missing"))
+    body = m.captures[1]
+    md, ms, mo = match(ST_DTYPE, body), match(ST_SHAPE, body), match(ST_OFFSETS, body)
+    (md === nothing || ms === nothing || mo === nothing) &&
+        throw(ArgumentError("Int8Index file: malformed tensor entry"))
+    T = get(ST_TYPES, md.captures[1]) do
+        throw(ArgumentError("Int8Index file: unsupported dtype $(md.captures[1])"))
+    end
+    shape = [parse(Int, s) for s in split(ms.captures[1], ',') if !isempty(strip(s))]
+    b, e = parse(Int, mo.captures[1]), parse(Int, mo.captures[2])
+    x = Array{T}(undef, reverse(shape)...)
+    e - b == sizeof(x) || throw(ArgumentError("Int8Index file: tensor byte count"))
+    seek(io, data0 + b)
+    read!(io, x)
+    ENDIAN_BOM == 0x04030201 || (x .= ltoh.(x))
+    x
+end
+
+"""
+    load_int8_index(path; device = true) -> Int8Index
+
+Read an Int8Index written by the Python host's `save_int8_index` (the
+safetensors layout described above): `codes (dim, Td, N)` Int8 and
+`scales (Td, N)` Float32 or Float16, moved to the GPU when `device`.
+"""
+function load_int8_index(path::AbstractString; device::Bool = true)
+    codes, scales = open(path, "r") do io
+        n = Int(ltoh(read(io, UInt64)))
+        header = String(read(io, n))
+        occursin(ST_FORMAT, header) ||
+            throw(ArgumentError("$path: not a flashmaxsim-int8-index-v1 file"))
+        data0 = 8 + n
+        st_tensor(io, header, data0, ST_ENTRY_CODES), st_tensor(io, header, data0, ST_ENTRY_SCALES)
+    end
+    eltype(codes) === Int8 || throw(ArgumentError("$path: codes must be Int8"))
+    eltype(scales) <: ScaleType || throw(ArgumentError("$path: scales must be Float32 or Float16"))
+    size(codes)[2:end] == size(scales) || throw(DimensionMismatch("Int8Index token count"))
+    device ? Int8Index(ROCArray(codes), ROCArray(scales)) : Int8Index(codes, scales)
 end
 
 end # module

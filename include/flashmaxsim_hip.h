@@ -189,10 +189,13 @@ fms_status fms_topk(const float* scores, int64_t nrows, int64_t ncols, int64_t k
  * nullable; scores (B,nq) receives S[b, i] = Sigma_t of query i against
  * document b (required); args (Tq,B,nq) nullable, tapes as in
  * fms_launch_packed_scan.  max_len >= every document's length (PackedSeq's
- * max_len; longer documents are clamped to it).  f16/bf16 with dim = 128,
- * Tq <= 32 and max_len <= 2048 run on MFMA; other shapes make one packed
- * scan per query.  Row i of the result equals fms_launch_packed_scan of
- * query i within the score tolerance (tapes equal except at near-ties).
+ * max_len).  f16/bf16 with dim = 128, Tq <= 32 and max_len <= 2048 run on
+ * MFMA; other shapes make one packed scan per query.  Row i of the result
+ * equals fms_launch_packed_scan of query i within the score tolerance (tapes
+ * equal except at near-ties).  On the MFMA path a document longer than
+ * max_len breaks that contract and is not scored: its scores are NaN and its
+ * tapes 0 (never a score of a truncated document; the per-query path does
+ * not read max_len).
  */
 fms_status fms_launch_packed_multi_scan(int32_t dtype, int32_t* args, float* scores,
                                         const void* Q, const void* tokens, const int32_t* cu,
@@ -214,24 +217,30 @@ fms_status fms_launch_varlen_scan(int32_t dtype, int32_t* args, float* partial,
                                   float* scores, int32_t normalize, void* stream);
 
 /*
- * Per-token symmetric INT8 quantisation of fp32 features, bit-exact with
- * quantize_int8_symmetric (src/quant.jl:42-49): scale = max(max(absmax,
- * 1f-8)/127f0, floatmin(Float32)) with IEEE division; code =
- * round-to-nearest-even(clamp(x/scale, -127, 127)).  X (dim,ntok) fp32 ->
- * codes (dim,ntok) int8, scales (ntok,) fp32.
+ * Per-token symmetric INT8 quantisation, bit-exact with
+ * quantize_int8_symmetric (src/quant.jl:42-49), computed in the feature type
+ * T = dtype (FMS_F32 or FMS_F16): scale = max(max(absmax, T(1f-8)) / T(127),
+ * floatmin(T)) with one correctly rounded division in T; code =
+ * round-to-nearest-even(clamp(x / scale, -127, 127)) where x / scale is
+ * itself rounded to T first.  X (dim,ntok) of T -> codes (dim,ntok) int8,
+ * scales (ntok,) of T.  Replaces the reference's broadcast for device arrays.
  */
-fms_status fms_int8_quantize(const float* X, int8_t* codes, float* scales,
+fms_status fms_int8_quantize(int32_t dtype, const void* X, int8_t* codes, void* scales,
                              int64_t dim, int64_t ntok, void* stream);
 
 /*
  * INT8 pair scan.  Replaces launch_int8_pair_scan!(backend, args, partial,
  * qc, qs, dc, ds, qmask, dmask) (src/quant.jl:139-154; CUDA override
  * ext/FlashMaxSimCUDAExt.jl:142-153).  Dots accumulate exactly in int32;
- * s = (qs[t]*ds[u]) * Float32(acc) evaluated left to right (src/quant.jl:113).
+ * s = (qs[t]*ds[u]) * Float32(acc) evaluated left to right in fp32
+ * (src/quant.jl:113, src/kernels_int8.jl:17-25).  The scales keep the eltype
+ * of the features they were quantised from: qs_dtype / ds_dtype is FMS_F32
+ * or FMS_F16 (widened exactly to fp32; dot_accum(Float16) = Float32), so
+ * partial is fp32 either way.
  */
 fms_status fms_launch_int8_pair_scan(int32_t* args, float* partial,
-                                     const int8_t* qc, const float* qs,
-                                     const int8_t* dc, const float* ds,
+                                     const int8_t* qc, const void* qs, int32_t qs_dtype,
+                                     const int8_t* dc, const void* ds, int32_t ds_dtype,
                                      const uint8_t* qmask, const uint8_t* dmask,
                                      int64_t dim, int64_t Tq, int64_t Td,
                                      float* score, int32_t normalize, void* stream);
@@ -239,11 +248,12 @@ fms_status fms_launch_int8_pair_scan(int32_t* args, float* partial,
 /*
  * INT8 paired scan.  Replaces launch_int8_paired_scan!(backend, args,
  * partial, Qc, Qs, Dc, Ds, qmask, dmask) (src/quant.jl:199-217; CUDA
- * override ext/FlashMaxSimCUDAExt.jl:155-167).
+ * override ext/FlashMaxSimCUDAExt.jl:155-167).  Scale types as for the pair
+ * scan.
  */
 fms_status fms_launch_int8_paired_scan(int32_t* args, float* partial,
-                                       const int8_t* Qc, const float* Qs,
-                                       const int8_t* Dc, const float* Ds,
+                                       const int8_t* Qc, const void* Qs, int32_t qs_dtype,
+                                       const int8_t* Dc, const void* Ds, int32_t ds_dtype,
                                        const uint8_t* qmask, const uint8_t* dmask,
                                        int64_t dim, int64_t Tq, int64_t Td, int64_t B,
                                        float* scores, int32_t normalize, void* stream);
@@ -255,8 +265,8 @@ fms_status fms_launch_int8_paired_scan(int32_t* args, float* partial,
  * (src/forward_layouts.jl:292-310): idx (C,B), invalid -> tape 0 / `neg`.
  */
 fms_status fms_launch_int8_candidates_scan(int32_t* args, float* partial,
-                                           const int8_t* Qc, const float* Qs,
-                                           const int8_t* Gc, const float* Gs,
+                                           const int8_t* Qc, const void* Qs, int32_t qs_dtype,
+                                           const int8_t* Gc, const void* Gs, int32_t ds_dtype,
                                            const void* idx, int32_t idx_bytes,
                                            const uint8_t* qmask, const uint8_t* dmask,
                                            int64_t dim, int64_t Tq, int64_t B,

@@ -21,7 +21,8 @@ Function-level parity pins (each is exercised in ``tests/test_oracle.py``):
   invalid idx => neg), an fp64 dense brute force (``dense_pair_f64``), an
   independent numpy materialising implementation, and layout invariants.
 * quantize_int8 -- closed-form cases (ties-to-even, clamp, eps and floatmin
-  floors) and numpy's round-half-even on random data.
+  floors) and numpy's round-half-even on random data; for Float16 features,
+  numpy's own float16 arithmetic (an independent binary16 implementation).
 * int8 dots / int8 scans -- exact integer arithmetic vs numpy int32 matmul,
   fixed dequant order ``(qs*ds)*float(acc)``.
 * backward (``*_backward``) -- an independent numpy scatter (``np.add.at``)
@@ -85,6 +86,10 @@ def _declare(L):
     L.fmso_varlen_forward.argtypes = [_int, _p, _p, _p, _p, _i64, _i64, _i64, _p, _p, _p, _int]
     L.fmso_quantize_int8.restype = None
     L.fmso_quantize_int8.argtypes = [_p, _i64, _i64, _p, _p]
+    L.fmso_quantize_int8_f16.restype = None
+    L.fmso_quantize_int8_f16.argtypes = [_p, _i64, _i64, _p, _p]
+    L.fmso_f32_to_f16.restype = None
+    L.fmso_f32_to_f16.argtypes = [_p, _i64, _p]
     L.fmso_int8_dots.restype = None
     L.fmso_int8_dots.argtypes = [_p, _p, _i64, _i64, _i64, _p]
     L.fmso_int8_paired_forward.restype = None
@@ -279,14 +284,27 @@ def varlen_forward(Qt, Dt, cu_q, cu_d, max_q=None, bf16=False, nthreads=0):
 
 
 def quantize_int8(x):
-    """quantize_int8_symmetric for Float32 (src/quant.jl:42-49). x (..., dim) fp32."""
-    x = _c(x, np.float32)
+    """quantize_int8_symmetric (src/quant.jl:42-49) for Float32 or Float16 features
+    x (..., dim); the scales keep x's dtype (computed in that type)."""
+    half = np.asarray(x).dtype == np.float16
+    x = _c(x, np.float16 if half else np.float32)
     dim = x.shape[-1]
     ntok = x.size // max(dim, 1) if dim > 0 else int(np.prod(x.shape[:-1]))
     codes = np.zeros(x.shape, np.int8)
-    scales = np.zeros(x.shape[:-1], np.float32)
-    lib().fmso_quantize_int8(_ptr(x), dim, ntok, _ptr(codes), _ptr(scales))
+    scales = np.zeros(x.shape[:-1], np.float16 if half else np.float32)
+    if half:
+        lib().fmso_quantize_int8_f16(_ptr(x), dim, ntok, _ptr(codes), _ptr(scales))
+    else:
+        lib().fmso_quantize_int8(_ptr(x), dim, ntok, _ptr(codes), _ptr(scales))
     return codes, scales
+
+
+def f32_to_f16(x):
+    """The oracle's binary32 -> binary16 rounding (RNE), as float16 values."""
+    x = _c(x, np.float32)
+    out = np.zeros(x.shape, np.uint16)
+    lib().fmso_f32_to_f16(_ptr(x), x.size, _ptr(out))
+    return out.view(np.float16)
 
 
 def int8_dots(qc, dc):

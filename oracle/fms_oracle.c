@@ -457,6 +457,75 @@ void fmso_quantize_int8(const float* x, int64_t dim, int64_t ntok, int8_t* codes
     }
 }
 
+/*
+ * binary32 -> binary16, round to nearest, ties to even (IEEE 754), with
+ * overflow to Inf and gradual underflow; NaN stays NaN.
+ */
+static uint16_t float_to_half_rne(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    uint32_t ax = x & 0x7fffffffu;
+    if (ax > 0x7f800000u) return (uint16_t)(sign | 0x7e00u);          /* NaN */
+    if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);         /* >= 65520: Inf */
+    int e = (int)(ax >> 23) - 127;
+    uint32_t mant = (ax & 0x7fffffu) | 0x800000u;                     /* 24-bit significand */
+    uint32_t q, rem, half;
+    int s;
+    if (e >= -14) {                   /* normal half: keep 11 significant bits */
+        s = 13;
+        q = ((uint32_t)(e + 15) << 10) + ((mant >> s) & 0x3ffu);
+    } else {                          /* subnormal half: units of 2^-24 */
+        if (e < -25) return (uint16_t)sign;
+        s = -e - 1;                   /* 14 .. 24 */
+        q = mant >> s;
+    }
+    rem = mant & ((1u << s) - 1u);
+    half = 1u << (s - 1);
+    if (rem > half || (rem == half && (q & 1u))) q += 1u;             /* carries into the exponent */
+    return (uint16_t)(sign | q);
+}
+
+/*
+ * quantize_int8_symmetric for Float16 features (src/quant.jl:21-49): the
+ * same steps with every operation in Float16 arithmetic, which Julia
+ * evaluates as the fp32 operation rounded back to Float16:
+ *   am    = max_k |x[k,t]|                              (exact)
+ *   raw   = Float16(max(am, Float16(1f-8)) / 127)       (Float16(1f-8) == 0)
+ *   scale = max(raw, floatmin(Float16))                 (2^-14)
+ *   code  = round(Int8, clamp(Float16(x / scale), -127, 127))
+ * x and scales are binary16 bit patterns.
+ */
+void fmso_quantize_int8_f16(const uint16_t* x, int64_t dim, int64_t ntok, int8_t* codes,
+                            uint16_t* scales) {
+    int64_t t, k;
+    const float eps = half_to_float(float_to_half_rne(1.0e-8f));
+    const float tmin = half_to_float(0x0400u);
+    for (t = 0; t < ntok; ++t) {
+        const uint16_t* xt = x + t * dim;
+        float am = 0.0f;
+        for (k = 0; k < dim; ++k) {
+            float a = fabsf(half_to_float(xt[k]));
+            if (a > am) am = a;
+        }
+        float raw = half_to_float(float_to_half_rne((am > eps ? am : eps) / 127.0f));
+        float sc = raw > tmin ? raw : tmin;
+        scales[t] = float_to_half_rne(sc);
+        for (k = 0; k < dim; ++k) {
+            float v = half_to_float(float_to_half_rne(half_to_float(xt[k]) / sc));
+            if (v > 127.0f) v = 127.0f;
+            else if (v < -127.0f) v = -127.0f;
+            codes[t * dim + k] = (int8_t)nearbyintf(v);
+        }
+    }
+}
+
+/* Test hook: float_to_half_rne over n values (pinned against numpy's conversion). */
+void fmso_f32_to_f16(const float* x, int64_t n, uint16_t* out) {
+    int64_t i;
+    for (i = 0; i < n; ++i) out[i] = float_to_half_rne(x[i]);
+}
+
 /* Raw int32 dot products out[u + Td*t] = sum_k qc[k,t]*dc[k,u] (quant.jl:109-112). */
 void fmso_int8_dots(const int8_t* qc, const int8_t* dc, int64_t dim, int64_t Tq, int64_t Td,
                     int32_t* out) {

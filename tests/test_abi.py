@@ -71,10 +71,22 @@ EINVAL, EUNSUP, OK = _lib.FMS_EINVAL, _lib.FMS_EUNSUPPORTED, _lib.FMS_OK
     (lambda L: L.fms_inbatch_device_scan(1, None, None, 1, 1, None, None, 8, 4, 2, 5, 3, 0, None), EINVAL),
     (lambda L: L.fms_launch_packed_scan(1, None, None, 1, 1, None, None, 8, 4, 3, 10, None, 0, None), EINVAL),
     (lambda L: L.fms_launch_varlen_scan(2, None, None, 1, 1, None, 1, 8, 4, 3, 10, 10, None, 0, None), EINVAL),
-    (lambda L: L.fms_int8_quantize(None, None, None, 8, 4, None), EINVAL),
-    (lambda L: L.fms_int8_quantize(None, None, None, 8, 0, None), OK),
-    (lambda L: L.fms_launch_int8_paired_scan(None, None, 1, None, 1, 1, None, None, 8, 4, 5, 2, None, 0, None), EINVAL),
-    (lambda L: L.fms_launch_int8_candidates_scan(None, None, 1, 1, 1, 1, 1, 2, None, None, 8, 4, 2, 5, 7, 3, None, 0.0, 0, None), EINVAL),
+    (lambda L: L.fms_int8_quantize(0, None, None, None, 8, 4, None), EINVAL),
+    (lambda L: L.fms_int8_quantize(1, None, None, None, 8, 4, None), EINVAL),
+    (lambda L: L.fms_int8_quantize(0, None, None, None, 8, 0, None), OK),
+    # INT8 quantisation and scales take Float32 or Float16 only
+    (lambda L: L.fms_int8_quantize(2, 1, 1, 1, 8, 4, None), EUNSUP),
+    (lambda L: L.fms_launch_int8_paired_scan(None, None, 1, None, 0, 1, 1, 0, None, None, 8, 4, 5, 2, None, 0, None), EINVAL),
+    (lambda L: L.fms_launch_int8_paired_scan(None, None, 1, 1, 2, 1, 1, 0, None, None, 8, 4, 5, 2, None, 0, None), EUNSUP),
+    (lambda L: L.fms_launch_int8_paired_scan(None, None, 1, 1, 0, 1, 1, 9, None, None, 8, 4, 5, 2, None, 0, None), EUNSUP),
+    (lambda L: L.fms_launch_int8_pair_scan(None, None, 1, 1, 1, 1, 1, 2, None, None, 8, 4, 5, None, 0, None), EUNSUP),
+    (lambda L: L.fms_launch_int8_candidates_scan(None, None, 1, 1, 0, 1, 1, 0, 1, 2, None, None, 8, 4, 2, 5, 7, 3, None, 0.0, 0, None), EINVAL),
+    (lambda L: L.fms_launch_int8_candidates_scan(None, None, 1, 1, 0, 1, 1, 2, 1, 8, None, None, 8, 4, 2, 5, 7, 3, None, 0.0, 0, None), EUNSUP),
+    # a scan whose grid would exceed 2^32 work-items (returns before any HIP call)
+    (lambda L: L.fms_launch_paired_scan(1, None, None, 1, 1, None, None, 8, 1, 1, 1 << 31, None, 0, None), EUNSUP),
+    (lambda L: L.fms_launch_candidates_scan(1, None, None, 1, 1, 1, 8, None, None, 8, 1, 1 << 16, 1, 7, 1 << 16, None, 0.0, 0, None), EUNSUP),
+    (lambda L: L.fms_launch_varlen_scan(1, None, None, 1, 1, 1, 1, 8, 1, 1 << 31, 10, 10, None, 0, None), EUNSUP),
+    (lambda L: L.fms_launch_int8_paired_scan(None, None, 1, 1, 0, 1, 1, 0, None, None, 8, 1, 1, 1 << 31, None, 0, None), EUNSUP),
     (lambda L: L.fms_int8_dots(None, 1, 1, 8, 4, 5, None), EINVAL),
     (lambda L: L.fms_length_normalize(None, None, 4, 3, 2, None, 0, 0, 0.0, None), EINVAL),
     (lambda L: L.fms_length_normalize(None, None, 4, 0, 2, None, 0, 0, 0.0, None), OK),

@@ -265,6 +265,65 @@ def test_quantize_vs_numpy():
     assert np.abs(c).max() == 127
 
 
+def test_f32_to_f16_matches_numpy():
+    """The oracle's binary32 -> binary16 RNE against numpy's conversion: random bit
+    patterns over the whole fp32 range, exact ties between neighbouring halves
+    (normal and subnormal), the overflow threshold, Inf and NaN."""
+    rng = np.random.default_rng(5)
+    bits = rng.integers(0, 2 ** 32, size=200_000, dtype=np.uint64).astype(np.uint32)
+    x = bits.view(np.float32)
+    h = np.arange(0, 0x7c00, dtype=np.uint16).view(np.float16).astype(np.float32)
+    ties = ((h[:-1].astype(np.float64) + h[1:].astype(np.float64)) / 2).astype(np.float32)
+    special = np.array([65504.0, 65519.99, 65520.0, 1e6, np.inf, -np.inf, 2.0 ** -25,
+                        2.0 ** -25 * 1.0000001, 2.0 ** -26, -0.0, 0.0], np.float32)
+    for arr in (x, ties, -ties, special):
+        got = oracle.f32_to_f16(arr)
+        with np.errstate(over="ignore"):
+            want = arr.astype(np.float16)
+        nan = np.isnan(want)
+        assert np.array_equal(np.isnan(got), nan)
+        assert np.array_equal(got[~nan].view(np.uint16), want[~nan].view(np.uint16))
+
+
+def np_quantize_f16(x):
+    """quantize_int8_symmetric in numpy float16 arithmetic (numpy rounds every float16
+    operation's fp32 result to float16, as Julia does)."""
+    x = x.astype(np.float16)
+    am = np.abs(x).max(-1)
+    raw = np.maximum(am, np.float16(1e-8)) / np.float16(127)
+    sc = np.maximum(raw, np.finfo(np.float16).tiny)
+    v = np.clip(x / sc[..., None], np.float16(-127), np.float16(127))
+    return np.rint(v).astype(np.int8), sc
+
+
+def test_quantize_f16_closed_forms():
+    x = np.array([[127.0, 0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 3.5],
+                  [0.0] * 8,
+                  [1e-7] * 8], np.float16)
+    c, s = oracle.quantize_int8(x)
+    assert s.dtype == np.float16
+    assert s[0] == np.float16(1.0)
+    assert c[0].tolist() == [127, 0, 2, 2, 0, -2, -2, 4]  # round half to even
+    # Float16(1f-8) == 0, so an all-zero token's scale is floatmin(Float16) = 2^-14
+    assert s[1] == np.float16(2.0 ** -14) and (c[1] == 0).all()
+    # a tiny token: absmax/127 underflows below floatmin -> floored at 2^-14
+    assert s[2] == np.float16(2.0 ** -14)
+
+
+def test_quantize_f16_vs_numpy_and_rounds_the_quotient():
+    """Random Float16 tokens: codes and scales bit-exact with numpy float16 arithmetic.
+    At least one code differs from what an fp32 quotient would give, so the
+    rounding of x / scale to Float16 before round(Int8, .) is pinned too."""
+    rng = np.random.default_rng(11)
+    x = (rng.standard_normal((2000, 64)) * rng.uniform(1e-3, 1e3, (2000, 1))).astype(np.float16)
+    c, s = oracle.quantize_int8(x)
+    c2, s2 = np_quantize_f16(x)
+    assert np.array_equal(s.view(np.uint16), s2.view(np.uint16))
+    assert np.array_equal(c, c2)
+    v32 = np.clip(x.astype(np.float32) / s.astype(np.float32)[:, None], -127, 127)
+    assert (np.rint(v32).astype(np.int8) != c).any()
+
+
 def test_int8_dots_and_scan_exact():
     rng = np.random.default_rng(42)
     dim, Tq, Td, B = 40, 7, 11, 3

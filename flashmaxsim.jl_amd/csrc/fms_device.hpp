@@ -258,64 +258,51 @@ __device__ __forceinline__ float dpp_add(float v) {
                                            0, __builtin_bit_cast(int, v), kCtrl, 0xf, 0xf, false));
 }
 
-// Merge the (max, token) of lanes l and l^32, which hold disjoint document
-// rows of the same query token.  Equal maxima keep the lower token, matching
-// a sequential ascending scan.  h = lane / 32.
-__device__ __forceinline__ void merge_halves(float& mx, int& tok, int h) {
-  const float omx = __builtin_bit_cast(float, lane_xor32(__builtin_bit_cast(uint32_t, mx), h));
-  const int otok = (int)lane_xor32((uint32_t)tok, h);
-  // Bitwise, not short-circuit: no exec-mask branches.
-  const bool take = (otok != 0) & ((tok == 0) | (omx > mx) | ((omx == mx) & (otok < tok)));
-  mx = take ? omx : mx;
-  tok = take ? otok : tok;
-}
-
-// The reference's running max starts empty, `arg == 0 || s > mx`
-// (kernels_forward.jl:49-52, forward_pair.jl:82-85): the first valid
-// document token u0 is always taken, whatever its score.  The scans start
-// from -Inf and take only s > mx instead, which agrees for every finite
-// score.  They differ in two cases only: score(u0) is NaN (the reference
-// then keeps (NaN, u0) for good, since nothing compares greater than NaN),
-// or no valid score exceeds -Inf (the reference keeps (score(u0), u0), the
-// scan would keep nothing).  FirstTok holds score(u0) from the chunk that
-// contains u0, and first_token_fix applies the reference's outcome at the
-// close of the (pair, query tile).
-struct FirstTok {
-  float s0;  // score of the first valid row (meaningful on lanes of half h0)
-  int h0;    // wave half whose accumulators hold that row
-  int u0;    // its 1-based document token; 0 = no valid row seen yet (uniform)
-};
-
 // NaN test on the bit pattern (no floating-point compare for the compiler
 // to rewrite).
 __device__ __forceinline__ bool is_nan_bits(float x) {
   return (__builtin_bit_cast(uint32_t, x) & 0x7fffffffu) > 0x7f800000u;
 }
 
-// Record the first valid row of chunk ch (m32: its row validity, uniform)
-// unless an earlier chunk held one.  Uniform control flow.
-__device__ __forceinline__ void capture_first(FirstTok& f, const float (&s)[16], uint32_t m32,
-                                              int ch) {
-  if (f.u0 == 0 && m32 != 0u) {
-    const int row = __builtin_ctz(m32);
-    const int reg = ((row >> 3) << 2) | (row & 3);  // acc_row(reg, (row >> 2) & 1) == row
-    float v = s[0];
-#pragma unroll
-    for (int r = 1; r < 16; ++r) v = (reg == r) ? s[r] : v;
-    f.s0 = v;
-    f.h0 = (row >> 2) & 1;
-    f.u0 = ch * kTile + row + 1;
-  }
+// Merge the (max, token) of lanes l and l^32, which hold disjoint document
+// rows of the same query token.  Equal maxima keep the lower token, matching
+// a sequential ascending scan.  h = lane / 32.
+__device__ __forceinline__ void merge_halves(float& mx, int& tok, int h) {
+  const float omx = __builtin_bit_cast(float, lane_xor32(__builtin_bit_cast(uint32_t, mx), h));
+  const int otok = (int)lane_xor32((uint32_t)tok, h);
+  // Bitwise, not short-circuit: no exec-mask branches.  A NaN maximum can
+  // only be the first valid token's (take_first_row) and it stands.
+  const bool nan_here = is_nan_bits(mx), nan_there = is_nan_bits(omx);
+  const bool take = (otok != 0) & !nan_here &
+                    ((tok == 0) | nan_there | (omx > mx) | ((omx == mx) & (otok < tok)));
+  mx = take ? omx : mx;
+  tok = take ? otok : tok;
 }
 
-// Apply the first-token rule to a merged (mx, tok) (after merge_halves).
-__device__ __forceinline__ void first_token_fix(const FirstTok& f, int h, float& mx, int& tok) {
-  const float other =
-      __builtin_bit_cast(float, lane_xor32(__builtin_bit_cast(uint32_t, f.s0), h));
-  const float s0 = (h == f.h0) ? f.s0 : other;
-  const bool fix = (f.u0 != 0) & ((tok == 0) | is_nan_bits(s0));
-  mx = fix ? s0 : mx;
-  tok = fix ? f.u0 : tok;
+// The reference's running max starts empty, `arg == 0 || s > mx`
+// (kernels_forward.jl:49-52, forward_pair.jl:82-85): the first valid
+// document token u0 is taken whatever its score, and only a strictly greater
+// score replaces it.  So a NaN score at u0 sticks (nothing compares greater
+// than NaN), all-(-Inf) scores keep u0, and NaN scores after u0 are skipped.
+// take_first_row starts the running max of the lanes holding u0 on u0's
+// score, in the first chunk with a valid row -- recognised without extra
+// state: no lane has taken a row yet.  The regular fold then continues with
+// strictly-greater takes (u0 itself is not greater than itself), and
+// merge_halves lets a NaN win, which only u0 can hold.  For finite scores
+// this gives exactly the plain max with first-index ties.  Uniform control.
+__device__ __forceinline__ void take_first_row(const float (&s)[16], uint32_t m32, int h, int ch,
+                                               float& mx, int& slot) {
+  if (m32 != 0u && __ballot(slot >= 0) == 0ull) {
+    const int row = __builtin_ctz(m32);
+    const int reg = ((row >> 3) << 2) | (row & 3);  // acc_row(reg, (row >> 2) & 1) == row
+    f32x16 sv;  // a uniform index into a register vector: one v_movrels
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sv[r] = s[r];
+    const float v = sv[reg];
+    const bool mine = h == ((row >> 2) & 1);
+    mx = mine ? v : mx;
+    slot = mine ? ch * 16 + reg : slot;
+  }
 }
 
 // Sum over lanes 0-31, returned in every lane (wave-uniform).  After

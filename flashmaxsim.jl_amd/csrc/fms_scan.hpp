@@ -174,11 +174,9 @@ __device__ __forceinline__ void update_chunk(const float (&s)[16], uint32_t m32,
 // this tile's contribution to the pair score (same value in every lane).
 template <class L>
 __device__ __forceinline__ float finish_tile(const ScanArgs<L>& A, int64_t out, int qt, int r32,
-                                             int h, bool tvalid, float mx, int slot,
-                                             const FirstTok& first) {
+                                             int h, bool tvalid, float mx, int slot) {
   int tok = slot_to_token(slot, h);
   merge_halves(mx, tok, h);
-  first_token_fix(first, h, mx, tok);
   const float part = (tvalid && tok != 0) ? mx : 0.0f;
   const int arg = tvalid ? tok : 0;
   const int t = qt * kTile + r32;
@@ -276,7 +274,6 @@ __global__ void __launch_bounds__(64 * kWaves) scan_fast(const ScanArgs<L> A) {
   int q_qt = -1;
   float mx = -INFINITY, score = 0.0f;
   int slot = -1;
-  FirstTok ftok = {0.0f, 0, 0};
 
   load_chunk<Op, NKB>(bufA, v, 0, nkb, rowbytes, lane_off, r32);
 
@@ -326,8 +323,8 @@ __global__ void __launch_bounds__(64 * kWaves) scan_fast(const ScanArgs<L> A) {
     for (int kb = 0; kb < NKB; ++kb) acc = Op::mma(cur.a[kb], q.f[kb], acc);
     float s[16];
     acc_to_scores<Op>(acc, q.qscale, cur.ds, h, s);
+    take_first_row(s, m32, h, ch, mx, slot);
     update_chunk(s, m32, h, ch, mx, slot);
-    capture_first(ftok, s, m32, ch);
 
     if (ch == nch - 1) {
       // The empty asm pins the query-mask test here: hoisted next to its
@@ -335,10 +332,9 @@ __global__ void __launch_bounds__(64 * kWaves) scan_fast(const ScanArgs<L> A) {
       uint32_t qmb = q.mbyte;
       asm volatile("" : "+v"(qmb));
       const bool tvalid = q.t < v.tq && mask_ok(v.qm, qmb);
-      score += finish_tile(A, v.out, qt, r32, h, tvalid, mx, slot, ftok);
+      score += finish_tile(A, v.out, qt, r32, h, tvalid, mx, slot);
       mx = -INFINITY;
       slot = -1;
-      ftok.u0 = 0;
       if (qt == A.nqt - 1) {
         write_score(A, v, score, lane);
         score = 0.0f;
@@ -402,8 +398,7 @@ __global__ void __launch_bounds__(64 * kWaves) scan_generic(const ScanArgs<L> A)
       if constexpr (Op::kInt) qscale = load_qscale(v, t);
       float mx = -INFINITY;
       int slot = -1;
-      FirstTok ftok = {0.0f, 0, 0};
-      for (int ch = 0; ch < nch; ++ch) {
+          for (int ch = 0; ch < nch; ++ch) {
         Acc acc = {};
         const int row = ch * kTile + r32;
         // split-d: 8 k-blocks of document and query fragments in flight per
@@ -426,10 +421,10 @@ __global__ void __launch_bounds__(64 * kWaves) scan_generic(const ScanArgs<L> A)
         float s[16];
         acc_to_scores<Op>(acc, qscale, ds, h, s);
         const uint32_t m32 = chunk_rows_valid(v, ch, r32, mbyte);
+        take_first_row(s, m32, h, ch, mx, slot);
         update_chunk(s, m32, h, ch, mx, slot);
-        capture_first(ftok, s, m32, ch);
       }
-      score += finish_tile(A, v.out, qt, r32, h, tvalid, mx, slot, ftok);
+      score += finish_tile(A, v.out, qt, r32, h, tvalid, mx, slot);
     }
     write_score(A, v, score, lane);
   }

@@ -117,7 +117,6 @@ __global__ void __launch_bounds__(64 * kWaves) scan_split(const ScanArgs<L> A) {
   Acc acc0 = {}, acc1 = {};
   float mx = -INFINITY, score = 0.0f;
   int slot = -1;
-  FirstTok ftok = {0.0f, 0, 0};
 
   load_split<Op, KBAT, kLdsQ>(bufA, v, 0, 0, 0, rowbytes, h, r32, qlds, A.nkb);
 
@@ -165,17 +164,16 @@ __global__ void __launch_bounds__(64 * kWaves) scan_split(const ScanArgs<L> A) {
       float s[16];
       acc_to_scores<Op>(acc, cur.qscale, cur.ds, h, s);
       const uint32_t m32 = chunk_rows_valid(v, ch, r32, cur.mbyte);
+      take_first_row(s, m32, h, ch, mx, slot);
       update_chunk(s, m32, h, ch, mx, slot);
-      capture_first(ftok, s, m32, ch);
       if (ch == nch - 1) {
         uint32_t qmb = cur.qmbyte;
         asm volatile("" : "+v"(qmb));
         const bool tvalid = (qt * kTile + r32) < v.tq && mask_ok(v.qm, qmb);
-        score += finish_tile(A, v.out, qt, r32, h, tvalid, mx, slot, ftok);
+        score += finish_tile(A, v.out, qt, r32, h, tvalid, mx, slot);
         mx = -INFINITY;
         slot = -1;
-        ftok.u0 = 0;
-        if (qt == A.nqt - 1) {
+          if (qt == A.nqt - 1) {
           write_score(A, v, score, lane);
           score = 0.0f;
         }

@@ -10,6 +10,7 @@
 #include <string.h>
 
 #include <atomic>
+#include <mutex>
 
 #include "../../include/flashmaxsim_hip.h"
 #include "fms_backward.hpp"
@@ -20,6 +21,9 @@
 #include "fms_scan_decl.hpp"
 
 #define FMS_VERSION_STRING "flashmaxsim-hip 0.1.0 (gfx950)"
+
+// Grouping workspace of fms_launch_candidates_scan_noalloc (see scratch_address).
+static __device__ __align__(256) unsigned char scratch[FMS_NOALLOC_SCRATCH_BYTES];
 
 namespace {
 
@@ -113,21 +117,80 @@ bool group_candidates(int64_t P, int64_t N, int64_t dbytes) {
   return distinct <= 0.7 * (double)P;
 }
 
+// Where a candidate call's document-grouping workspace comes from: the
+// library's stream-ordered memory pool, or the file-scope device array of
+// the no-allocation entry point.
+enum class Workspace { kPool, kScratch };
+
+// ---- scratch of the no-allocation entry point --------------------------------------
+// fms_launch_candidates_scan_noalloc takes its grouping workspace from this
+// array instead of the pool, so the call allocates nothing.  Every GPU the
+// library runs on holds its own copy for the life of the process; host code
+// uses the address hipGetSymbolAddress returns for the current device (the
+// array's name on the host is only a stand-in).  Calls on one GPU share it,
+// so calls that overlap on one GPU race.
+constexpr size_t kNoallocScratchBytes = (size_t)FMS_NOALLOC_SCRATCH_BYTES;
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// The device address of `scratch` on the stream's device, looked up once per
+// device with that device current.
+hipError_t scratch_address(hipStream_t st, void** out) {
+  int dev = 0;
+  hipError_t e = stream_device(st, &dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxScratchDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    int cur = 0;
+    e = hipGetDevice(&cur);
+    if (e != hipSuccess) return e;
+    if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return e;
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    const hipError_t er = cur != dev ? hipSetDevice(cur) : hipSuccess;
+    if (e != hipSuccess) return e;
+    if (er != hipSuccess) return er;
+    if (!p) return hipErrorInvalidSymbol;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return hipSuccess;
+}
+
 // Runs launch(layout) on the candidate layout, in document order when
-// group_candidates says so (workspace from the library pool, released on
-// the same stream), otherwise in output order.  An allocation failure falls
-// back to output order: the results are identical either way.
+// group_candidates says so, otherwise in output order.  The grouping
+// workspace comes from `ws`:
+//   kPool: the library pool, released on the same stream; an allocation
+//     failure falls back to output order (the results are identical);
+//   kScratch: the no-allocation array; a workspace larger than it is
+//     FMS_ESCRATCH (nothing is launched).  The grouping kernels clear every
+//     counter they use, so the array's previous contents do not matter.
 template <class Launch>
-fms_status run_candidates(const LayCand& lay, int64_t npairs, hipStream_t st, Launch&& launch) {
+fms_status run_candidates(const LayCand& lay, int64_t npairs, hipStream_t st, Workspace ws,
+                          Launch&& launch) {
   if (!scan_grid_fits(npairs)) return FMS_EUNSUPPORTED;  // 32-bit work-item count
   if (group_candidates(npairs, lay.N, lay.dbytes)) {
-    void* ws = nullptr;
-    if (workspace_alloc(&ws, group_workspace_bytes(npairs, lay.N), st) == hipSuccess) {
+    const size_t need = group_workspace_bytes(npairs, lay.N);
+    void* buf = nullptr;
+    if (ws == Workspace::kScratch) {
+      if (need > kNoallocScratchBytes) return FMS_ESCRATCH;
+      const hipError_t e = scratch_address(st, &buf);
+      if (e != hipSuccess) return from_hip(e);
       LayCandSorted sl;
       sl.c = lay;
-      hipError_t e = group_pairs_by_document(lay.idx, lay.idx64, npairs, lay.N, ws, &sl.order, st);
+      hipError_t eg = group_pairs_by_document(lay.idx, lay.idx64, npairs, lay.N, buf, &sl.order, st);
+      if (eg == hipSuccess) eg = launch(sl);
+      return from_hip(eg);
+    }
+    if (workspace_alloc(&buf, need, st) == hipSuccess) {
+      LayCandSorted sl;
+      sl.c = lay;
+      hipError_t e = group_pairs_by_document(lay.idx, lay.idx64, npairs, lay.N, buf, &sl.order, st);
       if (e == hipSuccess) e = launch(sl);
-      const hipError_t ef = workspace_free(ws, st);
+      const hipError_t ef = workspace_free(buf, st);
       return from_hip(e != hipSuccess ? e : ef);
     }
     (void)hipGetLastError();  // clear the failed allocation; scan in output order
@@ -202,6 +265,9 @@ const char* fms_status_string(fms_status s) {
     case FMS_EINVAL: return "invalid argument (shape, NULL pointer or alignment)";
     case FMS_EUNSUPPORTED: return "unsupported dtype or size";
     case FMS_EHIP: return "HIP runtime error";
+    case FMS_ESCRATCH:
+      return "the call needs more workspace than the no-allocation entry point's scratch "
+             "(FMS_NOALLOC_SCRATCH_BYTES)";
     default: return "unknown status";
   }
 }
@@ -249,12 +315,17 @@ fms_status fms_launch_pair_scan(int32_t dtype, int32_t* argmax_u, float* partial
                                 score, normalize, stream);
 }
 
-fms_status fms_launch_candidates_scan(int32_t dtype, int32_t* args, float* partial,
-                                      const void* Q, const void* gallery, const void* idx,
-                                      int32_t idx_bytes, const uint8_t* qmask,
-                                      const uint8_t* dmask, int64_t dim, int64_t Tq, int64_t B,
-                                      int64_t Td, int64_t N, int64_t C, float* scores, float neg,
-                                      int32_t normalize, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// fms_launch_candidates_scan and its no-allocation variant: the same checks,
+// kernels and results; only the grouping workspace differs.
+fms_status candidates_scan(Workspace ws, int32_t dtype, int32_t* args, float* partial,
+                           const void* Q, const void* gallery, const void* idx,
+                           int32_t idx_bytes, const uint8_t* qmask, const uint8_t* dmask,
+                           int64_t dim, int64_t Tq, int64_t B, int64_t Td, int64_t N, int64_t C,
+                           float* scores, float neg, int32_t normalize, void* stream) {
   const int esz = elem_bytes(dtype);
   if (esz == 0) return FMS_EUNSUPPORTED;
   if (dim < 0 || Tq < 0 || Td < 0 || B < 0 || N < 0 || C < 0 || (normalize & ~1))
@@ -281,10 +352,35 @@ fms_status fms_launch_candidates_scan(int32_t dtype, int32_t* args, float* parti
   lay.Td = (int)Td;
   const bool vec = vec_ok(esz, dim, {Q, gallery});
   const hipStream_t st = as_stream(stream);
-  return run_candidates(lay, C * B, st, [&](const auto& L) -> hipError_t {
+  return run_candidates(lay, C * B, st, ws, [&](const auto& L) -> hipError_t {
     return launch_float(dtype, L, (int)dim, (int)Tq, C * B, args, partial, scores, neg,
                         normalize != 0, vec, st);
   });
+}
+
+}  // namespace
+
+extern "C" {
+
+fms_status fms_launch_candidates_scan(int32_t dtype, int32_t* args, float* partial,
+                                      const void* Q, const void* gallery, const void* idx,
+                                      int32_t idx_bytes, const uint8_t* qmask,
+                                      const uint8_t* dmask, int64_t dim, int64_t Tq, int64_t B,
+                                      int64_t Td, int64_t N, int64_t C, float* scores, float neg,
+                                      int32_t normalize, void* stream) {
+  return candidates_scan(Workspace::kPool, dtype, args, partial, Q, gallery, idx, idx_bytes,
+                         qmask, dmask, dim, Tq, B, Td, N, C, scores, neg, normalize, stream);
+}
+
+fms_status fms_launch_candidates_scan_noalloc(int32_t dtype, int32_t* args, float* partial,
+                                              const void* Q, const void* gallery,
+                                              const void* idx, int32_t idx_bytes,
+                                              const uint8_t* qmask, const uint8_t* dmask,
+                                              int64_t dim, int64_t Tq, int64_t B, int64_t Td,
+                                              int64_t N, int64_t C, float* scores, float neg,
+                                              int32_t normalize, void* stream) {
+  return candidates_scan(Workspace::kScratch, dtype, args, partial, Q, gallery, idx, idx_bytes,
+                         qmask, dmask, dim, Tq, B, Td, N, C, scores, neg, normalize, stream);
 }
 
 fms_status fms_inbatch_device_scan(int32_t dtype, float* S, int32_t* args, const void* Q,
@@ -508,7 +604,7 @@ fms_status fms_launch_int8_candidates_scan(int32_t* args, float* partial, const 
   lay.ds_esz = ds_esz;
   const bool vec = vec_ok(1, dim, {Qc, Gc});
   const hipStream_t st = as_stream(stream);
-  return run_candidates(lay, C * B, st, [&](const auto& L) -> hipError_t {
+  return run_candidates(lay, C * B, st, Workspace::kPool, [&](const auto& L) -> hipError_t {
     return launch_int8(ds_esz, L, (int)dim, (int)Tq, C * B, args, partial, scores, neg,
                        normalize != 0, vec, st);
   });

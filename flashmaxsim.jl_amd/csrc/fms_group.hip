@@ -204,14 +204,6 @@ constexpr int kMaxDevices = 64;
 std::mutex g_pool_mutex;
 hipMemPool_t g_pool[kMaxDevices] = {};
 
-hipError_t stream_device(hipStream_t stream, int* dev) {
-  if (stream == nullptr) return hipGetDevice(dev);
-  hipDevice_t d;
-  const hipError_t e = hipStreamGetDevice(stream, &d);
-  *dev = (int)d;
-  return e;
-}
-
 hipError_t device_pool(int dev, hipMemPool_t* pool) {
   if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
   std::lock_guard<std::mutex> lock(g_pool_mutex);
@@ -234,6 +226,14 @@ hipError_t device_pool(int dev, hipMemPool_t* pool) {
 }
 
 }  // namespace
+
+hipError_t stream_device(hipStream_t stream, int* dev) {
+  if (stream == nullptr) return hipGetDevice(dev);
+  hipDevice_t d;
+  const hipError_t e = hipStreamGetDevice(stream, &d);
+  *dev = (int)d;
+  return e;
+}
 
 hipError_t workspace_alloc(void** ptr, size_t bytes, hipStream_t stream) {
   int dev = 0;

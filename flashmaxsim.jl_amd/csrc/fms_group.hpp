@@ -42,6 +42,9 @@ hipError_t group_pairs_by_document(const void* idx, int idx64, int64_t npairs, i
 size_t scan_workspace_bytes(int64_t n);
 hipError_t exclusive_scan_u32(uint32_t* counts, int64_t n, uint32_t* sums, hipStream_t stream);
 
+// The device a stream belongs to (the current device for the null stream).
+hipError_t stream_device(hipStream_t stream, int* dev);
+
 // Stream-ordered workspace from a library-owned memory pool of the stream's
 // device (created on first use, kept for the life of the process so repeated
 // calls do not return memory to the driver between synchronisations).

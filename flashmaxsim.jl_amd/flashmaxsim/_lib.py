@@ -19,7 +19,7 @@ _PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 # FLASHMAXSIM_HIP_LIB names another build of the same library (same ABI).
 LIB_PATH = os.environ.get("FLASHMAXSIM_HIP_LIB") or os.path.join(_PKG_DIR, "lib", "libflashmaxsim_hip.so")
 
-FMS_OK, FMS_EINVAL, FMS_EUNSUPPORTED, FMS_EHIP = 0, 1, 2, 3
+FMS_OK, FMS_EINVAL, FMS_EUNSUPPORTED, FMS_EHIP, FMS_ESCRATCH = 0, 1, 2, 3, 4
 FMS_F32, FMS_F16, FMS_BF16 = 0, 1, 2
 
 _p = ctypes.c_void_p
@@ -36,6 +36,8 @@ SIGNATURES = {
     "fms_launch_paired_scan": [_i32, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _i32, _p],
     "fms_launch_candidates_scan": [_i32, _p, _p, _p, _p, _p, _i32, _p, _p, _i64, _i64, _i64,
                                    _i64, _i64, _i64, _p, _f, _i32, _p],
+    "fms_launch_candidates_scan_noalloc": [_i32, _p, _p, _p, _p, _p, _i32, _p, _p, _i64, _i64,
+                                           _i64, _i64, _i64, _i64, _p, _f, _i32, _p],
     "fms_inbatch_device_scan": [_i32, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _p],
     "fms_launch_packed_scan": [_i32, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _i32, _p],
     "fms_launch_varlen_scan": [_i32, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _i32, _p],
@@ -99,7 +101,7 @@ def check(status: int, what: str) -> None:
     msg = f"{what}: {lib().fms_status_string(status).decode()}"
     if status == FMS_EINVAL:
         raise DimensionMismatch(msg)
-    if status == FMS_EUNSUPPORTED:
+    if status in (FMS_EUNSUPPORTED, FMS_ESCRATCH):
         raise UnsupportedError(msg)
     if status == FMS_EHIP:
         raise HIPError(msg)

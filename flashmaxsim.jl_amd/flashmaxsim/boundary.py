@@ -186,7 +186,11 @@ def launch_paired_scan(args, partial, Q, D, qmask, dmask, scores=None, normalize
 
 
 def launch_candidates_scan(args, partial, Q, gallery, idx, qmask, dmask, N, scores=None,
-                           neg=-1.0e4, normalize=False):
+                           neg=-1.0e4, normalize=False, noalloc=False):
+    """launch_candidates_scan! (forward_layouts.jl:292-310).  noalloc=True calls
+    fms_launch_candidates_scan_noalloc: the same scan with its grouping workspace in
+    the library's static device scratch instead of the memory pool (no device
+    allocation; UnsupportedError when a call needs more than that scratch)."""
     _feat(Q, "Q", 3)
     _feat(gallery, "gallery", 3, Q)
     B, Tq, dim = Q.shape
@@ -200,7 +204,9 @@ def launch_candidates_scan(args, partial, Q, gallery, idx, qmask, dmask, N, scor
     _buf(partial, "partial", torch.float32, B * C * Tq)
     _buf(scores, "scores", torch.float32, B * C)
     dev = require_device(args, partial, Q, gallery, idx, qmask, dmask, scores)
-    st = _lib.lib().fms_launch_candidates_scan(
+    fn = (_lib.lib().fms_launch_candidates_scan_noalloc if noalloc
+          else _lib.lib().fms_launch_candidates_scan)
+    st = fn(
         dtype_code(Q), ptr(args), ptr(partial), ptr(Q), ptr(gallery), ptr(idx), _idx_bytes(idx),
         ptr(_maskn(qmask, "qmask", B * Tq)), ptr(_maskn(dmask, "dmask", N * Td)), dim, Tq, B, Td, N,
         C, ptr(scores), float(neg), _norm(normalize), stream_handle(dev))

@@ -63,6 +63,7 @@ typedef int32_t fms_status;
 #define FMS_EINVAL 1       /* bad shape, NULL required pointer, misaligned buffer */
 #define FMS_EUNSUPPORTED 2 /* dtype / size the library does not implement */
 #define FMS_EHIP 3         /* a HIP runtime call or kernel launch failed */
+#define FMS_ESCRATCH 4     /* more workspace than fms_launch_candidates_scan_noalloc holds */
 
 /* Feature element types.  BF16 has no reference counterpart on device (the
  * reference's dot_accum(BFloat16) = BFloat16); here it accumulates in fp32. */
@@ -134,6 +135,33 @@ fms_status fms_launch_candidates_scan(int32_t dtype, int32_t* args, float* parti
  * 1 = always, 2 = never.  Returns the previous mode, or -1 for an invalid mode.
  */
 int32_t fms_candidates_grouping(int32_t mode);
+
+/*
+ * No reference counterpart: for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  fms_launch_candidates_scan with the same arguments and the
+ * same kernels and results, except that the document-grouping workspace
+ * comes from a static device array of FMS_NOALLOC_SCRATCH_BYTES per GPU
+ * (held from the first call on a GPU until the process ends) instead of the
+ * library pool: the call performs no hipMalloc / hipFree and calls no
+ * allocating library routine.  A call whose grouping workspace would exceed
+ * the array -- 8 bytes per pair plus 4 per gallery document, about 3.6M
+ * pairs over a 1M-document gallery -- returns FMS_ESCRATCH and launches
+ * nothing (fms_candidates_grouping(2) scans in output order, which needs no
+ * workspace).  Every call on one GPU uses that GPU's single array: calls that
+ * overlap on one GPU (concurrent streams) race and must be serialised by the
+ * caller.  The array's previous contents never matter (the kernels clear what
+ * they count).
+ */
+#define FMS_NOALLOC_SCRATCH_BYTES (32u << 20)
+fms_status fms_launch_candidates_scan_noalloc(int32_t dtype, int32_t* args, float* partial,
+                                              const void* Q, const void* gallery,
+                                              const void* idx, int32_t idx_bytes,
+                                              const uint8_t* qmask, const uint8_t* dmask,
+                                              int64_t dim, int64_t Tq, int64_t B,
+                                              int64_t Td, int64_t N, int64_t C,
+                                              float* scores, float neg, int32_t normalize,
+                                              void* stream);
 
 /*
  * In-batch scan.  Replaces inbatch_device_scan!(backend, S, args, Q, D,

@@ -140,3 +140,26 @@ def test_candidates_grouping_mode_switch():
         assert L.fms_candidates_grouping(0) == 0
     finally:
         L.fms_candidates_grouping(prev)
+
+
+def test_noalloc_rejects_workspace_beyond_its_scratch():
+    """fms_launch_candidates_scan_noalloc refuses (FMS_ESCRATCH, before any HIP call) a
+    grouped call whose workspace exceeds FMS_NOALLOC_SCRATCH_BYTES: 5M pairs need 40 MB
+    of order entries."""
+    L = _lib.lib()
+    prev = L.fms_candidates_grouping(1)
+    try:
+        st = L.fms_launch_candidates_scan_noalloc(1, None, None, 1, 1, 1, 8, None, None, 8, 1, 5,
+                                                  1, 1, 1_000_000, None, 0.0, 0, None)
+        assert st == _lib.FMS_ESCRATCH
+        assert b"scratch" in L.fms_status_string(st)
+        # the same validation as fms_launch_candidates_scan otherwise
+        assert L.fms_launch_candidates_scan_noalloc(9, None, None, 1, 1, 1, 8, None, None, 8, 1,
+                                                    5, 1, 1, 3, None, 0.0, 0, None) == EUNSUP
+        assert L.fms_launch_candidates_scan_noalloc(1, None, None, 1, 1, None, 8, None, None, 8,
+                                                    1, 5, 1, 1, 3, None, 0.0, 0, None) == EINVAL
+    finally:
+        L.fms_candidates_grouping(prev)
+    import flashmaxsim as fm
+    with pytest.raises(fm.UnsupportedError):
+        _lib.check(_lib.FMS_ESCRATCH, "x")

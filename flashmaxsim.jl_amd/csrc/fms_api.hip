@@ -19,6 +19,7 @@
 #include "fms_misc.hpp"
 #include "fms_topk.hpp"
 #include "fms_scan_decl.hpp"
+#include "fms_runs.hpp"
 
 #define FMS_VERSION_STRING "flashmaxsim-hip 0.1.0 (gfx950)"
 
@@ -160,40 +161,83 @@ hipError_t scratch_address(hipStream_t st, void** out) {
   return hipSuccess;
 }
 
+// The document-batch scan (fms_runs.hpp) for a grouped candidate call:
+// `runs.applies()` says whether it serves the call's type and dim (else
+// scan_fast runs over LayCandSorted), `runs(order, doc_end)` launches it.
+struct NoRuns {
+  bool applies() const { return false; }
+  hipError_t operator()(const PairRef*, const uint32_t*) const { return hipErrorInvalidValue; }
+};
+
+template <class Op>
+struct RunsLauncher {
+  const LayCand* lay;
+  int dim, rows;
+  int64_t npairs;
+  int32_t* args;
+  float* partial;
+  float* scores;
+  float neg;
+  bool norm, vec;
+  bool applies() const { return runs_supported<Op>(dim, vec); }
+  hipError_t operator()(const PairRef* order, const uint32_t* doc_end) const {
+    RunArgs A;
+    A.lay = *lay;
+    A.dim = dim;
+    A.nkb = (dim + Op::kKb - 1) / Op::kKb;
+    A.rows = rows;
+    A.nqt = rows > 0 ? (rows + kTile - 1) / kTile : 1;
+    A.ppw = 0;  // set by launch_runs
+    A.npairs = npairs;
+    A.args = args;
+    A.partial = partial;
+    A.scores = scores;
+    A.neg = neg;
+    A.norm = norm ? 1 : 0;
+    A.order = order;
+    A.doc_end = doc_end;
+    return launch_runs<Op>(A, st);
+  }
+  hipStream_t st;
+};
+
 // Runs launch(layout) on the candidate layout, in document order when
-// group_candidates says so, otherwise in output order.  The grouping
+// group_candidates says so (through `runs` when it serves the call, else
+// scan_fast over LayCandSorted), otherwise in output order.  The grouping
 // workspace comes from `ws`:
 //   kPool: the library pool, released on the same stream; an allocation
 //     failure falls back to output order (the results are identical);
 //   kScratch: the no-allocation array; a workspace larger than it is
 //     FMS_ESCRATCH (nothing is launched).  The grouping kernels clear every
 //     counter they use, so the array's previous contents do not matter.
-template <class Launch>
+template <class Runs, class Launch>
 fms_status run_candidates(const LayCand& lay, int64_t npairs, hipStream_t st, Workspace ws,
-                          Launch&& launch) {
+                          const Runs& runs, Launch&& launch) {
   if (!scan_grid_fits(npairs)) return FMS_EUNSUPPORTED;  // 32-bit work-item count
   if (group_candidates(npairs, lay.N, lay.dbytes)) {
     const size_t need = group_workspace_bytes(npairs, lay.N);
     void* buf = nullptr;
+    bool pooled = false;
     if (ws == Workspace::kScratch) {
       if (need > kNoallocScratchBytes) return FMS_ESCRATCH;
       const hipError_t e = scratch_address(st, &buf);
       if (e != hipSuccess) return from_hip(e);
-      LayCandSorted sl;
-      sl.c = lay;
-      hipError_t eg = group_pairs_by_document(lay.idx, lay.idx64, npairs, lay.N, buf, &sl.order, st);
-      if (eg == hipSuccess) eg = launch(sl);
-      return from_hip(eg);
+    } else if (workspace_alloc(&buf, need, st) == hipSuccess) {
+      pooled = true;
+    } else {
+      (void)hipGetLastError();  // clear the failed allocation; scan in output order
+      buf = nullptr;
     }
-    if (workspace_alloc(&buf, need, st) == hipSuccess) {
+    if (buf) {
       LayCandSorted sl;
       sl.c = lay;
-      hipError_t e = group_pairs_by_document(lay.idx, lay.idx64, npairs, lay.N, buf, &sl.order, st);
-      if (e == hipSuccess) e = launch(sl);
-      const hipError_t ef = workspace_free(buf, st);
+      const uint32_t* doc_end = nullptr;
+      hipError_t e = group_pairs_by_document(lay.idx, lay.idx64, npairs, lay.N, buf, &sl.order,
+                                             &doc_end, st);
+      if (e == hipSuccess) e = runs.applies() ? runs(sl.order, doc_end) : launch(sl);
+      const hipError_t ef = pooled ? workspace_free(buf, st) : hipSuccess;
       return from_hip(e != hipSuccess ? e : ef);
     }
-    (void)hipGetLastError();  // clear the failed allocation; scan in output order
   }
   return from_hip(launch(lay));
 }
@@ -352,10 +396,20 @@ fms_status candidates_scan(Workspace ws, int32_t dtype, int32_t* args, float* pa
   lay.Td = (int)Td;
   const bool vec = vec_ok(esz, dim, {Q, gallery});
   const hipStream_t st = as_stream(stream);
-  return run_candidates(lay, C * B, st, ws, [&](const auto& L) -> hipError_t {
+  auto launch = [&](const auto& L) -> hipError_t {
     return launch_float(dtype, L, (int)dim, (int)Tq, C * B, args, partial, scores, neg,
                         normalize != 0, vec, st);
-  });
+  };
+  if (dtype == FMS_F16 || dtype == FMS_BF16) {
+    const bool bf = dtype == FMS_BF16;
+    RunsLauncher<OpF16> r16{&lay, (int)dim, (int)Tq, C * B, args, partial, scores, neg,
+                            normalize != 0, vec, st};
+    RunsLauncher<OpBF16> rbf{&lay, (int)dim, (int)Tq, C * B, args, partial, scores, neg,
+                             normalize != 0, vec, st};
+    return bf ? run_candidates(lay, C * B, st, ws, rbf, launch)
+              : run_candidates(lay, C * B, st, ws, r16, launch);
+  }
+  return run_candidates(lay, C * B, st, ws, NoRuns{}, launch);
 }
 
 }  // namespace
@@ -604,10 +658,16 @@ fms_status fms_launch_int8_candidates_scan(int32_t* args, float* partial, const 
   lay.ds_esz = ds_esz;
   const bool vec = vec_ok(1, dim, {Qc, Gc});
   const hipStream_t st = as_stream(stream);
-  return run_candidates(lay, C * B, st, Workspace::kPool, [&](const auto& L) -> hipError_t {
+  auto launch = [&](const auto& L) -> hipError_t {
     return launch_int8(ds_esz, L, (int)dim, (int)Tq, C * B, args, partial, scores, neg,
                        normalize != 0, vec, st);
-  });
+  };
+  RunsLauncher<OpI8> r32{&lay, (int)dim, (int)Tq, C * B, args, partial, scores, neg,
+                         normalize != 0, vec, st};
+  RunsLauncher<OpI8H> r16{&lay, (int)dim, (int)Tq, C * B, args, partial, scores, neg,
+                          normalize != 0, vec, st};
+  return ds_esz == 2 ? run_candidates(lay, C * B, st, Workspace::kPool, r16, launch)
+                     : run_candidates(lay, C * B, st, Workspace::kPool, r32, launch);
 }
 
 int32_t fms_candidates_grouping(int32_t mode) {

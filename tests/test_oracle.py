@@ -365,3 +365,67 @@ def test_golden_fixtures():
         want = float(z[f"score{i}"])
         assert abs(float(s) - want) <= 1e-5 * max(1.0, abs(want)), i
         assert np.array_equal(a, z[f"tape{i}"]), i
+
+
+# ---- property tests of the reference (generator independent) -----------------------
+
+def test_sister_documents_separate_in_fp32():
+    """test_edge_cases.jl:26-84: a ranking gap below one Float16 score ulp survives
+    Float16 features because scores stay fp32 (pair, paired, candidates, in-batch,
+    packed layouts of the oracle)."""
+    import sisters
+    q, d, sis = sisters.sister_pair()
+    gap64 = sisters.maxsim_dense(q, d) - sisters.maxsim_dense(q, sis)
+    assert 1e-4 < gap64 < 0.02
+    q16, d16, s16 = (x.astype(np.float16) for x in (q, d, sis))
+    sa, sb = oracle.pair_forward(q16, d16)[0], oracle.pair_forward(q16, s16)[0]
+    assert sa.dtype == np.float32 and sa > sb
+    assert abs(float(sa) - float(sb)) < sisters.f16_ulp(float(sa))
+    D = np.stack([d16, s16])
+    Q2 = np.stack([q16, q16])
+    assert np.diff(oracle.paired_forward(Q2, D)[0])[0] < 0
+    Sc = oracle.candidates_forward(q16[None], D, np.array([[1, 2]]))[0]
+    assert Sc[0, 0] > Sc[0, 1]
+    Sib = oracle.inbatch_forward(q16[None], D)[0]
+    assert Sib[0, 0] > Sib[0, 1]
+    cu = np.array([1, 41, 81], np.int32)
+    sp = oracle.packed_forward(q16, np.concatenate([d16, s16]), cu)[0]
+    assert sp[0] > sp[1]
+
+
+def test_sister_ladder_order_matches_f64():
+    """test_edge_cases.jl:86-107: five sisters keep the fp64 order in fp32 scores,
+    though rounding the scores to Float16 would merge them."""
+    import sisters
+    q, docs = sisters.sister_ladder()
+    s64 = np.array([sisters.maxsim_dense(q, d) for d in docs])
+    q16 = q.astype(np.float16)
+    s16 = np.array([oracle.pair_forward(q16, d.astype(np.float16))[0] for d in docs])
+    assert (np.diff(s16) < 0).all()
+    assert (np.argsort(-s16) == np.argsort(-s64)).all()
+    assert len(np.unique(s16)) == len(s16)
+    assert len(np.unique(s16.astype(np.float16))) < len(s16)
+    assert (np.abs(np.diff(s64)) < sisters.F16_ULP_AT_32).all()
+
+
+def test_int8_ranking_vs_fp32():
+    """test_int8.jl:46-59: INT8 scores rank a 64-document gallery like fp32
+    (Spearman >= 0.95, top-20 overlap >= 0.7); the helpers themselves are
+    pinned on permutations."""
+    import sisters
+    assert abs(sisters.spearman([1, 2, 3, 4], [10, 20, 30, 40]) - 1.0) < 1e-12
+    assert abs(sisters.spearman([1, 2, 3, 4], [4, 3, 2, 1]) + 1.0) < 1e-12
+    # 1 - 6 sum(d^2) / (n (n^2 - 1)) for distinct ranks: d = (1, -1, 0, 0) -> 0.8
+    assert abs(sisters.spearman([1, 2, 3, 4], [2, 1, 3, 4]) - 0.8) < 1e-12
+    assert sisters.topk_overlap([5, 4, 3, 2, 1], [5, 4, 0, 0, 9], 2) == 0.5
+    rng = np.random.default_rng(41)
+    dim, Tq, Td, N = 32, 12, 20, 64
+    q = tokens(rng, (Tq, dim))
+    G = tokens(rng, (N, Td, dim))
+    s_fp = oracle.paired_forward(np.broadcast_to(q, (N, Tq, dim)).copy(), G)[0]
+    qc, qs = oracle.quantize_int8(q)
+    gc, gs = oracle.quantize_int8(G)
+    s_i8 = oracle.int8_paired_forward(np.broadcast_to(qc, (N, Tq, dim)).copy(),
+                                      np.broadcast_to(qs, (N, Tq)).copy(), gc, gs)[0]
+    assert sisters.spearman(s_fp, s_i8) >= 0.95
+    assert sisters.topk_overlap(s_fp, s_i8, 20) >= 0.7

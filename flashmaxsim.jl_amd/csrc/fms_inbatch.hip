@@ -47,9 +47,9 @@
 //     and DPP, not LDS shuffles, and no branches;
 //   * per-document tape (int16, Td <= 2048) / score go to LDS and leave in
 //     one coalesced pass at the end of the block.
-// Block -> (query block, document range) is XCD-aware: consecutive block ids
-// go to different XCDs, so each XCD's blocks share one slice of documents
-// (its L2) and iterate over all query blocks.
+// Block -> (query block, document range) is XCD-aware: the query blocks of
+// one document range run together on one XCD, so its L2 serves the range's
+// chunks to all of them.
 #include <hip/hip_runtime.h>
 #include <math.h>
 
@@ -258,19 +258,19 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
   const int tid = threadIdx.x, lane = tid & 63, wave = uniform(tid >> 6);
   const int r32 = lane & 31, h = lane >> 5;
 
-  // XCD-aware block mapping (blocks are dealt round-robin to the 8 XCDs).
+  // XCD-aware block mapping.  Blocks are dealt round-robin to the 8 XCDs
+  // (XCD = id % 8); in each XCD's own order k = id / 8 the query block runs
+  // fastest, so the nqb blocks of one document range are dispatched together
+  // on one XCD and stream the range's chunks through that XCD's L2 at about
+  // the same time: HBM delivers each range about once, not once per query
+  // block.  Document range db = (k / nqb) * 8 + XCD (the grid is padded to
+  // whole rows of 8 ranges).
   const int nqb = A.nqb, ndb = A.ndb;
   const int id = blockIdx.x;
-  int qb, db;
-  if (ndb % kXcds == 0) {
-    const int per = ndb / kXcds, xcd = id % kXcds, k = id / kXcds;
-    db = xcd * per + k % per;
-    qb = k / per;
-  } else {
-    db = id % ndb;
-    qb = id / ndb;
-  }
-  if (qb >= nqb) return;
+  const int xcd = id % kXcds, kx = id / kXcds;
+  const int qb = kx % nqb;
+  const int db = (kx / nqb) * kXcds + xcd;
+  if (db >= ndb) return;
 
   // ---- this block's documents -------------------------------------------------
   // Uniform: A.db per block.  Balanced (A.balance): the document blocks split
@@ -733,7 +733,7 @@ hipError_t launch_inbatch_mfma(int dtype_bf16, const InBatchArgs& args_in, hipSt
                        A.dm, A.D, dtype_bf16, A.Bd, A.Td, nch, cmask, dcount, dfirst);
   e = hipGetLastError();
   if (e == hipSuccess) {
-    const dim3 grid((unsigned)(A.nqb * A.ndb)), block(64 * kIbWaves);
+    const dim3 grid((unsigned)(A.nqb * ((A.ndb + kXcds - 1) / kXcds) * kXcds)), block(64 * kIbWaves);
     if (A.cu) {
       if (dtype_bf16)
         hipLaunchKernelGGL((inbatch_mfma<OpBF16, true>), grid, block, 0, stream, A);

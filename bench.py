@@ -121,8 +121,13 @@ def run_c2(args, torch, fm, boundary, dev):
     n_valid = C * B - n_invalid
     bytes_per_launch = (n_valid * (Ld * dim * 2 + Ld) + C * B * (4 * Lq + 4)
                         + B * (Lq * dim * 2 + Lq) + C * B * 8)
+    # compulsory bytes: every distinct referenced document once, plus the rest
+    n_docs = int(torch.unique(idx[idx > 0]).numel())
+    compulsory = (n_docs * (Ld * dim * 2 + Ld) + C * B * (4 * Lq + 4)
+                  + B * (Lq * dim * 2 + Lq) + C * B * 8)
     res = dict(pairs_per_step=C * B, bytes_per_launch=bytes_per_launch, wall=wall,
-               launch_ms=launch_ms, dtype="f16",
+               launch_ms=launch_ms, dtype="f16", compulsory_bytes=compulsory,
+               distinct_docs=n_docs,
                config={"workload": "c2_candidates_fp16", "dim": dim, "Lq": Lq, "Ld": Ld,
                        "C": C, "B": B, "N": N, "invalid_slots": n_invalid, "idx": "int64",
                        "masks": "all true (device Bool)", "outputs": "scores (C,B) + tape (Lq,C,B)"})
@@ -241,8 +246,12 @@ def run_c5(args, torch, fm, boundary, dev):
 
     wall, launch_ms = timed_steps(torch, step, args.steps, args.warmup)
     bytes_per_launch = C * B * (Ld * dim + Ld * 4 + Ld + 4 * Lq + 4) + C * B * 8 + B * Lq * (dim * 5 + 4)
+    n_docs = int(torch.unique(idx).numel())
+    compulsory = (n_docs * (Ld * dim + Ld * 4 + Ld) + C * B * (4 * Lq + 4) + C * B * 8
+                  + B * Lq * (dim * 5 + 4))
     res = dict(pairs_per_step=C * B, bytes_per_launch=bytes_per_launch, wall=wall,
-               launch_ms=launch_ms, dtype="int8", bound="hbm",
+               launch_ms=launch_ms, dtype="int8", bound="hbm", compulsory_bytes=compulsory,
+               distinct_docs=n_docs,
                config={"workload": "c5_int8_candidates", "dim": dim, "Lq": Lq, "Ld": Ld, "C": C,
                        "B": B, "N": N, "idx": "int64", "query": "fp32, quantised per step"})
     if not args.no_cpu or args.check:
@@ -516,6 +525,14 @@ def main():
         achieved = r["flops_per_launch"] / avg_launch_s / 1e12
         roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak,
                 "unit": "TFLOP/s", "frac": round(achieved / peak, 4)}
+    if "compulsory_bytes" in r:
+        # Beside the per-pair algorithmic bytes (every pair reads its document):
+        # the bytes no schedule can avoid -- each distinct referenced document
+        # once, plus queries, indices and outputs -- over the same launch time.
+        cb = r["compulsory_bytes"]
+        roof["compulsory"] = {"bytes": cb, "distinct_docs": r["distinct_docs"],
+                              "achieved": round(cb / avg_launch_s / 1e9, 1),
+                              "frac": round(cb / avg_launch_s / 1e9 / HBM_PEAK_GBS, 4)}
     roof["traffic"] = None
     prof = os.path.join(ROOT, "profiles", f"traffic_{args.workload}.json")
     if os.path.exists(prof):

@@ -138,6 +138,36 @@ def run_c2(args, torch, fm, boundary, dev):
     return res
 
 
+def blas_tiled_pairs(Qh, Gh, qi, di, threads, tile=64):
+    """The reference's CPU pair core over a list of pairs (q = Qh[qi[p]], d = Gh[di[p]]),
+    as src/forward_pair.jl:66-94 runs it: the query widened to fp32 once per pair, then
+    per 64-token document tile one fp32 GEMM (numpy matmul, i.e. OpenBLAS sgemm) and the
+    running max with the first-valid / strictly-greater rule.  All masks true (the
+    benchmark's).  Pairs are split over `threads` Python threads (numpy releases the
+    GIL; OpenBLAS itself is held to one thread per call).  Returns the scores."""
+    import numpy as np
+    from concurrent.futures import ThreadPoolExecutor
+    from threadpoolctl import threadpool_limits
+
+    def run(sl):
+        q = Qh[qi[sl]].astype(np.float32)            # (P, Tq, d)
+        qt = np.ascontiguousarray(q.transpose(0, 2, 1))
+        Td = Gh.shape[1]
+        mx = np.zeros((len(q), q.shape[1]), np.float32)
+        for u in range(0, Td, tile):
+            d = Gh[di[sl], u:u + tile].astype(np.float32)   # (P, w, d)
+            st = np.matmul(d, qt)                           # (P, w, Tq)
+            m = st.max(axis=1)
+            mx = m if u == 0 else np.where(m > mx, m, mx)
+        return mx.sum(axis=1)
+
+    n = len(qi)
+    step = max(1, min(2048, (n + threads - 1) // threads))
+    chunks = [slice(a, min(n, a + step)) for a in range(0, n, step)]
+    with threadpool_limits(limits=1), ThreadPoolExecutor(threads) as ex:
+        return np.concatenate(list(ex.map(run, chunks)))
+
+
 def cpu_candidates(args, torch, Q, G, idx, qmask, dmask, S, args_t, neg, fp16=False,
                    int8=None):
     """Bounded CPU baseline + full-size parity spot check on a random pair sample."""
@@ -213,6 +243,30 @@ def cpu_candidates(args, torch, Q, G, idx, qmask, dmask, S, args_t, neg, fp16=Fa
         out["cpu"] = {"value": n / dt, "unit": "pairs/s", "cores": nthreads, "kind": "port",
                       "sample": f"{n} random (c,b) pairs of the same workload, "
                                 f"{dt:.1f} s on {nthreads} host threads (C oracle, OpenMP)"}
+        # one thread, on a sixteenth of the sample
+        n1 = max(64, n // 16)
+        _, _, dt1 = run_oracle(pairs[:n1], 1)
+        out["cpu"]["single_thread"] = {"value": n1 / dt1, "sample": f"{n1} pairs, {dt1:.1f} s"}
+        if int8 is None:
+            # the reference's BLAS-tiled CPU core (sgemm per 64-token tile), same pairs
+            ub, uj, idx_c, keep = sample_problem(pairs)
+            ub_t = torch.from_numpy(ub).to(Q.device)
+            uj_t = torch.from_numpy(np.maximum(uj - 1, 0)).to(Q.device)
+            Qh = Q[ub_t].cpu().numpy()
+            Gh = G[uj_t].cpu().numpy()
+            flat = idx_c.reshape(-1)[keep]
+            qi = (keep // C).astype(np.int64)
+            ok = flat > 0
+            t0 = time.perf_counter()
+            sb = blas_tiled_pairs(Qh, Gh, qi[ok], flat[ok] - 1, nthreads)
+            dtb = time.perf_counter() - t0
+            Sc, _, _ = run_oracle(pairs, nthreads)[:3]
+            agree = float(np.abs(sb - Sc[ok]).max()) if ok.any() else 0.0
+            out["cpu"]["blas_tiled"] = {
+                "value": n / dtb, "cores": nthreads,
+                "sample": f"the same {n} pairs, {dtb:.1f} s: numpy matmul (OpenBLAS sgemm, one "
+                          f"thread per call) per 64-token document tile on {nthreads} threads, "
+                          f"as the reference's CPU pair core; max |score - oracle| {agree:.2e}"}
         log(f"cpu baseline: {out['cpu']}")
     return out
 
@@ -291,17 +345,20 @@ def run_c3(args, torch, fm, boundary, dev):
         Dh = D.cpu().numpy()
         dm = dmask.cpu().numpy().astype(np.uint8)
 
-        def run(n):
+        def run(n, threads=nthreads):
             ii = rng.integers(0, Bq, n)
             jj = rng.integers(0, Bd, n)
             t0 = time.perf_counter()
-            oracle.paired_forward(Qh[ii], Dh[jj], None, dm[jj], nthreads=nthreads)
+            oracle.paired_forward(Qh[ii], Dh[jj], None, dm[jj], nthreads=threads)
             return time.perf_counter() - t0
         dt = run(256)
         n = int(max(256, min(Bq * Bd, 256 * args.cpu_seconds / max(dt, 1e-6))))
         dt = run(n)
         res["cpu"] = {"value": n / dt, "unit": "pairs/s", "cores": nthreads, "kind": "port",
                       "sample": f"{n} random (i,j) pairs, {dt:.1f} s on {nthreads} threads"}
+        n1 = max(64, n // 16)
+        dt1 = run(n1, 1)
+        res["cpu"]["single_thread"] = {"value": n1 / dt1, "sample": f"{n1} pairs, {dt1:.1f} s"}
     return res
 
 
@@ -402,20 +459,23 @@ def run_c4(args, torch, fm, boundary, dev, dim=128):
         cu_h = cu.cpu().numpy()
         q0 = Qs[0].view(torch.int16).cpu().numpy().view(np.uint16)
 
-        def run(n):
+        def run(n, threads=nthreads):
             docs = np.sort(rng.choice(nd, size=n, replace=False))
             a, z = cu_h[docs] - 1, cu_h[docs + 1] - 1
             sel = np.concatenate([np.arange(x, y) for x, y in zip(a, z)])
             t_h = tok[torch.from_numpy(sel).to(dev)].view(torch.int16).cpu().numpy().view(np.uint16)
             cu_c = np.concatenate([[1], 1 + np.cumsum(z - a)]).astype(np.int32)
             t0 = time.perf_counter()
-            oracle.packed_forward(q0, t_h, cu_c, None, bf16=True, nthreads=nthreads)
+            oracle.packed_forward(q0, t_h, cu_c, None, bf16=True, nthreads=threads)
             return time.perf_counter() - t0
         dt = run(16)
         n = int(max(16, min(nd, 16 * args.cpu_seconds / max(dt, 1e-6))))
         dt = run(n)
         res["cpu"] = {"value": n / dt, "unit": "pairs/s", "cores": nthreads, "kind": "port",
                       "sample": f"{n} documents of one query, {dt:.1f} s on {nthreads} threads"}
+        n1 = max(16, n // 16)
+        dt1 = run(n1, 1)
+        res["cpu"]["single_thread"] = {"value": n1 / dt1, "sample": f"{n1} documents, {dt1:.1f} s"}
     return res
 
 

@@ -235,7 +235,12 @@ __device__ int block_exclusive_scan_i32(int v, int* total) {
 }
 
 // kPacked: documents are PackedSeq token ranges (A.cu), not Td-row slabs.
-template <class Op, bool kPacked>
+// kT24 (Tq == 24): a wave's 4 queries are 96 consecutive query tokens, which
+// fill 3 tiles of 32 exactly (instead of 4 tiles three-quarters full); a step
+// is then one phase -- three MFMA chains over the chunk while the previous
+// chunk's three tiles fold -- and a document's close sums each query over
+// the lanes (and tiles) that hold its tokens.
+template <class Op, bool kPacked, bool kT24>
 __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(const InBatchArgs A) {
   typedef typename Op::Acc Acc;
   typedef typename Op::Frag Frag;
@@ -344,26 +349,55 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
   // Query masks are loaded unconditionally (an empty resource when absent
   // reads 0) and tested only when a document closes.
   Frag qf[kIbQpw][kIbNkb];
-  uint32_t qmb[kIbQpw];
+  uint32_t qmb[kIbQpw];  // per query (kT24: per tile, this lane's token)
   bool qlive[kIbQpw];
   int qi[kIbQpw];
 #pragma unroll
   for (int q = 0; q < kIbQpw; ++q) {
     qi[q] = qb * kIbQueries + wave * kIbQpw + q;
-    const bool live = qi[q] < A.Bq;
-    qlive[q] = live;
-    const int iq = live ? qi[q] : 0;
-    const rsrc_t rq = make_rsrc(A.Q + (int64_t)iq * Tq * kIbRowBytes,
-                                live ? (uint32_t)Tq * kIbRowBytes : 0u);
-    const int base = r32 * kIbRowBytes + h * 16;
+    qlive[q] = qi[q] < A.Bq;
+  }
+  if constexpr (!kT24) {
 #pragma unroll
-    for (int kb = 0; kb < kIbNkb; ++kb) qf[q][kb] = Op::load(rq, base + kb * 32);
-    qmb[q] = buf_load1(make_rsrc(A.qm ? (const void*)(A.qm + (int64_t)iq * Tq) : (const void*)A.Q,
-                                 (A.qm && live) ? (uint32_t)Tq : 0u), r32);
+    for (int q = 0; q < kIbQpw; ++q) {
+      const bool live = qlive[q];
+      const int iq = live ? qi[q] : 0;
+      const rsrc_t rq = make_rsrc(A.Q + (int64_t)iq * Tq * kIbRowBytes,
+                                  live ? (uint32_t)Tq * kIbRowBytes : 0u);
+      const int base = r32 * kIbRowBytes + h * 16;
+#pragma unroll
+      for (int kb = 0; kb < kIbNkb; ++kb) qf[q][kb] = Op::load(rq, base + kb * 32);
+      qmb[q] = buf_load1(make_rsrc(A.qm ? (const void*)(A.qm + (int64_t)iq * Tq) : (const void*)A.Q,
+                                   (A.qm && live) ? (uint32_t)Tq : 0u), r32);
+    }
+  } else {
+    // The wave's live queries are consecutive rows of Q: tile t, lane r32 holds
+    // token 32t + r32 of the 96 (rows past the live queries read 0).
+    const int nlive = std::max(0, std::min(kIbQpw, A.Bq - qi[0]));
+    const rsrc_t rq = make_rsrc(A.Q + (int64_t)qi[0] * 24 * kIbRowBytes,
+                                (uint32_t)(nlive * 24 * kIbRowBytes));
+    const rsrc_t rm = make_rsrc(A.qm ? (const void*)(A.qm + (int64_t)qi[0] * 24) : (const void*)A.Q,
+                                A.qm ? (uint32_t)(nlive * 24) : 0u);
+#pragma unroll
+    for (int t = 0; t < 3; ++t) {
+      const int base = (32 * t + r32) * kIbRowBytes + h * 16;
+#pragma unroll
+      for (int kb = 0; kb < kIbNkb; ++kb) qf[t][kb] = Op::load(rq, base + kb * 32);
+      qmb[t] = buf_load1(rm, 32 * t + r32);
+    }
   }
   const bool has_qm = A.qm != nullptr;
   auto token_valid = [&](int q) {
     return qlive[q] && r32 < Tq && (!has_qm || qmb[q] != 0u);
+  };
+  // kT24: the query (0..3 in the wave) and token (0..23) of this lane in tile t,
+  // and whether that token is valid.
+  auto t24_query = [&](int t) { return (32 * t + r32) / 24; };
+  auto t24_token = [&](int t) { return (32 * t + r32) % 24; };
+  auto t24_valid = [&](int t) {
+    const int qq = t24_query(t);
+    const bool live = qq == 0 ? qlive[0] : qq == 1 ? qlive[1] : qq == 2 ? qlive[2] : qlive[3];
+    return live && (!has_qm || qmb[t] != 0u);
   };
 #pragma unroll
   for (int k = 0; k < kIbMaxChunkMasks / (64 * kIbWaves); ++k) {
@@ -517,6 +551,43 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
     }
   };
 
+  // kT24: close the three tiles of the document of entry `inf` together when
+  // it was the document's last chunk.  Each tile merges and maps back as
+  // `close` does; query sums then split tile t at lane 24, 16 and 8 (query
+  // q's 24 tokens are tokens 24q..24q+23 of the wave's 96), each part summed
+  // in the order half_sum uses.
+  auto close24_if_last = [&](uint32_t inf) {
+    if (inf & (1u << kInfoLastBit)) {
+      const int jj = (inf >> kInfoDocShift) & kInfoDocMask;
+      const int f = (int)((inf >> kInfoFirstShift) & kInfoFirstMask) - 1;
+      float part[3];
+#pragma unroll
+      for (int t = 0; t < 3; ++t) {
+        int tok = slot_to_token(slot[t], h);
+        float m = mx[t];
+        merge_halves(m, tok, h);
+        const int t0 = tok > 0 ? tok - 1 : 0;
+        const uint32_t mw = chunk_mask[jj * nch + (t0 >> 5)];
+        const bool real = (tok > 0) & (((mw >> (t0 & 31)) & 1u) != 0u);
+        tok = real ? tok : f + 1;
+        const bool tv = t24_valid(t);
+        part[t] = (tv & (tok != 0)) ? m : 0.0f;
+        if (h == 0) res_tape[wave][t24_query(t)][jj][t24_token(t)] = (int16_t)(tv ? tok : 0);
+        mx[t] = -INFINITY;
+        slot[t] = -1;
+      }
+      const float l0 = half_sum(r32 < 24 ? part[0] : 0.0f), u0 = half_sum(r32 < 24 ? 0.0f : part[0]);
+      const float l1 = half_sum(r32 < 16 ? part[1] : 0.0f), u1 = half_sum(r32 < 16 ? 0.0f : part[1]);
+      const float l2 = half_sum(r32 < 8 ? part[2] : 0.0f), u2 = half_sum(r32 < 8 ? 0.0f : part[2]);
+      if (lane == 0) {
+        res_score[wave][0][jj] = l0;
+        res_score[wave][1][jj] = u0 + l1;
+        res_score[wave][2][jj] = u1 + l2;
+        res_score[wave][3][jj] = u2;
+      }
+    }
+  };
+
   // One step: entry i+1 register -> LDS, refill that register stage with
   // entry i+3, read the list info for the next step, then two phases of 16
   // MFMAs (two independent accumulation chains each):
@@ -573,6 +644,44 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
     dma_barrier<(kIbBufs - 2) * kIbKbPerWave>();
   };
 
+  // kT24 step: entry i's chunk times the three tiles (three independent MFMA
+  // chains) while the three tiles of entry i-1 fold; one phase, closes after
+  // the fold.  Loads, list reads and the barrier as in `step`.
+  Acc lagt[3];
+#pragma unroll
+  for (int t = 0; t < 3; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) lagt[t][r] = -INFINITY;
+  auto step24 = [&](int i, const u32x4* cur, u32x4* ahead) {
+    chunk_load(ahead, (uint32_t)uniform((int)ld_m), (uint32_t)uniform((int)ld_info), uniform(ld_r0));
+    ld_m = lst_mask[ld_i];
+    ld_info = lst_info[ld_i];
+    if constexpr (kPacked) ld_r0 = lst_row0[ld_i];
+    const uint32_t next_info = lst_info[i + 1 < nsteps_pad ? i + 1 : i];
+    const uint32_t info = (uint32_t)uniform((int)cur_info);
+    const uint32_t pinfo = (uint32_t)uniform((int)prev_info);
+    Frag a[kIbNkb];
+#pragma unroll
+    for (int kb = 0; kb < kIbNkb; ++kb) a[kb] = cur[kb * 64 + lane];
+    Acc n0 = Acc{}, n1 = Acc{}, n2 = Acc{};
+#pragma unroll
+    for (int kb = 0; kb < kIbNkb; ++kb) {
+      n0 = Op::mma(a[kb], qf[0][kb], n0);
+      n1 = Op::mma(a[kb], qf[1][kb], n1);
+      n2 = Op::mma(a[kb], qf[2][kb], n2);
+    }
+    fold_close(0, lagt[0], pinfo);
+    fold_close(1, lagt[1], pinfo);
+    fold_close(2, lagt[2], pinfo);
+    close24_if_last(pinfo);
+    lagt[0] = n0;
+    lagt[1] = n1;
+    lagt[2] = n2;
+    prev_info = info;
+    cur_info = next_info;
+    dma_barrier<(kIbBufs - 2) * kIbKbPerWave>();
+  };
+
   if (nsteps_pad > 0) {
     auto row0_at = [&](int i) { return kPacked ? uniform(lst_row0[i]) : 0; };
     chunk_load(cbuf0, lst_mask[0], lst_info[0], row0_at(0));                // entry 0
@@ -586,7 +695,12 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
     dma_barrier<(kIbBufs - 2) * kIbKbPerWave>();  // entry 0 in LDS
     // Every load is unconditional and the buffers rotate statically.
     for (int i = 0; i < nsteps_pad; i += kIbBufs) {
-      if constexpr (kIbBufs == 4) {
+      if constexpr (kT24) {
+        static_assert(kIbBufs == 3, "the kT24 loop rotates 3 buffers");
+        step24(i, cbuf0, cbuf2);
+        step24(i + 1, cbuf1, cbuf0);
+        step24(i + 2, cbuf2, cbuf1);
+      } else if constexpr (kIbBufs == 4) {
         step(i, cbuf0, cbuf3);
         step(i + 1, cbuf1, cbuf0);
         step(i + 2, cbuf2, cbuf1);
@@ -599,11 +713,17 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
     }
     // No load into LDS may outlive the workgroup.
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-    // tiles 2,3 of the last entry
     const uint32_t pinfo = (uint32_t)uniform((int)prev_info);
-    fold_close(2, lag2, pinfo);
-    fold_close(3, lag3, pinfo);
-    close_if_last(2, 3, pinfo);
+    if constexpr (kT24) {  // the three tiles of the last entry
+      fold_close(0, lagt[0], pinfo);
+      fold_close(1, lagt[1], pinfo);
+      fold_close(2, lagt[2], pinfo);
+      close24_if_last(pinfo);
+    } else {  // tiles 2,3 of the last entry
+      fold_close(2, lag2, pinfo);
+      fold_close(3, lag3, pinfo);
+      close_if_last(2, 3, pinfo);
+    }
   }
 
   // ---- first-token rule for NaN scores -------------------------------------------
@@ -615,7 +735,48 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
   // staged results: score(f) is recomputed by the same MFMAs (row f as every
   // row of the A operand), and where it is NaN the token's tape becomes f
   // and the document's score NaN.  Finite features never enter this branch.
-  {
+  if constexpr (kT24) {
+    // The same rule with the packed tiles: tile t's lanes hold tokens of
+    // queries t24_query(t); a tile is examined when one of its valid tokens
+    // or the document's first row is not finite.
+    uint32_t tnf = 0u;  // bit t: some valid token of tile t is not finite
+#pragma unroll
+    for (int t = 0; t < 3; ++t) {
+      bool nf = false;
+#pragma unroll
+      for (int kb = 0; kb < kIbNkb; ++kb) nf |= frag_nonfinite<Op>(qf[t][kb]);
+      nf = ((uint32_t)nf | lane_xor32((uint32_t)nf, h)) != 0u;
+      tnf |= __ballot(nf & t24_valid(t)) != 0ull ? (1u << t) : 0u;
+    }
+    if (tnf != 0u || uniform(any_nf) != 0) {
+      for (int jj = 0; jj < ndoc; ++jj) {
+        const int df = uniform(doc_first[jj]);
+        if (df < 0) continue;  // no valid token: the document never closed
+        const int f = df & ~(1 << kPlanNfBit);
+        const bool dnf = ((df >> kPlanNfBit) & 1) != 0;
+        const int rowoff = ((kPacked ? doc_row0[jj] : jj * Td) + f) * kIbRowBytes;
+        Frag a[kIbNkb];
+#pragma unroll
+        for (int kb = 0; kb < kIbNkb; ++kb) a[kb] = Op::load(rd, rowoff + kb * 32 + h * 16);
+#pragma unroll
+        for (int t = 0; t < 3; ++t) {
+          if (!dnf && !((tnf >> t) & 1u)) continue;
+          Acc acc = Acc{};
+#pragma unroll
+          for (int kb = 0; kb < kIbNkb; ++kb) acc = Op::mma(a[kb], qf[t][kb], acc);
+          const float s0 = acc[0];  // every row is f: <f, this lane's query token>
+          const bool fix = t24_valid(t) && is_nan_bits(s0);
+          if (__ballot(fix) == 0ull) continue;
+          if (fix & (h == 0)) res_tape[wave][t24_query(t)][jj][t24_token(t)] = (int16_t)(f + 1);
+          const int qa = (32 * t) / 24;  // the tile's first query; the other is qa + 1
+          const bool fa = __ballot(fix && t24_query(t) == qa) != 0ull;
+          const bool fb = __ballot(fix && t24_query(t) == qa + 1) != 0ull;
+          if (lane == 0 && fa) res_score[wave][qa][jj] = __builtin_bit_cast(float, 0x7fc00000u);
+          if (lane == 0 && fb) res_score[wave][qa + 1][jj] = __builtin_bit_cast(float, 0x7fc00000u);
+        }
+      }
+    }
+  } else {
     uint32_t qnf = 0u;  // bit q: some valid token of query q is not finite
 #pragma unroll
     for (int q = 0; q < kIbQpw; ++q) {
@@ -671,7 +832,16 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
     // normalize epilogue: 1 / max(valid query tokens, 1) in fp32 (normalize.jl:4-10)
     float inv = 1.0f;
     if (A.norm) {
-      const float nf = (float)__builtin_popcountll(__ballot(h == 0 && token_valid(q)));
+      float nf;
+      if constexpr (kT24) {
+        int c = 0;
+#pragma unroll
+        for (int t = 0; t < 3; ++t)
+          c += __builtin_popcountll(__ballot(h == 0 && t24_query(t) == q && t24_valid(t)));
+        nf = (float)c;
+      } else {
+        nf = (float)__builtin_popcountll(__ballot(h == 0 && token_valid(q)));
+      }
       inv = 1.0f / (nf > 1.0f ? nf : 1.0f);
     }
     if (lane < ndoc) {
@@ -734,16 +904,19 @@ hipError_t launch_inbatch_mfma(int dtype_bf16, const InBatchArgs& args_in, hipSt
   e = hipGetLastError();
   if (e == hipSuccess) {
     const dim3 grid((unsigned)(A.nqb * ((A.ndb + kXcds - 1) / kXcds) * kXcds)), block(64 * kIbWaves);
+    // Tq == 24: four queries fill three tiles (kT24)
+    auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, block, 0, stream, A); };
+    const bool t24 = A.Tq == 24;
     if (A.cu) {
       if (dtype_bf16)
-        hipLaunchKernelGGL((inbatch_mfma<OpBF16, true>), grid, block, 0, stream, A);
+        t24 ? go(inbatch_mfma<OpBF16, true, true>) : go(inbatch_mfma<OpBF16, true, false>);
       else
-        hipLaunchKernelGGL((inbatch_mfma<OpF16, true>), grid, block, 0, stream, A);
+        t24 ? go(inbatch_mfma<OpF16, true, true>) : go(inbatch_mfma<OpF16, true, false>);
     } else {
       if (dtype_bf16)
-        hipLaunchKernelGGL((inbatch_mfma<OpBF16, false>), grid, block, 0, stream, A);
+        t24 ? go(inbatch_mfma<OpBF16, false, true>) : go(inbatch_mfma<OpBF16, false, false>);
       else
-        hipLaunchKernelGGL((inbatch_mfma<OpF16, false>), grid, block, 0, stream, A);
+        t24 ? go(inbatch_mfma<OpF16, false, true>) : go(inbatch_mfma<OpF16, false, false>);
     }
     e = hipGetLastError();
   }

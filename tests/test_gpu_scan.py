@@ -179,7 +179,9 @@ def test_inbatch_parity(device, dtype, shape):
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=lambda d: DT_ID[d])
 @pytest.mark.parametrize("shape", [(32, 180, 24, 21), (17, 65, 40, 33), (32, 32, 16, 16),
-                                   (8, 300, 20, 17), (5, 7, 18, 6)],
+                                   (8, 300, 20, 17), (5, 7, 18, 6),
+                                   # Tq = 24: four queries packed into three tiles
+                                   (24, 180, 24, 21), (24, 33, 9, 5), (24, 700, 37, 5)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_inbatch_masks_and_ties(device, dtype, shape):
     """Non-prefix document masks, leading masked tokens, fully masked and

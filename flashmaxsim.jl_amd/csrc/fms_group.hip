@@ -1,11 +1,16 @@
 // fms_group.hip -- counting sort of candidate pairs by document, and the
 // workspace pool it draws from.
 //
-// Six small launches: zero the N+1 counters, histogram the pairs (one
-// atomic per pair), exclusive scan of the counters (tile sums, scan of the
-// tile sums, apply), atomic scatter of the pair ids.  Cost is linear in
-// C*B + N and small next to the scan it feeds: for C*B = 256k, N = 100k
-// about 30 MB of HBM traffic (mostly atomic write-backs) and ~85 us.
+// Two levels, with every atomic in LDS (a device-scope atomic on an MI355X
+// is performed past the XCDs' L2s, at memory: one per pair cost ~33 us per
+// pass at C*B = 256k):
+//   1. buckets of D consecutive documents: each block histograms its tile of
+//      pairs by bucket in LDS, the (bucket, block) counts are prefix-summed,
+//      and each block scatters its pairs to their bucket's slots;
+//   2. one block per bucket counts its pairs per document in LDS, writes the
+//      documents' run ends and scatters the pairs into document order.
+// The older one-level sort (one global atomic per pair and per pass) remains
+// for galleries too large for the bucket tables.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -127,6 +132,121 @@ __global__ void __launch_bounds__(kScanThreads) scan_apply_kernel(uint32_t* c, i
   }
 }
 
+// ---- two-level sort ------------------------------------------------------------
+
+constexpr int kBucketTile = 1024;       // pairs per block in the bucket passes
+constexpr int kMaxBuckets = 4096;       // LDS counters of the bucket passes
+constexpr int kMaxBucketDocs = 8192;    // LDS counters of the per-bucket sort
+constexpr int64_t kMaxBucketCells = 1 << 22;  // (bucket, block) counts: 16 MB
+
+struct BucketPlan {
+  int64_t nb;   // buckets
+  int64_t D;    // documents (keys) per bucket
+  int64_t G;    // blocks of the bucket passes
+};
+
+inline bool bucket_plan(int64_t npairs, int64_t N, BucketPlan* bp) {
+  const int64_t nkeys = N + 1;  // key N: out-of-range index
+  int64_t nb = cdiv(nkeys, 128);
+  if (nb > kMaxBuckets) nb = kMaxBuckets;
+  const int64_t D = cdiv(nkeys, nb);
+  if (npairs <= 0 || D > kMaxBucketDocs) return false;
+  bp->nb = cdiv(nkeys, D);
+  bp->D = D;
+  bp->G = cdiv(npairs, kBucketTile);
+  return bp->nb * bp->G <= kMaxBucketCells;
+}
+
+__device__ __forceinline__ int64_t pair_key(const void* idx, int idx64, int64_t p, int64_t N) {
+  const int64_t j = load_index(idx, idx64, p);
+  return (j >= 1 && j <= N) ? j - 1 : N;
+}
+
+// H[b * G + g] = pairs of block g's tile in bucket b.
+__global__ void __launch_bounds__(kFlat) bucket_hist_kernel(const void* idx, int idx64, int64_t P,
+                                                            int64_t N, int64_t D, int64_t nb,
+                                                            int64_t G, uint32_t* H) {
+  __shared__ uint32_t cnt[kMaxBuckets];
+  for (int64_t b = threadIdx.x; b < nb; b += kFlat) cnt[b] = 0u;
+  __syncthreads();
+  const int64_t p0 = (int64_t)blockIdx.x * kBucketTile;
+  const int64_t p1 = p0 + kBucketTile < P ? p0 + kBucketTile : P;
+  for (int64_t p = p0 + threadIdx.x; p < p1; p += kFlat)
+    atomicAdd(&cnt[pair_key(idx, idx64, p, N) / D], 1u);
+  __syncthreads();
+  for (int64_t b = threadIdx.x; b < nb; b += kFlat) H[b * G + blockIdx.x] = cnt[b];
+}
+
+// Pairs of block g's tile to their bucket's slots: T[pos] = (p, key), pos from
+// the exclusive scan of H (bucket-major), so bucket b's pairs are contiguous.
+__global__ void __launch_bounds__(kFlat) bucket_scatter_kernel(const void* idx, int idx64, int64_t P,
+                                                               int64_t N, int64_t D, int64_t nb,
+                                                               int64_t G, const uint32_t* Hs,
+                                                               PairRef* T) {
+  __shared__ uint32_t cur[kMaxBuckets];
+  for (int64_t b = threadIdx.x; b < nb; b += kFlat) cur[b] = Hs[b * G + blockIdx.x];
+  __syncthreads();
+  const int64_t p0 = (int64_t)blockIdx.x * kBucketTile;
+  const int64_t p1 = p0 + kBucketTile < P ? p0 + kBucketTile : P;
+  for (int64_t p = p0 + threadIdx.x; p < p1; p += kFlat) {
+    const int64_t key = pair_key(idx, idx64, p, N);
+    const uint32_t pos = atomicAdd(&cur[key / D], 1u);
+    PairRef r;
+    r.p = (int32_t)p;
+    r.j = (int32_t)key;
+    T[pos] = r;
+  }
+}
+
+// Block b sorts bucket b (keys b*D .. b*D+D-1) by key: counts per key in LDS,
+// doc_end[key] = end of the key's run, then the scatter into `order`
+// (key N, the out-of-range indices, becomes j = -1).
+__global__ void __launch_bounds__(kScanThreads) bucket_sort_kernel(const PairRef* T, int64_t P,
+                                                                   int64_t N, int64_t D, int64_t nb,
+                                                                   int64_t G, const uint32_t* Hs,
+                                                                   uint32_t* doc_end,
+                                                                   PairRef* order) {
+  __shared__ uint32_t cnt[kMaxBucketDocs];
+  const int64_t b = blockIdx.x;
+  const int64_t k0 = b * D, nk = (k0 + D <= N + 1 ? D : N + 1 - k0);
+  const int64_t e0 = Hs[b * G], e1 = b + 1 < nb ? (int64_t)Hs[(b + 1) * G] : P;
+  for (int64_t k = threadIdx.x; k < nk; k += kScanThreads) cnt[k] = 0u;
+  __syncthreads();
+  for (int64_t e = e0 + threadIdx.x; e < e1; e += kScanThreads) atomicAdd(&cnt[T[e].j - k0], 1u);
+  __syncthreads();
+  // exclusive scan of the nk counters, kPer consecutive ones per thread
+  constexpr int kPer = kMaxBucketDocs / kScanThreads;
+  uint32_t v[kPer];
+  uint32_t s = 0u;
+  const int64_t base = (int64_t)threadIdx.x * kPer;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    v[i] = base + i < nk ? cnt[base + i] : 0u;
+    s += v[i];
+  }
+  uint32_t tot;
+  uint32_t ex = block_exclusive_scan(s, &tot) + (uint32_t)e0;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    if (base + i < nk) {
+      cnt[base + i] = ex;                 // cursor: start of the key's run
+      doc_end[k0 + base + i] = ex + v[i];  // end of the key's run
+    }
+    ex += v[i];
+  }
+  __syncthreads();
+  for (int64_t e = e0 + threadIdx.x; e < e1; e += kScanThreads) {
+    const PairRef t = T[e];
+    const uint32_t pos = atomicAdd(&cnt[t.j - k0], 1u);
+    PairRef r;
+    r.p = t.p;
+    r.j = t.j == N ? -1 : t.j;
+    order[pos] = r;
+  }
+}
+
+// ---- one-level sort (galleries beyond the bucket tables) -------------------------
+
 // order[cursor[key]++] = (p, document of p).
 __global__ void __launch_bounds__(kFlat) group_scatter_kernel(const void* idx, int idx64, int64_t P,
                                                               int64_t N, uint32_t* cursor,
@@ -145,8 +265,15 @@ __global__ void __launch_bounds__(kFlat) group_scatter_kernel(const void* idx, i
 
 size_t group_workspace_bytes(int64_t npairs, int64_t N) {
   const int64_t ncount = N + 1;
-  return align256((size_t)npairs * sizeof(PairRef)) + align256((size_t)ncount * 4) +
-         align256((size_t)cdiv(ncount, kScanTile) * 4);
+  size_t bytes = align256((size_t)npairs * sizeof(PairRef)) + align256((size_t)ncount * 4) +
+                 align256((size_t)cdiv(ncount, kScanTile) * 4);
+  BucketPlan bp;
+  if (bucket_plan(npairs, N, &bp)) {
+    const int64_t nh = bp.nb * bp.G;
+    bytes += align256((size_t)npairs * sizeof(PairRef)) + align256((size_t)nh * 4) +
+             align256((size_t)cdiv(nh, kScanTile) * 4);
+  }
+  return bytes;
 }
 
 hipError_t group_pairs_by_document(const void* idx, int idx64, int64_t npairs, int64_t N,
@@ -159,6 +286,25 @@ hipError_t group_pairs_by_document(const void* idx, int idx64, int64_t npairs, i
   uint32_t* counts = reinterpret_cast<uint32_t*>(w + align256((size_t)npairs * sizeof(PairRef)));
   uint32_t* sums = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(counts) +
                                                align256((size_t)ncount * 4));
+  BucketPlan bp;
+  if (bucket_plan(npairs, N, &bp)) {
+    // counts doubles as doc_end (the run ends the bucket sort writes)
+    char* t = reinterpret_cast<char*>(sums) + align256((size_t)nb * 4);
+    PairRef* T = reinterpret_cast<PairRef*>(t);
+    uint32_t* H = reinterpret_cast<uint32_t*>(t + align256((size_t)npairs * sizeof(PairRef)));
+    const int64_t nh = bp.nb * bp.G;
+    uint32_t* Hsums = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(H) + align256((size_t)nh * 4));
+    hipLaunchKernelGGL(bucket_hist_kernel, dim3((unsigned)bp.G), dim3(kFlat), 0, stream, idx, idx64,
+                       npairs, N, bp.D, bp.nb, bp.G, H);
+    hipError_t e = exclusive_scan_u32(H, nh, Hsums, stream);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(bucket_scatter_kernel, dim3((unsigned)bp.G), dim3(kFlat), 0, stream, idx,
+                       idx64, npairs, N, bp.D, bp.nb, bp.G, H, T);
+    hipLaunchKernelGGL(bucket_sort_kernel, dim3((unsigned)bp.nb), dim3(kScanThreads), 0, stream, T,
+                       npairs, N, bp.D, bp.nb, bp.G, H, counts, order);
+    *order_out = order;
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(group_zero_kernel, dim3(flat_blocks(ncount)), dim3(kFlat), 0, stream, counts,
                      ncount);
   hipLaunchKernelGGL(group_hist_kernel, dim3(flat_blocks(npairs)), dim3(kFlat), 0, stream, idx,

@@ -27,8 +27,8 @@ size_t group_workspace_bytes(int64_t npairs, int64_t N);
 
 // Fills `*order` (inside `workspace`) with all npairs pair ids, grouped by
 // document in ascending document order, out-of-range indices last.  The
-// order of the pairs of one document is unspecified (atomic scatter); each
-// pair's result does not depend on it.  Requires npairs, N < 2^31.
+// order of the pairs of one document is unspecified (LDS-atomic scatter);
+// each pair's result does not depend on it.  Requires npairs, N < 2^31.
 hipError_t group_pairs_by_document(const void* idx, int idx64, int64_t npairs, int64_t N,
                                    void* workspace, const PairRef** order, hipStream_t stream);
 // The same, also returning doc_end (N + 1 counters in `workspace`): the pairs of

@@ -145,8 +145,8 @@ int32_t fms_candidates_grouping(int32_t mode);
  * (held from the first call on a GPU until the process ends) instead of the
  * library pool: the call performs no hipMalloc / hipFree and calls no
  * allocating library routine.  A call whose grouping workspace would exceed
- * the array -- 8 bytes per pair plus 4 per gallery document, about 3.6M
- * pairs over a 1M-document gallery -- returns FMS_ESCRATCH and launches
+ * the array -- about 20 bytes per pair plus 4 per gallery document, some
+ * 1.4M pairs over a 1M-document gallery -- returns FMS_ESCRATCH and launches
  * nothing (fms_candidates_grouping(2) scans in output order, which needs no
  * workspace).  Every call on one GPU uses that GPU's single array: calls that
  * overlap on one GPU (concurrent streams) race and must be serialised by the

@@ -411,8 +411,14 @@ def run_c3bwd(args, torch, fm, boundary, dev):
     wq, _ = oracle.inbatch_backward(Qh[ii], Dh, ah[ii], Dlh[ii], ivh[ii])
     got = dQ[torch.from_numpy(ii).to(dev)].float().cpu().numpy().astype(np.float64)
     err = np.abs(got - wq) / (np.abs(wq) + 1e-3)
+    # and dD of a document depends only on its own column of pairs
+    jj = np.sort(rng.choice(Bd, size=4, replace=False))
+    _, wd = oracle.inbatch_backward(Qh, Dh[jj], ah[:, jj], Dlh[:, jj], ivh)
+    gotd = dD[torch.from_numpy(jj).to(dev)].float().cpu().numpy().astype(np.float64)
+    errd = np.abs(gotd - wd) / (np.abs(wd) + 1e-3)
     res["check"] = {"queries": ii.tolist(), "dQ_max_rel_err": float(err.max()),
-                    "ok": bool(err.max() < 4e-3)}
+                    "documents": jj.tolist(), "dD_max_rel_err": float(errd.max()),
+                    "ok": bool(err.max() < 4e-3 and errd.max() < 4e-3)}
     if not args.no_cpu:
         def run(n):
             sel = rng.choice(Bq, size=n, replace=False)

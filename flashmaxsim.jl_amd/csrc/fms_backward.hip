@@ -28,6 +28,7 @@
 #include <stdint.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "fms_backward.hpp"
 #include "fms_device.hpp"
@@ -830,6 +831,400 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_dd_vec_kernel(
   }
 }
 
+// ---- in-batch, 16-bit features: the feature-half path --------------------------------------
+// The kernels above gather whole rows.  In-batch, that sends every XCD after
+// all of Q for dD (Bq * Tq rows, about one XCD's L2) and leaves one fp32 dQ
+// partial per XCD.  Here each workgroup works on one half of the feature row,
+// h = XCD index & 1 (workgroups are dealt to the 8 XCDs round-robin by
+// workgroup index), so an XCD reads one half of Q (dD) or one half of one
+// quarter of D (dQ), a fraction of its L2:
+//   bwd_ib_compact  the tape as one byte per source, document-major:
+//                   ct[j][i][t] = u, or 0 where there is no source (masked
+//                   token, entry outside 1..Td, delta 0); query rows of Tqp
+//                   (Tq rounded up to 4) bytes, documents ct_stride bytes
+//                   apart; and delta document-major, dT[j][i].
+//   bwd_ib_dd       a workgroup per (document, half): counting sort of the
+//                   document's sources by row in LDS (one counter set per
+//                   wave), then each row's query half-rows summed in
+//                   registers, in list order.  Every row is written.
+//   bwd_ib_dq       a workgroup per (16 work items, half, document quarter):
+//                   the quarter's half-rows staged through LDS as in
+//                   bwd_dq_ib; one fp32 partial per quarter, summed in
+//                   quarter order by bwd_dq_reduce.  Deterministic.
+constexpr int kIbxMaxSrc = 32768;          // key bytes per document (Bq * Tqp)
+constexpr int kIbxMaxBq = 4096;            // queries
+constexpr int kIbxDdThreads = 512;         // bwd_ib_dd: 8 waves
+constexpr int kIbxDdWaves = kIbxDdThreads / 64;
+constexpr int kIbxKeep = kIbxMaxSrc / 16 / kIbxDdThreads;  // 16-byte key chunks a thread keeps
+constexpr int kIbxDdUnroll = 8;            // query half-rows in flight per row group
+constexpr int kIbxStage = 3 * kIbThreads;  // 16-byte chunks per LDS buffer of bwd_ib_dq (48 KB)
+constexpr int kIbxQuarters = 4;            // document quarters of bwd_ib_dq
+constexpr int kIbxDdLdsMax = 65536;        // dynamic LDS of bwd_ib_dd
+
+struct IbxGeo {
+  int64_t Bd;
+  int Bq, Tq, Tqp, Td;
+  int64_t ct_stride;  // bytes of ct per document: Bq * Tqp rounded up to 16
+  uint32_t mq, mqp;   // ibx_magic(Tq), ibx_magic(Tqp)
+};
+
+// n / d for n < 2^16, d < 2^16, with m = ceil(2^32 / d) (d >= 2) or 0 (d = 1):
+// the error of n * m / 2^32 against n / d is n * (m * d - 2^32) / (d * 2^32) < 1 / d.
+__device__ __forceinline__ uint32_t ibx_div(uint32_t n, uint32_t m) {
+  return m == 0u ? n : __umulhi(n, m);
+}
+
+// f(std::integral_constant<int, kI>()), ..., for kI < kN: a loop whose index is a
+// constant expression (ds_swizzle patterns are immediates).
+template <int kI, int kN, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (kI < kN) {
+    f(std::integral_constant<int, kI>());
+    static_for<kI + 1, kN>(f);
+  }
+}
+
+// Workgroup (j, y) covers dwords y * kIbxCompactSpan .. + kIbxCompactSpan - 1 of
+// document j's bytes; dword k holds tokens 4 * (k % (Tqp / 4)) .. + 3 of query
+// k / (Tqp / 4).  Each thread loads its kIbxCompactPer dwords' tape entries
+// before it combines any.  vec4: the tape rows start 16-byte aligned (Tq a
+// multiple of 4, aligned buffer).
+constexpr int kIbxCompactPer = 4;
+constexpr int kIbxCompactSpan = kIbxCompactPer * kBwdThreads;
+__global__ void __launch_bounds__(kBwdThreads) bwd_ib_compact_kernel(const int32_t* args,
+                                                                     const float* delta,
+                                                                     const uint8_t* qm, IbxGeo g,
+                                                                     int vec4, uint32_t* ct,
+                                                                     float* dT) {
+  const int64_t j = blockIdx.x;
+  const int tq4 = g.Tqp >> 2;
+  const int nk = (int)(g.ct_stride >> 2), nv = g.Bq * tq4;
+  uint32_t* out = ct + j * nk;
+  const int k0 = (int)blockIdx.y * kIbxCompactSpan + (int)threadIdx.x;
+  int u[kIbxCompactPer][4], iq[kIbxCompactPer], tq[kIbxCompactPer];
+  float dl[kIbxCompactPer];
+#pragma unroll
+  for (int q = 0; q < kIbxCompactPer; ++q) {
+    const int k = k0 + q * kBwdThreads;
+    const bool in = k < nv;
+    const int i = in ? k / tq4 : 0, t0 = in ? (k - i * tq4) * 4 : g.Tq;
+    iq[q] = i;
+    tq[q] = t0;
+    const int64_t p = j + g.Bd * i;
+    dl[q] = in ? delta[p] : 0.0f;
+    const int32_t* a = args + p * g.Tq;
+    if (in && vec4) {
+      const int4 v = *reinterpret_cast<const int4*>(a + t0);
+      u[q][0] = v.x;
+      u[q][1] = v.y;
+      u[q][2] = v.z;
+      u[q][3] = v.w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) u[q][e] = t0 + e < g.Tq ? a[t0 + e] : 0;
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < kIbxCompactPer; ++q) {
+    const int k = k0 + q * kBwdThreads;
+    uint32_t word = 0u;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int t = tq[q] + e;
+      const bool ok = t < g.Tq && u[q][e] >= 1 && u[q][e] <= g.Td && dl[q] != 0.0f &&
+                      (qm == nullptr || qm[(int64_t)iq[q] * g.Tq + t] != 0);
+      word |= (ok ? (uint32_t)u[q][e] : 0u) << (8 * e);
+    }
+    if (k < nk) out[k] = word;
+  }
+  if (blockIdx.y == 0)
+    for (int i = threadIdx.x; i < g.Bq; i += kBwdThreads) dT[j * g.Bq + i] = delta[j + g.Bd * i];
+}
+
+// dD rows of document j, feature half h.  Dynamic LDS: counters [256][waves / 2]
+// (two 16-bit counters a word, waves 2v and 2v + 1: no count or cursor passes
+// Bq * Tqp <= 32768), row starts [256], delta [Bq + 1] (the last 0), list
+// [Bq * Tqp] (uint16 query rows).  kHC: 16-byte chunks per half row; kHC lanes
+// per row, 64 / kHC rows per wave.
+// Waves per SIMD asked of bwd_ib_dd: 8 (64 registers, and 4 workgroups per CU
+// when the LDS allows) where that costs no spill, else the compiler's choice.
+template <class E, int kHC>
+struct IbxDdWaves {
+  static constexpr int kMin = (std::is_same<E, EF16>::value && kHC <= 8) ? 8 : 1;
+};
+
+template <class E, int kHC>
+__global__ void __launch_bounds__(kIbxDdThreads)
+    __attribute__((amdgpu_waves_per_eu(IbxDdWaves<E, kHC>::kMin, 8))) bwd_ib_dd_kernel(const uint32_t* ct,
+                                                                 const float* dT, IbxGeo g,
+                                                                 int64_t rb, const char* Q,
+                                                                 int64_t q_bytes, char* dD) {
+  constexpr int kRG = 64 / kHC;
+  constexpr int kCw = kIbxDdWaves / 2;        // counter words per row
+  constexpr int kB = kHC < 8 ? kHC : 8;       // query half-rows in flight per row group
+  constexpr int kSw = 0x1F & ~(kHC - 1);      // ds_swizzle and-mask: the group's first lane
+  extern __shared__ uint32_t ibx_smem[];
+  __shared__ uint32_t wtot[4];
+  uint32_t* cnt = ibx_smem;
+  uint32_t* rs = cnt + 256 * kCw;
+  float* dl = reinterpret_cast<float*>(rs + 256);
+  uint16_t* list = reinterpret_cast<uint16_t*>(dl + g.Bq + 1);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int xcd = blockIdx.x & 7, h = xcd & 1;
+  const int64_t j = (int64_t)(blockIdx.x >> 3) * 4 + (xcd >> 1);
+  if (j >= g.Bd) return;
+  const int nchunk = (int)(g.ct_stride >> 4);
+  const uint4* kj = reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(ct) + j * g.ct_stride);
+  uint4 key[kIbxKeep];
+#pragma unroll
+  for (int q = 0; q < kIbxKeep; ++q) {
+    const int c = q * kIbxDdThreads + tid;
+    key[q] = c < nchunk ? kj[c] : make_uint4(0u, 0u, 0u, 0u);
+  }
+  for (int x = tid; x < 256 * kCw; x += kIbxDdThreads) cnt[x] = 0u;
+  const float* dtj = dT + j * g.Bq;
+  for (int x = tid; x <= g.Bq; x += kIbxDdThreads) dl[x] = x < g.Bq ? dtj[x] : 0.0f;
+  __syncthreads();
+  uint32_t* cw = cnt + (w >> 1);
+  const int csh = 16 * (w & 1);
+  // fn(u, f) for every source of this thread: row u (1-based), key byte f of the document
+  auto each = [&](auto fn) {
+#pragma unroll
+    for (int q = 0; q < kIbxKeep; ++q) {
+      if (q * kIbxDdThreads >= nchunk) break;  // (uniform)
+      const uint32_t kw[4] = {key[q].x, key[q].y, key[q].z, key[q].w};
+      const uint32_t f0 = (uint32_t)(q * kIbxDdThreads + tid) * 16u;
+#pragma unroll
+      for (int d = 0; d < 4; ++d)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          const uint32_t u = (kw[d] >> (8 * b)) & 255u;
+          if (u != 0u) fn(u, f0 + (uint32_t)(d * 4 + b));
+        }
+    }
+  };
+  each([&](uint32_t u, uint32_t) { atomicAdd(&cw[u * kCw], 1u << csh); });
+  __syncthreads();
+  // Row r = u - 1 starts at rs[r]; wave v's sources of row r fill from
+  // rs[r] + (those of waves < v), its counter becoming that cursor.
+  uint32_t tot = 0u, x = 0u;
+  uint32_t cv[kIbxDdWaves];
+  if (tid < 256) {
+#pragma unroll
+    for (int v = 0; v < kIbxDdWaves; ++v)
+      cv[v] = tid < g.Td ? (cnt[(tid + 1) * kCw + (v >> 1)] >> (16 * (v & 1))) & 0xFFFFu : 0u;
+#pragma unroll
+    for (int v = 0; v < kIbxDdWaves; ++v) tot += cv[v];
+    x = tot;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t y = __shfl_up(x, o);
+      if (lane >= o) x += y;
+    }
+    if (lane == 63) wtot[w] = x;
+  }
+  __syncthreads();
+  if (tid < g.Td) {
+    uint32_t run = x - tot;
+    for (int v = 0; v < w; ++v) run += wtot[v];
+    rs[tid] = run;
+#pragma unroll
+    for (int v = 0; v < kIbxDdWaves; v += 2) {
+      const uint32_t lo = run, hi = run + cv[v];
+      cnt[(tid + 1) * kCw + (v >> 1)] = lo | (hi << 16);
+      run = hi + cv[v + 1];
+    }
+    if (tid == g.Td - 1) rs[g.Td] = run;
+  }
+  __syncthreads();
+  each([&](uint32_t u, uint32_t f) {
+    const uint32_t i = ibx_div(f, g.mqp);
+    const uint32_t qr = i * (uint32_t)g.Tq + (f - i * (uint32_t)g.Tqp);
+    const uint32_t old = atomicAdd(&cw[u * kCw], 1u << csh);
+    list[(old >> csh) & 0xFFFFu] = (uint16_t)qr;
+  });
+  __syncthreads();
+  // Row sums: lanes gq * kHC .. + kHC - 1 own row r, chunk c of the half row.
+  // Per batch of kHC entries lane c reads entry k + c (past the row's end:
+  // query row Bq * Tq, whose delta dl[Bq] is 0 and whose load falls outside Q
+  // and returns 0) and the group takes each entry's row offset and delta from
+  // its lane by ds_swizzle.
+  const int gq = lane / kHC, c = lane - gq * kHC;
+  const uint32_t cof = (uint32_t)(h * kHC + c) * 16u;
+  const uint32_t sent = (uint32_t)(g.Bq * g.Tq);
+  const rsrc_t rQ = make_rsrc_u(Q, (uint32_t)q_bytes);
+  char* dj = dD + j * (int64_t)g.Td * rb + cof;
+  for (int r0 = 0; r0 < g.Td; r0 += kIbxDdWaves * kRG) {
+    const int r = r0 + w * kRG + gq;
+    const bool rv = r < g.Td;
+    const uint32_t a = rv ? rs[r] : 0u;
+    const uint32_t n = rv ? rs[r + 1] - a : 0u;
+    const uint32_t nmax = wave_max_u32(n);
+    float acc[E::kV];
+#pragma unroll
+    for (int e = 0; e < E::kV; ++e) acc[e] = 0.0f;
+    for (uint32_t k = 0; k < nmax; k += kHC) {
+      const uint32_t idx = k + (uint32_t)c;
+      const uint32_t qr = idx < n ? (uint32_t)list[a + idx] : sent;
+      const int dlane = __float_as_int(dl[ibx_div(qr, g.mq)]);
+      const int olane = (int)(qr * (uint32_t)rb);
+      static_for<0, kHC / kB>([&](auto bc) {
+        uint4 raw[kB];
+        float d[kB];
+        static_for<0, kB>([&](auto ec) {
+          constexpr int e = decltype(ec)::value;
+          constexpr int pat = kSw | ((decltype(bc)::value * kB + e) << 5);
+          d[e] = __int_as_float(__builtin_amdgcn_ds_swizzle(dlane, pat));
+          const uint32_t off = (uint32_t)__builtin_amdgcn_ds_swizzle(olane, pat) + cof;
+          const u32x4 v = buf_load16(rQ, (int)off);
+          raw[e] = make_uint4(v[0], v[1], v[2], v[3]);
+        });
+#pragma unroll
+        for (int e = 0; e < kB; ++e) E::fma_chunk(raw[e], d[e], acc);
+      });
+    }
+    if (rv) *reinterpret_cast<uint4*>(dj + (int64_t)r * rb) = E::pack(acc);
+  }
+}
+
+// dQ partial of document quarter qd = XCD index >> 1, feature half h: work item
+// (query i, token block tb) per wave; lane (gq, c) owns tokens tb * kTpi + 4 gq
+// .. + 3, chunk c of the half row.  Each step stages kS documents' half rows:
+// document e of the step as Td + 1 rows from LDS chunk e * (Td + 1) * kHC, row
+// u holding its row u (1-based) and row 0 zeros, which a token with no source
+// (entry 0) reads.
+template <class E, int kHC, int kS>
+__global__ void __launch_bounds__(kIbThreads) bwd_ib_dq_kernel(const uint32_t* ct, const float* dT,
+                                                              const char* D, IbxGeo g, int ntb,
+                                                              int64_t nitems, int64_t rb,
+                                                              float* part, int64_t nq_rows,
+                                                              int dim) {
+  constexpr int kG = 64 / kHC;
+  constexpr int kTpi = 4 * kG;
+  constexpr int kPer = kIbxStage / kIbThreads;  // copies per thread per step
+  constexpr int kOps = kPer + 2 * kS;           // loads a wave issues per step
+  __shared__ uint4 dbuf0[kIbxStage], dbuf1[kIbxStage], dbuf2[kIbxStage];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = uniform(tid >> 6);
+  const int xcd = blockIdx.x & 7, h = xcd & 1, qd = xcd >> 1;
+  const int64_t item = (int64_t)(blockIdx.x >> 3) * kIbItems + w;
+  const bool live = item < nitems;  // (a dead wave still copies and meets the barriers)
+  const int64_t i = live ? item / ntb : 0;
+  const int tb = live ? (int)(item - i * ntb) : 0;
+  const int gq = lane / kHC, c = lane - gq * kHC;
+  const int t0 = tb * kTpi + 4 * gq;
+  const bool tl = live && t0 < g.Tqp;
+  const int64_t ps = (g.Bd + kIbxQuarters - 1) / kIbxQuarters;
+  const int64_t ja = std::min<int64_t>(g.Bd, qd * ps);
+  const int64_t len = std::min<int64_t>(g.Bd, ja + ps) - ja;
+  const int64_t nsteps = (len + kS - 1) / kS;
+  // Workgroups of one quarter start at different documents, so the quarter
+  // is requested from HBM by many workgroups at once rather than in lockstep.
+  const int64_t rot = len > 0 ? ((int64_t)(blockIdx.x >> 3) * 2 * kS) % len : 0;
+  const int docch = (g.Td + 1) * kHC;
+  int ce[kPer];
+  uint32_t coff[kPer];
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int x = (k * kIbItems + w) * 64 + lane;
+    const int e = x / docch, rem = x - e * docch, u = rem / kHC;
+    ce[k] = (e < kS && u >= 1) ? e : -1;  // (-1: the copy reads out of range and writes 0)
+    coff[k] = (uint32_t)((u - 1) * rb + (h * kHC + rem % kHC) * 16);
+  }
+  const rsrc_t rD = make_rsrc_u(D, (uint32_t)(g.Bd * g.Td * rb));
+  const rsrc_t rC = make_rsrc_u(ct, (uint32_t)(g.Bd * g.ct_stride));
+  const rsrc_t rT = make_rsrc_u(dT, (uint32_t)(g.Bd * g.Bq * 4));
+  float acc[4][E::kV];
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int e = 0; e < E::kV; ++e) acc[q][e] = 0.0f;
+  // step position s -> document (s >= len: the last one; its delta is not used)
+  auto docj = [&](int64_t s) {
+    int64_t x = rot + std::min<int64_t>(s, len - 1);
+    if (x >= len) x -= len;
+    return ja + x;
+  };
+  auto fetch = [&](int64_t k, uint4* buf, uint32_t(&cv)[kS], float(&dv)[kS]) {
+    int64_t jj[kS];
+#pragma unroll
+    for (int e = 0; e < kS; ++e) jj[e] = docj(k * kS + e);
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) {
+      int64_t jq = jj[0];
+#pragma unroll
+      for (int e = 1; e < kS; ++e)
+        if (ce[q] == e) jq = jj[e];
+      const uint32_t voff = ce[q] >= 0 ? (uint32_t)(jq * g.Td * rb) + coff[q] : 0x80000000u;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rD, (lds_ptr_t)(buf + (q * kIbItems + w) * 64), 16,
+                                               (int)voff, 0, 0, 0);
+    }
+#pragma unroll
+    for (int e = 0; e < kS; ++e) {
+      cv[e] = buf_load4(rC, tl ? (int)(jj[e] * g.ct_stride + i * g.Tqp + t0) : (int)0x80000000);
+      dv[e] = __uint_as_float(buf_load4(rT, (int)((jj[e] * g.Bq + i) * 4)));
+    }
+  };
+  // Entries are 0 or 1..Td (the compaction's output), entry 0 reading the zero
+  // row; a non-finite delta (0 * it is not 0) leaves entry 0 out instead.  (The
+  // branch on a zero delta also keeps each document's reads and multiply-adds
+  // in a block of their own: without it the scheduler interleaves the steps
+  // past the register budget.)
+  auto gather = [&](const uint4* rd, const uint32_t(&cv)[kS], const float(&dv)[kS], int64_t k) {
+    const uint32_t lb = lds_addr(rd) + (uint32_t)c * 16u;
+#pragma unroll
+    for (int e = 0; e < kS; ++e) {
+      const float de = (live && k * kS + e < len) ? uniform_f(dv[e]) : 0.0f;
+      if (de == 0.0f) continue;
+      const bool fin = __builtin_isfinite(de);
+      uint32_t addr[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        addr[q] = lb + (uint32_t)(e * docch) * 16u + ((cv[e] >> (8 * q)) & 255u) * (kHC * 16u);
+      uint4 raw[4];
+      lds_read4(raw, addr);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const bool src = fin || ((cv[e] >> (8 * q)) & 255u) != 0u;
+        E::fma_chunk(raw[q], src ? de : 0.0f, acc[q]);
+      }
+    }
+  };
+  uint32_t c0v[kS], c1v[kS], c2v[kS];
+  float d0v[kS], d1v[kS], d2v[kS];
+  if (len > 0) {
+    fetch(0, dbuf0, c0v, d0v);
+    fetch(std::min<int64_t>(1, nsteps - 1), dbuf1, c1v, d1v);
+  }
+  dma_wait_barrier<kOps>();  // step 0 ready
+  // step k: gather from `rd`; fetch step k + 2 into `wr` (read at step k - 1).
+  // Straight-line body (the last round pads with empty steps), so the
+  // compiler's own load counting stays exact across the back edge.
+  auto step = [&](int64_t k, const uint4* rd, uint4* wr, const uint32_t(&cc)[kS],
+                  const float(&dc)[kS], uint32_t(&cn)[kS], float(&dn)[kS]) {
+    fetch(std::min(k + 2, nsteps - 1), wr, cn, dn);
+    gather(rd, cc, dc, k);
+    dma_wait_barrier<kOps>();  // k + 1 ready; k + 2 may stay in flight
+  };
+  for (int64_t k = 0; k < nsteps; k += 3) {
+    step(k, dbuf0, dbuf2, c0v, d0v, c2v, d2v);
+    step(k + 1, dbuf1, dbuf0, c1v, d1v, c0v, d0v);
+    step(k + 2, dbuf2, dbuf1, c2v, d2v, c1v, d1v);
+  }
+  dma_wait_barrier<0>();  // no copy may land after the workgroup's LDS is released
+  if (!live) return;
+  float* pq = part + (int64_t)qd * nq_rows * dim + (int64_t)(h * kHC + c) * E::kV;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int t = t0 + q;
+    if (t >= g.Tq) continue;
+    float* dst = pq + (i * g.Tq + t) * dim;
+#pragma unroll
+    for (int e = 0; e < E::kV; e += 4)
+      *reinterpret_cast<float4*>(dst + e) = make_float4(acc[q][e], acc[q][e + 1], acc[q][e + 2], acc[q][e + 3]);
+  }
+}
+
 // ---- generic path (any row size) -----------------------------------------------------------
 
 // Sources of pair p: query tokens t < tq with qmask, a tape entry in 1..td,
@@ -1061,6 +1456,105 @@ void launch_dq_staged(const LayInBatch& lay, const PullbackArgs& a, const RowGeo
                        delta, a.args, a.rows, ntb, nsplit, nitems, geo, rb, a.dim, a.dQ, part, a.nq_rows);
 }
 
+// The feature-half in-batch path (16-bit features, half rows of 4, 8 or 16
+// chunks, Td <= 255 so a tape entry fits a byte, the document's sources
+// within the dD kernel's LDS, D within 31-bit buffer offsets): returns false
+// when the call does not fit it, else runs the whole pullback past delta and
+// sets *err.
+template <class E, class L>
+bool launch_ib_split(const L&, const PullbackArgs&, const float*, hipStream_t, hipError_t*) {
+  return false;
+}
+uint32_t ibx_magic(int d) {
+  return d <= 1 ? 0u : (uint32_t)(((uint64_t)1 << 32) / (uint64_t)d + (((uint64_t)1 << 32) % d != 0));
+}
+template <class E>
+bool launch_ib_split(const LayInBatch& lay, const PullbackArgs& a, const float* delta,
+                     hipStream_t st, hipError_t* err) {
+  if constexpr (E::kSz != 2) {
+    return false;
+  } else {
+    const int64_t rb = (int64_t)a.dim * 2;
+    const int hc = (int)(rb / 32);
+    if (rb % 32 != 0 || (hc != 4 && hc != 8 && hc != 16)) return false;
+    const int64_t Bd = lay.Bd;
+    if (Bd < 1 || a.npairs % Bd != 0) return false;
+    const int64_t Bq = a.npairs / Bd;
+    const int Tq = lay.Tq, Td = lay.Td, Tqp = (Tq + 3) & ~3;
+    if (Td < 1 || Td > 255 || Tq < 1 || a.rows != Tq || Bq > kIbxMaxBq || Bq * Tqp > kIbxMaxSrc)
+      return false;
+    if (lay.Q != a.Qbase || lay.D != a.Dbase || lay.qbytes != Tq * rb || lay.dbytes != Td * rb ||
+        a.nq_rows != Bq * Tq || a.nd_rows != Bd * Td)
+      return false;
+    const int64_t ct_stride = (Bq * Tqp + 15) & ~(int64_t)15;
+    if (Bd * Td * rb >= ((int64_t)1 << 31) || Bd * ct_stride >= ((int64_t)1 << 31)) return false;
+    const size_t dd_lds = (size_t)(kIbxDdWaves / 2 * 256 + 256) * 4 + (size_t)(Bq + 1) * 4 + (size_t)Bq * Tqp * 2;
+    if (dd_lds > (size_t)kIbxDdLdsMax) return false;
+    const int spare = kIbxStage / ((Td + 1) * hc);  // documents per dQ step
+    if (spare < 1) return false;
+    const int ks = spare >= 4 ? 4 : (spare >= 2 ? 2 : 1);
+
+    IbxGeo g;
+    g.Bd = Bd;
+    g.Bq = (int)Bq;
+    g.Tq = Tq;
+    g.Tqp = Tqp;
+    g.Td = Td;
+    g.ct_stride = ct_stride;
+    g.mq = ibx_magic(Tq);
+    g.mqp = ibx_magic(Tqp);
+    const size_t b_ct = al256((size_t)(Bd * ct_stride));
+    const size_t b_dt = al256((size_t)(Bd * Bq) * 4);
+    const size_t b_part = al256((size_t)(kIbxQuarters * a.nq_rows * a.dim) * 4);
+    void* ws = nullptr;
+    hipError_t e = workspace_alloc(&ws, b_ct + b_dt + b_part, st);
+    if (e != hipSuccess) {
+      *err = e;
+      return true;
+    }
+    char* w = static_cast<char*>(ws);
+    uint32_t* ct = reinterpret_cast<uint32_t*>(w);
+    float* dT = reinterpret_cast<float*>(w + b_ct);
+    float* part = reinterpret_cast<float*>(w + b_ct + b_dt);
+    const int vec4 = (Tq % 4 == 0) && (reinterpret_cast<uintptr_t>(a.args) & 15u) == 0;
+    const unsigned nsub = (unsigned)bcdiv(ct_stride / 4, kIbxCompactSpan);
+    hipLaunchKernelGGL(bwd_ib_compact_kernel, dim3((unsigned)Bd, nsub), dim3(kBwdThreads), 0, st,
+                       a.args, delta, lay.qm, g, vec4, ct, dT);
+    const unsigned dd_grid = (unsigned)(8 * bcdiv(Bd, 4));
+    const int64_t q_bytes = a.nq_rows * rb;
+    const int tpi = 256 / hc;
+    const int ntb = (int)bcdiv(Tq, tpi);
+    const int64_t nitems = Bq * ntb;
+    const unsigned dq_grid = (unsigned)(8 * bcdiv(nitems, kIbItems));
+    auto dq = [&](auto hck) {
+      constexpr int kHC = decltype(hck)::value;
+      hipLaunchKernelGGL((bwd_ib_dd_kernel<E, kHC>), dim3(dd_grid), dim3(kIbxDdThreads), dd_lds, st, ct,
+                         dT, g, rb, a.Qbase, q_bytes, a.dD);
+      if (ks == 4)
+        hipLaunchKernelGGL((bwd_ib_dq_kernel<E, kHC, 4>), dim3(dq_grid), dim3(kIbThreads), 0, st, ct, dT,
+                           a.Dbase, g, ntb, nitems, rb, part, a.nq_rows, a.dim);
+      else if (ks == 2)
+        hipLaunchKernelGGL((bwd_ib_dq_kernel<E, kHC, 2>), dim3(dq_grid), dim3(kIbThreads), 0, st, ct, dT,
+                           a.Dbase, g, ntb, nitems, rb, part, a.nq_rows, a.dim);
+      else
+        hipLaunchKernelGGL((bwd_ib_dq_kernel<E, kHC, 1>), dim3(dq_grid), dim3(kIbThreads), 0, st, ct, dT,
+                           a.Dbase, g, ntb, nitems, rb, part, a.nq_rows, a.dim);
+    };
+    if (hc == 4) dq(std::integral_constant<int, 4>());
+    else if (hc == 8) dq(std::integral_constant<int, 8>());
+    else dq(std::integral_constant<int, 16>());
+    const int64_t nchunks = a.nq_rows * rb / 16;
+    const unsigned blocks =
+        (unsigned)std::min<int64_t>(65536, std::max<int64_t>(1, bcdiv(nchunks, kBwdThreads)));
+    hipLaunchKernelGGL(bwd_dq_reduce_kernel<E>, dim3(blocks), dim3(kBwdThreads), 0, st, part,
+                       kIbxQuarters, nchunks, a.nq_rows * a.dim, a.dQ);
+    e = hipGetLastError();
+    const hipError_t ef = workspace_free(ws, st);
+    *err = e != hipSuccess ? e : ef;
+    return true;
+  }
+}
+
 // Vector-path geometry for rows of rb bytes, or false.
 bool vec_geometry(int64_t rb, int esz, RowGeo* g) {
   if (rb % 16 != 0) return false;
@@ -1084,6 +1578,8 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 template <class L, class E>
 hipError_t launch_vec(const L& lay, const PullbackArgs& a, const RowGeo& geo, const float* delta,
                       hipStream_t st) {
+  hipError_t eib = hipSuccess;
+  if (launch_ib_split<E>(lay, a, delta, st, &eib)) return eib;
   const int64_t rb = (int64_t)a.dim * E::kSz;
   const int64_t ngroups = a.npairs / a.G;
   const int ntb = (int)bcdiv(a.rows, geo.tpw);

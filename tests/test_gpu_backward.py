@@ -172,6 +172,45 @@ def test_inbatch_pullback_parity(device, dtype, shape):
     assert torch.equal(gQ.cpu(), dQ.cpu())
 
 
+# (dim, Tq, Td, Bq, Bd) for the in-batch feature-half path (16-bit features, Td <= 255):
+# half rows of 4, 8 and 16 chunks (dim 64, 128, 256); 4, 2 and 1 documents per dQ
+# step; Tq not a multiple of 4 (the byte tape from single-entry loads); Tq over one
+# token block (32 tokens at dim 128, 16 at dim 256); Td = 255, the largest entry a
+# byte holds; ragged and empty document quarters (Bd = 13, 3, 2); the C3 shape.
+HALF = [(128, 32, 180, 24, 13), (64, 7, 255, 9, 6), (256, 16, 90, 10, 5),
+        (256, 20, 180, 6, 3), (128, 40, 33, 12, 2), (128, 32, 180, 512, 512)]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("shape", HALF, ids=lambda s: "x".join(map(str, s)))
+def test_inbatch_pullback_feature_halves(device, dtype, shape):
+    """A random tape (with junk entries), a query mask and some zero cotangents."""
+    dim, Tq, Td, Bq, Bd = shape
+    rng = np.random.default_rng([11, dim, Tq, Td, Bq, Bd])
+    Qt, Qo, bf = as_feature(tokens(rng, (Bq, Tq, dim)), dtype)
+    Dt, Do, _ = as_feature(tokens(rng, (Bd, Td, dim)), dtype)
+    qm = rng.random((Bq, Tq)) < 0.85
+    args = _junk(rng, rng.integers(0, Td + 1, size=(Bq, Bd, Tq)).astype(np.int32), Td)
+    Dl_t, Dl = _vals(rng, (Bq, Bd), dtype, device)
+    zero = rng.random((Bq, Bd)) < 0.05
+    Dl[zero] = 0.0
+    Dl_t[torch.from_numpy(zero).to(device)] = 0.0
+    iv_t, iv = _vals(rng, (Bq,), dtype, device, positive=True)
+    want = oracle.inbatch_backward(Qo, Do, args, Dl, iv, qm, bf16=bf)
+    mag = oracle.inbatch_backward(_abs(Qo, bf), _abs(Do, bf), args, np.abs(Dl), iv, qm, bf16=bf)
+    Q, D = Qt.to(device), Dt.to(device)
+    qmt = torch.from_numpy(qm).to(device)
+    dQ, dD = _nan_like(Q.shape, dtype, device), _nan_like(D.shape, dtype, device)
+    at = torch.from_numpy(args).to(device)
+    boundary.inbatch_apply_pullback(dQ, dD, Q, D, qmt, at, Dl_t, iv_t)
+    torch.cuda.synchronize()
+    assert_grad(dQ, want[0], mag[0], dtype, "dQ")
+    assert_grad(dD, want[1], mag[1], dtype, "dD")
+    gQ, _ = bw.inbatch_pullback(Dl_t, Q, D, qmt, at, iv_t)
+    torch.cuda.synchronize()
+    assert torch.equal(gQ.cpu(), dQ.cpu())
+
+
 # ---- candidates -----------------------------------------------------------------------------
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: DT_ID[d])

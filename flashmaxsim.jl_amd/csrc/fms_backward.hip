@@ -884,19 +884,31 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
-// Workgroup (j, y) covers dwords y * kIbxCompactSpan .. + kIbxCompactSpan - 1 of
+// Workgroup (x, y) covers dwords y * kIbxCompactSpan .. + kIbxCompactSpan - 1 of
 // document j's bytes; dword k holds tokens 4 * (k % (Tqp / 4)) .. + 3 of query
-// k / (Tqp / 4).  Each thread loads its kIbxCompactPer dwords' tape entries
-// before it combines any.  vec4: the tape rows start 16-byte aligned (Tq a
-// multiple of 4, aligned buffer).
+// k / (Tqp / 4).  delta_p = Delta[p] * inv_n[i] in fp32, as bwd_delta computes
+// it.  Documents 512 m + 64 x' .. + 63 go to XCD x' (workgroup index x mod 8),
+// so the 64 documents whose cotangents share a 128-byte line of Delta meet in
+// one L2.  Each thread loads its kIbxCompactPer dwords' tape entries before it
+// combines any.  vec4: the tape rows start 16-byte aligned (Tq a multiple of
+// 4, aligned buffer).
 constexpr int kIbxCompactPer = 4;
 constexpr int kIbxCompactSpan = kIbxCompactPer * kBwdThreads;
+constexpr int kIbxCompactGroup = 64;  // documents per XCD in a row of 8 * 64
+template <class E>
 __global__ void __launch_bounds__(kBwdThreads) bwd_ib_compact_kernel(const int32_t* args,
-                                                                     const float* delta,
+                                                                     const char* Delta,
+                                                                     const char* inv_n,
                                                                      const uint8_t* qm, IbxGeo g,
                                                                      int vec4, uint32_t* ct,
                                                                      float* dT) {
-  const int64_t j = blockIdx.x;
+  const int64_t n = blockIdx.x >> 3;
+  const int64_t j = (n / kIbxCompactGroup) * (8 * kIbxCompactGroup) +
+                    (int64_t)(blockIdx.x & 7) * kIbxCompactGroup + n % kIbxCompactGroup;
+  if (j >= g.Bd) return;
+  auto delta = [&](int64_t p, int i) {
+    return E::ld(Delta + p * E::kSz) * (inv_n ? E::ld(inv_n + (int64_t)i * E::kSz) : 1.0f);
+  };
   const int tq4 = g.Tqp >> 2;
   const int nk = (int)(g.ct_stride >> 2), nv = g.Bq * tq4;
   uint32_t* out = ct + j * nk;
@@ -911,7 +923,7 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_ib_compact_kernel(const int32
     iq[q] = i;
     tq[q] = t0;
     const int64_t p = j + g.Bd * i;
-    dl[q] = in ? delta[p] : 0.0f;
+    dl[q] = in ? delta(p, i) : 0.0f;
     const int32_t* a = args + p * g.Tq;
     if (in && vec4) {
       const int4 v = *reinterpret_cast<const int4*>(a + t0);
@@ -938,10 +950,10 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_ib_compact_kernel(const int32
     if (k < nk) out[k] = word;
   }
   if (blockIdx.y == 0)
-    for (int i = threadIdx.x; i < g.Bq; i += kBwdThreads) dT[j * g.Bq + i] = delta[j + g.Bd * i];
+    for (int i = threadIdx.x; i < g.Bq; i += kBwdThreads) dT[j * g.Bq + i] = delta(j + g.Bd * i, i);
 }
 
-// dD rows of document j, feature half h.  Dynamic LDS: counters [256][waves / 2]
+// dD rows of document j, feature half h.  Dynamic LDS: counters [waves / 2][256]
 // (two 16-bit counters a word, waves 2v and 2v + 1: no count or cursor passes
 // Bq * Tqp <= 32768), row starts [256], delta [Bq + 1] (the last 0), list
 // [Bq * Tqp] (uint16 query rows).  kHC: 16-byte chunks per half row; kHC lanes
@@ -960,7 +972,7 @@ __global__ void __launch_bounds__(kIbxDdThreads)
                                                                  int64_t rb, const char* Q,
                                                                  int64_t q_bytes, char* dD) {
   constexpr int kRG = 64 / kHC;
-  constexpr int kCw = kIbxDdWaves / 2;        // counter words per row
+  constexpr int kCw = kIbxDdWaves / 2;        // counter sets (one per wave pair)
   constexpr int kB = kHC < 8 ? kHC : 8;       // query half-rows in flight per row group
   constexpr int kSw = 0x1F & ~(kHC - 1);      // ds_swizzle and-mask: the group's first lane
   extern __shared__ uint32_t ibx_smem[];
@@ -985,7 +997,7 @@ __global__ void __launch_bounds__(kIbxDdThreads)
   const float* dtj = dT + j * g.Bq;
   for (int x = tid; x <= g.Bq; x += kIbxDdThreads) dl[x] = x < g.Bq ? dtj[x] : 0.0f;
   __syncthreads();
-  uint32_t* cw = cnt + (w >> 1);
+  uint32_t* cw = cnt + (w >> 1) * 256;
   const int csh = 16 * (w & 1);
   // fn(u, f) for every source of this thread: row u (1-based), key byte f of the document
   auto each = [&](auto fn) {
@@ -1003,7 +1015,7 @@ __global__ void __launch_bounds__(kIbxDdThreads)
         }
     }
   };
-  each([&](uint32_t u, uint32_t) { atomicAdd(&cw[u * kCw], 1u << csh); });
+  each([&](uint32_t u, uint32_t) { atomicAdd(&cw[u], 1u << csh); });
   __syncthreads();
   // Row r = u - 1 starts at rs[r]; wave v's sources of row r fill from
   // rs[r] + (those of waves < v), its counter becoming that cursor.
@@ -1012,7 +1024,7 @@ __global__ void __launch_bounds__(kIbxDdThreads)
   if (tid < 256) {
 #pragma unroll
     for (int v = 0; v < kIbxDdWaves; ++v)
-      cv[v] = tid < g.Td ? (cnt[(tid + 1) * kCw + (v >> 1)] >> (16 * (v & 1))) & 0xFFFFu : 0u;
+      cv[v] = tid < g.Td ? (cnt[(v >> 1) * 256 + tid + 1] >> (16 * (v & 1))) & 0xFFFFu : 0u;
 #pragma unroll
     for (int v = 0; v < kIbxDdWaves; ++v) tot += cv[v];
     x = tot;
@@ -1031,7 +1043,7 @@ __global__ void __launch_bounds__(kIbxDdThreads)
 #pragma unroll
     for (int v = 0; v < kIbxDdWaves; v += 2) {
       const uint32_t lo = run, hi = run + cv[v];
-      cnt[(tid + 1) * kCw + (v >> 1)] = lo | (hi << 16);
+      cnt[(v >> 1) * 256 + tid + 1] = lo | (hi << 16);
       run = hi + cv[v + 1];
     }
     if (tid == g.Td - 1) rs[g.Td] = run;
@@ -1040,7 +1052,7 @@ __global__ void __launch_bounds__(kIbxDdThreads)
   each([&](uint32_t u, uint32_t f) {
     const uint32_t i = ibx_div(f, g.mqp);
     const uint32_t qr = i * (uint32_t)g.Tq + (f - i * (uint32_t)g.Tqp);
-    const uint32_t old = atomicAdd(&cw[u * kCw], 1u << csh);
+    const uint32_t old = atomicAdd(&cw[u], 1u << csh);
     list[(old >> csh) & 0xFFFFu] = (uint16_t)qr;
   });
   __syncthreads();
@@ -1145,24 +1157,33 @@ __global__ void __launch_bounds__(kIbThreads) bwd_ib_dq_kernel(const uint32_t* c
     if (x >= len) x -= len;
     return ja + x;
   };
+  // Per-lane parts of the tape and delta offsets (a lane past its query's
+  // tokens: out of range, the load returns 0); the document parts are uniform.
+  const uint32_t ctl = tl ? (uint32_t)(i * g.Tqp + t0) : 0x80000000u;
+  const uint32_t dtl = (uint32_t)(i * 4);
   auto fetch = [&](int64_t k, uint4* buf, uint32_t(&cv)[kS], float(&dv)[kS]) {
-    int64_t jj[kS];
+    uint32_t dbe[kS], cte[kS], dte[kS];
 #pragma unroll
-    for (int e = 0; e < kS; ++e) jj[e] = docj(k * kS + e);
+    for (int e = 0; e < kS; ++e) {
+      const int64_t jj = docj(k * kS + e);
+      dbe[e] = (uint32_t)(jj * g.Td * rb);
+      cte[e] = (uint32_t)(jj * g.ct_stride);
+      dte[e] = (uint32_t)(jj * g.Bq * 4);
+    }
 #pragma unroll
     for (int q = 0; q < kPer; ++q) {
-      int64_t jq = jj[0];
+      uint32_t b = dbe[0];
 #pragma unroll
       for (int e = 1; e < kS; ++e)
-        if (ce[q] == e) jq = jj[e];
-      const uint32_t voff = ce[q] >= 0 ? (uint32_t)(jq * g.Td * rb) + coff[q] : 0x80000000u;
+        if (ce[q] == e) b = dbe[e];
+      const uint32_t voff = ce[q] >= 0 ? b + coff[q] : 0x80000000u;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rD, (lds_ptr_t)(buf + (q * kIbItems + w) * 64), 16,
                                                (int)voff, 0, 0, 0);
     }
 #pragma unroll
     for (int e = 0; e < kS; ++e) {
-      cv[e] = buf_load4(rC, tl ? (int)(jj[e] * g.ct_stride + i * g.Tqp + t0) : (int)0x80000000);
-      dv[e] = __uint_as_float(buf_load4(rT, (int)((jj[e] * g.Bq + i) * 4)));
+      cv[e] = buf_load4(rC, (int)(cte[e] + ctl));
+      dv[e] = __uint_as_float(buf_load4(rT, (int)(dte[e] + dtl)));
     }
   };
   // Entries are 0 or 1..Td (the compaction's output), entry 0 reading the zero
@@ -1183,10 +1204,16 @@ __global__ void __launch_bounds__(kIbThreads) bwd_ib_dq_kernel(const uint32_t* c
         addr[q] = lb + (uint32_t)(e * docch) * 16u + ((cv[e] >> (8 * q)) & 255u) * (kHC * 16u);
       uint4 raw[4];
       lds_read4(raw, addr);
+      // One path for every delta (an if / else here copies all 32 accumulators
+      // at the join): the zero row times 0 for a non-finite delta, then that
+      // delta on the tokens with a source.
+      const float dm = fin ? de : 0.0f;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const bool src = fin || ((cv[e] >> (8 * q)) & 255u) != 0u;
-        E::fma_chunk(raw[q], src ? de : 0.0f, acc[q]);
+      for (int q = 0; q < 4; ++q) E::fma_chunk(raw[q], dm, acc[q]);
+      if (!fin) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (((cv[e] >> (8 * q)) & 255u) != 0u) E::fma_chunk(raw[q], de, acc[q]);
       }
     }
   };
@@ -1459,18 +1486,17 @@ void launch_dq_staged(const LayInBatch& lay, const PullbackArgs& a, const RowGeo
 // The feature-half in-batch path (16-bit features, half rows of 4, 8 or 16
 // chunks, Td <= 255 so a tape entry fits a byte, the document's sources
 // within the dD kernel's LDS, D within 31-bit buffer offsets): returns false
-// when the call does not fit it, else runs the whole pullback past delta and
-// sets *err.
+// when the call does not fit it, else runs the whole pullback and sets *err.
 template <class E, class L>
-bool launch_ib_split(const L&, const PullbackArgs&, const float*, hipStream_t, hipError_t*) {
+bool launch_ib_split(const L&, const PullbackArgs&, hipStream_t, hipError_t*) {
   return false;
 }
 uint32_t ibx_magic(int d) {
   return d <= 1 ? 0u : (uint32_t)(((uint64_t)1 << 32) / (uint64_t)d + (((uint64_t)1 << 32) % d != 0));
 }
 template <class E>
-bool launch_ib_split(const LayInBatch& lay, const PullbackArgs& a, const float* delta,
-                     hipStream_t st, hipError_t* err) {
+bool launch_ib_split(const LayInBatch& lay, const PullbackArgs& a, hipStream_t st,
+                     hipError_t* err) {
   if constexpr (E::kSz != 2) {
     return false;
   } else {
@@ -1492,7 +1518,8 @@ bool launch_ib_split(const LayInBatch& lay, const PullbackArgs& a, const float* 
     if (dd_lds > (size_t)kIbxDdLdsMax) return false;
     const int spare = kIbxStage / ((Td + 1) * hc);  // documents per dQ step
     if (spare < 1) return false;
-    const int ks = spare >= 4 ? 4 : (spare >= 2 ? 2 : 1);
+    // (bf16 widening takes more registers: 4 documents a step would spill)
+    const int ks = (spare >= 4 && E::kSz == 2 && std::is_same<E, EF16>::value) ? 4 : (spare >= 2 ? 2 : 1);
 
     IbxGeo g;
     g.Bd = Bd;
@@ -1518,8 +1545,10 @@ bool launch_ib_split(const LayInBatch& lay, const PullbackArgs& a, const float* 
     float* part = reinterpret_cast<float*>(w + b_ct + b_dt);
     const int vec4 = (Tq % 4 == 0) && (reinterpret_cast<uintptr_t>(a.args) & 15u) == 0;
     const unsigned nsub = (unsigned)bcdiv(ct_stride / 4, kIbxCompactSpan);
-    hipLaunchKernelGGL(bwd_ib_compact_kernel, dim3((unsigned)Bd, nsub), dim3(kBwdThreads), 0, st,
-                       a.args, delta, lay.qm, g, vec4, ct, dT);
+    const unsigned cgrid = (unsigned)(bcdiv(Bd, 8 * kIbxCompactGroup) * 8 * kIbxCompactGroup);
+    hipLaunchKernelGGL(bwd_ib_compact_kernel<E>, dim3(cgrid, nsub), dim3(kBwdThreads), 0, st, a.args,
+                       static_cast<const char*>(a.Delta), static_cast<const char*>(a.inv_n), lay.qm,
+                       g, vec4, ct, dT);
     const unsigned dd_grid = (unsigned)(8 * bcdiv(Bd, 4));
     const int64_t q_bytes = a.nq_rows * rb;
     const int tpi = 256 / hc;
@@ -1578,8 +1607,6 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 template <class L, class E>
 hipError_t launch_vec(const L& lay, const PullbackArgs& a, const RowGeo& geo, const float* delta,
                       hipStream_t st) {
-  hipError_t eib = hipSuccess;
-  if (launch_ib_split<E>(lay, a, delta, st, &eib)) return eib;
   const int64_t rb = (int64_t)a.dim * E::kSz;
   const int64_t ngroups = a.npairs / a.G;
   const int ntb = (int)bcdiv(a.rows, geo.tpw);
@@ -1713,6 +1740,13 @@ hipError_t launch_pullback(const L& lay, const PullbackArgs& a, hipStream_t st) 
     clear(a.dQ, a.nq_rows);
     clear(a.dD, a.nd_rows);
     return hipGetLastError();
+  }
+  if (!a.zero_dq && aligned16(a.dQ) && aligned16(a.dD) && aligned16(a.Qbase) && aligned16(a.Dbase)) {
+    hipError_t eib = hipSuccess;
+    const bool took = a.dtype == 1   ? launch_ib_split<EF16>(lay, a, st, &eib)
+                      : a.dtype == 2 ? launch_ib_split<EBF16>(lay, a, st, &eib)
+                                     : false;
+    if (took) return eib;
   }
   void* ws = nullptr;
   hipError_t e = workspace_alloc(&ws, al256((size_t)a.npairs * 4), st);

@@ -211,6 +211,43 @@ def test_inbatch_pullback_feature_halves(device, dtype, shape):
     assert torch.equal(gQ.cpu(), dQ.cpu())
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("shape", [(128, 32, 64, 8, 12), (128, 40, 33, 12, 2)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_inbatch_pullback_nonfinite_cotangent(device, dtype, shape):
+    """NaN and +-inf cotangents reach exactly the rows their sources reach (a token
+    with no source stays finite, src/backward_pair.jl:21-29); the rest within tolerance."""
+    dim, Tq, Td, Bq, Bd = shape
+    rng = np.random.default_rng([13, dim, Tq, Td, Bq, Bd])
+    Qt, Qo, bf = as_feature(tokens(rng, (Bq, Tq, dim)), dtype)
+    Dt, Do, _ = as_feature(tokens(rng, (Bd, Td, dim)), dtype)
+    qm = rng.random((Bq, Tq)) < 0.85
+    args = rng.integers(0, Td + 1, size=(Bq, Bd, Tq)).astype(np.int32)
+    args[1, 0, :Tq // 2] = 0  # a pair whose tokens partly have no source
+    Dl_t, Dl = _vals(rng, (Bq, Bd), dtype, device)
+    for (i, j), v in zip([(1, 0), (3, Bd - 1), (Bq - 1, 1)], [np.nan, np.inf, -np.inf]):
+        Dl[i, j] = v
+        Dl_t[i, j] = float(v)
+    iv_t, iv = _vals(rng, (Bq,), dtype, device, positive=True)
+    want = oracle.inbatch_backward(Qo, Do, args, Dl, iv, qm, bf16=bf)
+    fin = np.where(np.isfinite(Dl), np.abs(Dl), 0.0)
+    mag = oracle.inbatch_backward(_abs(Qo, bf), _abs(Do, bf), args, fin, iv, qm, bf16=bf)
+    Q, D = Qt.to(device), Dt.to(device)
+    qmt = torch.from_numpy(qm).to(device)
+    dQ, dD = _nan_like(Q.shape, dtype, device), _nan_like(D.shape, dtype, device)
+    boundary.inbatch_apply_pullback(dQ, dD, Q, D, qmt, torch.from_numpy(args).to(device), Dl_t, iv_t)
+    torch.cuda.synchronize()
+    for got, w, m, what in ((dQ, want[0], mag[0], "dQ"), (dD, want[1], mag[1], "dD")):
+        g = got.float().cpu().numpy().astype(np.float64)
+        for cls in (np.isnan, np.isposinf, np.isneginf):
+            assert np.array_equal(cls(g), cls(w)), (what, cls.__name__, int(cls(g).sum()), int(cls(w).sum()))
+        ok = np.isfinite(w)
+        assert ok.sum() > 0 and (~ok).sum() > 0
+        err = np.abs(g[ok] - w[ok])
+        tol = ROUND[dtype] * np.abs(w[ok]) + 1e-5 * m[ok] + FLOOR[dtype]
+        assert (err <= tol).all(), (what, float((err - tol).max()))
+
+
 # ---- candidates -----------------------------------------------------------------------------
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: DT_ID[d])

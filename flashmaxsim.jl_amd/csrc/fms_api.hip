@@ -460,6 +460,7 @@ fms_status fms_inbatch_device_scan(int32_t dtype, float* S, int32_t* args, const
     a.Bd = (int)Bd;
     a.Tq = (int)Tq;
     a.Td = (int)Td;
+    a.dim = (int)dim;
     a.norm = normalize;
     return from_hip(launch_inbatch_mfma(dtype == FMS_BF16, a, as_stream(stream)));
   }
@@ -530,6 +531,7 @@ fms_status fms_launch_packed_multi_scan(int32_t dtype, int32_t* args, float* sco
     a.Bd = (int)B;
     a.Tq = (int)Tq;
     a.Td = (int)max_len;
+    a.dim = (int)dim;
     a.norm = normalize;
     return from_hip(launch_inbatch_mfma(dtype == FMS_BF16, a, st));
   }

@@ -69,10 +69,7 @@ constexpr int kIbWaves = 8;
 constexpr int kIbQpw = 4;                          // query tiles per wave
 static_assert(kIbQpw == 4, "the step is written for two phases of two query tiles");
 constexpr int kIbQueries = kIbWaves * kIbQpw;      // queries per block
-constexpr int kIbNkb = 8;                          // dim == 128
-constexpr int kIbRowBytes = kIbNkb * 32;           // 256 B per token
-constexpr int kIbFrags = kIbNkb * 64;              // 16-byte fragments per chunk (8 KB)
-constexpr int kIbKbPerWave = kIbNkb / kIbWaves;    // k-blocks each wave moves into LDS
+constexpr int kIbMaxNkb = 8;                       // k-blocks of 16 features: dim <= 128
 constexpr int kIbBufs = 3;                         // LDS chunk buffers (kIbBufs - 1 chunks in flight)
 static_assert(kIbBufs == 3 || kIbBufs == 4, "the step loop rotates 3 or 4 buffers");
 constexpr int kXcds = 8;
@@ -132,11 +129,12 @@ __device__ __forceinline__ bool frag_nonfinite(const u32x4& w) {
 }
 
 
-// Whether the 256-byte feature row at `row` (16-bit elements, bf16 or fp16)
-// holds an Inf or NaN: one dword per lane, wave ballot.  Uniform result.
-__device__ __forceinline__ bool row_nonfinite(const char* row, int bf16) {
+// Whether the feature row of rb <= 256 bytes at `row` (16-bit elements, bf16
+// or fp16) holds an Inf or NaN: one dword per lane, wave ballot.  Uniform
+// result.
+__device__ __forceinline__ bool row_nonfinite(const char* row, int bf16, int rb) {
   const int lane = threadIdx.x & 63;
-  const uint32_t w = *reinterpret_cast<const uint32_t*>(row + lane * 4);
+  const uint32_t w = lane * 4 < rb ? *reinterpret_cast<const uint32_t*>(row + lane * 4) : 0u;
   const uint32_t e = bf16 ? 0x7f807f80u : 0x7c007c00u;
   const bool nf = ((w & (e & 0xffffu)) == (e & 0xffffu)) | ((w & (e & 0xffff0000u)) == (e & 0xffff0000u));
   return __ballot(nf) != 0ull;
@@ -148,7 +146,7 @@ __device__ __forceinline__ bool row_nonfinite(const char* row, int bf16) {
 // dcount[j] the chunks with a valid row, dfirst[j] the first valid token
 // (-1 = none) with kPlanNfBit set when that token's row is not finite.
 __global__ void __launch_bounds__(256) inbatch_plan_kernel(const uint8_t* dm, const char* D,
-                                                           int bf16, int Bd, int Td, int nch,
+                                                           int bf16, int rb, int Bd, int Td, int nch,
                                                            uint32_t* cmask, int32_t* dcount,
                                                            int32_t* dfirst) {
   const int lane = threadIdx.x & 63;
@@ -173,7 +171,7 @@ __global__ void __launch_bounds__(256) inbatch_plan_kernel(const uint8_t* dm, co
   if (nz != 0u) {
     const int k = __builtin_ctzll(nz);
     f = k * kTile + __builtin_ctz((uint32_t)__builtin_amdgcn_readlane((int)m, k));
-    if (row_nonfinite(D + ((int64_t)j * Td + f) * kIbRowBytes, bf16)) f |= 1 << kPlanNfBit;
+    if (row_nonfinite(D + ((int64_t)j * Td + f) * rb, bf16, rb)) f |= 1 << kPlanNfBit;
   }
   if (lane == 0) {
     dcount[j] = __builtin_popcountll(nz);
@@ -188,7 +186,7 @@ __global__ void __launch_bounds__(256) inbatch_plan_kernel(const uint8_t* dm, co
 // value kPlanTooLong, and the scan writes NaN scores for it rather than
 // scoring a truncated document.
 __global__ void __launch_bounds__(256) packed_plan_kernel(const int32_t* cu, const char* tokens,
-                                                          int bf16, int64_t ntok, int Bd, int Td,
+                                                          int bf16, int rb, int64_t ntok, int Bd, int Td,
                                                           int nch, uint32_t* cmask,
                                                           int32_t* dcount, int32_t* dfirst) {
   const int lane = threadIdx.x & 63;
@@ -202,7 +200,7 @@ __global__ void __launch_bounds__(256) packed_plan_kernel(const int32_t* cu, con
   const uint32_t m = rows >= kTile ? 0xffffffffu : (rows > 0 ? (1u << rows) - 1u : 0u);
   if (lane < nch) cmask[(int64_t)j * nch + lane] = m;
   int f = too_long ? kPlanTooLong : -1;
-  if (len > 0) f = row_nonfinite(tokens + a * kIbRowBytes, bf16) ? (1 << kPlanNfBit) : 0;
+  if (len > 0) f = row_nonfinite(tokens + a * rb, bf16, rb) ? (1 << kPlanNfBit) : 0;
   if (lane == 0) {
     dcount[j] = (len + kTile - 1) / kTile;
     dfirst[j] = f;
@@ -240,10 +238,19 @@ __device__ int block_exclusive_scan_i32(int v, int* total) {
 // is then one phase -- three MFMA chains over the chunk while the previous
 // chunk's three tiles fold -- and a document's close sums each query over
 // the lanes (and tiles) that hold its tokens.
-template <class Op, bool kPacked, bool kT24>
+// kNkb: k-blocks of 16 features per token (dim = 16 * kNkb, 2..8).  A chunk
+// is kNkb k-blocks of 1 KB; wave w copies k-block w mod kNkb of every chunk
+// (with fewer k-blocks than waves, two waves copy the same bytes to the same
+// place, so every wave issues the same loads per step).
+template <class Op, bool kPacked, bool kT24, int kNkb>
 __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(const InBatchArgs A) {
   typedef typename Op::Acc Acc;
   typedef typename Op::Frag Frag;
+  static_assert(kNkb >= 1 && kNkb <= kIbMaxNkb, "query tiles of dim <= 128 stay in registers");
+  constexpr int kIbNkb = kNkb;
+  constexpr int kIbRowBytes = kNkb * 32;                                // bytes per token row
+  constexpr int kIbFrags = kNkb * 64;                                   // 16-byte fragments per chunk
+  constexpr int kIbKbPerWave = (kNkb + kIbWaves - 1) / kIbWaves;        // copies per wave per chunk
   // Chunk buffers, in MFMA fragment order: fragment (kb, lane) at
   // [kb * 64 + lane].  Four separate arrays, so the compiler can tell which
   // buffer each load-to-LDS writes.
@@ -498,7 +505,7 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
     const int voff = ((kPacked ? row0 : jj * Td) + src) * kIbRowBytes + h * 16;
 #pragma unroll
     for (int k = 0; k < kIbKbPerWave; ++k) {
-      const int kb = kIbKbPerWave * wave + k;
+      const int kb = (kIbKbPerWave * wave + k) % kIbNkb;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rd, (lds_ptr_t)(buf + kb * 64), 16,
                                                voff + kb * 32, 0, 0, 0);
     }
@@ -895,41 +902,50 @@ hipError_t launch_inbatch_mfma(int dtype_bf16, const InBatchArgs& args_in, hipSt
   A.cmask = cmask;
   A.dcount = dcount;
   A.dfirst = dfirst;
+  const int rb = A.dim * 2;
   if (A.cu)
     hipLaunchKernelGGL(packed_plan_kernel, dim3((unsigned)((A.Bd + 3) / 4)), dim3(256), 0, stream,
-                       A.cu, A.D, dtype_bf16, A.ntok, A.Bd, A.Td, nch, cmask, dcount, dfirst);
+                       A.cu, A.D, dtype_bf16, rb, A.ntok, A.Bd, A.Td, nch, cmask, dcount, dfirst);
   else
     hipLaunchKernelGGL(inbatch_plan_kernel, dim3((unsigned)((A.Bd + 3) / 4)), dim3(256), 0, stream,
-                       A.dm, A.D, dtype_bf16, A.Bd, A.Td, nch, cmask, dcount, dfirst);
+                       A.dm, A.D, dtype_bf16, rb, A.Bd, A.Td, nch, cmask, dcount, dfirst);
   e = hipGetLastError();
   if (e == hipSuccess) {
     const dim3 grid((unsigned)(A.nqb * ((A.ndb + kXcds - 1) / kXcds) * kXcds)), block(64 * kIbWaves);
     // Tq == 24: four queries fill three tiles (kT24)
     auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, block, 0, stream, A); };
-    const bool t24 = A.Tq == 24;
-    if (A.cu) {
-      if (dtype_bf16)
-        t24 ? go(inbatch_mfma<OpBF16, true, true>) : go(inbatch_mfma<OpBF16, true, false>);
-      else
-        t24 ? go(inbatch_mfma<OpF16, true, true>) : go(inbatch_mfma<OpF16, true, false>);
-    } else {
-      if (dtype_bf16)
-        t24 ? go(inbatch_mfma<OpBF16, false, true>) : go(inbatch_mfma<OpBF16, false, false>);
-      else
-        t24 ? go(inbatch_mfma<OpF16, false, true>) : go(inbatch_mfma<OpF16, false, false>);
-    }
+    auto by_nkb = [&](auto op, auto packed, auto t24) {
+      typedef decltype(op) O;
+      constexpr bool P = decltype(packed)::value, T = decltype(t24)::value;
+      switch (A.dim / 16) {
+        case 2: go(inbatch_mfma<O, P, T, 2>); break;
+        case 4: go(inbatch_mfma<O, P, T, 4>); break;
+        case 6: go(inbatch_mfma<O, P, T, 6>); break;
+        default: go(inbatch_mfma<O, P, T, 8>); break;
+      }
+    };
+    auto by_t24 = [&](auto op, auto packed) {
+      if (A.Tq == 24) by_nkb(op, packed, std::true_type());
+      else by_nkb(op, packed, std::false_type());
+    };
+    auto by_packed = [&](auto op) {
+      if (A.cu) by_t24(op, std::true_type());
+      else by_t24(op, std::false_type());
+    };
+    if (dtype_bf16) by_packed(OpBF16());
+    else by_packed(OpF16());
     e = hipGetLastError();
   }
   const hipError_t ef = workspace_free(ws, stream);
   return e != hipSuccess ? e : ef;
 }
 
-// A block's documents span one buffer resource: ndoc * Td * 256 bytes <=
+// A block's documents span one buffer resource: ndoc * Td * dim * 2 bytes <=
 // kIbMaxChunkMasks * 32 * 256 = 4 MB.  Tape entries are staged as int16.
 bool inbatch_mfma_supported(int64_t dim, int64_t Tq, int64_t Td, const void* Q, const void* D) {
   const bool al = ((reinterpret_cast<uintptr_t>(Q) | reinterpret_cast<uintptr_t>(D)) & 15u) == 0;
-  return dim == kIbNkb * 16 && Tq >= 1 && Tq <= kTile && Td >= 0 &&
-         (Td + kTile - 1) / kTile <= kIbMaxChunks && al;
+  const bool dim_ok = dim == 32 || dim == 64 || dim == 96 || dim == 128;
+  return dim_ok && Tq >= 1 && Tq <= kTile && Td >= 0 && (Td + kTile - 1) / kTile <= kIbMaxChunks && al;
 }
 
 }  // namespace fms

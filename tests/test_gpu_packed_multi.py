@@ -5,7 +5,9 @@ of query i (the reference's ``maxsim(q, P)`` path) and the CPU oracle on the
 same inputs: fp16/bf16 scores within 2e-3 relative, fp32 within 1e-5; tapes
 equal except at near-ties within that tolerance.  Shapes: a query count that
 is not a multiple of the kernel's 32-query block, Lq = 24 with a random
-qmask, documents of length 0, 1, 31, 32, 33 and ColPali-like 700..1100.
+qmask, documents of length 0, 1, 31, 32, 33 and ColPali-like 700..1100, at
+dims 128, 96, 64 and 32 (the MFMA kernel's 8, 6, 4 and 2 k-blocks); dim 48 takes
+the per-query fallback.
 """
 import numpy as np
 import pytest
@@ -32,10 +34,12 @@ def _case(rng, dtype, dim, nq, Tq, lens, device):
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: DT_ID[d])
-@pytest.mark.parametrize("case", ["edges", "colpali"])
+@pytest.mark.parametrize("case", ["edges", "colpali", "edges_d64", "edges_d96", "colpali_d32"])
 def test_packed_multi_matches_single_and_oracle(device, dtype, case):
-    rng = np.random.default_rng({"edges": 61, "colpali": 62}[case])
-    dim = 128
+    rng = np.random.default_rng({"edges": 61, "colpali": 62, "edges_d64": 64, "edges_d96": 65,
+                                 "colpali_d32": 66}[case])
+    dim = {"edges_d64": 64, "edges_d96": 96, "colpali_d32": 32}.get(case, 128)
+    case = case.split("_")[0]
     if case == "edges":
         nq, Tq, lens = 40, 24, [5, 0, 1, 31, 32, 33, 64, 65, 0, 200, 17]
     else:
@@ -60,9 +64,9 @@ def test_packed_multi_matches_single_and_oracle(device, dtype, case):
 
 
 def test_packed_multi_fallback_shape_and_api(device):
-    """dim 64 (no MFMA path) makes one packed scan per query: bit-identical rows."""
+    """dim 48 (no MFMA path) makes one packed scan per query: bit-identical rows."""
     rng = np.random.default_rng(63)
-    Q, Qo, bf, P, to, cu, qm = _case(rng, torch.float16, 64, 5, 7, [3, 0, 9, 40], device)
+    Q, Qo, bf, P, to, cu, qm = _case(rng, torch.float16, 48, 5, 7, [3, 0, 9, 40], device)
     S, args = fm.packed_multi_forward(Q, P)
     for i in range(5):
         s1, a1 = fm.packed_forward(Q[i], P)

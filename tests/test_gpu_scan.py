@@ -156,7 +156,10 @@ def test_candidates_parity(device, dtype, shape, idx_dtype):
                                    (128, 32, 33, 20, 3), (128, 8, 40, 512, 1024),
                                    # long documents: a block's chunk stream holds the
                                    # full 512-entry list (padded past it)
-                                   (128, 32, 1000, 20, 40), (128, 16, 2048, 17, 9)],
+                                   (128, 32, 1000, 20, 40), (128, 16, 2048, 17, 9),
+                                   # dim 32, 64, 96: the same kernel with 2, 4, 6 k-blocks
+                                   (64, 32, 180, 40, 37), (96, 24, 65, 17, 9), (32, 16, 100, 33, 20),
+                                   (64, 8, 40, 300, 600), (96, 32, 1000, 20, 40)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_inbatch_parity(device, dtype, shape):
     dim, Tq, Td, Bq, Bd = shape
@@ -183,14 +186,14 @@ def test_inbatch_parity(device, dtype, shape):
                                    # Tq = 24: four queries packed into three tiles
                                    (24, 180, 24, 21), (24, 33, 9, 5), (24, 700, 37, 5)],
                          ids=lambda s: "x".join(map(str, s)))
-def test_inbatch_masks_and_ties(device, dtype, shape):
+@pytest.mark.parametrize("dim", [128, 64], ids=lambda d: f"d{d}")
+def test_inbatch_masks_and_ties(device, dtype, shape, dim):
     """Non-prefix document masks, leading masked tokens, fully masked and
     single-token documents, and exact duplicate tokens (exact ties must keep
     the first occurrence, forward_pair.jl:82-85) on the MFMA-tiled kernel,
     which substitutes masked rows by copies of the first valid token."""
     Tq, Td, Bq, Bd = shape
-    dim = 128
-    rng = np.random.default_rng(Tq * 1000 + Td)
+    rng = np.random.default_rng(Tq * 1000 + Td + dim)
     q32 = tokens(rng, (Bq, Tq, dim))
     d32 = tokens(rng, (Bd, Td, dim))
     dm = rng.random((Bd, Td)) < 0.7
@@ -233,15 +236,15 @@ def test_inbatch_masks_and_ties(device, dtype, shape):
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=lambda d: DT_ID[d])
 @pytest.mark.parametrize("shape", [(32, 180, 24, 21), (17, 65, 40, 33), (8, 300, 20, 17)],
                          ids=lambda s: "x".join(map(str, s)))
-def test_inbatch_negative_maxima(device, dtype, shape):
+@pytest.mark.parametrize("dim", [128, 96], ids=lambda d: f"d{d}")
+def test_inbatch_negative_maxima(device, dtype, shape, dim):
     """Every dot product negative (queries in the positive orthant, documents
     in the negative one), with exact duplicate tokens: every chunk maximum is
     below zero, which the MFMA-tiled kernel folds on its exact path; exact
     ties must still keep the first occurrence (forward_pair.jl:82-85) and
     the all-negative maxima stay negative (test_regressions.jl:136-147)."""
     Tq, Td, Bq, Bd = shape
-    dim = 128
-    rng = np.random.default_rng(Tq * 7 + Td)
+    rng = np.random.default_rng(Tq * 7 + Td + dim)
     q32 = np.abs(tokens(rng, (Bq, Tq, dim)))
     d32 = -np.abs(tokens(rng, (Bd, Td, dim)))
     q32 /= np.linalg.norm(q32, axis=-1, keepdims=True)

@@ -448,7 +448,7 @@ fms_status fms_inbatch_device_scan(int32_t dtype, float* S, int32_t* args, const
   if (Bq == 0 || Bd == 0) return FMS_OK;
   if (!S || (Tq * dim > 0 && !Q) || (Td * dim > 0 && !D)) return FMS_EINVAL;
   if ((dtype == FMS_F16 || dtype == FMS_BF16) && inbatch_mfma_supported(dim, Tq, Td, Q, D) &&
-      Bq <= kMaxTokens && Bd <= kMaxTokens) {
+      Bq * ((Tq + 31) / 32) <= kMaxTokens && Bd <= kMaxTokens) {
     InBatchArgs a;
     a.Q = static_cast<const char*>(Q);
     a.D = static_cast<const char*>(D);
@@ -517,7 +517,7 @@ fms_status fms_launch_packed_multi_scan(int32_t dtype, int32_t* args, float* sco
   if (!scores || !cu || (Tq * dim > 0 && !Q) || (ntokens * dim > 0 && !tokens)) return FMS_EINVAL;
   const hipStream_t st = as_stream(stream);
   if ((dtype == FMS_F16 || dtype == FMS_BF16) && inbatch_mfma_supported(dim, Tq, max_len, Q, tokens) &&
-      max_len >= 1 && ntokens <= kMaxTokens) {
+      max_len >= 1 && ntokens <= kMaxTokens && nq * ((Tq + 31) / 32) <= kMaxTokens) {
     InBatchArgs a;
     a.Q = static_cast<const char*>(Q);
     a.D = static_cast<const char*>(tokens);

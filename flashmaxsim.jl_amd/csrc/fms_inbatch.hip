@@ -70,6 +70,7 @@ constexpr int kIbQpw = 4;                          // query tiles per wave
 static_assert(kIbQpw == 4, "the step is written for two phases of two query tiles");
 constexpr int kIbQueries = kIbWaves * kIbQpw;      // queries per block
 constexpr int kIbMaxNkb = 8;                       // k-blocks of 16 features: dim <= 128
+constexpr int kIbMaxTq = 4096;                     // query tokens (tiles of 32 past 32)
 constexpr int kIbBufs = 3;                         // LDS chunk buffers (kIbBufs - 1 chunks in flight)
 static_assert(kIbBufs == 3 || kIbBufs == 4, "the step loop rotates 3 or 4 buffers");
 constexpr int kXcds = 8;
@@ -355,27 +356,33 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
   // ---- resident query tiles --------------------------------------------------
   // Query masks are loaded unconditionally (an empty resource when absent
   // reads 0) and tested only when a document closes.
+  // Query rows of the kernel: with A.ntq > 1 tiles per query (Tq > 32), row
+  // v is tokens 32 * (v % ntq) .. + 31 of query v / ntq (qrow, qt0, qtn: that
+  // query, first token and token count); else row v is query v.
   Frag qf[kIbQpw][kIbNkb];
   uint32_t qmb[kIbQpw];  // per query (kT24: per tile, this lane's token)
   bool qlive[kIbQpw];
-  int qi[kIbQpw];
+  int qi[kIbQpw], qrow[kIbQpw], qt0[kIbQpw], qtn[kIbQpw];
+  const int ntq = A.ntq, nqv = A.Bq * ntq;
 #pragma unroll
   for (int q = 0; q < kIbQpw; ++q) {
     qi[q] = qb * kIbQueries + wave * kIbQpw + q;
-    qlive[q] = qi[q] < A.Bq;
+    qlive[q] = qi[q] < nqv;
+    qrow[q] = qi[q] / ntq;
+    qt0[q] = (qi[q] - qrow[q] * ntq) * kTile;
+    qtn[q] = std::min(kTile, Tq - qt0[q]);
   }
   if constexpr (!kT24) {
 #pragma unroll
     for (int q = 0; q < kIbQpw; ++q) {
       const bool live = qlive[q];
-      const int iq = live ? qi[q] : 0;
-      const rsrc_t rq = make_rsrc(A.Q + (int64_t)iq * Tq * kIbRowBytes,
-                                  live ? (uint32_t)Tq * kIbRowBytes : 0u);
+      const int64_t tok0 = live ? (int64_t)qrow[q] * Tq + qt0[q] : 0;
+      const rsrc_t rq = make_rsrc(A.Q + tok0 * kIbRowBytes, live ? (uint32_t)qtn[q] * kIbRowBytes : 0u);
       const int base = r32 * kIbRowBytes + h * 16;
 #pragma unroll
       for (int kb = 0; kb < kIbNkb; ++kb) qf[q][kb] = Op::load(rq, base + kb * 32);
-      qmb[q] = buf_load1(make_rsrc(A.qm ? (const void*)(A.qm + (int64_t)iq * Tq) : (const void*)A.Q,
-                                   (A.qm && live) ? (uint32_t)Tq : 0u), r32);
+      qmb[q] = buf_load1(make_rsrc(A.qm ? (const void*)(A.qm + tok0) : (const void*)A.Q,
+                                   (A.qm && live) ? (uint32_t)qtn[q] : 0u), r32);
     }
   } else {
     // The wave's live queries are consecutive rows of Q: tile t, lane r32 holds
@@ -395,7 +402,7 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
   }
   const bool has_qm = A.qm != nullptr;
   auto token_valid = [&](int q) {
-    return qlive[q] && r32 < Tq && (!has_qm || qmb[q] != 0u);
+    return qlive[q] && r32 < qtn[q] && (!has_qm || qmb[q] != 0u);
   };
   // kT24: the query (0..3 in the wave) and token (0..23) of this lane in tile t,
   // and whether that token is valid.
@@ -821,20 +828,25 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
   __syncthreads();  // results of every wave staged
 
   // ---- write the block's tape and scores (coalesced) ------------------------------
-  // Query qi's tape for documents j0..j1-1 is one contiguous run of ndoc * Tq
-  // int32 in A.args; its scores are ndoc contiguous floats in A.S.
+  // Query row qi's tape for documents j0..j1-1 is ndoc runs of its qtn tokens
+  // (one contiguous run of ndoc * Tq int32 when a row is a whole query); its
+  // scores are ndoc contiguous floats in A.S (A.St, unnormalised, for tiles).
 #pragma unroll
   for (int q = 0; q < kIbQpw; ++q) {
-    if (qi[q] >= A.Bq) continue;
-    const int64_t p0 = (int64_t)qi[q] * A.Bd + j0;
+    if (!qlive[q]) continue;
+    const int64_t p0 = (int64_t)qrow[q] * A.Bd + j0;
     if (A.args) {
-      int32_t* const out = A.args + p0 * Tq;
-      const int n = ndoc * Tq;
+      int32_t* const out = A.args + p0 * Tq + qt0[q];
+      const int tn = qtn[q], n = ndoc * tn;
 #pragma unroll 4
       for (int e = lane; e < n; e += 64) {
-        const int jj = e / Tq, t = e - jj * Tq;
-        out[e] = res_tape[wave][q][jj][t];
+        const int jj = e / tn, t = e - jj * tn;
+        out[jj * Tq + t] = res_tape[wave][q][jj][t];
       }
+    }
+    if (ntq > 1) {
+      if (lane < ndoc) A.St[(int64_t)qi[q] * A.Bd + j0 + lane] = res_score[wave][q][lane];
+      continue;
     }
     // normalize epilogue: 1 / max(valid query tokens, 1) in fp32 (normalize.jl:4-10)
     float inv = 1.0f;
@@ -858,9 +870,38 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
   }
 }
 
+// S[i, j] = sum over tiles tb (in order) of St[i * ntq + tb, j], times
+// 1 / max(valid tokens of query i, 1) when normalising (the kernel's epilogue
+// rule, over all Tq tokens).  Grid (document blocks, query stride).
+__global__ void __launch_bounds__(256) inbatch_tile_sum_kernel(const float* St, int ntq, int Bq,
+                                                               int Bd, const uint8_t* qm, int Tq,
+                                                               int norm, float* S) {
+  __shared__ int cnt;
+  for (int i = blockIdx.y; i < Bq; i += gridDim.y) {
+    float inv = 1.0f;
+    if (norm) {
+      if (threadIdx.x == 0) cnt = 0;
+      __syncthreads();
+      int c = 0;
+      for (int t = threadIdx.x; t < Tq; t += 256) c += qm ? (qm[(int64_t)i * Tq + t] != 0) : 1;
+      atomicAdd(&cnt, c);
+      __syncthreads();
+      const float nf = (float)cnt;
+      inv = 1.0f / (nf > 1.0f ? nf : 1.0f);
+      __syncthreads();  // cnt read by every thread before the next query resets it
+    }
+    for (int j = blockIdx.x * 256 + threadIdx.x; j < Bd; j += gridDim.x * 256) {
+      float s = 0.0f;
+      for (int tb = 0; tb < ntq; ++tb) s += St[((int64_t)i * ntq + tb) * Bd + j];
+      S[(int64_t)i * Bd + j] = norm ? s * inv : s;
+    }
+  }
+}
+
 hipError_t launch_inbatch_mfma(int dtype_bf16, const InBatchArgs& args_in, hipStream_t stream) {
   InBatchArgs A = args_in;
-  A.nqb = (A.Bq + kIbQueries - 1) / kIbQueries;
+  A.ntq = A.Tq > kTile ? (A.Tq + kTile - 1) / kTile : 1;
+  A.nqb = (int)(((int64_t)A.Bq * A.ntq + kIbQueries - 1) / kIbQueries);
   // Documents per block: the grid should be a whole number of rounds of the
   // resident block slots (kIbBlocksPerCu per CU) -- a last round that
   // fills only part of the GPU idles the rest -- as few blocks as that
@@ -892,13 +933,15 @@ hipError_t launch_inbatch_mfma(int dtype_bf16, const InBatchArgs& args_in, hipSt
   // Plan workspace: chunk masks, chunk counts, first tokens.
   auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
   const size_t mask_bytes = al((size_t)A.Bd * nch * 4), vec_bytes = al((size_t)A.Bd * 4);
+  const size_t tile_bytes = A.ntq > 1 ? al((size_t)A.Bq * A.ntq * A.Bd * 4) : 0;
   void* ws = nullptr;
-  hipError_t e = workspace_alloc(&ws, mask_bytes + 2 * vec_bytes, stream);
+  hipError_t e = workspace_alloc(&ws, mask_bytes + 2 * vec_bytes + tile_bytes, stream);
   if (e != hipSuccess) return e;
   char* w = static_cast<char*>(ws);
   uint32_t* cmask = reinterpret_cast<uint32_t*>(w);
   int32_t* dcount = reinterpret_cast<int32_t*>(w + mask_bytes);
   int32_t* dfirst = reinterpret_cast<int32_t*>(w + mask_bytes + vec_bytes);
+  A.St = A.ntq > 1 ? reinterpret_cast<float*>(w + mask_bytes + 2 * vec_bytes) : nullptr;
   A.cmask = cmask;
   A.dcount = dcount;
   A.dfirst = dfirst;
@@ -934,6 +977,10 @@ hipError_t launch_inbatch_mfma(int dtype_bf16, const InBatchArgs& args_in, hipSt
     };
     if (dtype_bf16) by_packed(OpBF16());
     else by_packed(OpF16());
+    if (A.ntq > 1)
+      hipLaunchKernelGGL(inbatch_tile_sum_kernel,
+                         dim3((unsigned)std::min((A.Bd + 255) / 256, 64), (unsigned)std::min(A.Bq, 65535)),
+                         dim3(256), 0, stream, A.St, A.ntq, A.Bq, A.Bd, A.qm, A.Tq, A.norm, A.S);
     e = hipGetLastError();
   }
   const hipError_t ef = workspace_free(ws, stream);
@@ -945,7 +992,7 @@ hipError_t launch_inbatch_mfma(int dtype_bf16, const InBatchArgs& args_in, hipSt
 bool inbatch_mfma_supported(int64_t dim, int64_t Tq, int64_t Td, const void* Q, const void* D) {
   const bool al = ((reinterpret_cast<uintptr_t>(Q) | reinterpret_cast<uintptr_t>(D)) & 15u) == 0;
   const bool dim_ok = dim == 32 || dim == 64 || dim == 96 || dim == 128;
-  return dim_ok && Tq >= 1 && Tq <= kTile && Td >= 0 && (Td + kTile - 1) / kTile <= kIbMaxChunks && al;
+  return dim_ok && Tq >= 1 && Tq <= kIbMaxTq && Td >= 0 && (Td + kTile - 1) / kTile <= kIbMaxChunks && al;
 }
 
 }  // namespace fms

@@ -18,7 +18,11 @@ struct InBatchArgs {
   int32_t* args;       // (Bq, Bd, Tq) nullable
   int Bq, Bd, Tq, Td;
   int dim = 128;       // 32, 64, 96 or 128
-  int norm = 0;        // S *= 1 / max(valid tokens of query i, 1)
+  int norm = 0;
+  // filled by the launcher for Tq > 32: query rows of the kernel are tiles of
+  // 32 tokens, ntq per query, scored into St (Bq * ntq, Bd) and summed into S
+  int ntq = 1;
+  float* St = nullptr;        // S *= 1 / max(valid tokens of query i, 1)
   // filled by the launcher
   int nqb, ndb;        // query blocks, document blocks
   int db;              // documents per block of the uniform partition
@@ -29,7 +33,7 @@ struct InBatchArgs {
   const int32_t* dfirst;  // (Bd,) first valid token, -1 = none
 };
 
-// dim in {32, 64, 96, 128}, 1 <= Tq <= 32, 16-byte aligned features.
+// dim in {32, 64, 96, 128}, 1 <= Tq <= 4096, 16-byte aligned features.
 bool inbatch_mfma_supported(int64_t dim, int64_t Tq, int64_t Td, const void* Q, const void* D);
 // Runs the plan kernel (per-document chunk masks, in a workspace from the
 // library pool) and the in-batch kernel on `stream`.  With args.cu set the

@@ -71,9 +71,11 @@ def test_paired_and_candidates_fused_normalize(device, dtype, dim, Tq):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-def test_inbatch_and_packed_multi_fused_normalize(device, dtype):
-    rng = np.random.default_rng(3)
-    Bq, Bd, Tq, Td, dim = 37, 50, 24, 70, 128
+@pytest.mark.parametrize("Tq", [24, 70], ids=lambda t: f"Tq{t}")
+def test_inbatch_and_packed_multi_fused_normalize(device, dtype, Tq):
+    """Tq = 70: three query tiles per query, normalised over all 70 tokens."""
+    rng = np.random.default_rng(3 + Tq)
+    Bq, Bd, Td, dim = 37, 50, 70, 128
     print(f"normalize in-batch / multi-query dtype={dtype}", flush=True)
     Q = torch.from_numpy(tokens(rng, (Bq, Tq, dim))).to(device, dtype)
     D = torch.from_numpy(tokens(rng, (Bd, Td, dim))).to(device, dtype)

@@ -6,8 +6,8 @@ same inputs: fp16/bf16 scores within 2e-3 relative, fp32 within 1e-5; tapes
 equal except at near-ties within that tolerance.  Shapes: a query count that
 is not a multiple of the kernel's 32-query block, Lq = 24 with a random
 qmask, documents of length 0, 1, 31, 32, 33 and ColPali-like 700..1100, at
-dims 128, 96, 64 and 32 (the MFMA kernel's 8, 6, 4 and 2 k-blocks); dim 48 takes
-the per-query fallback.
+dims 128, 96, 64 and 32 (the MFMA kernel's 8, 6, 4 and 2 k-blocks), Lq = 40 and
+70 (query tiles of 32); dim 48 takes the per-query fallback.
 """
 import numpy as np
 import pytest
@@ -34,16 +34,19 @@ def _case(rng, dtype, dim, nq, Tq, lens, device):
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: DT_ID[d])
-@pytest.mark.parametrize("case", ["edges", "colpali", "edges_d64", "edges_d96", "colpali_d32"])
+@pytest.mark.parametrize("case", ["edges", "colpali", "edges_d64", "edges_d96", "colpali_d32",
+                                  "edges_t40", "colpali_t70"])
 def test_packed_multi_matches_single_and_oracle(device, dtype, case):
     rng = np.random.default_rng({"edges": 61, "colpali": 62, "edges_d64": 64, "edges_d96": 65,
-                                 "colpali_d32": 66}[case])
+                                 "colpali_d32": 66, "edges_t40": 67, "colpali_t70": 68}[case])
     dim = {"edges_d64": 64, "edges_d96": 96, "colpali_d32": 32}.get(case, 128)
+    Tq_over = {"edges_t40": 40, "colpali_t70": 70}.get(case)
     case = case.split("_")[0]
     if case == "edges":
         nq, Tq, lens = 40, 24, [5, 0, 1, 31, 32, 33, 64, 65, 0, 200, 17]
     else:
         nq, Tq, lens = 33, 24, list(rng.integers(700, 1101, size=9))
+    Tq = Tq_over or Tq
     Q, Qo, bf, P, to, cu, qm = _case(rng, dtype, dim, nq, Tq, lens, device)
     qmt = torch.from_numpy(qm).to(device)
     S, args = fm.packed_multi_forward(Q, P, qmt)

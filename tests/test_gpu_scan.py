@@ -159,7 +159,11 @@ def test_candidates_parity(device, dtype, shape, idx_dtype):
                                    (128, 32, 1000, 20, 40), (128, 16, 2048, 17, 9),
                                    # dim 32, 64, 96: the same kernel with 2, 4, 6 k-blocks
                                    (64, 32, 180, 40, 37), (96, 24, 65, 17, 9), (32, 16, 100, 33, 20),
-                                   (64, 8, 40, 300, 600), (96, 32, 1000, 20, 40)],
+                                   (64, 8, 40, 300, 600), (96, 32, 1000, 20, 40),
+                                   # Tq > 32: query tiles of 32 (2, 3, 4 per query; a last
+                                   # tile of 8, 32 and 4 tokens)
+                                   (128, 40, 65, 33, 9), (128, 64, 100, 20, 17), (64, 100, 50, 10, 12),
+                                   (96, 300, 33, 5, 7)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_inbatch_parity(device, dtype, shape):
     dim, Tq, Td, Bq, Bd = shape
@@ -184,7 +188,9 @@ def test_inbatch_parity(device, dtype, shape):
 @pytest.mark.parametrize("shape", [(32, 180, 24, 21), (17, 65, 40, 33), (32, 32, 16, 16),
                                    (8, 300, 20, 17), (5, 7, 18, 6),
                                    # Tq = 24: four queries packed into three tiles
-                                   (24, 180, 24, 21), (24, 33, 9, 5), (24, 700, 37, 5)],
+                                   (24, 180, 24, 21), (24, 33, 9, 5), (24, 700, 37, 5),
+                                   # Tq > 32: query tiles
+                                   (40, 65, 33, 9), (96, 180, 12, 11)],
                          ids=lambda s: "x".join(map(str, s)))
 @pytest.mark.parametrize("dim", [128, 64], ids=lambda d: f"d{d}")
 def test_inbatch_masks_and_ties(device, dtype, shape, dim):

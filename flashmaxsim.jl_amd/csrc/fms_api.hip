@@ -166,7 +166,10 @@ hipError_t scratch_address(hipStream_t st, void** out) {
 // scan_fast runs over LayCandSorted), `runs(order, doc_end)` launches it.
 struct NoRuns {
   bool applies() const { return false; }
-  hipError_t operator()(const PairRef*, const uint32_t*) const { return hipErrorInvalidValue; }
+  size_t qfrag_bytes() const { return 0; }
+  hipError_t operator()(const PairRef*, const uint32_t*, char*) const {
+    return hipErrorInvalidValue;
+  }
 };
 
 template <class Op>
@@ -180,7 +183,10 @@ struct RunsLauncher {
   float neg;
   bool norm, vec;
   bool applies() const { return runs_supported<Op>(dim, vec); }
-  hipError_t operator()(const PairRef* order, const uint32_t* doc_end) const {
+  // Workspace for the query tiles in fragment order (0: the scan loads them
+  // from Q directly).
+  size_t qfrag_bytes() const { return runs_qfrag_bytes<Op>(dim, rows, npairs / lay->C); }
+  hipError_t operator()(const PairRef* order, const uint32_t* doc_end, char* qfrag) const {
     RunArgs A;
     A.lay = *lay;
     A.dim = dim;
@@ -196,6 +202,7 @@ struct RunsLauncher {
     A.norm = norm ? 1 : 0;
     A.order = order;
     A.doc_end = doc_end;
+    A.qfrag = qfrag;
     return launch_runs<Op>(A, st);
   }
   hipStream_t st;
@@ -215,14 +222,19 @@ fms_status run_candidates(const LayCand& lay, int64_t npairs, hipStream_t st, Wo
                           const Runs& runs, Launch&& launch) {
   if (!scan_grid_fits(npairs)) return FMS_EUNSUPPORTED;  // 32-bit work-item count
   if (group_candidates(npairs, lay.N, lay.dbytes)) {
-    const size_t need = group_workspace_bytes(npairs, lay.N);
+    const size_t need = (group_workspace_bytes(npairs, lay.N) + 255) / 256 * 256;
+    // the document-batch scan's fragment-ordered query tiles follow the
+    // grouping workspace (dropped when the no-allocation scratch cannot
+    // hold both: the scan then loads the tiles from Q)
+    size_t qneed = runs.applies() ? runs.qfrag_bytes() : 0;
     void* buf = nullptr;
     bool pooled = false;
     if (ws == Workspace::kScratch) {
       if (need > kNoallocScratchBytes) return FMS_ESCRATCH;
+      if (qneed > kNoallocScratchBytes - need) qneed = 0;
       const hipError_t e = scratch_address(st, &buf);
       if (e != hipSuccess) return from_hip(e);
-    } else if (workspace_alloc(&buf, need, st) == hipSuccess) {
+    } else if (workspace_alloc(&buf, need + qneed, st) == hipSuccess) {
       pooled = true;
     } else {
       (void)hipGetLastError();  // clear the failed allocation; scan in output order
@@ -234,7 +246,8 @@ fms_status run_candidates(const LayCand& lay, int64_t npairs, hipStream_t st, Wo
       const uint32_t* doc_end = nullptr;
       hipError_t e = group_pairs_by_document(lay.idx, lay.idx64, npairs, lay.N, buf, &sl.order,
                                              &doc_end, st);
-      if (e == hipSuccess) e = runs.applies() ? runs(sl.order, doc_end) : launch(sl);
+      char* qfrag = qneed ? static_cast<char*>(buf) + need : nullptr;
+      if (e == hipSuccess) e = runs.applies() ? runs(sl.order, doc_end, qfrag) : launch(sl);
       const hipError_t ef = pooled ? workspace_free(buf, st) : hipSuccess;
       return from_hip(e != hipSuccess ? e : ef);
     }

@@ -2,6 +2,8 @@
 // scan (fms_runs.hpp) for 16-bit and INT8 features.
 #include "fms_runs.hpp"
 
+#include <type_traits>
+
 namespace fms {
 
 namespace {
@@ -14,6 +16,13 @@ constexpr int runs_kq() {
   return NKB * (Op::kKb == 32 ? 2 : 1) >= 16 ? 2 : 4;
 }
 
+// 16-bit features of d = 64 or 128 stream their chunks through LDS
+// (scan_runs_lds: two 8 KB slots per wave at d = 128, 64 KB per workgroup).
+template <class Op, int NKB>
+constexpr bool runs_lds() {
+  return !Op::kInt && (NKB == 4 || NKB == 8);
+}
+
 template <class Op, int NKB>
 hipError_t launch_nkb(const RunArgs& A, hipStream_t stream) {
   constexpr int KQ = runs_kq<Op, NKB>();
@@ -21,7 +30,22 @@ hipError_t launch_nkb(const RunArgs& A, hipStream_t stream) {
   a.ppw = run_ppw(A.npairs, KQ);
   const int64_t waves = (A.npairs + a.ppw - 1) / a.ppw;
   const dim3 grid((unsigned)((waves + kWaves - 1) / kWaves)), block(64 * kWaves);
-  hipLaunchKernelGGL((scan_runs<Op, NKB, KQ>), grid, block, 0, stream, a);
+  if constexpr (runs_lds<Op, NKB>()) {
+    if (a.qfrag) {
+      // the queries' tiles in fragment order first (same stream)
+      const int64_t B = a.npairs / a.lay.C;
+      const int64_t nunits = B * a.nqt * NKB * 64;
+      if (nunits > 0)
+        hipLaunchKernelGGL((query_frag_kernel<NKB>), dim3((unsigned)((nunits + 255) / 256)), dim3(256),
+                           0, stream, a.lay.Q, a.lay.Tq, a.dim * Op::kEsz, a.nqt, nunits,
+                           reinterpret_cast<u32x4*>(a.qfrag));
+      hipLaunchKernelGGL((scan_runs_lds<Op, NKB, KQ, true>), grid, block, 0, stream, a);
+    } else {
+      hipLaunchKernelGGL((scan_runs_lds<Op, NKB, KQ, false>), grid, block, 0, stream, a);
+    }
+  } else {
+    hipLaunchKernelGGL((scan_runs<Op, NKB, KQ>), grid, block, 0, stream, a);
+  }
   return hipGetLastError();
 }
 

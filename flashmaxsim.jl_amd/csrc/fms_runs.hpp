@@ -358,31 +358,41 @@ struct RunCursor {
   PairView dv;
 };
 
+// The byte offset, within a chunk, of the 16-byte unit that lane `lane`
+// copies in load i of a chunk: row R*i + lane/U, the unit that lands at slot
+// position lane%U of that row's swizzle.
+template <int NKB>
+__device__ __forceinline__ int lds_copy_offset(int i, int lane, int rowbytes) {
+  constexpr int U = lds_units<NKB>(), R = 64 / U;
+  const int row = R * i + lane / U;
+  return row * rowbytes + ((lane % U) ^ lds_key<NKB>(row)) * 16;
+}
+
 // Copy the chunk at stream position c into the LDS slot at `base`: NKB
-// loads of R whole rows each (lane l: row R*i + l/U, the unit that lands at
-// slot position l of that row's swizzle), then the mask byte of chunk row
-// l%32 into the slot's mask dwords (base + NKB*64; a zero-size resource
-// without a mask).  A device function rather than a lambda: a buffer
-// resource local to a lambda keeps the host compile from emitting the
-// kernel's launch stub.
+// loads of R whole rows each (lane offsets `off`, from lds_copy_offset,
+// relative to a resource that starts at the chunk and ends with the
+// document, so rows past it read 0), then the mask byte of chunk row l%32
+// into the slot's mask dwords (base + NKB*64; a zero-size resource without
+// a mask).  The fragment copies are non-temporal: every 128-byte line of
+// the chunk is read by exactly one of them, and the query tiles the scan
+// re-reads then stay in L2.  A device function rather than a lambda: a
+// buffer resource local to a lambda keeps the host compile from emitting
+// the kernel's launch stub.
 template <class Op, int NKB>
 __device__ __forceinline__ void copy_chunk_lds(const RunCursor& c, typename Op::Frag* base,
-                                               int rowbytes, int lane) {
+                                               const int* off, int rowbytes, int lane) {
   typedef __attribute__((address_space(3))) void* lds_void_t;
-  constexpr int U = lds_units<NKB>(), R = 64 / U;
-  const rsrc_t rd = make_rsrc_u(c.dv.d, (uint32_t)c.dv.td * (uint32_t)rowbytes);
-  const int lrow = lane / U;
   const int chunk0 = c.ch * kTile;
+  const int rows = c.dv.td - chunk0;
+  const rsrc_t rd = make_rsrc(c.dv.d + (int64_t)chunk0 * rowbytes,
+                              rows > 0 ? (uint32_t)rows * (uint32_t)rowbytes : 0u);
 #pragma unroll
-  for (int i = 0; i < NKB; ++i) {
-    const int row = R * i + lrow;
-    const int unit = (lane % U) ^ lds_key<NKB>(row);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rd, (lds_void_t)(base + i * 64), 16,
-                                             (chunk0 + row) * rowbytes + unit * 16, 0, 0, 0);
-  }
+  for (int i = 0; i < NKB; ++i)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rd, (lds_void_t)(base + i * 64), 16, off[i], 0, 0,
+                                             /*nt*/ 2);
   const bool has_m = c.dv.dm != nullptr;
-  const rsrc_t rm = make_rsrc_u(has_m ? (const void*)c.dv.dm : (const void*)c.dv.d,
-                                has_m ? (uint32_t)c.dv.td : 0u);
+  const rsrc_t rm = make_rsrc(has_m ? (const void*)c.dv.dm : (const void*)c.dv.d,
+                              has_m ? (uint32_t)c.dv.td : 0u);
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rm, (lds_void_t)(base + NKB * 64), 1,
                                            chunk0 + (lane & 31), 0, 0, 0);
 }
@@ -460,7 +470,12 @@ __global__ void __launch_bounds__(64 * kWaves, 2) scan_runs_lds(const RunArgs A)
     return true;
   };
   Frag* const wave_ring = &ring[wib][0][0];
-  auto copy_chunk = [&](const Cur& c, Frag* base) { copy_chunk_lds<Op, NKB>(c, base, rowbytes, lane); };
+  int coff[NKB];  // this lane's copy offsets within a chunk
+#pragma unroll
+  for (int i = 0; i < NKB; ++i) coff[i] = lds_copy_offset<NKB>(i, lane, rowbytes);
+  auto copy_chunk = [&](const Cur& c, Frag* base) {
+    copy_chunk_lds<Op, NKB>(c, base, coff, rowbytes, lane);
+  };
 
   Cur C, L;
   cur_at(C, k0);
@@ -519,7 +534,10 @@ __global__ void __launch_bounds__(64 * kWaves, 2) scan_runs_lds(const RunArgs A)
 #pragma unroll
         for (int r = 0; r < 16; ++r) s[r] = acc[r];
         take_first_row(s, m32, h, C.ch, mx[i], slot[i]);
-        update_chunk(s, m32, h, C.ch, mx[i], slot[i]);
+        if (m32 == 0xffffffffu)
+          fold_tree(s, C.ch * 16, mx[i], slot[i]);
+        else
+          update_chunk(s, m32, h, C.ch, mx[i], slot[i]);
       }
     }
     if (C.ch == C.nch - 1) {

@@ -286,13 +286,14 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
   if (db >= ndb) return;
 
   // ---- this block's documents -------------------------------------------------
-  // Uniform: A.db per block.  Balanced (A.balance): the document blocks split
-  // the documents by weight dcount + 1 (chunk steps plus the close), block b
-  // taking the documents whose weight prefix lies in [b, b+1) * total / ndb;
-  // every block checks that no block would exceed A.dbcap documents and
-  // falls back to the uniform split otherwise, so all blocks agree.
+  // Uniform: block b takes documents [b*Bd/ndb, (b+1)*Bd/ndb) (at most A.db).
+  // Balanced (A.balance): the document blocks split the documents by weight
+  // dcount + 1 (chunk steps plus the close), block b taking the documents
+  // whose weight prefix lies in [b, b+1) * total / ndb; every block checks
+  // that no block would exceed A.dbcap documents and falls back to the
+  // uniform split otherwise, so all blocks agree.
   __shared__ int part_j0, part_j1, part_bad;
-  int j0 = db * A.db, j1 = (j0 + A.db < A.Bd) ? j0 + A.db : A.Bd;
+  int j0 = (int)((int64_t)db * A.Bd / ndb), j1 = (int)((int64_t)(db + 1) * A.Bd / ndb);
   if (A.balance) {
     int32_t* const wpre = reinterpret_cast<int32_t*>(&res_tape[0][0][0][0]);  // (Bd + 1,)
     const int Bd = A.Bd;
@@ -918,16 +919,24 @@ hipError_t launch_inbatch_mfma(int dtype_bf16, const InBatchArgs& args_in, hipSt
   // With the balanced split (blocks of equal work) one round is enough; the
   // uniform split keeps two, so the dispatcher can even out lengths.
   const int balance = A.Bd <= kIbBalanceMaxDocs ? 1 : 0;
-  int db = 1;
+  // The document ranges split Bd evenly (fractional bounds: ranges of
+  // floor or ceil of Bd/ndb documents), so ndb can be exactly what fills the
+  // rounds: nqb * ndb <= rounds * slots.
+  int64_t ndb = (A.Bd + db_cap - 1) / db_cap;  // (fallback: the smallest grid that fits)
   for (int64_t rounds = balance ? 1 : 2; rounds <= 64; ++rounds) {
-    const int64_t ndb_want = (rounds * slots + A.nqb - 1) / A.nqb;
-    db = (int)std::max<int64_t>(1, (A.Bd + ndb_want - 1) / ndb_want);
-    if (db <= db_cap) break;
+    const int64_t ndb_want = std::max<int64_t>(1, rounds * slots / A.nqb);
+    if (ndb_want >= A.Bd) {
+      ndb = std::max<int64_t>(1, A.Bd);
+      break;
+    }
+    if ((A.Bd + ndb_want - 1) / ndb_want <= db_cap) {
+      ndb = ndb_want;
+      break;
+    }
   }
-  db = std::min(db, db_cap);
-  A.db = db;
+  A.ndb = (int)ndb;
+  A.db = (int)((A.Bd + ndb - 1) / ndb);  // most documents of a range
   A.dbcap = db_cap;
-  A.ndb = (A.Bd + db - 1) / db;
   A.balance = balance;
 
   // Plan workspace: chunk masks, chunk counts, first tokens.

@@ -25,7 +25,7 @@ struct InBatchArgs {
   float* St = nullptr;        // S *= 1 / max(valid tokens of query i, 1)
   // filled by the launcher
   int nqb, ndb;        // query blocks, document blocks
-  int db;              // documents per block of the uniform partition
+  int db;              // most documents of a block (uniform partition: ranges of floor or ceil of Bd/ndb)
   int dbcap;           // most documents a block can hold
   int balance;         // 1: partition documents by chunk count (Bd <= kIbBalanceMaxDocs)
   const uint32_t* cmask;  // (Bd, nch) valid rows per chunk (plan kernel)

@@ -74,7 +74,7 @@ constexpr int kIbMaxTq = 4096;                     // query tokens (tiles of 32 
 constexpr int kIbBufs = 3;                         // LDS chunk buffers (kIbBufs - 1 chunks in flight)
 static_assert(kIbBufs == 3 || kIbBufs == 4, "the step loop rotates 3 or 4 buffers");
 constexpr int kXcds = 8;
-constexpr int kIbMaxChunkMasks = 512;            // documents x chunks per block
+constexpr int kIbMaxChunkMasks = 1024;           // documents x chunks per block
 constexpr int kIbMaxDocs = 40;                   // documents per block
 constexpr int kIbMaxChunks = 64;                 // chunks per document (Td <= 2048)
 constexpr int kIbMaxList = (kIbMaxChunkMasks + kIbBufs - 1) / kIbBufs * kIbBufs;  // padded stream
@@ -997,7 +997,7 @@ hipError_t launch_inbatch_mfma(int dtype_bf16, const InBatchArgs& args_in, hipSt
 }
 
 // A block's documents span one buffer resource: ndoc * Td * dim * 2 bytes <=
-// kIbMaxChunkMasks * 32 * 256 = 4 MB.  Tape entries are staged as int16.
+// kIbMaxChunkMasks * 32 * 256 = 8 MB.  Tape entries are staged as int16.
 bool inbatch_mfma_supported(int64_t dim, int64_t Tq, int64_t Td, const void* Q, const void* D) {
   const bool al = ((reinterpret_cast<uintptr_t>(Q) | reinterpret_cast<uintptr_t>(D)) & 15u) == 0;
   const bool dim_ok = dim == 32 || dim == 64 || dim == 96 || dim == 128;

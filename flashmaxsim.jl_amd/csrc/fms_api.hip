@@ -93,7 +93,8 @@ fms_status run_float(int32_t dtype, const L& lay, int dim, int rows, int64_t npa
       launch_float(dtype, lay, dim, rows, npairs, args, partial, scores, neg, norm, vec, st));
 }
 
-// Candidate pair grouping (fms_candidates_grouping): 0 auto, 1 always, 2 never.
+// Candidate pair grouping (fms_candidates_grouping): 0 auto, 1 always, 2 never,
+// 3 always with the query tiles read from Q (no fragment-ordered copy).
 std::atomic<int> g_grouping{0};
 
 // Smallest candidate batch worth the five extra launches of the document sort.
@@ -111,7 +112,7 @@ bool group_candidates(int64_t P, int64_t N, int64_t dbytes) {
   if (P < 1 || P >= INT32_MAX || N < 1 || N >= INT32_MAX) return false;
   const int mode = g_grouping.load(std::memory_order_relaxed);
   if (mode == 2) return false;
-  if (mode == 1) return true;
+  if (mode == 1 || mode == 3) return true;
   if (P < kGroupMinPairs || (double)(N + 1) * 16.0 > 0.05 * (double)P * (double)dbytes)
     return false;
   const double distinct = -(double)N * expm1(-(double)P / (double)N);
@@ -226,7 +227,8 @@ fms_status run_candidates(const LayCand& lay, int64_t npairs, hipStream_t st, Wo
     // the document-batch scan's fragment-ordered query tiles follow the
     // grouping workspace (dropped when the no-allocation scratch cannot
     // hold both: the scan then loads the tiles from Q)
-    size_t qneed = runs.applies() ? runs.qfrag_bytes() : 0;
+    size_t qneed = runs.applies() && g_grouping.load(std::memory_order_relaxed) != 3
+                       ? runs.qfrag_bytes() : 0;
     void* buf = nullptr;
     bool pooled = false;
     if (ws == Workspace::kScratch) {
@@ -686,7 +688,7 @@ fms_status fms_launch_int8_candidates_scan(int32_t* args, float* partial, const 
 }
 
 int32_t fms_candidates_grouping(int32_t mode) {
-  if (mode < 0 || mode > 2) return -1;
+  if (mode < 0 || mode > 3) return -1;
   return g_grouping.exchange(mode);
 }
 

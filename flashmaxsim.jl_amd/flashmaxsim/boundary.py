@@ -213,12 +213,13 @@ def launch_candidates_scan(args, partial, Q, gallery, idx, qmask, dmask, N, scor
     _lib.check(st, "launch_candidates_scan")
 
 
-GROUPING_MODES = {"auto": 0, "always": 1, "never": 2}
+GROUPING_MODES = {"auto": 0, "always": 1, "never": 2, "always_direct_queries": 3}
 
 
 def candidates_grouping(mode: str) -> str:
-    """Set how candidate scans order their pairs ("auto", "always", "never"); returns
-    the previous mode.  In document order the pairs that share a gallery document are
+    """Set how candidate scans order their pairs ("auto", "always", "never", or
+    "always_direct_queries": in document order without the query-tile copy the 16-bit
+    document-batch scan otherwise makes, a test switch); returns the previous mode.  In document order the pairs that share a gallery document are
     scored together, so the document leaves HBM once per group; results are
     bit-identical either way.  Process-wide (fms_candidates_grouping)."""
     if mode not in GROUPING_MODES:

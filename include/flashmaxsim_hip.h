@@ -132,7 +132,10 @@ fms_status fms_launch_candidates_scan(int32_t dtype, int32_t* args, float* parti
  * pool and released on the same stream.  mode: 0 = automatic (C*B >= 16384,
  * the sort's O(N) passes cheap next to the scan, and uniformly drawn
  * indices would repeat enough to save >= 30% of the document reads),
- * 1 = always, 2 = never.  Returns the previous mode, or -1 for an invalid mode.
+ * 1 = always, 2 = never, 3 = always and without the query-tile copy (the
+ * 16-bit document-batch scan then reads the query tiles from Q, as it does
+ * when the no-allocation scratch cannot hold that copy; a test switch).
+ * Returns the previous mode, or -1 for an invalid mode.
  */
 int32_t fms_candidates_grouping(int32_t mode);
 

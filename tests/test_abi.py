@@ -135,9 +135,10 @@ def test_candidates_grouping_mode_switch():
     try:
         assert L.fms_candidates_grouping(2) == 1
         assert L.fms_candidates_grouping(0) == 2
-        assert L.fms_candidates_grouping(3) == -1
+        assert L.fms_candidates_grouping(3) == 0
+        assert L.fms_candidates_grouping(4) == -1
         assert L.fms_candidates_grouping(-1) == -1
-        assert L.fms_candidates_grouping(0) == 0
+        assert L.fms_candidates_grouping(0) == 3
     finally:
         L.fms_candidates_grouping(prev)
 

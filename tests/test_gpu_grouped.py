@@ -47,10 +47,16 @@ def _bitwise_equal(a, b):
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: DT_ID[d])
 @pytest.mark.parametrize("shape", [(128, 32, 180, 7, 33, 9), (40, 33, 65, 5, 9, 6),
-                                   (128, 24, 100, 3, 40, 8), (8, 6, 7, 1, 17, 5)],
+                                   (128, 24, 100, 3, 40, 8), (8, 6, 7, 1, 17, 5),
+                                   (64, 40, 70, 6, 25, 9), (128, 70, 33, 5, 20, 3),
+                                   (64, 32, 1, 4, 11, 2)],
                          ids=lambda s: "x".join(map(str, s)))
 @pytest.mark.parametrize("idx_dtype", [torch.int32, torch.int64], ids=["i32", "i64"])
 def test_grouped_matches_output_order_and_oracle(device, grouping, dtype, shape, idx_dtype):
+    """Document order (with and, for 16-bit d = 64 / 128, without the query tiles
+    copied in fragment order) against output order and the oracle.  Shapes cover
+    the LDS-streamed batch scan at d = 64 and 128, Tq of 24, 32, 40 and 70 (one to
+    three query tiles), ragged and one-token documents, and the generic dims."""
     dim, Tq, Td, N, C, B = shape
     rng = np.random.default_rng([dim, Tq, Td, N, C, B])
     Qt, Qo, bf = as_feature(tokens(rng, (B, Tq, dim)), dtype)
@@ -70,6 +76,8 @@ def test_grouped_matches_output_order_and_oracle(device, grouping, dtype, shape,
     grouping("always")
     got = _run_float(device, *dev_in, N, neg)
     _bitwise_equal(got, ref)
+    grouping("always_direct_queries")
+    _bitwise_equal(_run_float(device, *dev_in, N, neg), ref)
 
     S_o, a_o, p_o = oracle.candidates_forward(Qo, Go, idx, mask_np(qm), mask_np(dm), neg, bf16=bf)
     tol = FEATURE_TOL[dtype]

@@ -7,18 +7,21 @@
 //
 // Two launches.  A plan kernel reads the document masks once per call: the
 // valid rows of every 32-token chunk, each document's count of chunks with a
-// valid row and its first valid token.  The in-batch kernel then runs one
-// workgroup per CU (a single round of the grid):
+// valid row and its first valid token.  The in-batch kernel then runs two
+// workgroups per CU (at C3 a single round of the grid):
 //
-// Workgroup = 8 waves (two per SIMD), 32 queries x a range of documents.
+// Workgroup = 4 waves (one per SIMD), 16 queries x a range of documents.
 //   * document ranges split the documents by work (chunk steps plus one per
 //     document, from the plan), so the workgroups finish together; every
 //     workgroup checks the split against the per-block document limit and
 //     all fall back to an even split otherwise;
 //   * every wave keeps 4 query tiles (32 tokens x d=128 fp16/bf16) in
 //     registers for the whole workgroup lifetime, so each LDS fragment read
-//     feeds 4 MFMAs; the eight waves share one chunk stream (a barrier per
-//     step keeps the two waves of each SIMD in step);
+//     feeds 4 MFMAs; the four waves share one chunk stream (a barrier per
+//     step), and the two waves of a SIMD belong to different workgroups;
+//     issue priority falls as a step progresses, so the wave that is behind
+//     issues first and neither workgroup runs ahead (the SIMD otherwise
+//     favours the older wave, and the younger workgroup would finish alone);
 //   * the workgroup streams its documents in 32-token chunks: each chunk
 //     (8 KB) is fetched ONCE from L2/HBM straight into LDS (buffer_load ...
 //     lds, one 16-byte load per thread, no registers), in MFMA fragment
@@ -65,7 +68,7 @@ namespace fms {
 
 namespace {
 
-constexpr int kIbWaves = 8;
+constexpr int kIbWaves = 4;
 constexpr int kIbQpw = 4;                          // query tiles per wave
 static_assert(kIbQpw == 4, "the step is written for two phases of two query tiles");
 constexpr int kIbQueries = kIbWaves * kIbQpw;      // queries per block
@@ -74,11 +77,11 @@ constexpr int kIbMaxTq = 4096;                     // query tokens (tiles of 32 
 constexpr int kIbBufs = 3;                         // LDS chunk buffers (kIbBufs - 1 chunks in flight)
 static_assert(kIbBufs == 3 || kIbBufs == 4, "the step loop rotates 3 or 4 buffers");
 constexpr int kXcds = 8;
-constexpr int kIbMaxChunkMasks = 1024;           // documents x chunks per block
+constexpr int kIbMaxChunkMasks = 512;            // documents x chunks per block
 constexpr int kIbMaxDocs = 40;                   // documents per block
 constexpr int kIbMaxChunks = 64;                 // chunks per document (Td <= 2048)
 constexpr int kIbMaxList = (kIbMaxChunkMasks + kIbBufs - 1) / kIbBufs * kIbBufs;  // padded stream
-constexpr int kIbBlocksPerCu = 1;                // occupancy the launch bounds ask for
+constexpr int kIbBlocksPerCu = 2;                // occupancy the launch bounds ask for
 constexpr int kIbBalanceMaxDocs = 6144;          // partition weights fit the result area
 // List entry: chunk (6 bits) | document in block (6) | last chunk of its
 // document (1) | first valid token + 1 (19).
@@ -621,6 +624,10 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
   // i + kIbBufs - 1 into buffer `ahead` (the one entry i-1 used).
   auto step = [&](int i, const u32x4* cur, u32x4* ahead) {
     chunk_load(ahead, (uint32_t)uniform((int)ld_m), (uint32_t)uniform((int)ld_info), uniform(ld_r0));
+    // Issue priority falls as the step progresses (3, 2, 1): of the two waves
+    // on a SIMD (one from each of the CU's two blocks) the one further behind
+    // in its step issues first, so neither block runs ahead of the other.
+    __builtin_amdgcn_s_setprio(3);
     // List entries for the next step, read now so the LDS latency hides
     // behind this step's MFMAs instead of stalling before the barrier.
     ld_m = lst_mask[ld_i];
@@ -641,6 +648,7 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
     fold_close(2, lag2, pinfo);
     fold_close(3, lag3, pinfo);
     close_if_last(2, 3, pinfo);
+    __builtin_amdgcn_s_setprio(2);
     Acc n2 = Acc{}, n3 = Acc{};
 #pragma unroll
     for (int kb = 0; kb < kIbNkb; ++kb) {
@@ -650,6 +658,7 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
     fold_close(0, n0, info);
     fold_close(1, n1, info);
     close_if_last(0, 1, info);
+    __builtin_amdgcn_s_setprio(1);
     lag2 = n2;
     lag3 = n3;
     prev_info = info;

@@ -848,10 +848,27 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
     if (A.args) {
       int32_t* const out = A.args + p0 * Tq + qt0[q];
       const int tn = qtn[q], n = ndoc * tn;
+      const int16_t* const src = &res_tape[wave][q][0][0];
+      if (tn == kTile && Tq == kTile && ((reinterpret_cast<uintptr_t>(out) & 15u) == 0u)) {
+        // whole 32-token query rows (16-byte aligned output): the staged tape
+        // and the output run are both one contiguous run of n entries (n a
+        // multiple of 32), 4 per lane per pass: an 8-byte LDS read and a
+        // 16-byte store
+        for (int e = lane * 4; e < n; e += 256) {
+          const uint2 w = *reinterpret_cast<const uint2*>(src + e);
+          const i32x4 v = {(int32_t)(int16_t)(w.x & 0xffffu), (int32_t)(int16_t)(w.x >> 16),
+                           (int32_t)(int16_t)(w.y & 0xffffu), (int32_t)(int16_t)(w.y >> 16)};
+          *reinterpret_cast<i32x4*>(out + e) = v;
+        }
+      } else {
+        // e / tn as (e * ceil(2^32 / tn)) >> 32, exact for e < 2^27 (the
+        // factor is 2^32 itself for tn = 1, hence 64 bits)
+        const uint64_t mg = ((uint64_t)1 << 32) / (uint64_t)tn + (((uint64_t)1 << 32) % (uint64_t)tn != 0);
 #pragma unroll 4
-      for (int e = lane; e < n; e += 64) {
-        const int jj = e / tn, t = e - jj * tn;
-        out[jj * Tq + t] = res_tape[wave][q][jj][t];
+        for (int e = lane; e < n; e += 64) {
+          const int jj = (int)(((uint64_t)(uint32_t)e * mg) >> 32), t = e - jj * tn;
+          out[jj * Tq + t] = src[jj * kTile + t];
+        }
       }
     }
     if (ntq > 1) {

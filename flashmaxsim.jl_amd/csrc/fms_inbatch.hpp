@@ -28,6 +28,8 @@ struct InBatchArgs {
   int db;              // most documents of a block (uniform partition: ranges of floor or ceil of Bd/ndb)
   int dbcap;           // most documents a block can hold
   int balance;         // 1: partition documents by chunk count (Bd <= kIbBalanceMaxDocs)
+  int tilt;            // 1: balanced one-round grid of two blocks per CU, first half of
+                       //    the document ranges weighted 22 : 18 against the second
   const uint32_t* cmask;  // (Bd, nch) valid rows per chunk (plan kernel)
   const int32_t* dcount;  // (Bd,) chunks with a valid row
   const int32_t* dfirst;  // (Bd,) first valid token, -1 = none

@@ -71,23 +71,25 @@ def normalized_randn(torch, shape, gen, dtype, device, chunk_rows=4096):
 
 
 def timed_steps(torch, fn, steps, warmup):
-    """W untimed steps, then exactly K steps bracketed by synchronize; per-launch HIP
-    events on the current stream (the stream every scan is enqueued on)."""
+    """W untimed steps, then exactly K steps bracketed by synchronize, with one pair of
+    HIP events on the current stream (the stream every scan is enqueued on) around the
+    K steps: the per-launch figure is their elapsed time / K.  (An event pair around
+    every step would add ~10 us of GPU idle time per step: a timestamp packet is a
+    barrier for the command processor.)"""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
     st = torch.cuda.current_stream()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(steps)]
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
-    for e0, e1 in ev:
-        e0.record(st)
+    e0.record(st)
+    for _ in range(steps):
         fn()
-        e1.record(st)
+    e1.record(st)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    launch_ms = [e0.elapsed_time(e1) for e0, e1 in ev]
-    return wall, launch_ms
+    per = e0.elapsed_time(e1) / steps
+    return wall, [per] * steps
 
 
 def cpu_threads():

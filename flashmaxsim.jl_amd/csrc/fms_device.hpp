@@ -215,6 +215,25 @@ __device__ __forceinline__ void fold_tree(const float (&s)[16], int slot0, float
   slot = take ? slot0 + ci : slot;
 }
 
+// fold_tree8: the same update over one half of the registers, 0..7 (rows
+// 0..15 of the chunk) or 8..15 (rows 16..31), when the two halves of a chunk
+// belong to different documents.  slot = slot0 + register index within the
+// half.
+template <bool kUpper>
+__device__ __forceinline__ void fold_tree8(const float (&s)[16], int slot0, float& mx, int& slot) {
+  constexpr int o = kUpper ? 8 : 0;
+  const float m0 = max3_ieee(s[o + 0], s[o + 1], s[o + 2]);
+  const float m1 = max3_ieee(s[o + 3], s[o + 4], s[o + 5]);
+  const float m2 = max3_ieee(s[o + 6], s[o + 7], m0);
+  const float cm = max3_ieee(m1, m2, m2);
+  int ci = 7;
+#pragma unroll
+  for (int r = 6; r >= 0; --r) ci = (s[o + r] == cm) ? r : ci;
+  const bool take = cm > mx;
+  mx = take ? cm : mx;
+  slot = take ? slot0 + ci : slot;
+}
+
 // running_max_seq: the sequential scan itself, with row masking, for the
 // HBM-bound scans (fewest live registers).  `rowbits` is the
 // chunk validity shifted to this lane half (bit 8*(r/4) + r%4 = register r);
@@ -238,6 +257,16 @@ __device__ __forceinline__ void running_max_seq(const float (&s)[16], uint32_t r
 // 1-based document token of a slot for a lane in half h; 0 = none.
 __device__ __forceinline__ int slot_to_token(int slot, int h) {
   return slot < 0 ? 0 : (slot >> 4) * kTile + acc_row(slot & 15, h) + 1;
+}
+
+// The same for a stream of 16-row units: slot = (v + 1) * 16 + r, where the
+// chunk's row 0 is document row 16 v (v = -1 when the document starts in the
+// chunk's second half, whose registers are 8..15).
+// (masked with the sign of the slot, not selected: no control flow inside
+// a fold that the scheduler interleaves with MFMAs)
+__device__ __forceinline__ int slot_to_token16(int slot, int h) {
+  const int t = ((slot >> 4) - 1) * 16 + acc_row(slot & 15, h) + 1;
+  return t & ~(slot >> 31);
 }
 
 // Cross-lane exchanges without LDS.  v_permlane32_swap(a, b) trades lanes

@@ -92,8 +92,26 @@ constexpr uint32_t kInfoDocMask = 63u, kInfoFirstMask = 0x7ffffu;
 constexpr int kPlanNfBit = 30;
 constexpr int kPlanTooLong = -2;  // packed document longer than max_len
 static_assert(kIbMaxDocs <= (int)kInfoDocMask + 1, "document index fits its field");
+// In-batch layout: the stream is made of 16-row units (rows 16u .. 16u+15 of
+// a document), two per list entry, so a document's last unit and the next
+// document's first share a chunk.  Entry: unit of the chunk's first half
+// (7 bits) | unit of its second half (7) | their documents (6 + 6) | split:
+// the halves belong to different documents, the first closes after its half
+// (1) | last: the second half's document closes after the chunk (1).  A
+// separate word holds the two documents' first valid tokens (16 + 16 bits).
+constexpr int kHU1Shift = 7, kHDoc0Shift = 14, kHDoc1Shift = 20, kHSplitBit = 26, kHLastBit = 27;
+constexpr uint32_t kHUMask = 127u;
+static_assert(2 * kIbMaxChunks <= (int)kHUMask + 1, "unit index fits its field");
 
 }  // namespace
+
+// This lane's index, computed where it is used (volatile: not hoisted out of
+// a loop, so it does not hold a register across it).
+__device__ __forceinline__ int lane_id_here() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
 
 // Workgroup barrier that does not drain in-flight global loads: wait only
 // for this wave's LDS accesses (lgkmcnt(0)), then s_barrier.
@@ -251,6 +269,9 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
   typedef typename Op::Acc Acc;
   typedef typename Op::Frag Frag;
   static_assert(kNkb >= 1 && kNkb <= kIbMaxNkb, "query tiles of dim <= 128 stay in registers");
+  // The in-batch layout streams 16-row units; the packed layouts (long
+  // documents, little tail to save) stream whole 32-row document chunks.
+  constexpr bool kHalf = !kPacked && !kT24;
   constexpr int kIbNkb = kNkb;
   constexpr int kIbRowBytes = kNkb * 32;                                // bytes per token row
   constexpr int kIbFrags = kNkb * 64;                                   // 16-byte fragments per chunk
@@ -265,11 +286,15 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
   __shared__ uint32_t lst_mask[kIbMaxList];          // compacted chunk list
   __shared__ uint32_t lst_info[kIbMaxList];
   __shared__ int32_t lst_row0[kPacked ? kIbMaxList : 1];  // packed: document's first row
+  __shared__ uint32_t lst_first[kHalf ? kIbMaxList : 1];  // units: first valid tokens
+  __shared__ int unit_start[kHalf ? kIbMaxDocs + 1 : 1];  // units: a document's first entry unit
+  __shared__ int unit_first[kHalf ? kIbMaxDocs : 1];      //   and its first unit
   __shared__ int32_t doc_row0[kPacked ? kIbMaxDocs + 1 : 1];
   __shared__ int lst_count;
   __shared__ int any_nf;  // some document's first valid row is not finite
   __shared__ int16_t res_tape[kIbWaves][kIbQpw][kIbMaxDocs][kTile];  // Td <= 2048
   __shared__ float res_score[kIbWaves][kIbQpw][kIbMaxDocs];
+  __shared__ float score_sink[kHalf ? 64 : 1];  // branch-free close: the other lanes' stores
 
   const int tid = threadIdx.x, lane = tid & 63, wave = uniform(tid >> 6);
   const int r32 = lane & 31, h = lane >> 5;
@@ -452,54 +477,128 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
   }
 
   // ---- compacted chunk list ------------------------------------------------------
-  // Only chunks with at least one valid row are streamed and multiplied (a
-  // document's fully masked tail costs nothing).  Entry i: row validity
-  // lst_mask[i]; lst_info[i] packs (chunk, document, last chunk of its
-  // document, first valid token + 1) as the kInfo* constants describe.
-  if (wave == 0) {
-    int base = 0;
-    for (int c0 = 0; c0 < nall; c0 += 64) {
-      const int c = c0 + lane;
-      const uint32_t m = c < nall ? chunk_mask[c] : 0u;
-      const uint64_t bal = __ballot(m != 0u);
-      if (m != 0u) {
-        const int pos = base + __builtin_popcountll(bal & ((1ull << lane) - 1ull));
-        const int jj = c / nch, ch = c - jj * nch;
-        lst_mask[pos] = m;
-        const int df = doc_first[jj];
-        const uint32_t f1 = df < 0 ? 0u : (uint32_t)(df & ~(1 << kPlanNfBit)) + 1u;
-        lst_info[pos] = (uint32_t)ch | ((uint32_t)jj << kInfoDocShift) | (f1 << kInfoFirstShift);
-        if constexpr (kPacked) lst_row0[pos] = doc_row0[jj];
+  if constexpr (kHalf) {
+    // Unit stream.  A document's units run from its first unit with a valid
+    // row to its last (masked rows in between are substituted at load time),
+    // documents follow each other in the block's order, and entry e holds
+    // units 2e and 2e+1 (the last entry's second half, when the count is
+    // odd, is the next unit of its first half's document, all rows masked).
+    // Entry e: row validity lst_mask[e] (bits 0-15 the first half's rows,
+    // 16-31 the second's), lst_info[e] as the kH* constants describe,
+    // lst_first[e] the two documents' first valid tokens.
+    if (wave == 0) {
+      int fu = -1, lu = -1;
+      if (lane < ndoc) {
+        for (int c = 0; c < nch; ++c) {
+          const uint32_t m = chunk_mask[lane * nch + c];
+          if (m & 0xffffu) {
+            fu = fu < 0 ? 2 * c : fu;
+            lu = 2 * c;
+          }
+          if (m >> 16) {
+            fu = fu < 0 ? 2 * c + 1 : fu;
+            lu = 2 * c + 1;
+          }
+        }
       }
-      base += __builtin_popcountll(bal);
+      const int n = fu < 0 ? 0 : lu - fu + 1;
+      int incl = n;  // inclusive prefix over the lanes (documents), lanes >= ndoc add 0
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int v = __shfl_up(incl, o);
+        incl += lane >= o ? v : 0;
+      }
+      if (lane <= ndoc) unit_start[lane] = incl - n;  // unit_start[ndoc] = total
+      if (lane < ndoc) unit_first[lane] = fu;
+      if (lane == 63) lst_count = incl;
     }
-    if (lane == 0) lst_count = base;
+    __syncthreads();
+    const int nunit = lst_count;
+    const int nent = (nunit + 1) >> 1;
+    // document of unit k: the last document whose first unit is <= k (a
+    // document without units starts where the next one does)
+    auto doc_of = [&](int k) {
+      int lo = 0, hi = ndoc - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (unit_start[mid] <= k) lo = mid;
+        else hi = mid - 1;
+      }
+      return lo;
+    };
+    auto unit_bits = [&](int jj, int u) {
+      return (chunk_mask[jj * nch + (u >> 1)] >> ((u & 1) * 16)) & 0xffffu;
+    };
+    for (int e = tid; e < nent; e += 64 * kIbWaves) {
+      const int k0 = 2 * e, k1 = k0 + 1;
+      const int d0 = doc_of(k0), u0 = unit_first[d0] + (k0 - unit_start[d0]);
+      const bool has1 = k1 < nunit;
+      const int d1 = has1 ? doc_of(k1) : d0;
+      const int u1 = has1 ? unit_first[d1] + (k1 - unit_start[d1]) : u0 + 1;
+      const bool split = d1 != d0;
+      const bool lastu = !has1 || k1 + 1 == unit_start[d1 + 1];
+      lst_mask[e] = unit_bits(d0, u0) | (has1 ? unit_bits(d1, u1) << 16 : 0u);
+      lst_info[e] = (uint32_t)u0 | ((uint32_t)u1 << kHU1Shift) | ((uint32_t)d0 << kHDoc0Shift) |
+                    ((uint32_t)d1 << kHDoc1Shift) | ((uint32_t)split << kHSplitBit) |
+                    ((uint32_t)lastu << kHLastBit);
+      lst_first[e] = (uint32_t)(doc_first[d0] & 0xffff) | ((uint32_t)(doc_first[d1] & 0xffff) << 16);
+    }
+    if (tid == 0) lst_count = nent;
+    __syncthreads();
+  } else {
+    // Only chunks with at least one valid row are streamed and multiplied (a
+    // document's fully masked tail costs nothing).  Entry i: row validity
+    // lst_mask[i]; lst_info[i] packs (chunk, document, last chunk of its
+    // document, first valid token + 1) as the kInfo* constants describe.
+    if (wave == 0) {
+      int base = 0;
+      for (int c0 = 0; c0 < nall; c0 += 64) {
+        const int c = c0 + lane;
+        const uint32_t m = c < nall ? chunk_mask[c] : 0u;
+        const uint64_t bal = __ballot(m != 0u);
+        if (m != 0u) {
+          const int pos = base + __builtin_popcountll(bal & ((1ull << lane) - 1ull));
+          const int jj = c / nch, ch = c - jj * nch;
+          lst_mask[pos] = m;
+          const int df = doc_first[jj];
+          const uint32_t f1 = df < 0 ? 0u : (uint32_t)(df & ~(1 << kPlanNfBit)) + 1u;
+          lst_info[pos] = (uint32_t)ch | ((uint32_t)jj << kInfoDocShift) | (f1 << kInfoFirstShift);
+          if constexpr (kPacked) lst_row0[pos] = doc_row0[jj];
+        }
+        base += __builtin_popcountll(bal);
+      }
+      if (lane == 0) lst_count = base;
+    }
+    __syncthreads();
+    const int nst = uniform(lst_count);
+    bool last[kIbMaxChunkMasks / (64 * kIbWaves)];
+  #pragma unroll
+    for (int k = 0; k < kIbMaxChunkMasks / (64 * kIbWaves); ++k) {
+      const int i = tid + k * 64 * kIbWaves;
+      last[k] = i < nst && (i + 1 == nst ||
+                               ((lst_info[i + 1] >> kInfoDocShift) & kInfoDocMask) !=
+                                   ((lst_info[i] >> kInfoDocShift) & kInfoDocMask));
+    }
+    __syncthreads();
+  #pragma unroll
+    for (int k = 0; k < kIbMaxChunkMasks / (64 * kIbWaves); ++k)
+      if (last[k]) lst_info[tid + k * 64 * kIbWaves] |= 1u << kInfoLastBit;
+    __syncthreads();
   }
-  __syncthreads();
   const int nsteps = uniform(lst_count);
-  bool last[kIbMaxChunkMasks / (64 * kIbWaves)];
-#pragma unroll
-  for (int k = 0; k < kIbMaxChunkMasks / (64 * kIbWaves); ++k) {
-    const int i = tid + k * 64 * kIbWaves;
-    last[k] = i < nsteps && (i + 1 == nsteps ||
-                             ((lst_info[i + 1] >> kInfoDocShift) & kInfoDocMask) !=
-                                 ((lst_info[i] >> kInfoDocShift) & kInfoDocMask));
-  }
-  __syncthreads();
-#pragma unroll
-  for (int k = 0; k < kIbMaxChunkMasks / (64 * kIbWaves); ++k)
-    if (last[k]) lst_info[tid + k * 64 * kIbWaves] |= 1u << kInfoLastBit;
-  __syncthreads();
   // Pad the stream to whole rounds of the kIbBufs buffers with repeats of
-  // its last entry, close bit cleared: folding a chunk again changes no
-  // result (a running max only moves on a strictly greater score, and after
-  // the document's close nothing reads it).  The lists hold kIbMaxList.
+  // its last entry, close (and split) bits cleared: folding a chunk again
+  // changes no result (a running max only moves on a strictly greater score,
+  // and after the document's close nothing reads it).  The lists hold
+  // kIbMaxList.
   const int nsteps_pad = (nsteps + kIbBufs - 1) / kIbBufs * kIbBufs;
   static_assert(kIbBufs <= 64 * kIbWaves, "one thread per padding entry");
   if (tid < nsteps_pad - nsteps) {
     lst_mask[nsteps + tid] = lst_mask[nsteps - 1];
-    lst_info[nsteps + tid] = lst_info[nsteps - 1] & ~(1u << kInfoLastBit);
+    lst_info[nsteps + tid] = lst_info[nsteps - 1] & (kHalf ? ~((1u << kHSplitBit) | (1u << kHLastBit))
+                                                           : ~(1u << kInfoLastBit));
     if constexpr (kPacked) lst_row0[nsteps + tid] = lst_row0[nsteps - 1];
+    if constexpr (kHalf) lst_first[nsteps + tid] = lst_first[nsteps - 1];
   }
   __syncthreads();
 
@@ -518,12 +617,28 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
                     (uint32_t)std::min<int64_t>(A.ntok - prow0, 0xffffff) * kIbRowBytes)
       : make_rsrc(A.D + (int64_t)j0 * Td * kIbRowBytes, (uint32_t)(ndoc * Td * kIbRowBytes));
   int ld_i = 0;  // next list entry to request
+  // (units: `row0` is the entry's first-token word; row r32 of the chunk is
+  // row r32 % 16 of the unit of half r32 / 16)
   auto chunk_load = [&](u32x4* buf, uint32_t m, uint32_t info, int row0) {
-    const int ch = info & 63u, jj = (info >> kInfoDocShift) & kInfoDocMask;
-    const int f = (int)((info >> kInfoFirstShift) & kInfoFirstMask) - 1;
-    const int fsrc = f < 0 ? 0 : f;  // (never: listed chunks have a valid row)
-    const int src = ((m >> r32) & 1u) ? ch * kTile + r32 : fsrc;
-    const int voff = ((kPacked ? row0 : jj * Td) + src) * kIbRowBytes + h * 16;
+    int voff;
+    if constexpr (kHalf) {
+      // Every per-lane term is recomputed here from the lane id (an asm the
+      // compiler cannot hoist) and selects between uniform values, so no
+      // lane constant stays live across the step loop.
+      const int ln = lane_id_here();
+      const bool hi = (ln & 16) != 0;
+      const uint32_t ux = hi ? info >> kHU1Shift : info;
+      const uint32_t jx = hi ? info >> kHDoc1Shift : info >> kHDoc0Shift;
+      const uint32_t fx = hi ? (uint32_t)row0 >> 16 : (uint32_t)row0 & 0xffffu;
+      const int src = ((m >> (ln & 31)) & 1u) ? 16 * (int)(ux & kHUMask) + (ln & 15) : (int)fx;
+      voff = ((int)(jx & kInfoDocMask) * Td + src) * kIbRowBytes + ((ln >> 5) << 4);
+    } else {
+      const int ch = info & 63u, jj = (info >> kInfoDocShift) & kInfoDocMask;
+      const int f = (int)((info >> kInfoFirstShift) & kInfoFirstMask) - 1;
+      const int fsrc = f < 0 ? 0 : f;  // (never: listed chunks have a valid row)
+      const int src = ((m >> r32) & 1u) ? ch * kTile + r32 : fsrc;
+      voff = ((kPacked ? row0 : jj * Td) + src) * kIbRowBytes + h * 16;
+    }
 #pragma unroll
     for (int k = 0; k < kIbKbPerWave; ++k) {
       const int kb = (kIbKbPerWave * wave + k) % kIbNkb;
@@ -544,7 +659,7 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
   // scores are all -Inf closes on f with -Inf, as the reference's first-token
   // rule gives; the NaN case of that rule is settled after the loop.)
   auto close = [&](int q, int jj, int f) {
-    int tok = slot_to_token(slot[q], h);
+    int tok = kHalf ? slot_to_token16(slot[q], h) : slot_to_token(slot[q], h);
     float m = mx[q];
     merge_halves(m, tok, h);
     // Branch-free: the mask word is read for every lane (t0 is always a
@@ -556,8 +671,15 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
     const bool tv = token_valid(q);
     const float part = (tv & (tok != 0)) ? m : 0.0f;
     const float score = half_sum(part);
-    if (h == 0) res_tape[wave][q][jj][r32] = (int16_t)(tv ? tok : 0);
-    if (lane == 0) res_score[wave][q][jj] = score;
+    if constexpr (kHalf) {
+      // without branches: both halves hold the merged token and store it to
+      // the same place; lanes other than 0 store the score to a sink
+      res_tape[wave][q][jj][r32] = (int16_t)(tv ? tok : 0);
+      *(lane == 0 ? &res_score[wave][q][jj] : &score_sink[lane]) = score;
+    } else {
+      if (h == 0) res_tape[wave][q][jj][r32] = (int16_t)(tv ? tok : 0);
+      if (lane == 0) res_score[wave][q][jj] = score;
+    }
     mx[q] = -INFINITY;
     slot[q] = -1;
   };
@@ -678,6 +800,107 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
     dma_barrier<(kIbBufs - 2) * kIbKbPerWave>();
   };
 
+  // Unit-stream folds (kHalf).  An entry whose halves hold one document
+  // folds all 16 registers at once; a split entry folds registers 0..7 into
+  // the first document, closes it, and starts the second document with
+  // registers 8..15 (the close is branch-free, so the whole phase stays one
+  // block for the scheduler to interleave with its MFMAs).  Slots are
+  // (v + 1) * 16 + register, where chunk row 0 is document row 16 v
+  // (slot_to_token16).
+  auto fold_units = [&](int q0, int q1, const Acc& x0, const Acc& x1, uint32_t inf, auto split) {
+    float s0[16], s1[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) { s0[r] = x0[r]; s1[r] = x1[r]; }
+    const int v0 = (int)(inf & kHUMask);
+    if constexpr (decltype(split)::value) {
+      const int v1 = (int)((inf >> kHU1Shift) & kHUMask) - 1;
+      const int jj = (int)((inf >> kHDoc0Shift) & kInfoDocMask);
+      const int f = uniform(doc_first[jj]) & 0xffff;
+      fold_tree8<false>(s0, (v0 + 1) * 16, mx[q0], slot[q0]);
+      fold_tree8<false>(s1, (v0 + 1) * 16, mx[q1], slot[q1]);
+      close(q0, jj, f);
+      close(q1, jj, f);
+      fold_tree8<true>(s0, (v1 + 1) * 16 + 8, mx[q0], slot[q0]);
+      fold_tree8<true>(s1, (v1 + 1) * 16 + 8, mx[q1], slot[q1]);
+    } else {
+      fold_tree(s0, (v0 + 1) * 16, mx[q0], slot[q0]);
+      fold_tree(s1, (v0 + 1) * 16, mx[q1], slot[q1]);
+    }
+  };
+  // After a phase: the entry's last bit closes its second half's document.
+  auto close_units = [&](int q0, int q1, uint32_t inf) {
+    if (inf & (1u << kHLastBit)) {
+      const int jj = (int)((inf >> kHDoc1Shift) & kInfoDocMask);
+      const int f = uniform(doc_first[jj]) & 0xffff;
+      close(q0, jj, f);
+      close(q1, jj, f);
+    }
+  };
+  // A split phase's fold holds two closes; left to itself the scheduler
+  // issues all 16 MFMAs first and the VALU work after them.  This pins the
+  // interleave: each MFMA followed by 10 VALU instructions.
+  auto interleave_split = [&](auto split) {
+    if constexpr (decltype(split)::value) {
+#pragma unroll
+      for (int k = 0; k < 2 * kIbNkb; ++k) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);  // ten VALU
+      }
+    }
+  };
+  // The step of `step` over the unit stream: each phase is written out for
+  // both kinds of entry it folds (split or not), with its MFMAs, so the
+  // multiplies and the fold stay interleaved in one block either way.
+  auto step_units = [&](int i, const u32x4* cur, u32x4* ahead) {
+    chunk_load(ahead, (uint32_t)uniform((int)ld_m), (uint32_t)uniform((int)ld_info), uniform(ld_r0));
+    __builtin_amdgcn_s_setprio(3);
+    ld_m = lst_mask[ld_i];
+    ld_info = lst_info[ld_i];
+    ld_r0 = (int)lst_first[ld_i];
+    const uint32_t next_info = lst_info[i + 1 < nsteps_pad ? i + 1 : i];
+    const uint32_t info = (uint32_t)uniform((int)cur_info);
+    const uint32_t pinfo = (uint32_t)uniform((int)prev_info);
+    Frag a[kIbNkb];
+#pragma unroll
+    for (int kb = 0; kb < kIbNkb; ++kb) a[kb] = cur[kb * 64 + lane];
+    Acc n0, n1, n2, n3;
+    auto phase1 = [&](auto split) {
+      n0 = Acc{};
+      n1 = Acc{};
+#pragma unroll
+      for (int kb = 0; kb < kIbNkb; ++kb) {
+        n0 = Op::mma(a[kb], qf[0][kb], n0);
+        n1 = Op::mma(a[kb], qf[1][kb], n1);
+      }
+      fold_units(2, 3, lag2, lag3, pinfo, split);
+      interleave_split(split);
+    };
+    if (pinfo & (1u << kHSplitBit)) phase1(std::true_type());
+    else phase1(std::false_type());
+    close_units(2, 3, pinfo);
+    __builtin_amdgcn_s_setprio(2);
+    auto phase2 = [&](auto split) {
+      n2 = Acc{};
+      n3 = Acc{};
+#pragma unroll
+      for (int kb = 0; kb < kIbNkb; ++kb) {
+        n2 = Op::mma(a[kb], qf[2][kb], n2);
+        n3 = Op::mma(a[kb], qf[3][kb], n3);
+      }
+      fold_units(0, 1, n0, n1, info, split);
+      interleave_split(split);
+    };
+    if (info & (1u << kHSplitBit)) phase2(std::true_type());
+    else phase2(std::false_type());
+    close_units(0, 1, info);
+    __builtin_amdgcn_s_setprio(1);
+    lag2 = n2;
+    lag3 = n3;
+    prev_info = info;
+    cur_info = next_info;
+    dma_barrier<(kIbBufs - 2) * kIbKbPerWave>();
+  };
+
   // kT24 step: entry i's chunk times the three tiles (three independent MFMA
   // chains) while the three tiles of entry i-1 fold; one phase, closes after
   // the fold.  Loads, list reads and the barrier as in `step`.
@@ -717,7 +940,9 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
   };
 
   if (nsteps_pad > 0) {
-    auto row0_at = [&](int i) { return kPacked ? uniform(lst_row0[i]) : 0; };
+    auto row0_at = [&](int i) {
+      return kPacked ? uniform(lst_row0[i]) : kHalf ? uniform((int)lst_first[i]) : 0;
+    };
     chunk_load(cbuf0, lst_mask[0], lst_info[0], row0_at(0));                // entry 0
     chunk_load(cbuf1, lst_mask[ld_i], lst_info[ld_i], row0_at(ld_i));       // entry 1
     if constexpr (kIbBufs == 4)
@@ -725,6 +950,7 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
     ld_m = lst_mask[ld_i];
     ld_info = lst_info[ld_i];
     if constexpr (kPacked) ld_r0 = lst_row0[ld_i];
+    if constexpr (kHalf) ld_r0 = (int)lst_first[ld_i];
     cur_info = lst_info[0];
     dma_barrier<(kIbBufs - 2) * kIbKbPerWave>();  // entry 0 in LDS
     // Every load is unconditional and the buffers rotate statically.
@@ -734,6 +960,11 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
         step24(i, cbuf0, cbuf2);
         step24(i + 1, cbuf1, cbuf0);
         step24(i + 2, cbuf2, cbuf1);
+      } else if constexpr (kHalf) {
+        static_assert(kIbBufs == 3, "the unit-stream loop rotates 3 buffers");
+        step_units(i, cbuf0, cbuf2);
+        step_units(i + 1, cbuf1, cbuf0);
+        step_units(i + 2, cbuf2, cbuf1);
       } else if constexpr (kIbBufs == 4) {
         step(i, cbuf0, cbuf3);
         step(i + 1, cbuf1, cbuf0);
@@ -753,6 +984,10 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
       fold_close(1, lagt[1], pinfo);
       fold_close(2, lagt[2], pinfo);
       close24_if_last(pinfo);
+    } else if constexpr (kHalf) {  // tiles 2,3 of the last entry
+      if (pinfo & (1u << kHSplitBit)) fold_units(2, 3, lag2, lag3, pinfo, std::true_type());
+      else fold_units(2, 3, lag2, lag3, pinfo, std::false_type());
+      close_units(2, 3, pinfo);
     } else {  // tiles 2,3 of the last entry
       fold_close(2, lag2, pinfo);
       fold_close(3, lag3, pinfo);

@@ -239,6 +239,73 @@ def test_inbatch_masks_and_ties(device, dtype, shape, dim):
         assert not np.array_equal(Do[j, g], Do[j, w]), (i, j, t, g, w)
 
 
+def _unit_stream_case(rng, case):
+    """(Tq, Td, Bq, Bd, dim, dmask) for test_inbatch_unit_stream."""
+    if case == "short":
+        # documents of 0..40 rows (prefix masks), a third of them within one
+        # 16-row unit: split entries whose second document also closes there
+        Tq, Td, Bq, Bd, dim = 32, 40, 20, 96, 64
+        lens = rng.integers(0, Td + 1, Bd)
+        lens[::3] = rng.integers(1, 17, len(lens[::3]))
+        dm = np.arange(Td)[None, :] < lens[:, None]
+    elif case == "holes":
+        # valid rows in scattered runs: fully masked units inside a document
+        # (streamed, substituted), leading masked units (skipped), last valid
+        # row anywhere
+        Tq, Td, Bq, Bd, dim = 40, 100, 17, 45, 64
+        dm = np.zeros((Bd, Td), bool)
+        for j in range(Bd):
+            for _ in range(rng.integers(0, 4)):
+                a = int(rng.integers(0, Td))
+                dm[j, a:a + int(rng.integers(1, 12))] = True
+        dm[0, 37] = True
+        dm[1, :] = False
+        dm[2, [0, 99]] = True
+    else:  # "full_blocks": 40 documents per block (the per-block maximum)
+        Tq, Td, Bq, Bd, dim = 32, 48, 512, 640, 32
+        lens = rng.integers(1, Td + 1, Bd)
+        dm = np.arange(Td)[None, :] < lens[:, None]
+        dm &= rng.random((Bd, Td)) < 0.9
+        dm[:, 0] |= ~dm.any(1)
+    return Tq, Td, Bq, Bd, dim, dm
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=lambda d: DT_ID[d])
+@pytest.mark.parametrize("case", ["short", "holes", "full_blocks"])
+def test_inbatch_unit_stream(device, dtype, case):
+    """The in-batch kernel streams documents in 16-row units, two per chunk, so one
+    chunk can hold a document's last unit and the next document's first (folded as
+    two halves with a close between).  Short documents (split and close in one
+    chunk), masked runs inside documents, leading masked units, and blocks at the
+    40-document maximum, with exact duplicate tokens: scores and tapes against the
+    oracle (forward_layouts.jl:155-179), every recorded token a valid one."""
+    rng = np.random.default_rng({"short": 161, "holes": 162, "full_blocks": 163}[case])
+    Tq, Td, Bq, Bd, dim, dm = _unit_stream_case(rng, case)
+    q32 = tokens(rng, (Bq, Tq, dim))
+    d32 = tokens(rng, (Bd, Td, dim))
+    for j in range(0, Bd, 2):  # later rows copy earlier ones: exact ties
+        a, b = np.sort(rng.choice(Td, 2, replace=False))
+        d32[j, b] = d32[j, a]
+    Qt, Qo, bf = as_feature(q32, dtype)
+    Dt, Do, _ = as_feature(d32, dtype)
+    dmt = torch.from_numpy(dm)
+    S_o, a_o = oracle.inbatch_forward(Qo, Do, None, mask_np(dmt), bf16=bf)
+    S, args = fm.inbatch_forward(Qt.to(device), Dt.to(device), None, dmt.to(device))
+    torch.cuda.synchronize()
+    tol = FEATURE_TOL[dtype]
+    assert_scores(S.cpu(), S_o, tol, what="S")
+    got = args.cpu().numpy()
+    empty = ~dm.any(1)
+    assert (got[:, empty] == 0).all() and (S.cpu().numpy()[:, empty] == 0).all()
+    ii, jj, tt = np.nonzero(got)
+    assert dm[jj, got[ii, jj, tt] - 1].all()
+    Qf, Df = widened(Qo, bf), widened(Do, bf)
+    assert_tape(got, a_o, _pair_sims_fn(Qf, Df, lambda p: (Qf[p[0]], Df[p[1]])), tol)
+    for i, j, t in np.argwhere(got != a_o):
+        g, w = got[i, j, t] - 1, a_o[i, j, t] - 1
+        assert not np.array_equal(Do[j, g], Do[j, w]), (i, j, t, g, w)
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=lambda d: DT_ID[d])
 @pytest.mark.parametrize("shape", [(32, 180, 24, 21), (17, 65, 40, 33), (8, 300, 20, 17)],
                          ids=lambda s: "x".join(map(str, s)))

@@ -41,7 +41,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="c2",
-                    choices=["c2", "c3", "c3bwd", "c4", "c4d1024", "c4mq", "c5", "read"])
+                    choices=["c2", "c3", "c3bwd", "c4", "c4d1024", "c4mq", "c5", "read",
+                             "gather_c2", "gather_c5"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="target duration of the bounded CPU baseline sample")
@@ -562,6 +563,40 @@ def run_read(args, torch, fm, boundary, dev):
                 config={"workload": "hbm_read_ceiling", "bytes": nbytes, "blocks": blocks})
 
 
+def run_gather(args, torch, fm, boundary, dev, cfg):
+    """Read ceiling of a gathered-document stream: fms_debug_gather_bandwidth reads whole
+    documents (one 256-thread workgroup each, 16-byte nontemporal loads) from a gallery of
+    the workload's size, in the order its scan reads them.  gather_c2: the distinct
+    documents of C2's 256,000 uniform draws from 100,000 (46,080 B each), ascending, as the
+    grouped scan streams them.  gather_c5: C5's 256,000 draws from 1,000,000 int8
+    documents (23,040 B of codes each), in output order, repeats included."""
+    from flashmaxsim import _lib
+    N, doc_bytes, grouped = {"c2": (100_000, 180 * 128 * 2, True),
+                             "c5": (1_000_000, 180 * 128, False)}[cfg]
+    gallery = torch.empty(N * doc_bytes, dtype=torch.uint8, device=dev)
+    gallery.fill_(7)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(2 if cfg == "c2" else 5)
+    docs = torch.randint(0, N, (256_000,), generator=gen, device=dev)
+    if grouped:
+        docs = torch.unique(docs)  # sorted, distinct
+    docs = docs.to(torch.int32).contiguous()
+    nd = docs.numel()
+    out = torch.empty(nd * 256, dtype=torch.int32, device=dev)
+
+    def step():
+        _lib.check(_lib.lib().fms_debug_gather_bandwidth(
+            gallery.data_ptr(), gallery.numel(), doc_bytes, docs.data_ptr(), nd, out.data_ptr(),
+            torch.cuda.current_stream().cuda_stream), "gather_bandwidth")
+
+    wall, launch_ms = timed_steps(torch, step, args.steps, args.warmup)
+    return dict(pairs_per_step=0, bytes_per_launch=nd * doc_bytes, wall=wall, launch_ms=launch_ms,
+                dtype="u8", bound="hbm",
+                config={"workload": f"gathered_documents_{cfg}", "gallery_docs": N,
+                        "doc_bytes": doc_bytes, "documents_read": nd,
+                        "order": "distinct, ascending" if grouped else "output order"})
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -576,6 +611,8 @@ def main():
     boundary.candidates_grouping(args.grouping)
     runner = {"c2": run_c2, "c3": run_c3, "c3bwd": run_c3bwd, "c4": run_c4, "c5": run_c5,
               "c4mq": run_c4mq, "read": run_read,
+              "gather_c2": lambda *a: run_gather(*a, cfg="c2"),
+              "gather_c5": lambda *a: run_gather(*a, cfg="c5"),
               "c4d1024": lambda *a: run_c4(*a, dim=1024)}[args.workload]
     r = runner(args, torch, fm, boundary, dev)
     steps = args.steps
@@ -634,6 +671,10 @@ def main():
         out["roofline"]["padded_tflops"] = round(r["padded_flops"] / avg_launch_s / 1e12, 2)
     if args.workload == "read":
         out["metric"] = "HBM streaming read GB/s"
+        out["value"] = out["roofline"]["achieved"]
+        out["unit"] = "GB/s"
+    elif args.workload.startswith("gather_"):
+        out["metric"] = "HBM gathered-document read GB/s"
         out["value"] = out["roofline"]["achieved"]
         out["unit"] = "GB/s"
     elif args.workload != "c2":

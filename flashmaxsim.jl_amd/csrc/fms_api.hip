@@ -749,6 +749,16 @@ fms_status fms_debug_read_bandwidth(const void* p, int64_t bytes, uint32_t* out,
   return from_hip(read_bandwidth(p, bytes, out, blocks, as_stream(stream)));
 }
 
+fms_status fms_debug_gather_bandwidth(const void* g, int64_t gallery_bytes, int64_t doc_bytes,
+                                      const int32_t* docs, int64_t ndocs, uint32_t* out,
+                                      void* stream) {
+  if (gallery_bytes < 0 || doc_bytes <= 0 || doc_bytes % 16 != 0 || ndocs < 0 || ndocs > 0x7fffffff ||
+      (ndocs > 0 && (!docs || !out)) || (gallery_bytes > 0 && !g) || !aligned16(g))
+    return FMS_EINVAL;
+  if (ndocs == 0) return FMS_OK;
+  return from_hip(gather_bandwidth(g, gallery_bytes, doc_bytes, docs, ndocs, out, as_stream(stream)));
+}
+
 // ---- backward on the argmax tape ----------------------------------------------
 
 fms_status fms_paired_pullback(int32_t dtype, void* dQ, void* dD, const void* Q, const void* D,

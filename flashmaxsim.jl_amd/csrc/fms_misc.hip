@@ -261,6 +261,31 @@ hipError_t read_bandwidth(const void* p, int64_t bytes, uint32_t* out, int block
   return hipGetLastError();
 }
 
+// One workgroup per listed document: its doc16 16-byte units, nontemporal
+// (the document is read once), XOR-folded so the loads are kept.
+__global__ void __launch_bounds__(256) gather_bandwidth_kernel(const u32x4* __restrict__ g,
+                                                               int64_t gallery16, int64_t doc16,
+                                                               const int32_t* __restrict__ docs,
+                                                               uint32_t* out) {
+  const int64_t b = blockIdx.x;
+  const int64_t d0 = (int64_t)docs[b] * doc16;
+  uint32_t acc = 0u;
+  if (docs[b] >= 0 && d0 + doc16 <= gallery16) {
+    for (int64_t i = threadIdx.x; i < doc16; i += 256) {
+      const u32x4 a = __builtin_nontemporal_load(g + d0 + i);
+      acc ^= a[0] ^ a[1] ^ a[2] ^ a[3];
+    }
+  }
+  out[b * 256 + threadIdx.x] = acc;
+}
+
+hipError_t gather_bandwidth(const void* g, int64_t gallery_bytes, int64_t doc_bytes,
+                            const int32_t* docs, int64_t ndocs, uint32_t* out, hipStream_t stream) {
+  hipLaunchKernelGGL(gather_bandwidth_kernel, dim3((unsigned)ndocs), dim3(256), 0, stream,
+                     static_cast<const u32x4*>(g), gallery_bytes / 16, doc_bytes / 16, docs, out);
+  return hipGetLastError();
+}
+
 // Cross-lane helper probe (one wave): out[l] = lane_xor32(l), out[64 + l] =
 // half_sum(l) (the sum of lanes 0-31 in every lane), out[128 + l] /
 // out[192 + l] = the (token, max) merge_halves keeps when lane l holds

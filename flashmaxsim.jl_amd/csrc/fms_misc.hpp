@@ -19,5 +19,7 @@ hipError_t mfma_layout_probe(float* out, int op, hipStream_t stream);
 hipError_t cross_lane_probe(float* out, hipStream_t stream);
 hipError_t read_bandwidth(const void* p, int64_t bytes, uint32_t* out, int blocks,
                           hipStream_t stream);
+hipError_t gather_bandwidth(const void* g, int64_t gallery_bytes, int64_t doc_bytes,
+                            const int32_t* docs, int64_t ndocs, uint32_t* out, hipStream_t stream);
 
 }  // namespace fms

@@ -53,6 +53,7 @@ SIGNATURES = {
     "fms_varlen_normalize": [_p, _p, _i64, _p],
     "fms_debug_mfma_layout": [_p, _i32, _p],
     "fms_debug_read_bandwidth": [_p, _i64, _p, _i32, _p],
+    "fms_debug_gather_bandwidth": [_p, _i64, _i64, _p, _i64, _p, _p],
     "fms_candidates_grouping": [_i32],
     "fms_debug_cross_lane": [_p, _p],
     "fms_topk": [_p, _i64, _i64, _i64, _p, _p, _p],

@@ -435,6 +435,19 @@ fms_status fms_debug_cross_lane(float* out, void* stream);
 fms_status fms_debug_read_bandwidth(const void* p, int64_t bytes, uint32_t* out, int32_t blocks,
                                     void* stream);
 
+/*
+ * Test-only: gathered read of whole documents, the candidate scans' access
+ * pattern.  One 256-thread workgroup per entry of docs[0..ndocs) reads the
+ * doc_bytes (multiple of 16) at g + docs[i] * doc_bytes with 16-byte
+ * nontemporal loads; entries whose document does not lie inside the
+ * gallery's gallery_bytes are skipped.  out receives ndocs*256 words.  No
+ * reference counterpart: it measures the read ceiling of a gathered-document
+ * stream, reported beside the candidate scans' roofline.
+ */
+fms_status fms_debug_gather_bandwidth(const void* g, int64_t gallery_bytes, int64_t doc_bytes,
+                                      const int32_t* docs, int64_t ndocs, uint32_t* out,
+                                      void* stream);
+
 #ifdef __cplusplus
 }
 #endif

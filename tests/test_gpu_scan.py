@@ -54,6 +54,32 @@ def test_cross_lane_helpers(device):
         assert (o[128 + lane], o[192 + lane]) == (want[1], want[0]), (lane, o[128 + lane], o[192 + lane])
 
 
+def test_gather_bandwidth_probe(device):
+    """fms_debug_gather_bandwidth (the gathered-document read ceiling bench.py reports):
+    workgroup i XOR-folds the 16-byte units of document docs[i], each thread over units
+    tid, tid+256, ...; a document outside the gallery is skipped (its words stay 0)."""
+    rng = np.random.default_rng(7)
+    N, doc_bytes = 37, 1040
+    g = rng.integers(0, 2**32, size=N * doc_bytes // 4, dtype=np.uint64).astype(np.uint32)
+    docs = np.array([3, 0, 36, 3, 37, 12], np.int32)  # 37: past the end
+    out = torch.full((len(docs) * 256,), -1, dtype=torch.int32, device=device)
+    gt = torch.from_numpy(g.view(np.int32)).to(device)
+    dt = torch.from_numpy(docs).to(device)
+    _lib.check(_lib.lib().fms_debug_gather_bandwidth(gt.data_ptr(), N * doc_bytes, doc_bytes,
+                                                     dt.data_ptr(), len(docs), out.data_ptr(),
+                                                     torch.cuda.current_stream().cuda_stream),
+               "gather probe")
+    got = out.cpu().numpy().view(np.uint32).reshape(len(docs), 256)
+    units = g.reshape(N, doc_bytes // 16, 4)
+    for i, d in enumerate(docs):
+        for t in range(256):
+            want = 0
+            if d < N:
+                for u in range(t, doc_bytes // 16, 256):
+                    want ^= int(np.bitwise_xor.reduce(units[d, u]))
+            assert got[i, t] == want, (i, t)
+
+
 def _masks(rng, B, Tq, Td, kind):
     if kind == "none":
         return None, None

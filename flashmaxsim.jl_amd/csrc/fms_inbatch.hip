@@ -22,7 +22,10 @@
 //     issue priority falls as a step progresses, so the wave that is behind
 //     issues first and neither workgroup runs ahead (the SIMD otherwise
 //     favours the older wave, and the younger workgroup would finish alone);
-//   * the workgroup streams its documents in 32-token chunks: each chunk
+//   * the workgroup streams its documents in 32-row chunks (in the in-batch
+//     layout, chunks of two 16-row units, so a document's last unit and the
+//     next document's first share a chunk, folded as two register halves
+//     with the first document's close between them): each chunk
 //     (8 KB) is fetched ONCE from L2/HBM straight into LDS (buffer_load ...
 //     lds, one 16-byte load per thread, no registers), in MFMA fragment
 //     order: the 64 lanes of one fragment read cover 1 KB contiguously (no

@@ -112,6 +112,29 @@ __global__ void __launch_bounds__(kScanThreads) scan_sums_kernel(uint32_t* sums,
   }
 }
 
+// Counters -> exclusive offsets, in place, for at most kScanThreads tiles:
+// block b first sums the totals of tiles 0..b-1 itself (one per thread).
+__global__ void __launch_bounds__(kScanThreads) scan_apply_self_kernel(uint32_t* c, int64_t n,
+                                                                       const uint32_t* tile_sums) {
+  uint32_t off;
+  block_exclusive_scan(threadIdx.x < blockIdx.x ? tile_sums[threadIdx.x] : 0u, &off);
+  const int64_t base = (int64_t)blockIdx.x * kScanTile + (int64_t)threadIdx.x * kScanPer;
+  uint32_t v[kScanPer];
+  uint32_t s = 0u;
+#pragma unroll
+  for (int i = 0; i < kScanPer; ++i) {
+    v[i] = base + i < n ? c[base + i] : 0u;
+    s += v[i];
+  }
+  uint32_t tot;
+  uint32_t ex = block_exclusive_scan(s, &tot) + off;
+#pragma unroll
+  for (int i = 0; i < kScanPer; ++i) {
+    if (base + i < n) c[base + i] = ex;
+    ex += v[i];
+  }
+}
+
 // Counters -> exclusive offsets, in place.
 __global__ void __launch_bounds__(kScanThreads) scan_apply_kernel(uint32_t* c, int64_t n,
                                                                   const uint32_t* sums) {
@@ -309,11 +332,8 @@ hipError_t group_pairs_by_document(const void* idx, int idx64, int64_t npairs, i
                      ncount);
   hipLaunchKernelGGL(group_hist_kernel, dim3(flat_blocks(npairs)), dim3(kFlat), 0, stream, idx,
                      idx64, npairs, N, counts);
-  hipLaunchKernelGGL(scan_tile_sums_kernel, dim3((unsigned)nb), dim3(kScanThreads), 0, stream,
-                     counts, ncount, sums);
-  hipLaunchKernelGGL(scan_sums_kernel, dim3(1), dim3(kScanThreads), 0, stream, sums, nb);
-  hipLaunchKernelGGL(scan_apply_kernel, dim3((unsigned)nb), dim3(kScanThreads), 0, stream, counts,
-                     ncount, sums);
+  const hipError_t e = exclusive_scan_u32(counts, ncount, sums, stream);
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL(group_scatter_kernel, dim3(flat_blocks(npairs)), dim3(kFlat), 0, stream, idx,
                      idx64, npairs, N, counts, order);
   *order_out = order;
@@ -336,6 +356,13 @@ hipError_t exclusive_scan_u32(uint32_t* counts, int64_t n, uint32_t* sums, hipSt
   const int64_t nb = cdiv(n, kScanTile);
   hipLaunchKernelGGL(scan_tile_sums_kernel, dim3((unsigned)nb), dim3(kScanThreads), 0, stream,
                      counts, n, sums);
+  if (nb <= kScanThreads) {
+    // at most one tile total per thread: every apply block sums the totals
+    // before it (one launch fewer; `sums` keeps the tile totals)
+    hipLaunchKernelGGL(scan_apply_self_kernel, dim3((unsigned)nb), dim3(kScanThreads), 0, stream,
+                       counts, n, sums);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(scan_sums_kernel, dim3(1), dim3(kScanThreads), 0, stream, sums, nb);
   hipLaunchKernelGGL(scan_apply_kernel, dim3((unsigned)nb), dim3(kScanThreads), 0, stream, counts,
                      n, sums);

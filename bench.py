@@ -621,28 +621,41 @@ def main():
     launches = r.get("launches_per_step", 1)
     launch_ms = sorted(r["launch_ms"])
     avg_launch_s = (sum(launch_ms) / len(launch_ms)) / 1e3 / launches
-    if r["bound"] == "hbm":
+    if r["bound"] == "hbm" and "compulsory_bytes" in r:
+        # Candidate scans: the bytes the call must move -- every distinct
+        # referenced document once, plus queries, indices and outputs -- over the
+        # launch time.  A document shared by several pairs is read once, so the
+        # per-pair basis (one document read per pair) can exceed the HBM peak; it
+        # is kept beside the fraction as `per_pair`, not as the fraction.
+        cb = r["compulsory_bytes"]
+        achieved = cb / avg_launch_s / 1e9
+        per_pair = r["bytes_per_launch"] / avg_launch_s / 1e9
+        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "basis": "compulsory bytes: distinct documents once + queries + idx + outputs",
+                "bytes_per_launch": cb, "distinct_docs": r["distinct_docs"],
+                "per_pair": {"bytes": r["bytes_per_launch"], "effective_GBps": round(per_pair, 1)}}
+    elif r["bound"] == "hbm":
         achieved = r["bytes_per_launch"] / avg_launch_s / 1e9
         roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4)}
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "bytes_per_launch": r["bytes_per_launch"]}
     else:
         peak = FP16_PEAK_TFLOPS
         achieved = r["flops_per_launch"] / avg_launch_s / 1e12
         roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak,
                 "unit": "TFLOP/s", "frac": round(achieved / peak, 4)}
-    if "compulsory_bytes" in r:
-        # Beside the per-pair algorithmic bytes (every pair reads its document):
-        # the bytes no schedule can avoid -- each distinct referenced document
-        # once, plus queries, indices and outputs -- over the same launch time.
-        cb = r["compulsory_bytes"]
-        roof["compulsory"] = {"bytes": cb, "distinct_docs": r["distinct_docs"],
-                              "achieved": round(cb / avg_launch_s / 1e9, 1),
-                              "frac": round(cb / avg_launch_s / 1e9 / HBM_PEAK_GBS, 4)}
     roof["traffic"] = None
     prof = os.path.join(ROOT, "profiles", f"traffic_{args.workload}.json")
     if os.path.exists(prof):
+        # HBM bytes per launch from two rocprofv3 --pmc passes (FETCH_SIZE,
+        # WRITE_SIZE, calibrated on a copy of known size), committed beside the
+        # kernel and source commit they were measured on.
         with open(prof) as f:
-            roof["traffic"] = json.load(f).get("hbm_bytes_per_launch")
+            t = json.load(f)
+        roof["traffic"] = t.get("hbm_bytes_per_launch")
+        roof["traffic_source"] = {"file": os.path.relpath(prof, ROOT),
+                                  "kernel": t.get("kernel"), "commit": t.get("commit")}
     out = {
         "metric": "MaxSim pairs/sec (Lq32 Ld180 d128 fp16 candidates); % HBM roofline",
         "value": round(pairs / wall, 1),

@@ -94,8 +94,9 @@ fms_status run_float(int32_t dtype, const L& lay, int dim, int rows, int64_t npa
 }
 
 // Candidate pair grouping (fms_candidates_grouping): 0 auto, 1 always, 2 never,
-// 3 always with the query tiles read from Q (no fragment-ordered copy).
-std::atomic<int> g_grouping{0};
+// 3 always with the query tiles read from Q (no fragment-ordered copy).  Per
+// host thread: a caller that sets it changes no other thread's calls.
+thread_local int t_grouping = 0;
 
 // Smallest candidate batch worth the five extra launches of the document sort.
 constexpr int64_t kGroupMinPairs = 16384;
@@ -110,7 +111,7 @@ constexpr int64_t kGroupMinPairs = 16384;
 // Pair ids and document ids must fit 32 bits.
 bool group_candidates(int64_t P, int64_t N, int64_t dbytes) {
   if (P < 1 || P >= INT32_MAX || N < 1 || N >= INT32_MAX) return false;
-  const int mode = g_grouping.load(std::memory_order_relaxed);
+  const int mode = t_grouping;
   if (mode == 2) return false;
   if (mode == 1 || mode == 3) return true;
   if (P < kGroupMinPairs || (double)(N + 1) * 16.0 > 0.05 * (double)P * (double)dbytes)
@@ -215,9 +216,12 @@ struct RunsLauncher {
 // workspace comes from `ws`:
 //   kPool: the library pool, released on the same stream; an allocation
 //     failure falls back to output order (the results are identical);
-//   kScratch: the no-allocation array; a workspace larger than it is
-//     FMS_ESCRATCH (nothing is launched).  The grouping kernels clear every
-//     counter they use, so the array's previous contents do not matter.
+//   kScratch: the no-allocation array.  A workspace larger than it scans in
+//     output order under automatic grouping (the order is only a
+//     performance choice; the results are identical) and is FMS_ESCRATCH
+//     when grouping was forced (nothing is launched).  The grouping kernels
+//     clear every counter they use, so the array's previous contents do not
+//     matter.
 template <class Runs, class Launch>
 fms_status run_candidates(const LayCand& lay, int64_t npairs, hipStream_t st, Workspace ws,
                           const Runs& runs, Launch&& launch) {
@@ -227,12 +231,13 @@ fms_status run_candidates(const LayCand& lay, int64_t npairs, hipStream_t st, Wo
     // the document-batch scan's fragment-ordered query tiles follow the
     // grouping workspace (dropped when the no-allocation scratch cannot
     // hold both: the scan then loads the tiles from Q)
-    size_t qneed = runs.applies() && g_grouping.load(std::memory_order_relaxed) != 3
-                       ? runs.qfrag_bytes() : 0;
+    size_t qneed = runs.applies() && t_grouping != 3 ? runs.qfrag_bytes() : 0;
     void* buf = nullptr;
     bool pooled = false;
-    if (ws == Workspace::kScratch) {
-      if (need > kNoallocScratchBytes) return FMS_ESCRATCH;
+    if (ws == Workspace::kScratch && need > kNoallocScratchBytes) {
+      if (t_grouping != 0) return FMS_ESCRATCH;  // forced grouping cannot be honoured
+      // automatic grouping: buf stays null and the call scans in output order
+    } else if (ws == Workspace::kScratch) {
       if (qneed > kNoallocScratchBytes - need) qneed = 0;
       const hipError_t e = scratch_address(st, &buf);
       if (e != hipSuccess) return from_hip(e);
@@ -334,11 +339,21 @@ const char* fms_status_string(fms_status s) {
 const char* fms_version(void) { return FMS_VERSION_STRING; }
 
 int fms_arch_supported(void) {
+  // Asked before every call by the Julia overrides, so the answer is cached per
+  // device (0 = not yet asked, 1 = gfx950, 2 = other); racing first calls store
+  // the same value.
+  static std::atomic<int> known[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (dev >= 0 && dev < 64) {
+    const int k = known[dev].load(std::memory_order_relaxed);
+    if (k != 0) return k == 1 ? 1 : 0;
+  }
   hipDeviceProp_t prop;
   if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return 0;
-  return strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : 0;
+  const int ok = strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : 0;
+  if (dev >= 0 && dev < 64) known[dev].store(ok ? 1 : 2, std::memory_order_relaxed);
+  return ok;
 }
 
 fms_status fms_launch_paired_scan(int32_t dtype, int32_t* args, float* partial, const void* Q,
@@ -689,8 +704,12 @@ fms_status fms_launch_int8_candidates_scan(int32_t* args, float* partial, const 
 
 int32_t fms_candidates_grouping(int32_t mode) {
   if (mode < 0 || mode > 3) return -1;
-  return g_grouping.exchange(mode);
+  const int32_t prev = t_grouping;
+  t_grouping = mode;
+  return prev;
 }
+
+uint64_t fms_debug_workspace_allocs(void) { return workspace_alloc_count(); }
 
 fms_status fms_int8_dots(int32_t* out, const int8_t* qc, const int8_t* dc, int64_t dim,
                          int64_t Tq, int64_t Td, void* stream) {

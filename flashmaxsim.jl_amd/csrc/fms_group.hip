@@ -14,6 +14,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
 #include <mutex>
 
 #include "fms_group.hpp"
@@ -408,7 +409,14 @@ hipError_t stream_device(hipStream_t stream, int* dev) {
   return e;
 }
 
+namespace {
+std::atomic<uint64_t> g_workspace_allocs{0};
+}  // namespace
+
+uint64_t workspace_alloc_count() { return g_workspace_allocs.load(std::memory_order_relaxed); }
+
 hipError_t workspace_alloc(void** ptr, size_t bytes, hipStream_t stream) {
+  g_workspace_allocs.fetch_add(1, std::memory_order_relaxed);
   int dev = 0;
   hipError_t e = stream_device(stream, &dev);
   if (e != hipSuccess) return e;

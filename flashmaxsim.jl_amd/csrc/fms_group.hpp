@@ -49,6 +49,8 @@ hipError_t stream_device(hipStream_t stream, int* dev);
 // device (created on first use, kept for the life of the process so repeated
 // calls do not return memory to the driver between synchronisations).
 hipError_t workspace_alloc(void** ptr, size_t bytes, hipStream_t stream);
+// Number of workspace_alloc calls so far in this process (a test probe).
+uint64_t workspace_alloc_count();
 hipError_t workspace_free(void* ptr, hipStream_t stream);
 
 }  // namespace fms

@@ -16,8 +16,8 @@ import torch  # noqa: F401  (must precede the CDLL load, see module docstring)
 from .errors import ArgumentError, DimensionMismatch, HIPError, UnsupportedError
 
 _PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-# FLASHMAXSIM_HIP_LIB names another build of the same library (same ABI).
-LIB_PATH = os.environ.get("FLASHMAXSIM_HIP_LIB") or os.path.join(_PKG_DIR, "lib", "libflashmaxsim_hip.so")
+# The in-tree build, and only it: every run loads the library built from this tree.
+LIB_PATH = os.path.join(_PKG_DIR, "lib", "libflashmaxsim_hip.so")
 
 FMS_OK, FMS_EINVAL, FMS_EUNSUPPORTED, FMS_EHIP, FMS_ESCRATCH = 0, 1, 2, 3, 4
 FMS_F32, FMS_F16, FMS_BF16 = 0, 1, 2
@@ -55,6 +55,7 @@ SIGNATURES = {
     "fms_debug_read_bandwidth": [_p, _i64, _p, _i32, _p],
     "fms_debug_gather_bandwidth": [_p, _i64, _i64, _p, _i64, _p, _p],
     "fms_candidates_grouping": [_i32],
+    "fms_debug_workspace_allocs": [],
     "fms_debug_cross_lane": [_p, _p],
     "fms_topk": [_p, _i64, _i64, _i64, _p, _p, _p],
     "fms_launch_packed_multi_scan": [_i32, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64,
@@ -73,6 +74,7 @@ _RESTYPES = {
     "fms_status_string": ctypes.c_char_p,
     "fms_arch_supported": ctypes.c_int,
     "fms_version": ctypes.c_char_p,
+    "fms_debug_workspace_allocs": ctypes.c_uint64,
 }
 
 _lib = None

@@ -190,7 +190,8 @@ def launch_candidates_scan(args, partial, Q, gallery, idx, qmask, dmask, N, scor
     """launch_candidates_scan! (forward_layouts.jl:292-310).  noalloc=True calls
     fms_launch_candidates_scan_noalloc: the same scan with its grouping workspace in
     the library's static device scratch instead of the memory pool (no device
-    allocation; UnsupportedError when a call needs more than that scratch)."""
+    allocation).  A call that needs more than that scratch scans in output order
+    under automatic grouping and raises UnsupportedError under forced grouping."""
     _feat(Q, "Q", 3)
     _feat(gallery, "gallery", 3, Q)
     B, Tq, dim = Q.shape
@@ -219,9 +220,11 @@ GROUPING_MODES = {"auto": 0, "always": 1, "never": 2, "always_direct_queries": 3
 def candidates_grouping(mode: str) -> str:
     """Set how candidate scans order their pairs ("auto", "always", "never", or
     "always_direct_queries": in document order without the query-tile copy the 16-bit
-    document-batch scan otherwise makes, a test switch); returns the previous mode.  In document order the pairs that share a gallery document are
-    scored together, so the document leaves HBM once per group; results are
-    bit-identical either way.  Process-wide (fms_candidates_grouping)."""
+    document-batch scan otherwise makes, a test switch); returns the previous mode.
+    In document order the pairs that share a gallery document are scored together,
+    so the document leaves HBM once per group; results are bit-identical either
+    way.  Per host thread (fms_candidates_grouping): it changes this thread's later
+    calls only."""
     if mode not in GROUPING_MODES:
         raise ArgumentError(f"grouping mode must be one of {sorted(GROUPING_MODES)}")
     prev = _lib.lib().fms_candidates_grouping(GROUPING_MODES[mode])

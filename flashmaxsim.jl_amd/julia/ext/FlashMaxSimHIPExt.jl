@@ -54,25 +54,39 @@
 # returns without synchronising (src/ka.jl:3-5).  A nonzero status becomes
 # an ArgumentError, like the reference's pre-launch checks.
 #
+# Two guards keep every other case on the reference's own path, as the CUDA
+# extension does when its tensor cores are off (ext/FlashMaxSimCUDAExt.jl:60-66):
+#   - the architecture: each method first asks the library whether the current
+#     device is gfx950 (cached per device) and otherwise `@invoke`s the method
+#     it overrides (the KernelAbstractions tile kernels, the reference drivers,
+#     the reference quantiser and pullbacks);
+#   - the array kind: only dense ROCArrays have a pointer the library may read,
+#     so masks, indices, inverse counts and PackedSeq storage are typed as
+#     dense device arrays in the signatures.  A wrapped array (a
+#     PermutedDimsArray, a strided view, src/colocation.jl:18-24) matches none
+#     of these methods and dispatch keeps the reference method.
+#
 # Julia is not installed in the build container, so this file is written to
 # the AMDGPU.jl 1.x API and its `ccall`s are checked against the C header by
 # a parser in the repository's CPU tests (symbol, arity, argument types and
-# argument order); the Python host mirror (flashmaxsim.jl_amd/flashmaxsim)
-# drives the same C ABI on the GPU.
+# argument order, the guards above); the Python host mirror
+# (flashmaxsim.jl_amd/flashmaxsim) drives the same C ABI on the GPU.
 module FlashMaxSimHIPExt
 
 using AMDGPU
 using FlashMaxSim
 using FlashMaxSim: PackedSeq, Int8Index
 
-const libfms = get(ENV, "FLASHMAXSIM_HIP_LIB",
-                   joinpath(@__DIR__, "..", "..", "lib", "libflashmaxsim_hip.so"))
+const libfms = joinpath(@__DIR__, "..", "..", "lib", "libflashmaxsim_hip.so")
 
 const FMS_F32 = Int32(0)
 const FMS_F16 = Int32(1)
 const FMS_BF16 = Int32(2)
 
 const ROCBackend = AMDGPU.ROCBackend
+# The backend types the overridden reference methods are declared on.
+const KABackend = FlashMaxSim.KernelAbstractions.Backend
+const KAGPU = FlashMaxSim.KernelAbstractions.GPU
 
 # Feature types whose reference-allocated partial / score buffers are Float32.
 const ScanFeature = Union{Float16, Float32}
@@ -88,6 +102,15 @@ end
 dtype_code(::Type{Float32}) = FMS_F32
 dtype_code(::Type{Float16}) = FMS_F16
 
+# Arguments whose pointer reaches the library: dense device arrays only.
+const DenseMask{N} = ROCArray{Bool,N}
+const MaybeMask{N} = Union{ROCArray{Bool,N}, Nothing}
+# Index eltypes the library reads (4 or 8 bytes; a value outside 1..N is invalid
+# under either signedness).
+const IndexEltype = Union{Int32, Int64, UInt32, UInt64}
+const DenseIndex = ROCMatrix{<:IndexEltype}
+const DensePacked{T} = PackedSeq{<:ROCMatrix{T}, <:ROCVector{Int32}}
+
 stream_ptr() = AMDGPU.stream().stream
 dptr(x::ROCArray) = Ptr{Cvoid}(UInt(pointer(x)))
 dptr(::Nothing) = C_NULL
@@ -98,7 +121,13 @@ function check(status::Int32, what::AbstractString)
     throw(ArgumentError("FlashMaxSim HIP $what: $msg"))
 end
 
+# Whether the current device runs the library's kernels (gfx950).  The library
+# caches the answer per device; the ccall itself costs a few nanoseconds.
 gfx950() = ccall((:fms_arch_supported, libfms), Cint, ()) == 1
+
+# The extension-only functions have no reference method to fall back to.
+require_gfx950(what) = gfx950() ||
+    throw(ArgumentError("FlashMaxSim HIP $what: the current device is not gfx950"))
 
 FlashMaxSim.tensor_cores_active(::ROCBackend, ::Type{T}) where {T<:AnyFeature} = gfx950()
 FlashMaxSim.tensor_cores_active(::ROCBackend, ::Type{Int8}) = gfx950()
@@ -167,61 +196,71 @@ function c_varlen_scan(dtype, args, partial, Qtokens, Dtokens, cu_q, cu_d, dim, 
 end
 
 # ---- float scans: the boundary methods (reference-allocated Float32 buffers) ------
+# Each falls back to the reference's KernelAbstractions tile kernels
+# (`launch_*_scan!(backend::GPU, ...)`, e.g. src/forward_pair.jl:130-132) on any
+# other AMD architecture.
 
-function FlashMaxSim.launch_pair_scan!(::ROCBackend, argmax_u::ROCVector{Int32},
+function FlashMaxSim.launch_pair_scan!(backend::ROCBackend, argmax_u::ROCVector{Int32},
                                        partial::ROCVector{Float32},
                                        q::ROCMatrix{T}, d::ROCMatrix{T},
-                                       qmask, dmask) where {T<:ScanFeature}
+                                       qmask::DenseMask{1}, dmask::DenseMask{1}) where {T<:ScanFeature}
+    gfx950() || return @invoke FlashMaxSim.launch_pair_scan!(backend::KAGPU, argmax_u, partial, q, d, qmask, dmask)
     dim, Tq = size(q)
     c_pair_scan(dtype_code(T), argmax_u, partial, q, d, qmask, dmask, dim, Tq, size(d, 2),
                 nothing)
     nothing
 end
 
-function FlashMaxSim.launch_paired_scan!(::ROCBackend, args::ROCMatrix{Int32},
+function FlashMaxSim.launch_paired_scan!(backend::ROCBackend, args::ROCMatrix{Int32},
                                          partial::ROCMatrix{Float32},
                                          Q::ROCArray{T,3}, D::ROCArray{T,3},
-                                         qmask, dmask) where {T<:ScanFeature}
+                                         qmask::DenseMask{2}, dmask::DenseMask{2}) where {T<:ScanFeature}
+    gfx950() || return @invoke FlashMaxSim.launch_paired_scan!(backend::KAGPU, args, partial, Q, D, qmask, dmask)
     dim, Tq, B = size(Q)
     c_paired_scan(dtype_code(T), args, partial, Q, D, qmask, dmask, dim, Tq, size(D, 2), B,
                   nothing)
     nothing
 end
 
-function FlashMaxSim.launch_candidates_scan!(::ROCBackend, args::ROCArray{Int32,3},
+function FlashMaxSim.launch_candidates_scan!(backend::ROCBackend, args::ROCArray{Int32,3},
                                              partial::ROCArray{Float32,3},
-                                             Q::ROCArray{T,3}, gallery::ROCArray{T,3}, idx,
-                                             qmask, dmask, N) where {T<:ScanFeature}
+                                             Q::ROCArray{T,3}, gallery::ROCArray{T,3},
+                                             idx::DenseIndex, qmask::DenseMask{2},
+                                             dmask::DenseMask{2}, N) where {T<:ScanFeature}
+    gfx950() || return @invoke FlashMaxSim.launch_candidates_scan!(backend::KAGPU, args, partial, Q, gallery, idx, qmask, dmask, N)
     dim, Tq, B = size(Q)
     c_candidates_scan(dtype_code(T), args, partial, Q, gallery, idx, qmask, dmask,
                       dim, Tq, B, size(gallery, 2), N, size(idx, 1), nothing, 0)
     nothing
 end
 
-function FlashMaxSim.inbatch_device_scan!(::ROCBackend, S::ROCMatrix{Float32},
+function FlashMaxSim.inbatch_device_scan!(backend::ROCBackend, S::ROCMatrix{Float32},
                                           args::ROCArray{Int32,3},
                                           Q::ROCArray{T,3}, D::ROCArray{T,3},
-                                          qmask, dmask) where {T<:ScanFeature}
+                                          qmask::DenseMask{2}, dmask::DenseMask{2}) where {T<:ScanFeature}
+    gfx950() || return @invoke FlashMaxSim.inbatch_device_scan!(backend::Any, S, args, Q, D, qmask, dmask)
     dim, Tq, Bq = size(Q)
     c_inbatch_scan(dtype_code(T), S, args, Q, D, qmask, dmask, dim, Tq, Bq, size(D, 2),
                    size(D, 3))
     nothing
 end
 
-function FlashMaxSim.launch_packed_scan!(::ROCBackend, args::ROCMatrix{Int32},
+function FlashMaxSim.launch_packed_scan!(backend::ROCBackend, args::ROCMatrix{Int32},
                                          partial::ROCMatrix{Float32}, q::ROCMatrix{T},
                                          tokens::ROCMatrix{T}, cu::ROCVector{Int32},
-                                         qmask) where {T<:ScanFeature}
+                                         qmask::DenseMask{1}) where {T<:ScanFeature}
+    gfx950() || return @invoke FlashMaxSim.launch_packed_scan!(backend::KAGPU, args, partial, q, tokens, cu, qmask)
     dim, Tq = size(q)
     c_packed_scan(dtype_code(T), args, partial, q, tokens, cu, qmask, dim, Tq,
                   length(cu) - 1, size(tokens, 2), nothing)
     nothing
 end
 
-function FlashMaxSim.launch_varlen_scan!(::ROCBackend, args::ROCMatrix{Int32},
+function FlashMaxSim.launch_varlen_scan!(backend::ROCBackend, args::ROCMatrix{Int32},
                                          partial::ROCMatrix{Float32}, Qtokens::ROCMatrix{T},
                                          Dtokens::ROCMatrix{T}, cu_q::ROCVector{Int32},
                                          cu_d::ROCVector{Int32}) where {T<:ScanFeature}
+    gfx950() || return @invoke FlashMaxSim.launch_varlen_scan!(backend::KAGPU, args, partial, Qtokens, Dtokens, cu_q, cu_d)
     c_varlen_scan(dtype_code(T), args, partial, Qtokens, Dtokens, cu_q, cu_d,
                   size(Qtokens, 1), size(args, 1), size(args, 2), size(Qtokens, 2),
                   size(Dtokens, 2), nothing)
@@ -233,11 +272,13 @@ end
 # (score_eltype(T) for Float16 / Float32 features; Float32 in place of BFloat16
 # for BFloat16 features, see the header).  Σ_t and the `neg` fill run inside
 # the scan kernel instead of the separate `sum(partial; dims = 1)` and
-# `ifelse.` kernels.
+# `ifelse.` kernels.  On another architecture each invokes the reference
+# driver it replaces.
 
-function FlashMaxSim.pair_forward_ka(::ROCBackend, q::ROCMatrix{T}, d::ROCMatrix{T},
-                                     qmask::AbstractVector{Bool}, dmask::AbstractVector{Bool},
-                                     ::T) where {T<:AnyFeature}
+function FlashMaxSim.pair_forward_ka(backend::ROCBackend, q::ROCMatrix{T}, d::ROCMatrix{T},
+                                     qmask::DenseMask{1}, dmask::DenseMask{1},
+                                     neg::T) where {T<:AnyFeature}
+    gfx950() || return @invoke FlashMaxSim.pair_forward_ka(backend::KABackend, q, d, qmask, dmask, neg)
     dim, Tq, Td = FlashMaxSim.require_pair_shapes(q, d, qmask, dmask)
     argmax_u = AMDGPU.zeros(Int32, Tq)
     score = AMDGPU.zeros(Float32, 1)     # length-1, stays on the device
@@ -245,10 +286,10 @@ function FlashMaxSim.pair_forward_ka(::ROCBackend, q::ROCMatrix{T}, d::ROCMatrix
     score, argmax_u
 end
 
-function FlashMaxSim.paired_forward_ka(::ROCBackend, Q::ROCArray{T,3}, D::ROCArray{T,3},
-                                       qmask::AbstractMatrix{Bool},
-                                       dmask::AbstractMatrix{Bool},
-                                       ::T) where {T<:AnyFeature}
+function FlashMaxSim.paired_forward_ka(backend::ROCBackend, Q::ROCArray{T,3}, D::ROCArray{T,3},
+                                       qmask::DenseMask{2}, dmask::DenseMask{2},
+                                       neg::T) where {T<:AnyFeature}
+    gfx950() || return @invoke FlashMaxSim.paired_forward_ka(backend::Any, Q, D, qmask, dmask, neg)
     dim, Tq, Td, B = FlashMaxSim.require_paired_shapes(Q, D, qmask, dmask)
     args = AMDGPU.zeros(Int32, Tq, B)
     scores = AMDGPU.zeros(Float32, B)
@@ -256,10 +297,10 @@ function FlashMaxSim.paired_forward_ka(::ROCBackend, Q::ROCArray{T,3}, D::ROCArr
     scores, args
 end
 
-function FlashMaxSim.inbatch_forward_ka(::ROCBackend, Q::ROCArray{T,3}, D::ROCArray{T,3},
-                                        qmask::AbstractMatrix{Bool},
-                                        dmask::AbstractMatrix{Bool},
-                                        ::T) where {T<:AnyFeature}
+function FlashMaxSim.inbatch_forward_ka(backend::ROCBackend, Q::ROCArray{T,3}, D::ROCArray{T,3},
+                                        qmask::DenseMask{2}, dmask::DenseMask{2},
+                                        neg::T) where {T<:AnyFeature}
+    gfx950() || return @invoke FlashMaxSim.inbatch_forward_ka(backend::Any, Q, D, qmask, dmask, neg)
     dim, Tq, Bq, Td, Bd = FlashMaxSim.require_inbatch_shapes(Q, D, qmask, dmask)
     S = AMDGPU.zeros(Float32, Bd, Bq)
     args = AMDGPU.zeros(Int32, Tq, Bd, Bq)
@@ -268,12 +309,11 @@ function FlashMaxSim.inbatch_forward_ka(::ROCBackend, Q::ROCArray{T,3}, D::ROCAr
     S, args
 end
 
-function FlashMaxSim.candidates_forward_ka(::ROCBackend, Q::ROCArray{T,3},
-                                           gallery::ROCArray{T,3},
-                                           idxs::AbstractMatrix{<:Integer},
-                                           qmask::AbstractMatrix{Bool},
-                                           dmask::AbstractMatrix{Bool},
+function FlashMaxSim.candidates_forward_ka(backend::ROCBackend, Q::ROCArray{T,3},
+                                           gallery::ROCArray{T,3}, idxs::DenseIndex,
+                                           qmask::DenseMask{2}, dmask::DenseMask{2},
                                            neg::T) where {T<:AnyFeature}
+    gfx950() || return @invoke FlashMaxSim.candidates_forward_ka(backend::Any, Q, gallery, idxs, qmask, dmask, neg)
     dim, Tq, B, Td, N = FlashMaxSim.require_candidates_shapes(Q, gallery, idxs, qmask, dmask)
     idx = FlashMaxSim.indices_on(Q, idxs)
     C = size(idx, 1)
@@ -284,12 +324,11 @@ function FlashMaxSim.candidates_forward_ka(::ROCBackend, Q::ROCArray{T,3},
     scores, args
 end
 
-function FlashMaxSim.packed_forward_ka(::ROCBackend, q::ROCMatrix{T}, P::PackedSeq,
-                                       qmask::AbstractVector{Bool}, ::T) where {T<:AnyFeature}
+function FlashMaxSim.packed_forward_ka(backend::ROCBackend, q::ROCMatrix{T}, P::DensePacked{T},
+                                       qmask::DenseMask{1}, neg::T) where {T<:AnyFeature}
+    gfx950() || return @invoke FlashMaxSim.packed_forward_ka(backend::KABackend, q, P, qmask, neg)
     Tq, B = FlashMaxSim.require_packed_shapes(q, P, qmask)
     tokens, cu = P.tokens, P.cu
-    eltype(tokens) === T || throw(ArgumentError("PackedSeq tokens must have the query eltype"))
-    eltype(cu) === Int32 || throw(ArgumentError("PackedSeq cu must be Int32 on the device"))
     args = AMDGPU.zeros(Int32, Tq, B)
     scores = AMDGPU.zeros(Float32, B)
     c_packed_scan(dtype_code(T), args, nothing, q, tokens, cu, qmask, size(q, 1), Tq, B,
@@ -297,12 +336,11 @@ function FlashMaxSim.packed_forward_ka(::ROCBackend, q::ROCMatrix{T}, P::PackedS
     scores, args
 end
 
-function FlashMaxSim.varlen_forward_ka(::ROCBackend, Q::PackedSeq{<:ROCMatrix{T}},
-                                       D::PackedSeq{<:ROCMatrix{T}}, ::T) where {T<:AnyFeature}
+function FlashMaxSim.varlen_forward_ka(backend::ROCBackend, Q::DensePacked{T},
+                                       D::DensePacked{T}, neg::T) where {T<:AnyFeature}
+    gfx950() || return @invoke FlashMaxSim.varlen_forward_ka(backend::KABackend, Q, D, neg)
     N, max_q = FlashMaxSim.require_varlen_shapes(Q, D)
     Qtokens, Dtokens, cu_q, cu_d = Q.tokens, D.tokens, Q.cu, D.cu
-    (eltype(cu_q) === Int32 && eltype(cu_d) === Int32) ||
-        throw(ArgumentError("PackedSeq cu must be Int32 on the device"))
     args = AMDGPU.zeros(Int32, max_q, N)
     scores = AMDGPU.zeros(Float32, N)
     c_varlen_scan(dtype_code(T), args, nothing, Qtokens, Dtokens, cu_q, cu_d, size(Qtokens, 1),
@@ -320,6 +358,7 @@ scale_code(::Type{Float32}) = FMS_F32
 scale_code(::Type{Float16}) = FMS_F16
 
 function FlashMaxSim.quantize_int8_symmetric(X::ROCArray{T}) where {T<:ScaleType}
+    gfx950() || return @invoke FlashMaxSim.quantize_int8_symmetric(X::AbstractArray{T})
     ndims(X) in (2, 3) || throw(ArgumentError("quantize_int8_symmetric takes (dim, T[, B]) features"))
     dim = size(X, 1)
     codes = similar(X, Int8)
@@ -333,11 +372,12 @@ function FlashMaxSim.quantize_int8_symmetric(X::ROCArray{T}) where {T<:ScaleType
     Int8Index(codes, scales)
 end
 
-function FlashMaxSim.launch_int8_pair_scan!(::ROCBackend, args::ROCVector{Int32},
+function FlashMaxSim.launch_int8_pair_scan!(backend::ROCBackend, args::ROCVector{Int32},
                                             partial::ROCVector{Float32}, qc::ROCMatrix{Int8},
                                             qs::ROCVector{S1}, dc::ROCMatrix{Int8},
-                                            ds::ROCVector{S2}, qmask,
-                                            dmask) where {S1<:ScaleType, S2<:ScaleType}
+                                            ds::ROCVector{S2}, qmask::DenseMask{1},
+                                            dmask::DenseMask{1}) where {S1<:ScaleType, S2<:ScaleType}
+    gfx950() || return @invoke FlashMaxSim.launch_int8_pair_scan!(backend::KAGPU, args, partial, qc, qs, dc, ds, qmask, dmask)
     dim, Tq = size(qc)
     check(ccall((:fms_launch_int8_pair_scan, libfms), Int32,
                 (Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Int32, Ptr{Cvoid}, Ptr{Cvoid},
@@ -350,11 +390,12 @@ function FlashMaxSim.launch_int8_pair_scan!(::ROCBackend, args::ROCVector{Int32}
     nothing
 end
 
-function FlashMaxSim.launch_int8_paired_scan!(::ROCBackend, args::ROCMatrix{Int32},
+function FlashMaxSim.launch_int8_paired_scan!(backend::ROCBackend, args::ROCMatrix{Int32},
                                               partial::ROCMatrix{Float32},
                                               Qc::ROCArray{Int8,3}, Qs::ROCMatrix{S1},
                                               Dc::ROCArray{Int8,3}, Ds::ROCMatrix{S2},
-                                              qmask, dmask) where {S1<:ScaleType, S2<:ScaleType}
+                                              qmask::DenseMask{2}, dmask::DenseMask{2}) where {S1<:ScaleType, S2<:ScaleType}
+    gfx950() || return @invoke FlashMaxSim.launch_int8_paired_scan!(backend::KAGPU, args, partial, Qc, Qs, Dc, Ds, qmask, dmask)
     dim, Tq, B = size(Qc)
     check(ccall((:fms_launch_int8_paired_scan, libfms), Int32,
                 (Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Int32, Ptr{Cvoid}, Ptr{Cvoid},
@@ -373,13 +414,17 @@ end
 The INT8 candidate layout (no reference method: the candidate conventions of
 `maxsim(Q, gallery, idxs)`, src/forward_layouts.jl:272-290, applied to an Int8Index
 gallery).  Q is quantised on the fly; `S (C, B)` Float32 with `neg` at invalid
-indices, `args (Tq, C, B)`.
+indices, `args (Tq, C, B)`.  gfx950 only (there is no reference method to fall
+back to).
 """
-function int8_candidates_scan(Q::ROCArray{T,3}, D::Int8Index, idxs::ROCMatrix{<:Integer};
-                              qmask = nothing, dmask = nothing,
+function int8_candidates_scan(Q::ROCArray{T,3}, D::Int8Index, idxs::DenseIndex;
+                              qmask::MaybeMask{2} = nothing, dmask::MaybeMask{2} = nothing,
                               neg::Real = -1.0f4) where {T<:ScaleType}
+    require_gfx950("INT8 candidate scan")
     QQ = FlashMaxSim.quantize_int8_symmetric(Q)
     Qc, Qs, Gc, Gs = QQ.codes, QQ.scales, D.codes, D.scales
+    (Gc isa ROCArray{Int8,3} && Gs isa ROCMatrix) ||
+        throw(ArgumentError("int8_candidates_scan: the Int8Index must be dense device arrays"))
     dim, Tq, B = size(Qc)
     Td, N = size(Gc, 2), size(Gc, 3)
     size(Gc, 1) == dim || throw(DimensionMismatch("feature dim"))
@@ -404,16 +449,18 @@ end
 # ---- pullbacks on the argmax tape ----------------------------------------------
 # Δ and inv_n arrive in the feature eltype (convert_scores in src/rrule.jl), and the
 # gradients are feature-eltype buffers, which is what the library reads and writes
-# for every feature type; inv_n === nothing passes NULL (all ones).
+# for every feature type; inv_n === nothing passes NULL (all ones).  On another
+# architecture each invokes the reference method for the same strategy marker.
 
 for M in (FlashMaxSim.AtomicUnified, FlashMaxSim.InvGrid)
     @eval begin
-        function FlashMaxSim.pair_apply_pullback!(::$M, ::ROCBackend, dq::ROCMatrix{T},
+        function FlashMaxSim.pair_apply_pullback!(mode::$M, backend::ROCBackend, dq::ROCMatrix{T},
                                                   dd::ROCMatrix{T}, q::ROCMatrix{T},
-                                                  d::ROCMatrix{T}, qmask,
+                                                  d::ROCMatrix{T}, qmask::MaybeMask{1},
                                                   argmax_u::ROCVector{Int32},
                                                   delta::ROCVector{T}, dim, Tq,
                                                   Td) where {T<:AnyFeature}
+            gfx950() || return @invoke FlashMaxSim.pair_apply_pullback!(mode, backend::Any, dq, dd, q, d, qmask, argmax_u, delta, dim, Tq, Td)
             check(ccall((:fms_pair_pullback, libfms), Int32,
                         (Int32, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid},
                          Ptr{Cvoid}, Ptr{Cvoid}, Int64, Int64, Int64, Ptr{Cvoid}),
@@ -423,12 +470,13 @@ for M in (FlashMaxSim.AtomicUnified, FlashMaxSim.InvGrid)
             nothing
         end
 
-        function FlashMaxSim.paired_apply_pullback!(::$M, ::ROCBackend, dQ::ROCArray{T,3},
+        function FlashMaxSim.paired_apply_pullback!(mode::$M, backend::ROCBackend, dQ::ROCArray{T,3},
                                                     dD::ROCArray{T,3}, Q::ROCArray{T,3},
-                                                    D::ROCArray{T,3}, qmask,
+                                                    D::ROCArray{T,3}, qmask::MaybeMask{2},
                                                     args::ROCMatrix{Int32}, Delta::ROCVector{T},
-                                                    inv_n, dim, Tq, B,
+                                                    inv_n::Union{ROCVector{T}, Nothing}, dim, Tq, B,
                                                     Td) where {T<:AnyFeature}
+            gfx950() || return @invoke FlashMaxSim.paired_apply_pullback!(mode, backend::Any, dQ, dD, Q, D, qmask, args, Delta, inv_n, dim, Tq, B, Td)
             check(ccall((:fms_paired_pullback, libfms), Int32,
                         (Int32, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid},
                          Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Int64, Int64, Int64, Int64, Ptr{Cvoid}),
@@ -438,12 +486,14 @@ for M in (FlashMaxSim.AtomicUnified, FlashMaxSim.InvGrid)
             nothing
         end
 
-        function FlashMaxSim.inbatch_apply_pullback!(::$M, ::ROCBackend, dQ::ROCArray{T,3},
+        function FlashMaxSim.inbatch_apply_pullback!(mode::$M, backend::ROCBackend, dQ::ROCArray{T,3},
                                                      dD::ROCArray{T,3}, Q::ROCArray{T,3},
-                                                     D::ROCArray{T,3}, qmask,
+                                                     D::ROCArray{T,3}, qmask::MaybeMask{2},
                                                      args::ROCArray{Int32,3},
-                                                     Delta::ROCMatrix{T}, inv_n, dim, Tq, Bq,
+                                                     Delta::ROCMatrix{T},
+                                                     inv_n::Union{ROCVector{T}, Nothing}, dim, Tq, Bq,
                                                      Td, Bd) where {T<:AnyFeature}
+            gfx950() || return @invoke FlashMaxSim.inbatch_apply_pullback!(mode, backend::Any, dQ, dD, Q, D, qmask, args, Delta, inv_n, dim, Tq, Bq, Td, Bd)
             check(ccall((:fms_inbatch_pullback, libfms), Int32,
                         (Int32, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid},
                          Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Int64, Int64, Int64, Int64, Int64,
@@ -454,12 +504,15 @@ for M in (FlashMaxSim.AtomicUnified, FlashMaxSim.InvGrid)
             nothing
         end
 
-        function FlashMaxSim.candidates_apply_pullback!(::$M, ::ROCBackend, dQ::ROCArray{T,3},
+        function FlashMaxSim.candidates_apply_pullback!(mode::$M, backend::ROCBackend, dQ::ROCArray{T,3},
                                                         dG::ROCArray{T,3}, Q::ROCArray{T,3},
-                                                        gallery::ROCArray{T,3}, idx, qmask,
+                                                        gallery::ROCArray{T,3}, idx::DenseIndex,
+                                                        qmask::MaybeMask{2},
                                                         args::ROCArray{Int32,3},
-                                                        Delta::ROCMatrix{T}, inv_n, dim, Tq, B,
+                                                        Delta::ROCMatrix{T},
+                                                        inv_n::Union{ROCVector{T}, Nothing}, dim, Tq, B,
                                                         Td, C, N) where {T<:AnyFeature}
+            gfx950() || return @invoke FlashMaxSim.candidates_apply_pullback!(mode, backend::Any, dQ, dG, Q, gallery, idx, qmask, args, Delta, inv_n, dim, Tq, B, Td, C, N)
             check(ccall((:fms_candidates_pullback, libfms), Int32,
                         (Int32, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Int32,
                          Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Int64, Int64, Int64,
@@ -471,12 +524,12 @@ for M in (FlashMaxSim.AtomicUnified, FlashMaxSim.InvGrid)
             nothing
         end
 
-        function FlashMaxSim.packed_apply_pullback!(::$M, ::ROCBackend, Delta::ROCVector{T},
-                                                    q::ROCMatrix{T}, P::PackedSeq, qmask,
-                                                    args::ROCMatrix{Int32},
-                                                    inv_n) where {T<:AnyFeature}
+        function FlashMaxSim.packed_apply_pullback!(mode::$M, backend::ROCBackend, Delta::ROCVector{T},
+                                                    q::ROCMatrix{T}, P::DensePacked{T},
+                                                    qmask::MaybeMask{1}, args::ROCMatrix{Int32},
+                                                    inv_n::Union{ROCVector{T}, Nothing}) where {T<:AnyFeature}
+            gfx950() || return @invoke FlashMaxSim.packed_apply_pullback!(mode, backend::Any, Delta, q, P, qmask, args, inv_n)
             tokens, cu = P.tokens, P.cu
-            eltype(tokens) === T || throw(ArgumentError("PackedSeq tokens must have the query eltype"))
             dq = similar(q)
             dP = similar(tokens)
             dim, Tq = size(q)
@@ -491,11 +544,11 @@ for M in (FlashMaxSim.AtomicUnified, FlashMaxSim.InvGrid)
             dq, dP
         end
 
-        function FlashMaxSim.varlen_apply_pullback!(::$M, ::ROCBackend, Delta::ROCVector{T},
-                                                    Q::PackedSeq{<:ROCMatrix{T}},
-                                                    D::PackedSeq{<:ROCMatrix{T}},
+        function FlashMaxSim.varlen_apply_pullback!(mode::$M, backend::ROCBackend, Delta::ROCVector{T},
+                                                    Q::DensePacked{T}, D::DensePacked{T},
                                                     args::ROCMatrix{Int32},
-                                                    inv_n) where {T<:AnyFeature}
+                                                    inv_n::Union{ROCVector{T}, Nothing}) where {T<:AnyFeature}
+            gfx950() || return @invoke FlashMaxSim.varlen_apply_pullback!(mode, backend::Any, Delta, Q, D, args, inv_n)
             Qtokens, Dtokens, cu_q, cu_d = Q.tokens, D.tokens, Q.cu, D.cu
             dQ = similar(Qtokens)
             dD = similar(Dtokens)
@@ -516,7 +569,8 @@ end
 # ---- extensions without a reference method -------------------------------------
 # Called as FlashMaxSimHIPExt.packed_multi_scan(Q, P), FlashMaxSimHIPExt.topk(S, k) and
 # FlashMaxSimHIPExt.load_int8_index(path)
-# (Base.get_extension(FlashMaxSim, :FlashMaxSimHIPExt)).
+# (Base.get_extension(FlashMaxSim, :FlashMaxSimHIPExt)).  The first two run on
+# gfx950 only and say so otherwise.
 
 """
     packed_multi_scan(Q::ROCArray{T,3}, P::PackedSeq; qmask = nothing) -> (S, args)
@@ -526,11 +580,11 @@ Float32 and the 1-based document-local tape `args (Tq, B, nq)`.  Column i equals
 `maxsim(Q[:, :, i], P, qmask[:, i]; normalize)` (src/packed.jl:178-210) within the
 score tolerance; `normalize` is fused into the scan's score write.
 """
-function packed_multi_scan(Q::ROCArray{T,3}, P::PackedSeq;
-                           qmask = nothing, normalize::Bool = false) where {T<:AnyFeature}
+function packed_multi_scan(Q::ROCArray{T,3}, P::DensePacked{T};
+                           qmask::MaybeMask{2} = nothing, normalize::Bool = false) where {T<:AnyFeature}
+    require_gfx950("multi-query packed scan")
     dim, Tq, nq = size(Q)
     tokens, cu, max_len = P.tokens, P.cu, P.max_len
-    eltype(tokens) === T || throw(ArgumentError("PackedSeq tokens must have the query eltype"))
     B = length(cu) - 1
     scores = AMDGPU.zeros(Float32, B, nq)
     args = AMDGPU.zeros(Int32, Tq, B, nq)
@@ -553,6 +607,7 @@ descending, `idx (k, ncols)` 1-based row indices -- `partialsortperm(S[:, i], 1:
 rev = true)` with a stable sort, for every column in one launch.  1 <= k <= 1024.
 """
 function topk(scores::ROCMatrix{Float32}, k::Integer)
+    require_gfx950("topk")
     ncols, nrows = size(scores)   # C rows: one score row per query column
     vals = AMDGPU.zeros(Float32, k, nrows)
     idx = AMDGPU.zeros(Int32, k, nrows)

@@ -47,7 +47,8 @@
  * Reentrant: concurrent calls on different streams are independent.  The
  * only process-wide state is a per-device memory pool that the candidate
  * scans draw their stream-ordered workspace from (kept for the life of the
- * process) and the grouping mode of fms_candidates_grouping.
+ * process) and the no-allocation entry point's per-device scratch array;
+ * the grouping mode of fms_candidates_grouping is per host thread.
  */
 #ifndef FLASHMAXSIM_HIP_H
 #define FLASHMAXSIM_HIP_H
@@ -135,7 +136,9 @@ fms_status fms_launch_candidates_scan(int32_t dtype, int32_t* args, float* parti
  * 1 = always, 2 = never, 3 = always and without the query-tile copy (the
  * 16-bit document-batch scan then reads the query tiles from Q, as it does
  * when the no-allocation scratch cannot hold that copy; a test switch).
- * Returns the previous mode, or -1 for an invalid mode.
+ * The mode belongs to the calling host thread and applies to that thread's
+ * later calls only.  Returns the thread's previous mode, or -1 for an
+ * invalid mode.
  */
 int32_t fms_candidates_grouping(int32_t mode);
 
@@ -149,9 +152,10 @@ int32_t fms_candidates_grouping(int32_t mode);
  * library pool: the call performs no hipMalloc / hipFree and calls no
  * allocating library routine.  A call whose grouping workspace would exceed
  * the array -- about 20 bytes per pair plus 4 per gallery document, some
- * 1.4M pairs over a 1M-document gallery -- returns FMS_ESCRATCH and launches
- * nothing (fms_candidates_grouping(2) scans in output order, which needs no
- * workspace).  Every call on one GPU uses that GPU's single array: calls that
+ * 1.4M pairs over a 1M-document gallery -- scans in output order (identical
+ * results, no workspace) when the thread's grouping mode is automatic, and
+ * returns FMS_ESCRATCH and launches nothing when grouping was forced
+ * (modes 1 and 3).  Every call on one GPU uses that GPU's single array: calls that
  * overlap on one GPU (concurrent streams) race and must be serialised by the
  * caller.  The array's previous contents never matter (the kernels clear what
  * they count).
@@ -425,6 +429,13 @@ fms_status fms_debug_mfma_layout(float* out, int32_t dtype_or_int8, void* stream
  * token l + 1 -- what the scans' tile close relies on.
  */
 fms_status fms_debug_cross_lane(float* out, void* stream);
+
+/*
+ * Test-only: the number of workspace allocations the library has requested
+ * from its stream-ordered pool in this process (no reference counterpart).
+ * Lets a test show that fms_launch_candidates_scan_noalloc takes none.
+ */
+uint64_t fms_debug_workspace_allocs(void);
 
 /*
  * Test-only: streaming read of `bytes` (multiple of 16, 16-byte aligned)

@@ -138,11 +138,11 @@ static float pair_core(int dtype, const void* q, const void* d,
     int64_t t, u, uu, k;
     float* dT = tile;                         /* DOC_TILE x dim, token-fastest */
     float* St = tile + dim * FMSO_DOC_TILE;   /* DOC_TILE x Tq, fp32 */
-    for (t = 0; t < Tq; ++t) { argmax_u[t] = 0; mx[t] = 0.0f; } /* :126-127 */
-    widen_f32(dtype, q, dim * Tq, qf);                            /* :128 */
-    for (u = 0; u < Td; u += FMSO_DOC_TILE) {                     /* :130 */
+    for (t = 0; t < Tq; ++t) { argmax_u[t] = 0; mx[t] = 0.0f; } /* :68-69 */
+    widen_f32(dtype, q, dim * Tq, qf);                            /* :70 */
+    for (u = 0; u < Td; u += FMSO_DOC_TILE) {                     /* :72-74 */
         int64_t w = (Td - u < FMSO_DOC_TILE) ? (Td - u) : FMSO_DOC_TILE;
-        /* widen the tile (:133), stored transposed so the GEMM below
+        /* widen the tile (:75), stored transposed so the GEMM below
          * vectorises over document tokens */
         for (uu = 0; uu < w; ++uu) {
             const void* src = advance(d, (u + uu) * dim, dtype);
@@ -157,7 +157,7 @@ static float pair_core(int dtype, const void* q, const void* d,
                 for (k = 0; k < dim; ++k) dT[k * FMSO_DOC_TILE + uu] = bf16_to_float(s[k]);
             }
         }
-        /* Stile = dA' * qA  (:134).  Each cell accumulates k = 1..dim in
+        /* Stile = dA' * qA  (:76).  Each cell accumulates k = 1..dim in
          * order (the KA token kernel's order, kernels_forward.jl:45-48);
          * the loop nest only vectorises across document tokens. */
         for (t = 0; t < Tq; ++t) {
@@ -170,7 +170,7 @@ static float pair_core(int dtype, const void* q, const void* d,
                 for (uu = 0; uu < w; ++uu) st[uu] += dk[uu] * qk;
             }
         }
-        for (t = 0; t < Tq; ++t) {                                 /* :135-145 */
+        for (t = 0; t < Tq; ++t) {                                 /* :77-87 */
             if (qmask && !qmask[t]) continue;
             for (uu = 0; uu < w; ++uu) {
                 if (dmask && !dmask[u + uu]) continue;
@@ -182,7 +182,7 @@ static float pair_core(int dtype, const void* q, const void* d,
             }
         }
     }
-    float score = 0.0f;                                            /* :148-151 */
+    float score = 0.0f;                                            /* :90-93 */
     for (t = 0; t < Tq; ++t) {
         if ((!qmask || qmask[t]) && argmax_u[t] > 0) score += mx[t];
         else mx[t] = 0.0f;
@@ -687,7 +687,7 @@ double fmso_dense_pair_f64(int dtype, const void* q, const void* d,
  * with accumulate_doc! AtomicUnified, accumulate.jl:12-29): for every query token t
  * with qmask[t] and 1 <= u = argmax[t] <= Td,
  *     dq[:, t] += delta * d[:, u]      and      dd[:, u] += delta * q[:, t],
- * t ascending.  InvGrid (accumulate.jl:31-39, invgrid.jl:43-65) visits the same
+ * t ascending.  InvGrid (accumulate.jl:31-39, invgrid.jl:46-65) visits the same
  * sources of each destination in the same (ascending t) order.
  * The reference computes in the feature type T; this restatement pins the
  * mathematics: delta and both accumulations in fp64.  dq/dd are ADDED to.
@@ -724,7 +724,7 @@ void fmso_paired_backward(int dtype, const void* Q, const void* D, const uint8_t
                           dQ + b * Tq * dim, dD + b * Td * dim);
 }
 
-/* inbatch_pullback CPU (backward_layouts.jl:68-94): j outer, i inner; pair (i, j) has
+/* inbatch_pullback CPU (backward_layouts.jl:69-94): j outer, i inner; pair (i, j) has
  * delta = Delta[j, i] * inv_n[i] (Delta (Bd, Bq) column-major: j + Bd*i) and tape
  * args[t, j, i] at t + Tq*(j + Bd*i). */
 void fmso_inbatch_backward(int dtype, const void* Q, const void* D, const uint8_t* qmask,
@@ -744,7 +744,7 @@ void fmso_inbatch_backward(int dtype, const void* Q, const void* D, const uint8_
         }
 }
 
-/* candidates_pullback CPU (backward_layouts.jl:136-165): b outer, c inner; pair
+/* candidates_pullback CPU (backward_layouts.jl:137-165): b outer, c inner; pair
  * p = c + C*b scores Q_b against gallery doc idxs[p] (1-based; outside 1..N the
  * pair contributes nothing); delta = Delta[p] * inv_n[b]. */
 void fmso_candidates_backward(int dtype, const void* Q, const void* G, const int64_t* idxs,

@@ -136,3 +136,41 @@ def test_grouped_int8_bit_exact(device, grouping, idx_dtype):
     assert np.array_equal(args.numpy(), a_o)
     assert np.array_equal(part.numpy().view(np.uint32), p_o.view(np.uint32))
     np.testing.assert_allclose(S.numpy(), S_o, rtol=1e-6, atol=1e-6)
+
+
+def test_one_level_sort_and_three_launch_scan(device, grouping):
+    """A gallery too large for the two-level bucket sort: 4,200,000 one-token
+    documents (d = 32, 269 MB) and 1,126,400 pairs give 4,096 buckets x 1,100
+    pair tiles, past the bucket table, so the pairs take the one-level sort, and
+    4,200,001 document counters are 1,026 prefix-scan tiles, past the 1,024 that
+    the two-launch scan handles.  Forced document order must equal output order
+    bit for bit, and a sample of queries must match the oracle."""
+    rng = np.random.default_rng(4200)
+    N, Td, dim, Tq, B, C = 4_200_000, 1, 32, 4, 1100, 1024
+    gen = torch.Generator(device=device)
+    gen.manual_seed(4200)
+    Q = torch.randn(B, Tq, dim, generator=gen, device=device).to(torch.float16)
+    G = torch.randn(N, Td, dim, generator=gen, device=device).to(torch.float16)
+    idx = torch.randint(1, N + 1, (B, C), generator=gen, device=device, dtype=torch.int64)
+    idx.view(-1)[::101] = 0
+    qm = torch.ones(B, Tq, dtype=torch.bool, device=device)
+    dm = torch.ones(N, Td, dtype=torch.bool, device=device)
+    grouping("always")
+    grouped = _run_float(device, Q, G, idx, qm, dm, N, -2.0)
+    grouping("never")
+    direct = _run_float(device, Q, G, idx, qm, dm, N, -2.0)
+    _bitwise_equal(grouped, direct)
+    rows = rng.choice(B, size=32, replace=False)
+    rows_t = torch.from_numpy(rows).to(device)
+    sub = idx[rows_t].cpu().numpy()
+    used = np.unique(sub[sub > 0])
+    remap = np.zeros(N + 1, np.int64)
+    remap[used] = np.arange(1, len(used) + 1)
+    Go = G[torch.from_numpy(used - 1).to(device)].cpu().numpy()
+    S_o, a_o, _ = oracle.candidates_forward(Q[rows_t].cpu().numpy(), Go, remap[sub],
+                                            np.ones((32, Tq), np.uint8),
+                                            np.ones((len(used), Td), np.uint8), -2.0)
+    S_g = grouped[0].numpy()[rows]
+    a_g = grouped[1].numpy()[rows]
+    assert np.allclose(S_g, S_o, rtol=2e-3, atol=2e-3)
+    assert np.array_equal(a_g, a_o)

@@ -187,6 +187,134 @@ def test_bfloat16_reaches_the_library_only_through_drivers():
             "c_inbatch_scan" in body, m.group(1)
 
 
+# The backend type each overridden reference method is declared on, so that
+# `@invoke` with that annotation selects the reference method and never the
+# extension's ROCBackend one.
+REFERENCE_BACKEND = {
+    # src/forward_pair.jl:130, src/forward_layouts.jl:139,306, src/packed.jl,
+    # src/quant.jl: launch_*_scan!(backend::GPU, ...) run the KA tile kernels
+    "launch_pair_scan!": "KAGPU", "launch_paired_scan!": "KAGPU",
+    "launch_candidates_scan!": "KAGPU", "launch_packed_scan!": "KAGPU",
+    "launch_varlen_scan!": "KAGPU", "launch_int8_pair_scan!": "KAGPU",
+    "launch_int8_paired_scan!": "KAGPU",
+    # src/forward_layouts.jl:201: inbatch_device_scan!(backend, ...) untyped
+    "inbatch_device_scan!": "Any",
+    # src/forward_pair.jl:104, src/packed.jl:178,262: (backend::Backend, ...)
+    "pair_forward_ka": "KABackend", "packed_forward_ka": "KABackend",
+    "varlen_forward_ka": "KABackend",
+    # src/forward_layouts.jl:112,188,272: untyped backend
+    "paired_forward_ka": "Any", "inbatch_forward_ka": "Any", "candidates_forward_ka": "Any",
+    # src/backward_*.jl, src/packed.jl: (::Strategy, backend, ...) untyped backend
+    "pair_apply_pullback!": "Any", "paired_apply_pullback!": "Any",
+    "inbatch_apply_pullback!": "Any", "candidates_apply_pullback!": "Any",
+    "packed_apply_pullback!": "Any", "varlen_apply_pullback!": "Any",
+}
+
+
+def arg_list(sig):
+    """[(name, type or None)] of a Julia signature's positional arguments."""
+    out = []
+    for a in split_top(sig.split(";")[0]):
+        a = " ".join(a.split())
+        m = re.fullmatch(r"(\w*)\s*(?:::\s*(.+))?", a)
+        assert m, a
+        out.append((m.group(1), m.group(2)))
+    return out
+
+
+def override_bodies(text, prefix=r"FlashMaxSim\."):
+    """(name, signature, first body statement) of every `function FlashMaxSim.<name>(`
+    (or of the plain functions `function <name>(` with prefix "")."""
+    out = []
+    for m in re.finditer(r"function " + prefix + r"(\w+!?)\(", text):
+        i, depth = m.end(), 1
+        while depth:
+            depth += {"(": 1, ")": -1}.get(text[i], 0)
+            i += 1
+        rest = text[i:].split("\n", 1)[1]
+        first = next(line.strip() for line in rest.split("\n") if line.strip())
+        out.append((m.group(1), text[m.end():i - 1], first))
+    return out
+
+
+def test_every_override_falls_back_to_the_reference_off_gfx950():
+    """On an AMD GPU that is not gfx950 every override keeps the reference's own
+    method, as the CUDA extension does when its tensor cores are off
+    (ext/FlashMaxSimCUDAExt.jl:60-66): its first statement is
+    `gfx950() || return @invoke FlashMaxSim.<same method>(<same arguments>)` with the
+    backend annotated as the reference method declares it."""
+    text = open(EXT).read()
+    bodies = override_bodies(text)
+    names = {b[0] for b in bodies}
+    assert set(REFERENCE_BACKEND) | {"quantize_int8_symmetric"} == names, names
+    for name, sig, first in bodies:
+        m = re.fullmatch(r"gfx950\(\) \|\| return @invoke FlashMaxSim\.(\w+!?)\((.*)\)", first)
+        assert m, f"{name}: first statement {first!r}"
+        assert m.group(1) == name, f"{name}: invokes {m.group(1)}"
+        declared = [n for n, _ in arg_list(sig)]
+        invoked = arg_list(m.group(2))
+        assert [n for n, _ in invoked] == declared, f"{name}: {invoked} vs {declared}"
+        if name == "quantize_int8_symmetric":
+            assert invoked == [("X", "AbstractArray{T}")], invoked
+            continue
+        bi = declared.index("backend")
+        assert arg_list(sig)[bi][1] == "ROCBackend", name
+        assert invoked[bi][1] == REFERENCE_BACKEND[name], f"{name}: backend::{invoked[bi][1]}"
+        # only the backend (and nothing else) is widened
+        assert all(t is None for k, (_, t) in enumerate(invoked) if k != bi), name
+    # the extension-only entry points have no reference method: they refuse clearly
+    plain = {n: f for n, _, f in override_bodies(text, prefix="")}
+    for fn in ("packed_multi_scan", "topk", "int8_candidates_scan"):
+        assert plain[fn].startswith("require_gfx950("), f"{fn}: {plain[fn]!r}"
+
+
+# Arguments whose device pointer the library reads, and the dense types they must
+# carry so that a wrapped array never reaches a raw-pointer ccall.
+POINTER_ARG_TYPES = {
+    "qmask": r"(DenseMask|MaybeMask)\{[123]\}",
+    "dmask": r"(DenseMask|MaybeMask)\{[123]\}",
+    "idx": r"DenseIndex", "idxs": r"DenseIndex",
+    "inv_n": r"Union\{ROCVector\{T\}, Nothing\}",
+    "P": r"DensePacked\{T\}", "Q": r"ROCArray\{T,3\}|DensePacked\{T\}",
+    "D": r"ROCArray\{T,3\}|DensePacked\{T\}|Int8Index",
+}
+SCALAR_ARGS = {"dim", "Tq", "Td", "B", "Bq", "Bd", "C", "N", "neg", "normalize"}
+
+
+def test_pointer_arguments_are_dense_device_arrays():
+    """Masks, indices, inverse counts and PackedSeq storage are typed as dense
+    ROCArrays in every override: a PermutedDimsArray or strided view mask
+    (accepted by the reference, src/colocation.jl:18-24) then matches no
+    extension method and keeps the reference path instead of reaching `dptr`."""
+    text = open(EXT).read()
+    assert re.search(r"^const DenseMask\{N\} = ROCArray\{Bool,N\}$", text, re.M)
+    assert re.search(r"^const MaybeMask\{N\} = Union\{ROCArray\{Bool,N\}, Nothing\}$", text, re.M)
+    assert re.search(r"^const DenseIndex = ROCMatrix\{<:IndexEltype\}$", text, re.M)
+    assert re.search(r"^const DensePacked\{T\} = PackedSeq\{<:ROCMatrix\{T\}, <:ROCVector\{Int32\}\}$",
+                     text, re.M)
+    # dptr exists only for dense device arrays and nothing
+    assert set(re.findall(r"^dptr\((.*?)\) =", text, re.M)) == {"x::ROCArray", "::Nothing"}
+    sigs = [(n, s) for n, s, _ in override_bodies(text)]
+    plain = {n: s for n, s, _ in override_bodies(text, prefix="")}
+    for fn in ("int8_candidates_scan", "packed_multi_scan", "topk"):
+        sigs.append((fn, plain[fn]))
+    for name, sig in sigs:
+        args = arg_list(sig)
+        kw = sig.split(";")[1] if ";" in sig else ""
+        for a in split_top(kw):
+            mk = re.fullmatch(r"(\w+)\s*::\s*(.+?)\s*=.*", " ".join(a.split()))
+            if mk:
+                args.append((mk.group(1), mk.group(2)))
+        for arg, typ in args:
+            if arg in ("backend", "mode") or arg in SCALAR_ARGS or name == "topk":
+                continue
+            assert typ is not None, f"{name}: argument {arg} is untyped"
+            if arg in POINTER_ARG_TYPES:
+                assert re.fullmatch(POINTER_ARG_TYPES[arg], typ), f"{name}: {arg}::{typ}"
+            else:
+                assert re.match(r"ROC(Array|Vector|Matrix)\{|Int8Index$", typ), f"{name}: {arg}::{typ}"
+
+
 def test_project_fragment_wires_the_extension():
     toml = open(PROJECT).read()
     weak = re.search(r"\[weakdeps\]\s*\n(.*?)(\n\[|\Z)", toml, flags=re.S)

@@ -187,15 +187,22 @@ __device__ __forceinline__ constexpr int acc_row(int r, int h) {
 // register equal to it -- short dependency chains, ~2.6 VALU ops per score.
 // Every row must hold a valid token (callers substitute masked rows).
 //
-// The maxima are v_max3_f32 written out: in the IEEE mode compute kernels
-// run in, a quiet NaN operand is ignored (the hardware's maxNum), so NaN
-// scores never become the chunk maximum -- as NaN never compares greater in
-// the reference's `s > mx`.  Written through the compiler's fmax it would
-// insert an input canonicalisation per tree unless told NaNs cannot occur.
+// The maxima are IEEE 754-2019 maximumNumber: a NaN operand is ignored, so
+// NaN scores never become the chunk maximum -- as NaN never compares greater
+// in the reference's `s > mx`.  That is what v_max3_f32 does in the IEEE
+// mode compute kernels run in, and the compiler emits it for these chains
+// (with the occasional input canonicalisation).  It must stay compiler
+// visible: the tree's operands are MFMA results, and the compiler inserts
+// the wait states an MFMA result needs before a VALU reads it only for
+// instructions it can see -- an inline-asm v_max3 placed right after the
+// MFMAs read accumulators that were not yet written.  Written as
+// max(max(a, b), c) and with every node of the tree a three-input max (the
+// root's third input -inf), the chains lower to v_max3_f32 alone; a lone
+// two-input max over MFMA results would get an input canonicalisation per
+// operand.  (A chunk whose scores are all NaN then has maximum -inf instead
+// of NaN; neither is ever strictly greater than the running max.)
 __device__ __forceinline__ float max3_ieee(float a, float b, float c) {
-  float r;
-  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-  return r;
+  return __builtin_fmaximum_numf(__builtin_fmaximum_numf(a, b), c);
 }
 
 __device__ __forceinline__ void fold_tree(const float (&s)[16], int slot0, float& mx, int& slot) {
@@ -206,7 +213,7 @@ __device__ __forceinline__ void fold_tree(const float (&s)[16], int slot0, float
   const float m4 = max3_ieee(s[12], s[13], s[14]);
   const float m5 = max3_ieee(s[15], m0, m1);
   const float m6 = max3_ieee(m2, m3, m4);
-  const float cm = max3_ieee(m5, m6, m6);
+  const float cm = max3_ieee(m5, m6, -INFINITY);
   int ci = 15;
 #pragma unroll
   for (int r = 14; r >= 0; --r) ci = (s[r] == cm) ? r : ci;
@@ -225,7 +232,7 @@ __device__ __forceinline__ void fold_tree8(const float (&s)[16], int slot0, floa
   const float m0 = max3_ieee(s[o + 0], s[o + 1], s[o + 2]);
   const float m1 = max3_ieee(s[o + 3], s[o + 4], s[o + 5]);
   const float m2 = max3_ieee(s[o + 6], s[o + 7], m0);
-  const float cm = max3_ieee(m1, m2, m2);
+  const float cm = max3_ieee(m1, m2, -INFINITY);
   int ci = 7;
 #pragma unroll
   for (int r = 6; r >= 0; --r) ci = (s[o + r] == cm) ? r : ci;

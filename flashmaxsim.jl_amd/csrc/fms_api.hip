@@ -16,6 +16,7 @@
 #include "fms_backward.hpp"
 #include "fms_group.hpp"
 #include "fms_inbatch.hpp"
+#include "fms_inbatch_split.hpp"
 #include "fms_misc.hpp"
 #include "fms_topk.hpp"
 #include "fms_scan_decl.hpp"
@@ -118,6 +119,21 @@ bool group_candidates(int64_t P, int64_t N, int64_t dbytes) {
     return false;
   const double distinct = -(double)N * expm1(-(double)P / (double)N);
   return distinct <= 0.7 * (double)P;
+}
+
+// The in-batch kernel for a call: 1 the register-resident MFMA kernel
+// (16-bit, dim 32..128 in steps of 32), 2 the split-K kernel (fp32, other
+// 16-bit dims whose rows are whole 16-byte units), 0 the per-pair scan.
+int inbatch_path(int32_t dtype, int64_t dim, int64_t Tq, int64_t Td, int64_t Bq, int64_t Bd,
+                 const void* Q, const void* D) {
+  const int esz = elem_bytes(dtype);
+  if ((dtype == FMS_F16 || dtype == FMS_BF16) && inbatch_mfma_supported(dim, Tq, Td, Q, D) &&
+      Bq * ((Tq + 31) / 32) <= kMaxTokens && Bd <= kMaxTokens)
+    return 1;
+  if (esz != 0 && inbatch_split_supported(esz, dim, Tq, Td, Bq, Bd, Q, D) &&
+      Tq * dim * esz < kMaxSeqBytes)
+    return 2;
+  return 0;
 }
 
 // Where a candidate call's document-grouping workspace comes from: the
@@ -477,8 +493,8 @@ fms_status fms_inbatch_device_scan(int32_t dtype, float* S, int32_t* args, const
   if (!seq_ok(Tq, dim, esz) || !seq_ok(Td, dim, esz)) return FMS_EUNSUPPORTED;
   if (Bq == 0 || Bd == 0) return FMS_OK;
   if (!S || (Tq * dim > 0 && !Q) || (Td * dim > 0 && !D)) return FMS_EINVAL;
-  if ((dtype == FMS_F16 || dtype == FMS_BF16) && inbatch_mfma_supported(dim, Tq, Td, Q, D) &&
-      Bq * ((Tq + 31) / 32) <= kMaxTokens && Bd <= kMaxTokens) {
+  const int path = inbatch_path(dtype, dim, Tq, Td, Bq, Bd, Q, D);
+  if (path == 1) {
     InBatchArgs a;
     a.Q = static_cast<const char*>(Q);
     a.D = static_cast<const char*>(D);
@@ -494,7 +510,26 @@ fms_status fms_inbatch_device_scan(int32_t dtype, float* S, int32_t* args, const
     a.norm = normalize;
     return from_hip(launch_inbatch_mfma(dtype == FMS_BF16, a, as_stream(stream)));
   }
-  // other shapes / fp32: the per-pair scan over p = j + Bd*i
+  // fp32, and 16-bit dims the register-resident kernel does not take: the
+  // split-K kernel (query and document slices staged through LDS)
+  if (path == 2) {
+    InBatchSplitArgs a;
+    a.Q = static_cast<const char*>(Q);
+    a.D = static_cast<const char*>(D);
+    a.qm = qmask;
+    a.dm = dmask;
+    a.S = S;
+    a.args = args;
+    a.Bq = (int)Bq;
+    a.Bd = (int)Bd;
+    a.Tq = (int)Tq;
+    a.Td = (int)Td;
+    a.rowbytes = (int)(dim * esz);
+    a.norm = normalize;
+    return from_hip(launch_inbatch_split(dtype, a, as_stream(stream)));
+  }
+  // other shapes (rows not a multiple of 16 bytes, unaligned bases): the
+  // per-pair scan over p = j + Bd*i
   LayInBatch lay;
   lay.Q = static_cast<const char*>(Q);
   lay.D = static_cast<const char*>(D);
@@ -710,6 +745,11 @@ int32_t fms_candidates_grouping(int32_t mode) {
 }
 
 uint64_t fms_debug_workspace_allocs(void) { return workspace_alloc_count(); }
+
+int32_t fms_debug_inbatch_kernel(int32_t dtype, int64_t dim, int64_t Tq, int64_t Td, int64_t Bq,
+                                 int64_t Bd, const void* Q, const void* D) {
+  return inbatch_path(dtype, dim, Tq, Td, Bq, Bd, Q, D);
+}
 
 fms_status fms_int8_dots(int32_t* out, const int8_t* qc, const int8_t* dc, int64_t dim,
                          int64_t Tq, int64_t Td, void* stream) {

@@ -1,0 +1,325 @@
+// fms_inbatch_split.hip -- InBatch() MaxSim with the feature dimension split
+// into K slices, for query tiles that do not fit in registers: 16-bit
+// features of any dim that is a multiple of 8 other than 32, 64, 96, 128
+// (those run the register-resident kernel of fms_inbatch.hip), and fp32
+// features of any dim that is a multiple of 4.
+//
+// S[j, i] = sum_t max_u <Q_i[t], D_j[u]> (forward_layouts.jl:202-225, where
+// the reference materialises D'Q chunks and runs an argmax-accumulate); the
+// same fused scores and argmax tape as the other in-batch kernel.
+//
+// Block = one document j x kRows query rows (a query row is a 32-token tile
+// of a query: query v / ntq, tokens 32 (v % ntq) ..), 4 waves, one block per
+// CU.  The document's chunks are taken kCg at a time (a chunk group); per
+// group the block runs the whole K loop:
+//   * K advances by a slice of 128 bytes of every row (64 features of a
+//     16-bit type, 32 of fp32).  Both operands' slices go HBM/L2 -> LDS with
+//     direct buffer-to-LDS loads (no registers in between), in MFMA fragment
+//     order: 1 KB per (chunk or query row, unit pair m), lane l's 16 bytes
+//     at l * 16 = row l % 32, 16-byte unit 2m + l / 32 of the slice.  A
+//     fragment read is then 1 KB contiguous over the wave (no bank
+//     conflicts).  Rows past the document or the query, and units past the
+//     row (the last slice of a dim that is not a multiple of it) read
+//     zeros (buffer bounds);
+//   * two slice buffers: slice s + 2 is requested while slice s is
+//     multiplied; a barrier before a slice is read (every wave's share has
+//     landed) and one after (the buffer may be refilled);
+//   * wave w holds the accumulators of query rows 2w, 2w + 1 for the whole
+//     chunk group (2 x kCg 32x32 tiles): each query fragment read feeds kCg
+//     MFMA chains and each document fragment read two;
+//   * 16-bit: one v_mfma_f32_32x32x16 per unit pair.  fp32: the 16 bytes of
+//     a unit pair are four k-blocks of v_mfma_f32_32x32x2f32; dword e of
+//     the lanes of half h is feature 8m + 4h + e of the slice, the same
+//     bijection for both operands, so the four MFMAs sum the 8 features of
+//     the unit pair;
+//   * after the K loop each accumulator tile is folded, chunk by chunk in
+//     document order, into the running max / argmax exactly as the scans
+//     fold (first valid row taken, then strictly greater; chunk masks from
+//     dmask and Td), and the last group closes the tiles: wave halves
+//     merged, tape rows and the score written straight to global memory.
+// Block -> (document, query group) is XCD-aware: the query groups of one
+// document are consecutive in one XCD's order, so they stream its slices
+// through that XCD's L2 at about the same time.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include <algorithm>
+
+#include "fms_device.hpp"
+#include "fms_group.hpp"
+#include "fms_inbatch_split.hpp"
+#include "fms_scan.hpp"
+
+namespace fms {
+
+namespace {
+
+constexpr int kSpWaves = 4;
+constexpr int kRows = 2 * kSpWaves;     // query rows per block (two per wave)
+constexpr int kCg = 6;                  // document chunks per group
+constexpr int kSliceBytes = 128;        // bytes of every row per K step
+constexpr int kPairs = kSliceBytes / 32;  // unit pairs per slice (4)
+constexpr int kDFrags = kCg * kPairs;   // 1 KB blocks of a document slice
+constexpr int kQFrags = kRows * kPairs;  // 1 KB blocks of a query slice
+constexpr int kLoadsPerWave = (kDFrags + kQFrags) / kSpWaves;
+static_assert(kDFrags % kSpWaves == 0 && kQFrags % kSpWaves == 0, "every wave loads unit pair m = wave");
+constexpr int kSpXcds = 8;
+
+// The block's waves have all landed their loads of the slice to be read next
+// (each leaves only its kVm most recent loads in flight) and finished their
+// LDS accesses; the asm statements keep the compiler from moving LDS
+// accesses across.
+template <int kVm>
+__device__ __forceinline__ void slice_barrier() {
+  static_assert(kVm >= 0 && kVm < 64, "vmcnt field");
+  asm volatile("" ::: "memory");
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(kVm) : "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// acc += the products of one unit pair (16 bytes per lane of each operand).
+template <class Op>
+__device__ __forceinline__ typename Op::Acc mma_pair(u32x4 a, u32x4 b, typename Op::Acc acc) {
+  if constexpr (Op::kEsz == 4) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc = Op::mma(a[e], b[e], acc);
+    return acc;
+  } else {
+    return Op::mma(a, b, acc);
+  }
+}
+
+template <class Op>
+__global__ void __launch_bounds__(64 * kSpWaves, 1) inbatch_split(const InBatchSplitArgs A) {
+  typedef typename Op::Acc Acc;
+  typedef __attribute__((address_space(3))) void* lds_void_t;
+  __shared__ u32x4 sbuf[2][(kDFrags + kQFrags) * 64];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = uniform(tid >> 6);
+  const int r32 = lane & 31, h = lane >> 5;
+
+  // XCD-aware mapping: blocks are dealt round-robin to the 8 XCDs; in each
+  // XCD's order k = id / 8 the query group runs fastest, so the groups of
+  // document (k / nqg) * 8 + xcd follow each other on that XCD.
+  const int id = blockIdx.x, xcd = id % kSpXcds, kx = id / kSpXcds;
+  const int qg = kx % A.nqg;
+  const int j = (kx / A.nqg) * kSpXcds + xcd;
+  if (j >= A.Bd) return;
+
+  const int rowbytes = A.rowbytes, Tq = A.Tq, Td = A.Td, ntq = A.ntq;
+  const int nslices = (rowbytes + kSliceBytes - 1) / kSliceBytes;
+  const int nch = Td > 0 ? (Td + kTile - 1) / kTile : 0;
+  const int nqv = A.Bq * ntq;
+
+  // This wave's two query rows: query, first token, token count, liveness.
+  int qi[2], qt0[2], qtn[2], qv[2];
+  bool qlive[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    qv[q] = qg * kRows + 2 * wave + q;
+    qlive[q] = qv[q] < nqv;
+    qi[q] = qlive[q] ? qv[q] / ntq : 0;
+    qt0[q] = (qv[q] - qi[q] * ntq) * kTile;
+    qtn[q] = qlive[q] ? std::min(kTile, Tq - qt0[q]) : 0;
+  }
+  // Query token validity of this lane (token r32 of each row).
+  bool tvalid[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const bool in = qlive[q] && r32 < qtn[q];
+    tvalid[q] = in && (A.qm == nullptr || A.qm[(int64_t)qi[q] * Tq + qt0[q] + r32] != 0);
+  }
+
+  // Loads of this wave per slice: unit pair m = wave of every document chunk
+  // of the group (kCg) and of every query row of the block (kRows).  Lane l
+  // reads row l % 32, unit 2m + l / 32 of the slice; a unit past the row
+  // reads out of range (zeros).
+  const int unit_off = (2 * wave + h) * 16;
+  const rsrc_t rdoc = make_rsrc_u(A.D + (int64_t)j * Td * rowbytes, (uint32_t)Td * (uint32_t)rowbytes);
+  rsrc_t rq[kRows];
+#pragma unroll
+  for (int t = 0; t < kRows; ++t) {
+    const int v = qg * kRows + t;
+    const bool live = v < nqv;
+    const int i = live ? v / ntq : 0, t0 = live ? (v - i * ntq) * kTile : 0;
+    const int tn = live ? std::min(kTile, Tq - t0) : 0;
+    rq[t] = make_rsrc_u(A.Q + ((int64_t)i * Tq + t0) * rowbytes, (uint32_t)tn * (uint32_t)rowbytes);
+  }
+
+  auto issue_slice = [&](int g, int s, int buf) {
+    const int so = s * kSliceBytes + unit_off;
+    const int voff_in = so < rowbytes ? so : 0x7fffffff;  // past the row: out of range
+#pragma unroll
+    for (int c = 0; c < kCg; ++c) {
+      const int row = (g * kCg + c) * kTile + r32;
+      const int voff = so < rowbytes && row < Td ? row * rowbytes + so : 0x7fffffff;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rdoc, (lds_void_t)&sbuf[buf][(c * kPairs + wave) * 64], 16, voff, 0, 0, 0);
+    }
+#pragma unroll
+    for (int t = 0; t < kRows; ++t)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rq[t], (lds_void_t)&sbuf[buf][(kDFrags + t * kPairs + wave) * 64], 16,
+          voff_in == 0x7fffffff ? voff_in : r32 * rowbytes + so, 0, 0, 0);
+  };
+
+  float mx[2] = {-INFINITY, -INFINITY};
+  int slot[2] = {-1, -1};
+  const int ngroups = nch > 0 ? (nch + kCg - 1) / kCg : 0;
+  for (int g = 0; g < ngroups; ++g) {
+    const int gc = std::min(kCg, nch - g * kCg);  // chunks in this group
+    // chunk row validity (lane row r32 of each chunk), ballotted after the K loop
+    uint32_t mbyte[kCg];
+#pragma unroll
+    for (int c = 0; c < kCg; ++c) {
+      const int row = (g * kCg + c) * kTile + r32;
+      mbyte[c] = (row < Td && (A.dm == nullptr || A.dm[(int64_t)j * Td + row] != 0)) ? 1u : 0u;
+    }
+    Acc acc[kCg][2];
+#pragma unroll
+    for (int c = 0; c < kCg; ++c) { acc[c][0] = Acc{}; acc[c][1] = Acc{}; }
+
+    issue_slice(g, 0, 0);
+    issue_slice(g, nslices > 1 ? 1 : 0, 1);  // (re-reads slice 0 when there is one slice)
+    for (int s = 0; s < nslices; ++s) {
+      const int buf = s & 1;
+      slice_barrier<kLoadsPerWave>();  // slice s has landed everywhere
+      const u32x4* B = &sbuf[buf][0];
+#pragma unroll
+      for (int m = 0; m < kPairs; ++m) {
+        const u32x4 b0 = B[(kDFrags + (2 * wave) * kPairs + m) * 64 + lane];
+        const u32x4 b1 = B[(kDFrags + (2 * wave + 1) * kPairs + m) * 64 + lane];
+#pragma unroll
+        for (int c = 0; c < kCg; ++c) {
+          if (c < gc) {
+            const u32x4 a = B[(c * kPairs + m) * 64 + lane];
+            acc[c][0] = mma_pair<Op>(a, b0, acc[c][0]);
+            acc[c][1] = mma_pair<Op>(a, b1, acc[c][1]);
+          }
+        }
+      }
+      slice_barrier<kLoadsPerWave>();  // every wave is done with this buffer
+      // slice s + 2 (or a re-read of the last slice: the load count per step
+      // stays constant, so the vmcnt waits above stay exact)
+      issue_slice(g, std::min(s + 2, nslices - 1), buf);
+    }
+    slice_barrier<0>();  // no load into LDS outlives the group
+
+    // fold the group's chunks in document order
+#pragma unroll
+    for (int c = 0; c < kCg; ++c) {
+      if (c >= gc) continue;
+      const int ch = g * kCg + c;
+      const uint32_t m32 = (uint32_t)__ballot(mbyte[c] != 0u);
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        float s[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[r] = acc[c][q][r];
+        take_first_row(s, m32, h, ch, mx[q], slot[q]);
+        if (m32 == 0xffffffffu)
+          fold_tree(s, ch * 16, mx[q], slot[q]);
+        else
+          update_chunk(s, m32, h, ch, mx[q], slot[q]);
+      }
+    }
+  }
+
+  // close the document for both query rows
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    if (!qlive[q]) continue;
+    int tok = slot_to_token(slot[q], h);
+    float m = mx[q];
+    merge_halves(m, tok, h);
+    const float part = (tvalid[q] && tok != 0) ? m : 0.0f;
+    const int64_t p = (int64_t)qi[q] * A.Bd + j;
+    if (A.args && h == 0 && r32 < qtn[q]) A.args[p * Tq + qt0[q] + r32] = tvalid[q] ? tok : 0;
+    const float score = half_sum(part);
+    if (ntq > 1) {
+      if (lane == 0) A.St[(int64_t)qv[q] * A.Bd + j] = score;
+    } else {
+      float inv = 1.0f;
+      if (A.norm) {
+        const float nf = (float)__builtin_popcountll(__ballot(h == 0 && tvalid[q]));
+        inv = 1.0f / (nf > 1.0f ? nf : 1.0f);
+      }
+      if (lane == 0) A.S[p] = A.norm ? score * inv : score;
+    }
+  }
+}
+
+// S[i, j] = sum over tiles tb (in order) of St[i * ntq + tb, j], times
+// 1 / max(valid tokens of query i, 1) when normalising.
+__global__ void __launch_bounds__(256) split_tile_sum_kernel(const float* St, int ntq, int Bq,
+                                                             int Bd, const uint8_t* qm, int Tq,
+                                                             int norm, float* S) {
+  __shared__ int cnt;
+  for (int i = blockIdx.y; i < Bq; i += gridDim.y) {
+    float inv = 1.0f;
+    if (norm) {
+      if (threadIdx.x == 0) cnt = 0;
+      __syncthreads();
+      int c = 0;
+      for (int t = threadIdx.x; t < Tq; t += 256) c += qm ? (qm[(int64_t)i * Tq + t] != 0) : 1;
+      atomicAdd(&cnt, c);
+      __syncthreads();
+      const float nf = (float)cnt;
+      inv = 1.0f / (nf > 1.0f ? nf : 1.0f);
+      __syncthreads();
+    }
+    for (int jj = blockIdx.x * 256 + threadIdx.x; jj < Bd; jj += gridDim.x * 256) {
+      float s = 0.0f;
+      for (int tb = 0; tb < ntq; ++tb) s += St[((int64_t)i * ntq + tb) * Bd + jj];
+      S[(int64_t)i * Bd + jj] = norm ? s * inv : s;
+    }
+  }
+}
+
+}  // namespace
+
+bool inbatch_split_supported(int esz, int64_t dim, int64_t Tq, int64_t Td, int64_t Bq,
+                             int64_t Bd, const void* Q, const void* D) {
+  const bool al = ((reinterpret_cast<uintptr_t>(Q) | reinterpret_cast<uintptr_t>(D)) & 15u) == 0;
+  const int64_t rowbytes = dim * esz;
+  const int64_t ntq = Tq > kTile ? (Tq + kTile - 1) / kTile : 1;
+  return (esz == 2 || esz == 4) && dim > 0 && rowbytes % 16 == 0 && al && Tq >= 1 && Td >= 0 &&
+         Bq >= 1 && Bd >= 1 && Bq * ntq <= ((int64_t)1 << 30) && Bd <= ((int64_t)1 << 26);
+}
+
+hipError_t launch_inbatch_split(int32_t dtype, const InBatchSplitArgs& args_in,
+                                hipStream_t stream) {
+  InBatchSplitArgs A = args_in;
+  A.ntq = A.Tq > kTile ? (A.Tq + kTile - 1) / kTile : 1;
+  A.nqg = (int)(((int64_t)A.Bq * A.ntq + kRows - 1) / kRows);
+  void* ws = nullptr;
+  if (A.ntq > 1) {
+    hipError_t e = workspace_alloc(&ws, (size_t)A.Bq * A.ntq * A.Bd * sizeof(float), stream);
+    if (e != hipSuccess) return e;
+    A.St = static_cast<float*>(ws);
+  }
+  const int64_t blocks = (int64_t)A.nqg * ((A.Bd + kSpXcds - 1) / kSpXcds) * kSpXcds;
+  const dim3 grid((unsigned)blocks), block(64 * kSpWaves);
+  switch (dtype) {
+    case 1: hipLaunchKernelGGL(inbatch_split<OpF16>, grid, block, 0, stream, A); break;
+    case 2: hipLaunchKernelGGL(inbatch_split<OpBF16>, grid, block, 0, stream, A); break;
+    default: hipLaunchKernelGGL(inbatch_split<OpF32>, grid, block, 0, stream, A); break;
+  }
+  hipError_t e = hipGetLastError();
+  if (e == hipSuccess && A.ntq > 1) {
+    hipLaunchKernelGGL(split_tile_sum_kernel,
+                       dim3((unsigned)std::min((A.Bd + 255) / 256, 64),
+                            (unsigned)std::min(A.Bq, 65535)),
+                       dim3(256), 0, stream, A.St, A.ntq, A.Bq, A.Bd, A.qm, A.Tq, A.norm, A.S);
+    e = hipGetLastError();
+  }
+  if (ws) {
+    const hipError_t ef = workspace_free(ws, stream);
+    if (e == hipSuccess) e = ef;
+  }
+  return e;
+}
+
+}  // namespace fms

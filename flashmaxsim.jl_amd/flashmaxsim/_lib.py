@@ -56,6 +56,7 @@ SIGNATURES = {
     "fms_debug_gather_bandwidth": [_p, _i64, _i64, _p, _i64, _p, _p],
     "fms_candidates_grouping": [_i32],
     "fms_debug_workspace_allocs": [],
+    "fms_debug_inbatch_kernel": [_i32, _i64, _i64, _i64, _i64, _i64, _p, _p],
     "fms_debug_cross_lane": [_p, _p],
     "fms_topk": [_p, _i64, _i64, _i64, _p, _p, _p],
     "fms_launch_packed_multi_scan": [_i32, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64,

@@ -438,6 +438,15 @@ fms_status fms_debug_cross_lane(float* out, void* stream);
 uint64_t fms_debug_workspace_allocs(void);
 
 /*
+ * Test-only: which kernel fms_inbatch_device_scan runs for these arguments
+ * (no reference counterpart): 1 the register-resident MFMA kernel (16-bit
+ * features, dim 32, 64, 96 or 128), 2 the split-K MFMA kernel (fp32, and
+ * 16-bit dims whose rows are whole 16-byte units), 0 the per-pair scan.
+ */
+int32_t fms_debug_inbatch_kernel(int32_t dtype, int64_t dim, int64_t Tq, int64_t Td, int64_t Bq,
+                                 int64_t Bd, const void* Q, const void* D);
+
+/*
  * Test-only: streaming read of `bytes` (multiple of 16, 16-byte aligned)
  * with `blocks` workgroups of 256 threads; out receives blocks*256 words.
  * No reference counterpart: it measures the HBM read ceiling reported

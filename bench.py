@@ -28,6 +28,7 @@ for _p in (ROOT, os.path.join(ROOT, "flashmaxsim.jl_amd")):
 
 HBM_PEAK_GBS = 8000.0      # MI355X HBM3E, published
 FP16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16/bf16 MFMA, published
+FP32_PEAK_TFLOPS = 157.3   # MI355X dense fp32 MFMA, published
 INT8_PEAK_TOPS = 5000.0
 
 
@@ -41,7 +42,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="c2",
-                    choices=["c2", "c3", "c3bwd", "c4", "c4d1024", "c4mq", "c5", "read",
+                    choices=["c2", "c3", "c3d768", "c3f32", "c3bwd", "c4", "c4d1024", "c4mq", "c5",
+                             "read",
                              "gather_c2", "gather_c5"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
@@ -317,13 +319,19 @@ def run_c5(args, torch, fm, boundary, dev):
     return res
 
 
-def run_c3(args, torch, fm, boundary, dev):
+def run_c3(args, torch, fm, boundary, dev, dim=128, dtype=None):
+    """The C3 in-batch launch.  dim = 768 and fp32 run the split-K kernel (query and
+    document K slices staged through LDS) and are also timed against the per-pair scan
+    they replace: the candidate layout with every document a candidate of every query,
+    in output order -- each (query, document) pair scanned on its own."""
     import numpy as np
-    dim, Lq, Ld, Bq, Bd = 128, 32, 180, 512, 512
+    dtype = dtype or torch.float16
+    Lq, Ld, Bq, Bd = 32, 180, 512, 512
+    dname = {torch.float16: "f16", torch.bfloat16: "bf16", torch.float32: "f32"}[dtype]
     gen = torch.Generator(device=dev)
     gen.manual_seed(3)
-    Q = normalized_randn(torch, (Bq, Lq, dim), gen, torch.float16, dev)
-    D = normalized_randn(torch, (Bd, Ld, dim), gen, torch.float16, dev)
+    Q = normalized_randn(torch, (Bq, Lq, dim), gen, dtype, dev)
+    D = normalized_randn(torch, (Bd, Ld, dim), gen, dtype, dev)
     lens = torch.randint(64, Ld + 1, (Bd,), generator=gen, device=dev)
     dmask = torch.arange(Ld, device=dev)[None, :] < lens[:, None]
     qmask = torch.ones(Bq, Lq, dtype=torch.bool, device=dev)
@@ -335,11 +343,34 @@ def run_c3(args, torch, fm, boundary, dev):
 
     wall, launch_ms = timed_steps(torch, step, args.steps, args.warmup)
     valid_flops = 2 * dim * Lq * Bq * int(lens.sum().item())
+    name = "c3_inbatch_fp16" if (dim, dtype) == (128, torch.float16) else f"c3_inbatch_{dname}_d{dim}"
     res = dict(pairs_per_step=Bq * Bd, flops_per_launch=valid_flops, wall=wall,
-               launch_ms=launch_ms, dtype="f16", bound="mfma",
+               launch_ms=launch_ms, dtype=dname, bound="mfma",
                padded_flops=2 * dim * Lq * Ld * Bq * Bd,
-               config={"workload": "c3_inbatch_fp16", "dim": dim, "Lq": Lq, "Ld": Ld, "Bq": Bq,
+               config={"workload": name, "dim": dim, "Lq": Lq, "Ld": Ld, "Bq": Bq,
                        "Bd": Bd, "doc_len": "U[64,180], tail masked"})
+    if dtype == torch.float32:
+        res["peak_tflops"] = FP32_PEAK_TFLOPS
+    if (dim, dtype) != (128, torch.float16):
+        # the per-pair scan this launch replaces, on the same inputs
+        idx = torch.arange(1, Bd + 1, device=dev, dtype=torch.int32).repeat(Bq, 1)
+        Sp = torch.empty(Bq, Bd, dtype=torch.float32, device=dev)
+        ap = torch.empty(Bq, Bd, Lq, dtype=torch.int32, device=dev)
+        prev = boundary.candidates_grouping("never")
+
+        def pair_step():
+            boundary.launch_candidates_scan(ap, None, Q, D, idx, qmask, dmask, Bd, Sp, -1.0e4)
+        try:
+            _, pms = timed_steps(torch, pair_step, max(2, args.steps // 4), 1)
+        finally:
+            boundary.candidates_grouping(prev)
+        pp = sum(pms) / len(pms)
+        me = sum(launch_ms) / len(launch_ms)
+        agree = float(((S - Sp).abs() / Sp.abs().clamp(min=1e-3)).max())
+        res["per_pair_scan"] = {"ms_per_call": round(pp, 4), "speedup": round(pp / me, 2),
+                                "max_rel_diff_scores": agree,
+                                "call": "candidate layout, every document a candidate of "
+                                        "every query, output order (the per-pair scan)"}
     if not args.no_cpu:
         import oracle
         rng = np.random.default_rng(0)
@@ -613,7 +644,9 @@ def main():
               "c4mq": run_c4mq, "read": run_read,
               "gather_c2": lambda *a: run_gather(*a, cfg="c2"),
               "gather_c5": lambda *a: run_gather(*a, cfg="c5"),
-              "c4d1024": lambda *a: run_c4(*a, dim=1024)}[args.workload]
+              "c4d1024": lambda *a: run_c4(*a, dim=1024),
+              "c3d768": lambda *a: run_c3(*a, dim=768),
+              "c3f32": lambda *a: run_c3(*a, dim=128, dtype=torch.float32)}[args.workload]
     r = runner(args, torch, fm, boundary, dev)
     steps = args.steps
     wall = r["wall"]
@@ -641,7 +674,7 @@ def main():
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                 "bytes_per_launch": r["bytes_per_launch"]}
     else:
-        peak = FP16_PEAK_TFLOPS
+        peak = r.get("peak_tflops", FP16_PEAK_TFLOPS)
         achieved = r["flops_per_launch"] / avg_launch_s / 1e12
         roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak,
                 "unit": "TFLOP/s", "frac": round(achieved / peak, 4)}
@@ -677,6 +710,8 @@ def main():
         out["parity_check"] = r["check"]
     if "topk" in r:
         out["topk"] = r["topk"]
+    if "per_pair_scan" in r:
+        out["per_pair_scan"] = r["per_pair_scan"]
     if "gather_bytes" in r:
         out["roofline"]["gather_bytes"] = r["gather_bytes"]
         out["roofline"]["gather_GBps"] = round(r["gather_bytes"] / avg_launch_s / 1e9, 1)

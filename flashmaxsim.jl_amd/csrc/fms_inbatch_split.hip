@@ -13,17 +13,19 @@
 // CU.  The document's chunks are taken kCg at a time (a chunk group); per
 // group the block runs the whole K loop:
 //   * K advances by a slice of 128 bytes of every row (64 features of a
-//     16-bit type, 32 of fp32).  Both operands' slices go HBM/L2 -> LDS with
-//     direct buffer-to-LDS loads (no registers in between), in MFMA fragment
-//     order: 1 KB per (chunk or query row, unit pair m), lane l's 16 bytes
-//     at l * 16 = row l % 32, 16-byte unit 2m + l / 32 of the slice.  A
-//     fragment read is then 1 KB contiguous over the wave (no bank
-//     conflicts).  Rows past the document or the query, and units past the
-//     row (the last slice of a dim that is not a multiple of it) read
-//     zeros (buffer bounds);
-//   * two slice buffers: slice s + 2 is requested while slice s is
-//     multiplied; a barrier before a slice is read (every wave's share has
-//     landed) and one after (the buffer may be refilled);
+//     16-bit type, 32 of fp32).  The document's slice (shared by the four
+//     waves) goes HBM/L2 -> LDS with direct buffer-to-LDS loads (no
+//     registers in between), in MFMA fragment order: 1 KB per (chunk, unit
+//     pair m), lane l's 16 bytes at l * 16 = row l % 32, 16-byte unit
+//     2m + l / 32 of the slice, so a fragment read is 1 KB contiguous over
+//     the wave (no bank conflicts).  A wave's own query rows' fragments are
+//     loaded straight into registers in the same order.  Rows past the
+//     document or the query, and units past the row (the last slice of a
+//     dim that is not a multiple of it) read zeros (buffer bounds);
+//   * three stages: slice s + 2 is requested while slice s is multiplied;
+//     one barrier per slice (every wave's share of slice s has landed, and
+//     every wave is done with the stage slice s - 1 used, which the request
+//     of slice s + 2 then refills);
 //   * wave w holds the accumulators of query rows 2w, 2w + 1 for the whole
 //     chunk group (2 x kCg 32x32 tiles): each query fragment read feeds kCg
 //     MFMA chains and each document fragment read two;
@@ -61,9 +63,16 @@ constexpr int kCg = 6;                  // document chunks per group
 constexpr int kSliceBytes = 128;        // bytes of every row per K step
 constexpr int kPairs = kSliceBytes / 32;  // unit pairs per slice (4)
 constexpr int kDFrags = kCg * kPairs;   // 1 KB blocks of a document slice
-constexpr int kQFrags = kRows * kPairs;  // 1 KB blocks of a query slice
-constexpr int kLoadsPerWave = (kDFrags + kQFrags) / kSpWaves;
-static_assert(kDFrags % kSpWaves == 0 && kQFrags % kSpWaves == 0, "every wave loads unit pair m = wave");
+constexpr int kStages = 3;              // document slice buffers in LDS (2 slices ahead)
+static_assert(kDFrags % kSpWaves == 0, "every wave copies unit pair m = wave of each chunk");
+// Vector memory operations per slice and wave: kCg document copies into LDS,
+// then 2 x kPairs query fragment loads into registers.
+constexpr int kQLoads = 2 * kPairs;
+constexpr int kOpsPerSlice = kCg + kQLoads;
+// Issued after a slice's document copies by the time that slice is read: its
+// own query loads and the two slices requested since.
+constexpr int kAfterCopies = kQLoads + (kStages - 2) * kOpsPerSlice;
+static_assert(kAfterCopies < 64, "vmcnt field");
 constexpr int kSpXcds = 8;
 
 // The block's waves have all landed their loads of the slice to be read next
@@ -95,7 +104,7 @@ template <class Op>
 __global__ void __launch_bounds__(64 * kSpWaves, 1) inbatch_split(const InBatchSplitArgs A) {
   typedef typename Op::Acc Acc;
   typedef __attribute__((address_space(3))) void* lds_void_t;
-  __shared__ u32x4 sbuf[2][(kDFrags + kQFrags) * 64];
+  __shared__ u32x4 dbuf[kStages][kDFrags * 64];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = uniform(tid >> 6);
   const int r32 = lane & 31, h = lane >> 5;
@@ -132,37 +141,49 @@ __global__ void __launch_bounds__(64 * kSpWaves, 1) inbatch_split(const InBatchS
     tvalid[q] = in && (A.qm == nullptr || A.qm[(int64_t)qi[q] * Tq + qt0[q] + r32] != 0);
   }
 
-  // Loads of this wave per slice: unit pair m = wave of every document chunk
-  // of the group (kCg) and of every query row of the block (kRows).  Lane l
-  // reads row l % 32, unit 2m + l / 32 of the slice; a unit past the row
-  // reads out of range (zeros).
-  const int unit_off = (2 * wave + h) * 16;
+  // Loads of this wave per slice: the document copies, unit pair m = wave of
+  // every chunk of the group into LDS (the block's four waves together copy
+  // the whole slice), and this wave's own query fragments, both rows x kPairs
+  // unit pairs, into registers.  Lane l reads row l % 32, unit 2m + l / 32 of
+  // the slice; a unit past the row reads out of range (zeros).
+  const int copy_off = (2 * wave + h) * 16;
   const rsrc_t rdoc = make_rsrc_u(A.D + (int64_t)j * Td * rowbytes, (uint32_t)Td * (uint32_t)rowbytes);
-  rsrc_t rq[kRows];
+  rsrc_t rq[2];
 #pragma unroll
-  for (int t = 0; t < kRows; ++t) {
-    const int v = qg * kRows + t;
-    const bool live = v < nqv;
-    const int i = live ? v / ntq : 0, t0 = live ? (v - i * ntq) * kTile : 0;
-    const int tn = live ? std::min(kTile, Tq - t0) : 0;
-    rq[t] = make_rsrc_u(A.Q + ((int64_t)i * Tq + t0) * rowbytes, (uint32_t)tn * (uint32_t)rowbytes);
-  }
+  for (int q = 0; q < 2; ++q)
+    rq[q] = make_rsrc_u(A.Q + ((int64_t)qi[q] * Tq + qt0[q]) * rowbytes,
+                        (uint32_t)qtn[q] * (uint32_t)rowbytes);
+  // Query fragments of kStages slices in flight: set k holds slices
+  // kStages * n + k.
+  u32x4 qf[kStages][2][kPairs];
 
-  auto issue_slice = [&](int g, int s, int buf) {
-    const int so = s * kSliceBytes + unit_off;
-    const int voff_in = so < rowbytes ? so : 0x7fffffff;  // past the row: out of range
+  // Slice s of group g: its document copies into stage s % kStages, its query
+  // fragments into set s % kStages (kSet, a constant: the slice loop is
+  // unrolled by kStages).  A slice index past the last re-reads the last
+  // slice, so every step issues the same operations.
+  auto issue = [&](auto SETc, int g, int s) {
+    constexpr int kSet = decltype(SETc)::value;
+    // Rows past the document or the query lie outside their resources; a unit
+    // past the row end is pushed out of range with all low 31 bits set
+    // (branch-free: a select here became divergent branches around the loads).
+    const int sc = std::min(s, nslices - 1);
+    const int so = sc * kSliceBytes + copy_off;
+    const int dpast = -(int)(so >= rowbytes) & 0x7fffffff;
 #pragma unroll
     for (int c = 0; c < kCg; ++c) {
       const int row = (g * kCg + c) * kTile + r32;
-      const int voff = so < rowbytes && row < Td ? row * rowbytes + so : 0x7fffffff;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rdoc, (lds_void_t)&sbuf[buf][(c * kPairs + wave) * 64], 16, voff, 0, 0, 0);
+          rdoc, (lds_void_t)&dbuf[kSet][(c * kPairs + wave) * 64], 16, (row * rowbytes + so) | dpast,
+          0, 0, 0);
     }
 #pragma unroll
-    for (int t = 0; t < kRows; ++t)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rq[t], (lds_void_t)&sbuf[buf][(kDFrags + t * kPairs + wave) * 64], 16,
-          voff_in == 0x7fffffff ? voff_in : r32 * rowbytes + so, 0, 0, 0);
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+      for (int m = 0; m < kPairs; ++m) {
+        const int o = sc * kSliceBytes + (2 * m + h) * 16;
+        const int qpast = -(int)(o >= rowbytes) & 0x7fffffff;
+        qf[kSet][q][m] = buf_load16(rq[q], (r32 * rowbytes + o) | qpast);
+      }
   };
 
   float mx[2] = {-INFINITY, -INFINITY};
@@ -181,31 +202,42 @@ __global__ void __launch_bounds__(64 * kSpWaves, 1) inbatch_split(const InBatchS
 #pragma unroll
     for (int c = 0; c < kCg; ++c) { acc[c][0] = Acc{}; acc[c][1] = Acc{}; }
 
-    issue_slice(g, 0, 0);
-    issue_slice(g, nslices > 1 ? 1 : 0, 1);  // (re-reads slice 0 when there is one slice)
-    for (int s = 0; s < nslices; ++s) {
-      const int buf = s & 1;
-      slice_barrier<kLoadsPerWave>();  // slice s has landed everywhere
-      const u32x4* B = &sbuf[buf][0];
+    // Prologue: slices 0 and 1.  Step s then waits for its copies (exactly
+    // kAfterCopies operations were issued after them), a barrier makes every
+    // wave's share visible and frees the stage step s - 1 read, slice s + 2
+    // is requested into that stage and query set, and slice s is multiplied.
+    // Chunks past the document (the last group of a long one) read zeros:
+    // their MFMAs run unguarded and their accumulators are never folded.
+    issue(std::integral_constant<int, 0>(), g, 0);
+    issue(std::integral_constant<int, 1>(), g, 1);
+    auto step = [&](auto SETc, int s) {
+      constexpr int kSet = decltype(SETc)::value;
+      slice_barrier<kAfterCopies>();
+      issue(std::integral_constant<int, (kSet + 2) % kStages>(), g, s + 2);
+      const u32x4* B = &dbuf[kSet][0];
 #pragma unroll
       for (int m = 0; m < kPairs; ++m) {
-        const u32x4 b0 = B[(kDFrags + (2 * wave) * kPairs + m) * 64 + lane];
-        const u32x4 b1 = B[(kDFrags + (2 * wave + 1) * kPairs + m) * 64 + lane];
 #pragma unroll
         for (int c = 0; c < kCg; ++c) {
-          if (c < gc) {
-            const u32x4 a = B[(c * kPairs + m) * 64 + lane];
-            acc[c][0] = mma_pair<Op>(a, b0, acc[c][0]);
-            acc[c][1] = mma_pair<Op>(a, b1, acc[c][1]);
-          }
+          const u32x4 a = B[(c * kPairs + m) * 64 + lane];
+          acc[c][0] = mma_pair<Op>(a, qf[kSet][0][m], acc[c][0]);
+          acc[c][1] = mma_pair<Op>(a, qf[kSet][1][m], acc[c][1]);
         }
       }
-      slice_barrier<kLoadsPerWave>();  // every wave is done with this buffer
-      // slice s + 2 (or a re-read of the last slice: the load count per step
-      // stays constant, so the vmcnt waits above stay exact)
-      issue_slice(g, std::min(s + 2, nslices - 1), buf);
+    };
+    // Whole rounds of three steps, then the one or two slices left: no branch
+    // inside a round, so the compiler's wait counts see only the straight path
+    // (a skip edge inside a round made it drain the loads of later slices).
+    static_assert(kStages == 3, "the slice loop below is unrolled by three");
+    int s0 = 0;
+    for (; s0 + kStages <= nslices; s0 += kStages) {
+      step(std::integral_constant<int, 0>(), s0);
+      step(std::integral_constant<int, 1>(), s0 + 1);
+      step(std::integral_constant<int, 2>(), s0 + 2);
     }
-    slice_barrier<0>();  // no load into LDS outlives the group
+    if (s0 < nslices) step(std::integral_constant<int, 0>(), s0);
+    if (s0 + 1 < nslices) step(std::integral_constant<int, 1>(), s0 + 1);
+    slice_barrier<0>();  // no copy into LDS outlives the group (the next refills the stages)
 
     // fold the group's chunks in document order
 #pragma unroll

@@ -39,9 +39,11 @@
 //     fold (first valid row taken, then strictly greater; chunk masks from
 //     dmask and Td), and the last group closes the tiles: wave halves
 //     merged, tape rows and the score written straight to global memory.
-// Block -> (document, query group) is XCD-aware: the query groups of one
-// document are consecutive in one XCD's order, so they stream its slices
-// through that XCD's L2 at about the same time.
+// Block -> (document, query group) is XCD-aware: each XCD takes every 8th
+// document, in bands of kBand documents; within a band the document runs
+// fastest, so the XCD's 32 CUs hold kBand documents x 32 / kBand query groups
+// at a time, and the band's documents stay in that XCD's L2 while all query
+// groups pass over them.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -74,6 +76,7 @@ constexpr int kOpsPerSlice = kCg + kQLoads;
 constexpr int kAfterCopies = kQLoads + (kStages - 2) * kOpsPerSlice;
 static_assert(kAfterCopies < 64, "vmcnt field");
 constexpr int kSpXcds = 8;
+constexpr int kBand = 8;  // documents an XCD keeps in flight together
 
 // The block's waves have all landed their loads of the slice to be read next
 // (each leaves only its kVm most recent loads in flight) and finished their
@@ -88,7 +91,8 @@ __device__ __forceinline__ void slice_barrier() {
   asm volatile("" ::: "memory");
 }
 
-// acc += the products of one unit pair (16 bytes per lane of each operand).
+// acc += the products of one unit pair (16 bytes per lane of each operand):
+// kMmaPerPair MFMAs.
 template <class Op>
 __device__ __forceinline__ typename Op::Acc mma_pair(u32x4 a, u32x4 b, typename Op::Acc acc) {
   if constexpr (Op::kEsz == 4) {
@@ -103,18 +107,24 @@ __device__ __forceinline__ typename Op::Acc mma_pair(u32x4 a, u32x4 b, typename 
 template <class Op>
 __global__ void __launch_bounds__(64 * kSpWaves, 1) inbatch_split(const InBatchSplitArgs A) {
   typedef typename Op::Acc Acc;
+  constexpr int kMmaPerPair = Op::kEsz == 4 ? 4 : 1;
   typedef __attribute__((address_space(3))) void* lds_void_t;
   __shared__ u32x4 dbuf[kStages][kDFrags * 64];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = uniform(tid >> 6);
   const int r32 = lane & 31, h = lane >> 5;
 
-  // XCD-aware mapping: blocks are dealt round-robin to the 8 XCDs; in each
-  // XCD's order k = id / 8 the query group runs fastest, so the groups of
-  // document (k / nqg) * 8 + xcd follow each other on that XCD.
+  // XCD-aware mapping: blocks are dealt round-robin to the 8 XCDs; XCD x
+  // serves documents 8 dl + x, dl < ndx.  Its order k = id / 8 walks bands
+  // of kBand consecutive dl: inside a band dl runs fastest, then the query
+  // group.
   const int id = blockIdx.x, xcd = id % kSpXcds, kx = id / kSpXcds;
-  const int qg = kx % A.nqg;
-  const int j = (kx / A.nqg) * kSpXcds + xcd;
+  const int ndx = (A.Bd + kSpXcds - 1) / kSpXcds;
+  const int band = kx / (kBand * A.nqg);
+  const int bsz = std::min(kBand, ndx - band * kBand);
+  const int within = kx - band * kBand * A.nqg;
+  const int qg = within / bsz;
+  const int j = (band * kBand + within % bsz) * kSpXcds + xcd;
   if (j >= A.Bd) return;
 
   const int rowbytes = A.rowbytes, Tq = A.Tq, Td = A.Td, ntq = A.ntq;
@@ -214,16 +224,35 @@ __global__ void __launch_bounds__(64 * kSpWaves, 1) inbatch_split(const InBatchS
       constexpr int kSet = decltype(SETc)::value;
       slice_barrier<kAfterCopies>();
       issue(std::integral_constant<int, (kSet + 2) % kStages>(), g, s + 2);
-      const u32x4* B = &dbuf[kSet][0];
+      // Document fragments of unit pair m + 1 are read while pair m's MFMAs
+      // run (two register sets).
+      const u32x4* B = &dbuf[kSet][lane];
+      u32x4 a[2][kCg];
+#pragma unroll
+      for (int c = 0; c < kCg; ++c) a[0][c] = B[(c * kPairs) * 64];
 #pragma unroll
       for (int m = 0; m < kPairs; ++m) {
+        if (m + 1 < kPairs) {
+#pragma unroll
+          for (int c = 0; c < kCg; ++c) a[(m + 1) & 1][c] = B[(c * kPairs + m + 1) * 64];
+        }
 #pragma unroll
         for (int c = 0; c < kCg; ++c) {
-          const u32x4 a = B[(c * kPairs + m) * 64 + lane];
-          acc[c][0] = mma_pair<Op>(a, qf[kSet][0][m], acc[c][0]);
-          acc[c][1] = mma_pair<Op>(a, qf[kSet][1][m], acc[c][1]);
+          acc[c][0] = mma_pair<Op>(a[m & 1][c], qf[kSet][0][m], acc[c][0]);
+          acc[c][1] = mma_pair<Op>(a[m & 1][c], qf[kSet][1][m], acc[c][1]);
         }
       }
+      // Schedule: the first pair's reads, then per chunk of each pair one read
+      // of the next pair and the chunk's MFMAs (the compiler otherwise puts
+      // every read right before its MFMAs and waits for it there).
+      __builtin_amdgcn_sched_group_barrier(0x100, kCg, 0);
+#pragma unroll
+      for (int m = 0; m < kPairs; ++m)
+#pragma unroll
+        for (int c = 0; c < kCg; ++c) {
+          if (m + 1 < kPairs) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, 2 * kMmaPerPair, 0);
+        }
     };
     // Whole rounds of three steps, then the one or two slices left: no branch
     // inside a round, so the compiler's wait counts see only the straight path

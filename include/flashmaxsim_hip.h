@@ -148,8 +148,10 @@ int32_t fms_candidates_grouping(int32_t mode);
  * hipMalloc).  fms_launch_candidates_scan with the same arguments and the
  * same kernels and results, except that the document-grouping workspace
  * comes from a static device array of FMS_NOALLOC_SCRATCH_BYTES per GPU
- * (held from the first call on a GPU until the process ends) instead of the
- * library pool: the call performs no hipMalloc / hipFree and calls no
+ * instead of the library pool.  The array is part of the library's code
+ * object, so every GPU the library runs any kernel on holds it from then
+ * until the process ends, whether or not this entry point is called (32 MiB
+ * of 288 GB).  The call performs no hipMalloc / hipFree and calls no
  * allocating library routine.  A call whose grouping workspace would exceed
  * the array -- about 20 bytes per pair plus 4 per gallery document, some
  * 1.4M pairs over a 1M-document gallery -- scans in output order (identical

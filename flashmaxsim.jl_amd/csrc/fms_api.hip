@@ -511,7 +511,8 @@ fms_status fms_inbatch_device_scan(int32_t dtype, float* S, int32_t* args, const
     return from_hip(launch_inbatch_mfma(dtype == FMS_BF16, a, as_stream(stream)));
   }
   // fp32, and 16-bit dims the register-resident kernel does not take: the
-  // split-K kernel (query and document slices staged through LDS)
+  // split-K kernel (document slices staged through LDS, query fragments in
+  // registers, a K slice at a time)
   if (path == 2) {
     InBatchSplitArgs a;
     a.Q = static_cast<const char*>(Q);

@@ -49,6 +49,7 @@
 #include <stdint.h>
 
 #include <algorithm>
+#include <atomic>
 
 #include "fms_device.hpp"
 #include "fms_group.hpp"
@@ -104,6 +105,50 @@ __device__ __forceinline__ typename Op::Acc mma_pair(u32x4 a, u32x4 b, typename 
   }
 }
 
+// Valid-row words of the call, one launch before the scan: plan[j * nch + c]
+// bit r = row 32c + r of document j is below Td and unmasked; plan[ndw + v]
+// bit r = token 32 (v % ntq) + r of query v / ntq is below Tq and unmasked.
+// The scan reads them with scalar loads (a wave-uniform word per chunk or
+// query row), which leaves the vector-memory counter to the slice stream.
+__global__ void __launch_bounds__(256) split_plan_kernel(const uint8_t* dm, const uint8_t* qm,
+                                                         int Bd, int Td, int nch, int Bq, int Tq,
+                                                         int ntq, uint32_t* plan) {
+  const int64_t ndw = (int64_t)Bd * nch, total = ndw + (int64_t)Bq * ntq;
+  const int lane = threadIdx.x & 63;
+  // two words per wave and pass: lanes 0..31 word w, lanes 32..63 word w + 1
+  for (int64_t w = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 2; w < total;
+       w += (int64_t)gridDim.x * 8) {
+    const int64_t wi = w + (lane >> 5);
+    bool bit = false;
+    if (wi < ndw) {
+      const int64_t j = wi / nch;
+      const int row = (int)(wi - j * nch) * kTile + (lane & 31);
+      bit = row < Td && (dm == nullptr || dm[j * Td + row] != 0);
+    } else if (wi < total) {
+      const int64_t v = wi - ndw, i = v / ntq;
+      const int t = (int)(v - i * ntq) * kTile + (lane & 31);
+      bit = t < Tq && (qm == nullptr || qm[i * Tq + t] != 0);
+    }
+    const uint64_t b = __ballot(bit);
+    if ((lane & 31) == 0 && wi < total) plan[wi] = (uint32_t)(b >> (lane & 32));
+  }
+}
+
+// Slot x of the block order -> (document, query group).  Slots are dealt
+// round-robin to the 8 XCDs (slot x runs on XCD x % 8: the grid is a multiple
+// of 8 and each block walks slots blockIdx.x + n * gridDim.x); XCD x serves
+// documents 8 dl + x, dl < ndx, in bands of kBand consecutive dl: inside a
+// band dl runs fastest, then the query group.  A document index >= Bd marks
+// a slot with no work (the last band when Bd is not a multiple of 8).
+__device__ __forceinline__ int split_slot_doc(int x, int nqg, int ndx, int& qg) {
+  const int xcd = x % kSpXcds, kx = x / kSpXcds;
+  const int band = kx / (kBand * nqg);
+  const int bsz = std::min(kBand, ndx - band * kBand);
+  const int within = kx - band * kBand * nqg;
+  qg = within / bsz;
+  return (band * kBand + within % bsz) * kSpXcds + xcd;
+}
+
 template <class Op>
 __global__ void __launch_bounds__(64 * kSpWaves, 1) inbatch_split(const InBatchSplitArgs A) {
   typedef typename Op::Acc Acc;
@@ -114,74 +159,89 @@ __global__ void __launch_bounds__(64 * kSpWaves, 1) inbatch_split(const InBatchS
   const int tid = threadIdx.x, lane = tid & 63, wave = uniform(tid >> 6);
   const int r32 = lane & 31, h = lane >> 5;
 
-  // XCD-aware mapping: blocks are dealt round-robin to the 8 XCDs; XCD x
-  // serves documents 8 dl + x, dl < ndx.  Its order k = id / 8 walks bands
-  // of kBand consecutive dl: inside a band dl runs fastest, then the query
-  // group.
-  const int id = blockIdx.x, xcd = id % kSpXcds, kx = id / kSpXcds;
-  const int ndx = (A.Bd + kSpXcds - 1) / kSpXcds;
-  const int band = kx / (kBand * A.nqg);
-  const int bsz = std::min(kBand, ndx - band * kBand);
-  const int within = kx - band * kBand * A.nqg;
-  const int qg = within / bsz;
-  const int j = (band * kBand + within % bsz) * kSpXcds + xcd;
-  if (j >= A.Bd) return;
-
-  const int rowbytes = A.rowbytes, Tq = A.Tq, Td = A.Td, ntq = A.ntq;
+  const int rowbytes = A.rowbytes, Tq = A.Tq, Td = A.Td, ntq = A.ntq, Bd = A.Bd, nqg = A.nqg;
   const int nslices = (rowbytes + kSliceBytes - 1) / kSliceBytes;
   const int nch = Td > 0 ? (Td + kTile - 1) / kTile : 0;
+  const int ngroups = (nch + kCg - 1) / kCg;
   const int nqv = A.Bq * ntq;
+  const int ndx = (Bd + kSpXcds - 1) / kSpXcds;
+  const int G = gridDim.x;
+  // The plan words are read through the constant address space: scalar
+  // loads (wave-uniform words, lgkmcnt), nothing in the vector-memory count
+  // that the slice waits rely on.  The kernel never writes them.
+  typedef __attribute__((address_space(4))) const uint32_t* cword_ptr;
+  const cword_ptr cmask = (cword_ptr)(uintptr_t)A.plan;
+  const cword_ptr qmask = cmask + (int64_t)Bd * nch;
 
-  // This wave's two query rows: query, first token, token count, liveness.
-  int qi[2], qt0[2], qtn[2], qv[2];
-  bool qlive[2];
-#pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    qv[q] = qg * kRows + 2 * wave + q;
-    qlive[q] = qv[q] < nqv;
-    qi[q] = qlive[q] ? qv[q] / ntq : 0;
-    qt0[q] = (qv[q] - qi[q] * ntq) * kTile;
-    qtn[q] = qlive[q] ? std::min(kTile, Tq - qt0[q]) : 0;
-  }
-  // Query token validity of this lane (token r32 of each row).
-  bool tvalid[2];
-#pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const bool in = qlive[q] && r32 < qtn[q];
-    tvalid[q] = in && (A.qm == nullptr || A.qm[(int64_t)qi[q] * Tq + qt0[q] + r32] != 0);
-  }
+  // This block's slots with a document, in order.
+  auto next_slot = [&](int x) {
+    for (; x < A.nslots; x += G) {
+      int qg;
+      if (split_slot_doc(x, nqg, ndx, qg) < Bd) break;
+    }
+    return x;
+  };
 
-  // Loads of this wave per slice: the document copies, unit pair m = wave of
-  // every chunk of the group into LDS (the block's four waves together copy
-  // the whole slice), and this wave's own query fragments, both rows x kPairs
-  // unit pairs, into registers.  Lane l reads row l % 32, unit 2m + l / 32 of
-  // the slice; a unit past the row reads out of range (zeros).
+  // Query rows of a wave for query group qg: query, first token, token count.
+  struct Rows {
+    int qv[2], qi[2], qt0[2], qtn[2];
+  };
+  auto rows_of = [&](int qg) {
+    Rows R;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int v = qg * kRows + 2 * wave + q;
+      const bool live = v < nqv;
+      R.qv[q] = live ? v : -1;
+      R.qi[q] = live ? v / ntq : 0;
+      R.qt0[q] = live ? (v - R.qi[q] * ntq) * kTile : 0;
+      R.qtn[q] = live ? std::min(kTile, Tq - R.qt0[q]) : 0;
+    }
+    return R;
+  };
+
+  // ---- the load stream ---------------------------------------------------------
+  // A block's work is one sequence of slice tasks: its slots (items) in order,
+  // each item its chunk groups in order, each group its K slices.  The stream
+  // requests task p + 2 while task p is multiplied, across group and item
+  // boundaries, so a new item's first slices arrive while the previous item
+  // folds and closes.  Per task and wave: kCg document copies into LDS (unit
+  // pair m = wave of every chunk of the group; the four waves together copy
+  // the whole slice), then this wave's own query fragments (2 rows x kPairs
+  // unit pairs) into registers.  Lane l reads row l % 32, unit 2m + l / 32 of
+  // the slice; rows past the document or query and units past the row read
+  // out of range (zeros).  Past the last task the resources are empty: the
+  // same operations, no memory traffic.
   const int copy_off = (2 * wave + h) * 16;
-  const rsrc_t rdoc = make_rsrc_u(A.D + (int64_t)j * Td * rowbytes, (uint32_t)Td * (uint32_t)rowbytes);
-  rsrc_t rq[2];
+  int is_slot = next_slot(blockIdx.x), is_g = 0, is_s = 0;
+  rsrc_t rdoc, rq[2];
+  auto set_issue_item = [&]() {
+    if (is_slot < A.nslots) {
+      int qg;
+      const int j = split_slot_doc(is_slot, nqg, ndx, qg);
+      const Rows R = rows_of(qg);
+      rdoc = make_rsrc_u(A.D + (int64_t)j * Td * rowbytes, (uint32_t)Td * (uint32_t)rowbytes);
 #pragma unroll
-  for (int q = 0; q < 2; ++q)
-    rq[q] = make_rsrc_u(A.Q + ((int64_t)qi[q] * Tq + qt0[q]) * rowbytes,
-                        (uint32_t)qtn[q] * (uint32_t)rowbytes);
-  // Query fragments of kStages slices in flight: set k holds slices
-  // kStages * n + k.
+      for (int q = 0; q < 2; ++q)
+        rq[q] = make_rsrc_u(A.Q + ((int64_t)R.qi[q] * Tq + R.qt0[q]) * rowbytes,
+                            (uint32_t)R.qtn[q] * (uint32_t)rowbytes);
+    } else {
+      rdoc = make_rsrc_u(A.D, 0u);
+      rq[0] = rq[1] = make_rsrc_u(A.Q, 0u);
+    }
+  };
+  set_issue_item();
+  // Query fragments of kStages tasks in flight: set k holds tasks 3n + k.
   u32x4 qf[kStages][2][kPairs];
-
-  // Slice s of group g: its document copies into stage s % kStages, its query
-  // fragments into set s % kStages (kSet, a constant: the slice loop is
-  // unrolled by kStages).  A slice index past the last re-reads the last
-  // slice, so every step issues the same operations.
-  auto issue = [&](auto SETc, int g, int s) {
+  auto issue = [&](auto SETc) {
     constexpr int kSet = decltype(SETc)::value;
-    // Rows past the document or the query lie outside their resources; a unit
-    // past the row end is pushed out of range with all low 31 bits set
+    // A unit past the row end is pushed out of range with all low 31 bits set
     // (branch-free: a select here became divergent branches around the loads).
-    const int sc = std::min(s, nslices - 1);
-    const int so = sc * kSliceBytes + copy_off;
+    const int so = is_s * kSliceBytes + copy_off;
     const int dpast = -(int)(so >= rowbytes) & 0x7fffffff;
 #pragma unroll
     for (int c = 0; c < kCg; ++c) {
-      const int row = (g * kCg + c) * kTile + r32;
+      const int row = (is_g * kCg + c) * kTile + r32;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           rdoc, (lds_void_t)&dbuf[kSet][(c * kPairs + wave) * 64], 16, (row * rowbytes + so) | dpast,
           0, 0, 0);
@@ -190,42 +250,103 @@ __global__ void __launch_bounds__(64 * kSpWaves, 1) inbatch_split(const InBatchS
     for (int q = 0; q < 2; ++q)
 #pragma unroll
       for (int m = 0; m < kPairs; ++m) {
-        const int o = sc * kSliceBytes + (2 * m + h) * 16;
+        const int o = is_s * kSliceBytes + (2 * m + h) * 16;
         const int qpast = -(int)(o >= rowbytes) & 0x7fffffff;
         qf[kSet][q][m] = buf_load16(rq[q], (r32 * rowbytes + o) | qpast);
       }
+    if (++is_s == nslices) {
+      is_s = 0;
+      if (++is_g == ngroups) {
+        is_g = 0;
+        is_slot = next_slot(is_slot + G);
+        set_issue_item();
+      }
+    }
   };
 
+  // ---- the compute side -----------------------------------------------------------
+  int c_slot = next_slot(blockIdx.x), c_g = 0, c_s = 0;
+  int j = 0;
+  Rows R{};
+  auto set_compute_item = [&]() {
+    int qg = 0;
+    j = c_slot < A.nslots ? split_slot_doc(c_slot, nqg, ndx, qg) : 0;
+    R = rows_of(qg);
+  };
+  set_compute_item();
   float mx[2] = {-INFINITY, -INFINITY};
   int slot[2] = {-1, -1};
-  const int ngroups = nch > 0 ? (nch + kCg - 1) / kCg : 0;
-  for (int g = 0; g < ngroups; ++g) {
-    const int gc = std::min(kCg, nch - g * kCg);  // chunks in this group
-    // chunk row validity (lane row r32 of each chunk), ballotted after the K loop
-    uint32_t mbyte[kCg];
-#pragma unroll
-    for (int c = 0; c < kCg; ++c) {
-      const int row = (g * kCg + c) * kTile + r32;
-      mbyte[c] = (row < Td && (A.dm == nullptr || A.dm[(int64_t)j * Td + row] != 0)) ? 1u : 0u;
-    }
-    Acc acc[kCg][2];
-#pragma unroll
-    for (int c = 0; c < kCg; ++c) { acc[c][0] = Acc{}; acc[c][1] = Acc{}; }
 
-    // Prologue: slices 0 and 1.  Step s then waits for its copies (exactly
-    // kAfterCopies operations were issued after them), a barrier makes every
-    // wave's share visible and frees the stage step s - 1 read, slice s + 2
-    // is requested into that stage and query set, and slice s is multiplied.
-    // Chunks past the document (the last group of a long one) read zeros:
-    // their MFMAs run unguarded and their accumulators are never folded.
-    issue(std::integral_constant<int, 0>(), g, 0);
-    issue(std::integral_constant<int, 1>(), g, 1);
-    auto step = [&](auto SETc, int s) {
-      constexpr int kSet = decltype(SETc)::value;
-      slice_barrier<kAfterCopies>();
-      issue(std::integral_constant<int, (kSet + 2) % kStages>(), g, s + 2);
-      // Document fragments of unit pair m + 1 are read while pair m's MFMAs
-      // run (two register sets).
+  // Close the item's document for both query rows: wave halves merged, tape
+  // row and score written straight to global memory.  Both rows' running
+  // max starts again for the block's next item, a row past the last query
+  // (whose folds saw zeros) included.
+  auto close_item = [&]() {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      if (R.qv[q] < 0) {
+        mx[q] = -INFINITY;
+        slot[q] = -1;
+        continue;
+      }
+      const uint32_t qw = qmask[R.qv[q]];
+      const bool tv = ((qw >> r32) & 1u) != 0u;
+      int tok = slot_to_token(slot[q], h);
+      float m = mx[q];
+      merge_halves(m, tok, h);
+      const float part = (tv && tok != 0) ? m : 0.0f;
+      const int64_t p = (int64_t)R.qi[q] * Bd + j;
+      if (A.args && h == 0 && r32 < R.qtn[q]) A.args[p * Tq + R.qt0[q] + r32] = tv ? tok : 0;
+      const float score = half_sum(part);
+      if (ntq > 1) {
+        if (lane == 0) A.St[(int64_t)R.qv[q] * Bd + j] = score;
+      } else {
+        const float nf = (float)__builtin_popcount(qw);
+        const float inv = 1.0f / (nf > 1.0f ? nf : 1.0f);
+        if (lane == 0) A.S[p] = A.norm ? score * inv : score;
+      }
+      mx[q] = -INFINITY;
+      slot[q] = -1;
+    }
+  };
+
+  if (ngroups == 0) {  // Td = 0: every pair scores 0 with an all-zero tape
+    for (; c_slot < A.nslots; c_slot = next_slot(c_slot + G)) {
+      set_compute_item();
+      close_item();
+    }
+    return;
+  }
+
+  int ntasks = 0;
+  for (int x = c_slot; x < A.nslots; x = next_slot(x + G)) ntasks += ngroups * nslices;
+  if (ntasks == 0) return;
+
+  Acc acc[kCg][2];
+  uint32_t gmask[kCg];  // the group's chunk words (scalar loads at its first slice)
+
+  // Task p: wait for its copies (exactly kAfterCopies vector operations were
+  // issued after them: its own query loads and the whole of task p + 1), a
+  // barrier makes every wave's share visible and frees the stage task p - 1
+  // read, task p + 2 is requested into that stage and query set, and task p
+  // is multiplied; after a group's last slice the group folds, after an
+  // item's last group the item closes.  Chunks past the document read zeros:
+  // their MFMAs run unguarded and their accumulators are never folded.
+  auto step = [&](auto SETc) {
+    constexpr int kSet = decltype(SETc)::value;
+    slice_barrier<kAfterCopies>();
+    issue(std::integral_constant<int, (kSet + 2) % kStages>());
+    if (c_s == 0) {
+#pragma unroll
+      for (int c = 0; c < kCg; ++c) {
+        const int ch = std::min(c_g * kCg + c, nch - 1);
+        gmask[c] = cmask[(int64_t)j * nch + ch];
+      }
+    }
+    // Document fragments of unit pair m + 1 are read while pair m's MFMAs run
+    // (two register sets); a group's first slice starts its accumulators.
+    auto multiply = [&](auto FIRSTc) {
+      constexpr bool kFirst = decltype(FIRSTc)::value;
       const u32x4* B = &dbuf[kSet][lane];
       u32x4 a[2][kCg];
 #pragma unroll
@@ -237,10 +358,11 @@ __global__ void __launch_bounds__(64 * kSpWaves, 1) inbatch_split(const InBatchS
           for (int c = 0; c < kCg; ++c) a[(m + 1) & 1][c] = B[(c * kPairs + m + 1) * 64];
         }
 #pragma unroll
-        for (int c = 0; c < kCg; ++c) {
-          acc[c][0] = mma_pair<Op>(a[m & 1][c], qf[kSet][0][m], acc[c][0]);
-          acc[c][1] = mma_pair<Op>(a[m & 1][c], qf[kSet][1][m], acc[c][1]);
-        }
+        for (int c = 0; c < kCg; ++c)
+#pragma unroll
+          for (int q = 0; q < 2; ++q)
+            acc[c][q] = mma_pair<Op>(a[m & 1][c], qf[kSet][q][m],
+                                     (kFirst && m == 0) ? Acc{} : acc[c][q]);
       }
       // Schedule: the first pair's reads, then per chunk of each pair one read
       // of the next pair and the chunk's MFMAs (the compiler otherwise puts
@@ -254,62 +376,53 @@ __global__ void __launch_bounds__(64 * kSpWaves, 1) inbatch_split(const InBatchS
           __builtin_amdgcn_sched_group_barrier(0x008, 2 * kMmaPerPair, 0);
         }
     };
-    // Whole rounds of three steps, then the one or two slices left: no branch
-    // inside a round, so the compiler's wait counts see only the straight path
-    // (a skip edge inside a round made it drain the loads of later slices).
-    static_assert(kStages == 3, "the slice loop below is unrolled by three");
-    int s0 = 0;
-    for (; s0 + kStages <= nslices; s0 += kStages) {
-      step(std::integral_constant<int, 0>(), s0);
-      step(std::integral_constant<int, 1>(), s0 + 1);
-      step(std::integral_constant<int, 2>(), s0 + 2);
-    }
-    if (s0 < nslices) step(std::integral_constant<int, 0>(), s0);
-    if (s0 + 1 < nslices) step(std::integral_constant<int, 1>(), s0 + 1);
-    slice_barrier<0>();  // no copy into LDS outlives the group (the next refills the stages)
+    if (c_s == 0) multiply(std::true_type());
+    else multiply(std::false_type());
 
-    // fold the group's chunks in document order
+    if (++c_s == nslices) {
+      c_s = 0;
+      // fold the group's chunks in document order
 #pragma unroll
-    for (int c = 0; c < kCg; ++c) {
-      if (c >= gc) continue;
-      const int ch = g * kCg + c;
-      const uint32_t m32 = (uint32_t)__ballot(mbyte[c] != 0u);
+      for (int c = 0; c < kCg; ++c) {
+        const int ch = c_g * kCg + c;
+        if (ch >= nch) continue;
+        const uint32_t m32 = gmask[c];
 #pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        float s[16];
+        for (int q = 0; q < 2; ++q) {
+          float s[16];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) s[r] = acc[c][q][r];
-        take_first_row(s, m32, h, ch, mx[q], slot[q]);
-        if (m32 == 0xffffffffu)
-          fold_tree(s, ch * 16, mx[q], slot[q]);
-        else
-          update_chunk(s, m32, h, ch, mx[q], slot[q]);
+          for (int r = 0; r < 16; ++r) s[r] = acc[c][q][r];
+          take_first_row(s, m32, h, ch, mx[q], slot[q]);
+          if (m32 == 0xffffffffu)
+            fold_tree(s, ch * 16, mx[q], slot[q]);
+          else
+            update_chunk(s, m32, h, ch, mx[q], slot[q]);
+        }
+      }
+      if (++c_g == ngroups) {
+        c_g = 0;
+        close_item();
+        c_slot = next_slot(c_slot + G);
+        set_compute_item();
       }
     }
-  }
+  };
 
-  // close the document for both query rows
-#pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    if (!qlive[q]) continue;
-    int tok = slot_to_token(slot[q], h);
-    float m = mx[q];
-    merge_halves(m, tok, h);
-    const float part = (tvalid[q] && tok != 0) ? m : 0.0f;
-    const int64_t p = (int64_t)qi[q] * A.Bd + j;
-    if (A.args && h == 0 && r32 < qtn[q]) A.args[p * Tq + qt0[q] + r32] = tvalid[q] ? tok : 0;
-    const float score = half_sum(part);
-    if (ntq > 1) {
-      if (lane == 0) A.St[(int64_t)qv[q] * A.Bd + j] = score;
-    } else {
-      float inv = 1.0f;
-      if (A.norm) {
-        const float nf = (float)__builtin_popcountll(__ballot(h == 0 && tvalid[q]));
-        inv = 1.0f / (nf > 1.0f ? nf : 1.0f);
-      }
-      if (lane == 0) A.S[p] = A.norm ? score * inv : score;
-    }
+  issue(std::integral_constant<int, 0>());
+  issue(std::integral_constant<int, 1>());
+  // Whole rounds of three steps, then the one or two tasks left: no branch
+  // around a step inside a round, so the compiler's wait counts see every
+  // step's loads (a skip edge made it drain the loads of later tasks).
+  static_assert(kStages == 3, "the task loop below is unrolled by three");
+  int p = 0;
+  for (; p + kStages <= ntasks; p += kStages) {
+    step(std::integral_constant<int, 0>());
+    step(std::integral_constant<int, 1>());
+    step(std::integral_constant<int, 2>());
   }
+  if (p < ntasks) step(std::integral_constant<int, 0>());
+  if (p + 1 < ntasks) step(std::integral_constant<int, 1>());
+  slice_barrier<0>();  // the empty requests past the last task
 }
 
 // S[i, j] = sum over tiles tb (in order) of St[i * ntq + tb, j], times
@@ -346,29 +459,69 @@ bool inbatch_split_supported(int esz, int64_t dim, int64_t Tq, int64_t Td, int64
   const bool al = ((reinterpret_cast<uintptr_t>(Q) | reinterpret_cast<uintptr_t>(D)) & 15u) == 0;
   const int64_t rowbytes = dim * esz;
   const int64_t ntq = Tq > kTile ? (Tq + kTile - 1) / kTile : 1;
+  const int64_t nqg = (Bq * ntq + kRows - 1) / kRows, ndx = (Bd + kSpXcds - 1) / kSpXcds;
+  // 32-bit buffer offsets: a document's rows, a query tile's rows, the slot count
+  const int64_t lim = ((int64_t)1 << 31) - 4096;
   return (esz == 2 || esz == 4) && dim > 0 && rowbytes % 16 == 0 && al && Tq >= 1 && Td >= 0 &&
-         Bq >= 1 && Bd >= 1 && Bq * ntq <= ((int64_t)1 << 30) && Bd <= ((int64_t)1 << 26);
+         Bq >= 1 && Bd >= 1 && Bq * ntq <= ((int64_t)1 << 30) && Bd <= ((int64_t)1 << 26) &&
+         (Td + kTile * kCg) * rowbytes < lim && kTile * rowbytes < lim &&
+         nqg <= lim / kSpXcds / ndx;
 }
+
+namespace {
+
+// Compute units of the current device (cached per device; gfx950: 256).
+int device_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 256;
+  if (dev < 64) {
+    const int c = cache[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+  }
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+    n = 256;
+  if (dev < 64) cache[dev].store(n, std::memory_order_relaxed);
+  return n;
+}
+
+}  // namespace
 
 hipError_t launch_inbatch_split(int32_t dtype, const InBatchSplitArgs& args_in,
                                 hipStream_t stream) {
   InBatchSplitArgs A = args_in;
   A.ntq = A.Tq > kTile ? (A.Tq + kTile - 1) / kTile : 1;
   A.nqg = (int)(((int64_t)A.Bq * A.ntq + kRows - 1) / kRows);
+  const int ndx = (A.Bd + kSpXcds - 1) / kSpXcds;
+  A.nslots = A.nqg * ndx * kSpXcds;
+  // One workspace: the plan words (documents' chunk words, then query rows'
+  // words), then, with several tiles per query, the tile scores St.
+  const int nch = A.Td > 0 ? (A.Td + kTile - 1) / kTile : 0;
+  const int64_t nwords = (int64_t)A.Bd * nch + (int64_t)A.Bq * A.ntq;
+  const size_t plan_bytes = ((size_t)nwords * sizeof(uint32_t) + 255) / 256 * 256;
+  const size_t st_bytes = A.ntq > 1 ? (size_t)A.Bq * A.ntq * A.Bd * sizeof(float) : 0;
   void* ws = nullptr;
-  if (A.ntq > 1) {
-    hipError_t e = workspace_alloc(&ws, (size_t)A.Bq * A.ntq * A.Bd * sizeof(float), stream);
-    if (e != hipSuccess) return e;
-    A.St = static_cast<float*>(ws);
+  hipError_t e = workspace_alloc(&ws, plan_bytes + st_bytes, stream);
+  if (e != hipSuccess) return e;
+  A.plan = static_cast<uint32_t*>(ws);
+  if (A.ntq > 1) A.St = reinterpret_cast<float*>(static_cast<char*>(ws) + plan_bytes);
+  hipLaunchKernelGGL(split_plan_kernel, dim3((unsigned)std::min<int64_t>((nwords + 7) / 8, 1024)),
+                     dim3(256), 0, stream, A.dm, A.qm, A.Bd, A.Td, nch, A.Bq, A.Tq, A.ntq,
+                     static_cast<uint32_t*>(ws));
+  e = hipGetLastError();
+  // One block per CU (a multiple of 8, so slot x stays on XCD x % 8), each
+  // walking its slots.
+  const int cus = std::max(kSpXcds, device_cus() / kSpXcds * kSpXcds);
+  const dim3 grid((unsigned)std::min(A.nslots, cus)), block(64 * kSpWaves);
+  if (e == hipSuccess) {
+    switch (dtype) {
+      case 1: hipLaunchKernelGGL(inbatch_split<OpF16>, grid, block, 0, stream, A); break;
+      case 2: hipLaunchKernelGGL(inbatch_split<OpBF16>, grid, block, 0, stream, A); break;
+      default: hipLaunchKernelGGL(inbatch_split<OpF32>, grid, block, 0, stream, A); break;
+    }
+    e = hipGetLastError();
   }
-  const int64_t blocks = (int64_t)A.nqg * ((A.Bd + kSpXcds - 1) / kSpXcds) * kSpXcds;
-  const dim3 grid((unsigned)blocks), block(64 * kSpWaves);
-  switch (dtype) {
-    case 1: hipLaunchKernelGGL(inbatch_split<OpF16>, grid, block, 0, stream, A); break;
-    case 2: hipLaunchKernelGGL(inbatch_split<OpBF16>, grid, block, 0, stream, A); break;
-    default: hipLaunchKernelGGL(inbatch_split<OpF32>, grid, block, 0, stream, A); break;
-  }
-  hipError_t e = hipGetLastError();
   if (e == hipSuccess && A.ntq > 1) {
     hipLaunchKernelGGL(split_tile_sum_kernel,
                        dim3((unsigned)std::min((A.Bd + 255) / 256, 64),
@@ -376,10 +529,8 @@ hipError_t launch_inbatch_split(int32_t dtype, const InBatchSplitArgs& args_in,
                        dim3(256), 0, stream, A.St, A.ntq, A.Bq, A.Bd, A.qm, A.Tq, A.norm, A.S);
     e = hipGetLastError();
   }
-  if (ws) {
-    const hipError_t ef = workspace_free(ws, stream);
-    if (e == hipSuccess) e = ef;
-  }
+  const hipError_t ef = workspace_free(ws, stream);
+  if (e == hipSuccess) e = ef;
   return e;
 }
 

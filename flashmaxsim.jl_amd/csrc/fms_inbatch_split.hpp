@@ -1,5 +1,5 @@
-// fms_inbatch_split.hpp -- launcher of the split-K InBatch() kernel (query
-// tiles staged through LDS a K slice at a time): 16-bit features with dims the
+// fms_inbatch_split.hpp -- launcher of the split-K InBatch() kernel (the
+// feature dim taken a K slice at a time): 16-bit features with dims the
 // register-resident kernel does not take, and fp32 features.
 #pragma once
 
@@ -23,6 +23,11 @@ struct InBatchSplitArgs {
   // groups of 8 query rows per document
   int ntq = 1, nqg = 1;
   float* St = nullptr;
+  // filled by the launcher: the plan words (valid rows of every 32-row
+  // document chunk, then valid tokens of every query row) and the number of
+  // block-order slots (nqg x 8 x ceil(Bd / 8), some past Bd)
+  const uint32_t* plan = nullptr;
+  int nslots = 0;
 };
 
 // Element bytes 2 or 4; rows a multiple of 16 bytes; 16-byte aligned bases.

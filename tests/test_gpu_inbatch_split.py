@@ -103,6 +103,21 @@ def test_split_dims(device, dtype, dim):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.float32], ids=lambda d: DT_ID[d])
+@pytest.mark.parametrize("shape", [(8, 40, 300, 64, 256), (40, 400, 75, 40, 72)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_split_many_items_per_block(device, dtype, shape):
+    """A block walks many (document, query group) items in turn, its loads
+    running ahead across item and chunk-group boundaries: 300 queries of 8
+    tokens (the last group's rows past query 299 hold no query) x 64
+    documents is some 2,400 items for 256 blocks; 75 queries of 40 tokens (two
+    tiles each, 150 rows) x 40 documents of 400 tokens (three chunk groups)
+    at d = 72.  Every item must start from a clean running max, whatever the
+    block's previous item was."""
+    Tq, Td, Bq, Bd, dim = shape
+    _run(device, dtype, dim, Tq, Td, Bq, Bd, seed=Tq * 7 + Bq, ties=True)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32], ids=lambda d: DT_ID[d])
 def test_split_normalize(device, dtype):
     """The normalize epilogue (1 / max(valid query tokens, 1), normalize.jl:4-10) for
     one tile per query and for queries of several tiles (summed after the scan)."""
@@ -151,3 +166,25 @@ def test_split_c3_shape_d768_sampled(device):
     assert_scores(S.cpu()[rows], S_o, tol, what="S")
     Qf, Df = widened(Qo, False), widened(D.cpu().numpy(), False)
     _tape_check(args.cpu().numpy()[rows], a_o, Qf, Df, tol)
+
+
+@pytest.mark.parametrize("Tq", [20, 45], ids=lambda t: f"Tq{t}")
+def test_split_empty_documents(device, Tq):
+    """Documents with no tokens (Td = 0): every pair scores 0 and the tape is
+    all zeros, with one tile per query and with two (summed after the scan),
+    normalised or not (test_regressions.jl:65-86: an empty document gives 0).
+    The host API answers Td = 0 itself; the boundary call here reaches the
+    kernel, with the outputs filled beforehand so that every write shows."""
+    from flashmaxsim import boundary
+    dim, Bq, Bd = 256, 3, 5
+    Q = torch.randn(Bq, Tq, dim, device=device).to(torch.float16)
+    D = torch.empty(Bd, 0, dim, dtype=torch.float16, device=device)
+    assert _kernel(Q, D) == 2
+    for normalize in (False, True):
+        S = torch.full((Bq, Bd), 7.0, device=device)
+        args = torch.full((Bq, Bd, Tq), 5, dtype=torch.int32, device=device)
+        boundary.inbatch_device_scan(S, args, Q, D, None, None, normalize)
+        torch.cuda.synchronize()
+        assert torch.equal(S.cpu(), torch.zeros(Bq, Bd))
+        assert (args.cpu() == 0).all()
+

@@ -8,10 +8,11 @@
 // the reference materialises D'Q chunks and runs an argmax-accumulate); the
 // same fused scores and argmax tape as the other in-batch kernel.
 //
-// Block = one document j x kRows query rows (a query row is a 32-token tile
-// of a query: query v / ntq, tokens 32 (v % ntq) ..), 4 waves, one block per
-// CU.  The document's chunks are taken kCg at a time (a chunk group); per
-// group the block runs the whole K loop:
+// Work item = one document j x kRows query rows (a query row is a 32-token
+// tile of a query: query v / ntq, tokens 32 (v % ntq) ..).  One block of 4
+// waves per CU walks its items in turn (a persistent grid).  An item's
+// document chunks are taken kCg at a time (a chunk group); per group the
+// block runs the whole K loop:
 //   * K advances by a slice of 128 bytes of every row (64 features of a
 //     16-bit type, 32 of fp32).  The document's slice (shared by the four
 //     waves) goes HBM/L2 -> LDS with direct buffer-to-LDS loads (no
@@ -22,10 +23,13 @@
 //     loaded straight into registers in the same order.  Rows past the
 //     document or the query, and units past the row (the last slice of a
 //     dim that is not a multiple of it) read zeros (buffer bounds);
-//   * three stages: slice s + 2 is requested while slice s is multiplied;
-//     one barrier per slice (every wave's share of slice s has landed, and
-//     every wave is done with the stage slice s - 1 used, which the request
-//     of slice s + 2 then refills);
+//   * the block's slices (items, their groups, their K slices, in order)
+//     form one stream with three stages: slice task p + 2 is requested
+//     while task p is multiplied, across group and item boundaries, so an
+//     item's first slices arrive while the previous item folds and closes;
+//     one barrier per task (every wave's share of task p has landed, and
+//     every wave is done with the stage task p - 1 used, which the request
+//     of task p + 2 then refills);
 //   * wave w holds the accumulators of query rows 2w, 2w + 1 for the whole
 //     chunk group (2 x kCg 32x32 tiles): each query fragment read feeds kCg
 //     MFMA chains and each document fragment read two;
@@ -34,12 +38,13 @@
 //     the lanes of half h is feature 8m + 4h + e of the slice, the same
 //     bijection for both operands, so the four MFMAs sum the 8 features of
 //     the unit pair;
-//   * after the K loop each accumulator tile is folded, chunk by chunk in
-//     document order, into the running max / argmax exactly as the scans
-//     fold (first valid row taken, then strictly greater; chunk masks from
-//     dmask and Td), and the last group closes the tiles: wave halves
-//     merged, tape rows and the score written straight to global memory.
-// Block -> (document, query group) is XCD-aware: each XCD takes every 8th
+//   * after a group's last slice each accumulator tile is folded, chunk by
+//     chunk in document order, into the running max / argmax exactly as the
+//     scans fold (first valid row taken, then strictly greater; chunk valid
+//     words from a plan kernel over dmask and Td), and the item's last group
+//     closes the tiles: wave halves merged, tape rows and the score written
+//     straight to global memory.
+// Item -> (document, query group) is XCD-aware: each XCD takes every 8th
 // document, in bands of kBand documents; within a band the document runs
 // fastest, so the XCD's 32 CUs hold kBand documents x 32 / kBand query groups
 // at a time, and the band's documents stay in that XCD's L2 while all query

@@ -217,7 +217,17 @@ __global__ void __launch_bounds__(64 * kSpWaves, 1) inbatch_split(const InBatchS
   // the slice; rows past the document or query and units past the row read
   // out of range (zeros).  Past the last task the resources are empty: the
   // same operations, no memory traffic.
-  const int copy_off = (2 * wave + h) * 16;
+  // Document copies read whole rows: a wave's copy of chunk c is its rows
+  // 8w .. 8w + 7 (1 KB, 8 cache lines), lane l taking row 8w + l / 8 and the
+  // unit that leaves the chunk row-major with each row's 8 units
+  // XOR-swizzled: unit u of row r at r * 8 + (u ^ key(r)), key(r) =
+  // (r / 2) % 8.  The fragment reads (lane: row r32, unit 2m + h) then fall
+  // on 16 distinct 16-byte bank groups for any 16 consecutive lanes.
+  const int crow = 8 * wave + (lane >> 3);
+  const int copy_off = ((lane & 7) ^ ((crow >> 1) & 7)) * 16;
+  int roff[kPairs];  // fragment m of a chunk: u32x4 index in the chunk's 4 KB
+#pragma unroll
+  for (int m = 0; m < kPairs; ++m) roff[m] = r32 * 8 + ((2 * m + h) ^ ((r32 >> 1) & 7));
   int is_slot = next_slot(blockIdx.x), is_g = 0, is_s = 0;
   rsrc_t rdoc, rq[2];
   auto set_issue_item = [&]() {
@@ -246,9 +256,9 @@ __global__ void __launch_bounds__(64 * kSpWaves, 1) inbatch_split(const InBatchS
     const int dpast = -(int)(so >= rowbytes) & 0x7fffffff;
 #pragma unroll
     for (int c = 0; c < kCg; ++c) {
-      const int row = (is_g * kCg + c) * kTile + r32;
+      const int row = (is_g * kCg + c) * kTile + crow;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rdoc, (lds_void_t)&dbuf[kSet][(c * kPairs + wave) * 64], 16, (row * rowbytes + so) | dpast,
+          rdoc, (lds_void_t)&dbuf[kSet][c * 256 + wave * 64], 16, (row * rowbytes + so) | dpast,
           0, 0, 0);
     }
 #pragma unroll
@@ -352,15 +362,15 @@ __global__ void __launch_bounds__(64 * kSpWaves, 1) inbatch_split(const InBatchS
     // (two register sets); a group's first slice starts its accumulators.
     auto multiply = [&](auto FIRSTc) {
       constexpr bool kFirst = decltype(FIRSTc)::value;
-      const u32x4* B = &dbuf[kSet][lane];
+      const u32x4* B = &dbuf[kSet][0];
       u32x4 a[2][kCg];
 #pragma unroll
-      for (int c = 0; c < kCg; ++c) a[0][c] = B[(c * kPairs) * 64];
+      for (int c = 0; c < kCg; ++c) a[0][c] = B[c * 256 + roff[0]];
 #pragma unroll
       for (int m = 0; m < kPairs; ++m) {
         if (m + 1 < kPairs) {
 #pragma unroll
-          for (int c = 0; c < kCg; ++c) a[(m + 1) & 1][c] = B[(c * kPairs + m + 1) * 64];
+          for (int c = 0; c < kCg; ++c) a[(m + 1) & 1][c] = B[c * 256 + roff[m + 1]];
         }
 #pragma unroll
         for (int c = 0; c < kCg; ++c)

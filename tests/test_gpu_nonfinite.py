@@ -124,11 +124,13 @@ def test_candidates_nonfinite(device, dtype, order):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-def test_inbatch_nonfinite(device, dtype):
-    """f16 / bf16 take the MFMA kernel (dim 128, Tq <= 32); fp32 the per-pair scan.
-    Query tokens and documents with non-finite first rows sit in both query blocks."""
+@pytest.mark.parametrize("dim", [128, 256], ids=lambda d: f"d{d}")
+def test_inbatch_nonfinite(device, dtype, dim):
+    """dim 128: f16 / bf16 take the register-resident MFMA kernel (Tq <= 32), fp32
+    the split-K kernel; dim 256: all three take the split-K kernel.  Query tokens
+    and documents with non-finite first rows sit in several query groups."""
     rng = np.random.default_rng(17)
-    Bq, Bd, Tq, Td, dim = 40, 37, 24, 70, 128
+    Bq, Bd, Tq, Td = 40, 37, 24, 70
     Q = tokens(rng, (Bq, Tq, dim))
     D = tokens(rng, (Bd, Td, dim))
     qm = np.ones((Bq, Tq), np.uint8)

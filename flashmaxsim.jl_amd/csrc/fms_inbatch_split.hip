@@ -71,8 +71,8 @@ constexpr int kCg = 6;                  // document chunks per group
 constexpr int kSliceBytes = 128;        // bytes of every row per K step
 constexpr int kPairs = kSliceBytes / 32;  // unit pairs per slice (4)
 constexpr int kDFrags = kCg * kPairs;   // 1 KB blocks of a document slice
-constexpr int kStages = 3;              // document slice buffers in LDS (2 slices ahead)
-static_assert(kDFrags % kSpWaves == 0, "every wave copies unit pair m = wave of each chunk");
+constexpr int kStages = 3;              // document slice stages in LDS (2 slices ahead)
+static_assert(kTile == 8 * kSpWaves, "every wave copies 8 whole rows of each chunk");
 // Vector memory operations per slice and wave: kCg document copies into LDS,
 // then 2 x kPairs query fragment loads into registers.
 constexpr int kQLoads = 2 * kPairs;
@@ -210,13 +210,12 @@ __global__ void __launch_bounds__(64 * kSpWaves, 1) inbatch_split(const InBatchS
   // each item its chunk groups in order, each group its K slices.  The stream
   // requests task p + 2 while task p is multiplied, across group and item
   // boundaries, so a new item's first slices arrive while the previous item
-  // folds and closes.  Per task and wave: kCg document copies into LDS (unit
-  // pair m = wave of every chunk of the group; the four waves together copy
-  // the whole slice), then this wave's own query fragments (2 rows x kPairs
-  // unit pairs) into registers.  Lane l reads row l % 32, unit 2m + l / 32 of
-  // the slice; rows past the document or query and units past the row read
-  // out of range (zeros).  Past the last task the resources are empty: the
-  // same operations, no memory traffic.
+  // folds and closes.  Per task and wave: kCg document copies into LDS (the
+  // four waves together copy the whole slice), then this wave's own query
+  // fragments (2 rows x kPairs unit pairs) into registers, lane l reading
+  // row l % 32, unit 2m + l / 32 of the slice.  Rows past the document or
+  // query and units past the row read out of range (zeros).  Past the last
+  // task the resources are empty: the same operations, no memory traffic.
   // Document copies read whole rows: a wave's copy of chunk c is its rows
   // 8w .. 8w + 7 (1 KB, 8 cache lines), lane l taking row 8w + l / 8 and the
   // unit that leaves the chunk row-major with each row's 8 units

@@ -154,7 +154,10 @@ __device__ __forceinline__ int split_slot_doc(int x, int nqg, int ndx, int& qg) 
   return (band * kBand + within % bsz) * kSpXcds + xcd;
 }
 
-template <class Op>
+// kWhole: rows are whole slices (rowbytes a multiple of kSliceBytes, as at
+// d = 768 in 16 bits or d = 128 in fp32), so no unit lies past a row's end
+// and the slice's byte offset goes to the loads' scalar offset.
+template <class Op, bool kWhole>
 __global__ void __launch_bounds__(64 * kSpWaves, 1) inbatch_split(const InBatchSplitArgs A) {
   typedef typename Op::Acc Acc;
   constexpr int kMmaPerPair = Op::kEsz == 4 ? 4 : 1;
@@ -251,23 +254,40 @@ __global__ void __launch_bounds__(64 * kSpWaves, 1) inbatch_split(const InBatchS
     constexpr int kSet = decltype(SETc)::value;
     // A unit past the row end is pushed out of range with all low 31 bits set
     // (branch-free: a select here became divergent branches around the loads).
-    const int so = is_s * kSliceBytes + copy_off;
-    const int dpast = -(int)(so >= rowbytes) & 0x7fffffff;
+    if constexpr (kWhole) {
+      const int so = is_s * kSliceBytes;  // uniform: the loads' scalar offset
 #pragma unroll
-    for (int c = 0; c < kCg; ++c) {
-      const int row = (is_g * kCg + c) * kTile + crow;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rdoc, (lds_void_t)&dbuf[kSet][c * 256 + wave * 64], 16, (row * rowbytes + so) | dpast,
-          0, 0, 0);
-    }
-#pragma unroll
-    for (int q = 0; q < 2; ++q)
-#pragma unroll
-      for (int m = 0; m < kPairs; ++m) {
-        const int o = is_s * kSliceBytes + (2 * m + h) * 16;
-        const int qpast = -(int)(o >= rowbytes) & 0x7fffffff;
-        qf[kSet][q][m] = buf_load16(rq[q], (r32 * rowbytes + o) | qpast);
+      for (int c = 0; c < kCg; ++c) {
+        const int row = (is_g * kCg + c) * kTile + crow;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rdoc, (lds_void_t)&dbuf[kSet][c * 256 + wave * 64],
+                                                 16, row * rowbytes + copy_off, so, 0, 0);
       }
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+#pragma unroll
+        for (int m = 0; m < kPairs; ++m)
+          qf[kSet][q][m] = __builtin_bit_cast(
+              u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq[q], r32 * rowbytes + (2 * m + h) * 16,
+                                                           so, 0));
+    } else {
+      const int so = is_s * kSliceBytes + copy_off;
+      const int dpast = -(int)(so >= rowbytes) & 0x7fffffff;
+#pragma unroll
+      for (int c = 0; c < kCg; ++c) {
+        const int row = (is_g * kCg + c) * kTile + crow;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rdoc, (lds_void_t)&dbuf[kSet][c * 256 + wave * 64], 16, (row * rowbytes + so) | dpast,
+            0, 0, 0);
+      }
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+#pragma unroll
+        for (int m = 0; m < kPairs; ++m) {
+          const int o = is_s * kSliceBytes + (2 * m + h) * 16;
+          const int qpast = -(int)(o >= rowbytes) & 0x7fffffff;
+          qf[kSet][q][m] = buf_load16(rq[q], (r32 * rowbytes + o) | qpast);
+        }
+    }
     if (++is_s == nslices) {
       is_s = 0;
       if (++is_g == ngroups) {
@@ -529,10 +549,20 @@ hipError_t launch_inbatch_split(int32_t dtype, const InBatchSplitArgs& args_in,
   const int cus = std::max(kSpXcds, device_cus() / kSpXcds * kSpXcds);
   const dim3 grid((unsigned)std::min(A.nslots, cus)), block(64 * kSpWaves);
   if (e == hipSuccess) {
+    const bool whole = A.rowbytes % kSliceBytes == 0;
     switch (dtype) {
-      case 1: hipLaunchKernelGGL(inbatch_split<OpF16>, grid, block, 0, stream, A); break;
-      case 2: hipLaunchKernelGGL(inbatch_split<OpBF16>, grid, block, 0, stream, A); break;
-      default: hipLaunchKernelGGL(inbatch_split<OpF32>, grid, block, 0, stream, A); break;
+      case 1:
+        if (whole) hipLaunchKernelGGL((inbatch_split<OpF16, true>), grid, block, 0, stream, A);
+        else hipLaunchKernelGGL((inbatch_split<OpF16, false>), grid, block, 0, stream, A);
+        break;
+      case 2:
+        if (whole) hipLaunchKernelGGL((inbatch_split<OpBF16, true>), grid, block, 0, stream, A);
+        else hipLaunchKernelGGL((inbatch_split<OpBF16, false>), grid, block, 0, stream, A);
+        break;
+      default:
+        if (whole) hipLaunchKernelGGL((inbatch_split<OpF32, true>), grid, block, 0, stream, A);
+        else hipLaunchKernelGGL((inbatch_split<OpF32, false>), grid, block, 0, stream, A);
+        break;
     }
     e = hipGetLastError();
   }

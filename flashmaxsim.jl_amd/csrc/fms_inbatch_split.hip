@@ -352,8 +352,8 @@ __global__ void __launch_bounds__(64 * kSpWaves, 1) inbatch_split(const InBatchS
     return;
   }
 
-  int ntasks = 0;
-  for (int x = c_slot; x < A.nslots; x = next_slot(x + G)) ntasks += ngroups * nslices;
+  int64_t ntasks = 0;  // (items x groups x slices can pass 2^31 at extreme shapes)
+  for (int x = c_slot; x < A.nslots; x = next_slot(x + G)) ntasks += (int64_t)ngroups * nslices;
   if (ntasks == 0) return;
 
   Acc acc[kCg][2];
@@ -448,7 +448,7 @@ __global__ void __launch_bounds__(64 * kSpWaves, 1) inbatch_split(const InBatchS
   // around a step inside a round, so the compiler's wait counts see every
   // step's loads (a skip edge made it drain the loads of later tasks).
   static_assert(kStages == 3, "the task loop below is unrolled by three");
-  int p = 0;
+  int64_t p = 0;
   for (; p + kStages <= ntasks; p += kStages) {
     step(std::integral_constant<int, 0>());
     step(std::integral_constant<int, 1>());

@@ -205,6 +205,36 @@ __device__ __forceinline__ float max3_ieee(float a, float b, float c) {
   return __builtin_fmaximum_numf(__builtin_fmaximum_numf(a, b), c);
 }
 
+// Three steps of the reverse scan for the first register equal to the
+// chunk maximum: ci = R2 if x2 == cm, else R1 if x1 == cm, else R0 if
+// x0 == cm, else ci (x0, x1, x2 are registers R0 > R1 > R2, scanned in that
+// order).  A compare writes its lane mask to an SGPR pair, and gfx950 needs
+// two wait states between a VALU write of an SGPR and a VALU read of it;
+// the compiler routes every compare of the scan through VCC and so pads
+// each select with an s_nop.  Here the three compares go to three SGPR
+// pairs and each select reads its mask three instructions later, with no
+// padding.  The operands are MFMA results, but every caller's
+// compiler-visible max3 tree has read all of them before cm exists, so the
+// MFMA-result wait states are already behind (see max3_ieee).
+template <int R0, int R1, int R2>
+__device__ __forceinline__ void first_equal3(int& ci, float x0, float x1, float x2, float cm) {
+  uint64_t e0, e1, e2;
+  asm("v_cmp_eq_f32_e64 %1, %4, %7\n\t"
+      "v_cmp_eq_f32_e64 %2, %5, %7\n\t"
+      "v_cmp_eq_f32_e64 %3, %6, %7\n\t"
+      "v_cndmask_b32_e64 %0, %0, %8, %1\n\t"
+      "v_cndmask_b32_e64 %0, %0, %9, %2\n\t"
+      "v_cndmask_b32_e64 %0, %0, %10, %3"
+      : "+v"(ci), "=&s"(e0), "=&s"(e1), "=&s"(e2)
+      : "v"(x0), "v"(x1), "v"(x2), "v"(cm), "n"(R0), "n"(R1), "n"(R2));
+}
+
+// kPadFree: the reverse scan as first_equal3 blocks (no wait-state
+// padding).  Those blocks are opaque to the scheduler, which then cannot
+// spread a tile's fold between the MFMAs of the next tiles as it does with
+// the compiler's own compares; the in-batch kernel, whose throughput rests
+// on that interleave, keeps the compiler's form.
+template <bool kPadFree>
 __device__ __forceinline__ void fold_tree(const float (&s)[16], int slot0, float& mx, int& slot) {
   const float m0 = max3_ieee(s[0], s[1], s[2]);
   const float m1 = max3_ieee(s[3], s[4], s[5]);
@@ -215,8 +245,16 @@ __device__ __forceinline__ void fold_tree(const float (&s)[16], int slot0, float
   const float m6 = max3_ieee(m2, m3, m4);
   const float cm = max3_ieee(m5, m6, -INFINITY);
   int ci = 15;
+  if constexpr (kPadFree) {
+    first_equal3<14, 13, 12>(ci, s[14], s[13], s[12], cm);
+    first_equal3<11, 10, 9>(ci, s[11], s[10], s[9], cm);
+    first_equal3<8, 7, 6>(ci, s[8], s[7], s[6], cm);
+    first_equal3<5, 4, 3>(ci, s[5], s[4], s[3], cm);
+    first_equal3<2, 1, 0>(ci, s[2], s[1], s[0], cm);
+  } else {
 #pragma unroll
-  for (int r = 14; r >= 0; --r) ci = (s[r] == cm) ? r : ci;
+    for (int r = 14; r >= 0; --r) ci = (s[r] == cm) ? r : ci;
+  }
   const bool take = cm > mx;
   mx = take ? cm : mx;
   slot = take ? slot0 + ci : slot;

@@ -693,7 +693,7 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
     float sc[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) sc[r] = ac[r];
-    fold_tree(sc, (int)(inf & 63u) * 16, mx[q], slot[q]);
+    fold_tree<false>(sc, (int)(inf & 63u) * 16, mx[q], slot[q]);
   };
   auto close_if_last = [&](int q0, int q1, uint32_t inf) {
     if (inf & (1u << kInfoLastBit)) {
@@ -826,8 +826,8 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
       fold_tree8<true>(s0, (v1 + 1) * 16 + 8, mx[q0], slot[q0]);
       fold_tree8<true>(s1, (v1 + 1) * 16 + 8, mx[q1], slot[q1]);
     } else {
-      fold_tree(s0, (v0 + 1) * 16, mx[q0], slot[q0]);
-      fold_tree(s1, (v0 + 1) * 16, mx[q1], slot[q1]);
+      fold_tree<false>(s0, (v0 + 1) * 16, mx[q0], slot[q0]);
+      fold_tree<false>(s1, (v0 + 1) * 16, mx[q1], slot[q1]);
     }
   };
   // After a phase: the entry's last bit closes its second half's document.

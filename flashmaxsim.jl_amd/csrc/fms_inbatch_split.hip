@@ -428,7 +428,7 @@ __global__ void __launch_bounds__(64 * kSpWaves, 1) inbatch_split(const InBatchS
           for (int r = 0; r < 16; ++r) s[r] = acc[c][q][r];
           take_first_row(s, m32, h, ch, mx[q], slot[q]);
           if (m32 == 0xffffffffu)
-            fold_tree(s, ch * 16, mx[q], slot[q]);
+            fold_tree<true>(s, ch * 16, mx[q], slot[q]);
           else
             update_chunk(s, m32, h, ch, mx[q], slot[q]);
         }

@@ -535,7 +535,7 @@ __global__ void __launch_bounds__(64 * kWaves, 2) scan_runs_lds(const RunArgs A)
         for (int r = 0; r < 16; ++r) s[r] = acc[r];
         take_first_row(s, m32, h, C.ch, mx[i], slot[i]);
         if (m32 == 0xffffffffu)
-          fold_tree(s, C.ch * 16, mx[i], slot[i]);
+          fold_tree<true>(s, C.ch * 16, mx[i], slot[i]);
         else
           update_chunk(s, m32, h, C.ch, mx[i], slot[i]);
       }

@@ -874,16 +874,6 @@ __device__ __forceinline__ uint32_t ibx_div(uint32_t n, uint32_t m) {
   return m == 0u ? n : __umulhi(n, m);
 }
 
-// f(std::integral_constant<int, kI>()), ..., for kI < kN: a loop whose index is a
-// constant expression (ds_swizzle patterns are immediates).
-template <int kI, int kN, class F>
-__device__ __forceinline__ void static_for(F&& f) {
-  if constexpr (kI < kN) {
-    f(std::integral_constant<int, kI>());
-    static_for<kI + 1, kN>(f);
-  }
-}
-
 // Workgroup (x, y) covers dwords y * kIbxCompactSpan .. + kIbxCompactSpan - 1 of
 // document j's bytes; dword k holds tokens 4 * (k % (Tqp / 4)) .. + 3 of query
 // k / (Tqp / 4).  delta_p = Delta[p] * inv_n[i] in fp32, as bwd_delta computes

@@ -22,6 +22,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace fms {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -258,6 +260,59 @@ __device__ __forceinline__ void fold_tree(const float (&s)[16], int slot0, float
   const bool take = cm > mx;
   mx = take ? cm : mx;
   slot = take ? slot0 + ci : slot;
+}
+
+// f(std::integral_constant<int, kI>()), ..., for kI < kN: a loop whose index
+// is a constant expression (immediates, compile-time dispatch).
+template <int kI, int kN, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (kI < kN) {
+    f(std::integral_constant<int, kI>());
+    static_for<kI + 1, kN>(f);
+  }
+}
+
+// fold_tree<true> cut into eight pieces of four to six VALU instructions,
+// for a kernel that places one piece after each of its MFMAs itself (the
+// scheduler cannot spread the opaque scan blocks): pieces 0 and 1 the max3
+// tree, 2 to 6 the reverse scan, 7 the update.  Same operations, same
+// results.  Piece 1 completes the tree, so every score has been read by a
+// compiler-visible instruction before the scan's asm reads it.
+struct FoldPieces {
+  float m0, m1, m2, m3, cm;
+  int ci;
+};
+
+template <int kP>
+__device__ __forceinline__ void fold_piece(FoldPieces& f, const float (&s)[16], int slot0,
+                                           float& mx, int& slot) {
+  static_assert(kP >= 0 && kP < 8, "eight pieces");
+  if constexpr (kP == 0) {
+    f.m0 = max3_ieee(s[0], s[1], s[2]);
+    f.m1 = max3_ieee(s[3], s[4], s[5]);
+    f.m2 = max3_ieee(s[6], s[7], s[8]);
+    f.m3 = max3_ieee(s[9], s[10], s[11]);
+  } else if constexpr (kP == 1) {
+    const float m4 = max3_ieee(s[12], s[13], s[14]);
+    const float m5 = max3_ieee(s[15], f.m0, f.m1);
+    const float m6 = max3_ieee(f.m2, f.m3, m4);
+    f.cm = max3_ieee(m5, m6, -INFINITY);
+    f.ci = 15;
+  } else if constexpr (kP == 2) {
+    first_equal3<14, 13, 12>(f.ci, s[14], s[13], s[12], f.cm);
+  } else if constexpr (kP == 3) {
+    first_equal3<11, 10, 9>(f.ci, s[11], s[10], s[9], f.cm);
+  } else if constexpr (kP == 4) {
+    first_equal3<8, 7, 6>(f.ci, s[8], s[7], s[6], f.cm);
+  } else if constexpr (kP == 5) {
+    first_equal3<5, 4, 3>(f.ci, s[5], s[4], s[3], f.cm);
+  } else if constexpr (kP == 6) {
+    first_equal3<2, 1, 0>(f.ci, s[2], s[1], s[0], f.cm);
+  } else {
+    const bool take = f.cm > mx;
+    mx = take ? f.cm : mx;
+    slot = take ? slot0 + f.ci : slot;
+  }
 }
 
 // fold_tree8: the same update over one half of the registers, 0..7 (rows

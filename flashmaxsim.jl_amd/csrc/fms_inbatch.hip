@@ -867,7 +867,38 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
 #pragma unroll
     for (int kb = 0; kb < kIbNkb; ++kb) a[kb] = cur[kb * 64 + lane];
     Acc n0, n1, n2, n3;
+    // A phase whose folded entry is not split: tiles (qa, qb) x this chunk
+    // as two MFMA chains, and after each MFMA one eighth of the fold of tile
+    // fa or fb (scores x0, x1 of entry `inf`), fenced so that every MFMA
+    // has its share of VALU work beside it and the fold's compares need no
+    // wait-state padding.
+    auto mma_fold_pinned = [&](Acc& na, Acc& nb, int qa, int qb, const Acc& x0, const Acc& x1,
+                               int fa, int fb, uint32_t inf) {
+      float s0[16], s1[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) { s0[r] = x0[r]; s1[r] = x1[r]; }
+      const int slot0 = ((int)(inf & kHUMask) + 1) * 16;
+      na = Acc{};
+      nb = Acc{};
+      FoldPieces pa, pb;
+      constexpr int kM = 2 * kIbNkb;  // MFMAs of the phase
+      static_for<0, kM>([&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        if constexpr (k % 2 == 0) na = Op::mma(a[k / 2], qf[qa][k / 2], na);
+        else nb = Op::mma(a[k / 2], qf[qb][k / 2], nb);
+        static_for<(16 * k + kM - 1) / kM, (16 * (k + 1) + kM - 1) / kM>([&](auto pc) {
+          constexpr int p = decltype(pc)::value;
+          if constexpr (p < 8) fold_piece<p>(pa, s0, slot0, mx[fa], slot[fa]);
+          else fold_piece<p - 8>(pb, s1, slot0, mx[fb], slot[fb]);
+        });
+        __builtin_amdgcn_sched_barrier(0);
+      });
+    };
     auto phase1 = [&](auto split) {
+      if constexpr (!decltype(split)::value) {
+        mma_fold_pinned(n0, n1, 0, 1, lag2, lag3, 2, 3, pinfo);
+        return;
+      }
       n0 = Acc{};
       n1 = Acc{};
 #pragma unroll
@@ -883,6 +914,10 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
     close_units(2, 3, pinfo);
     __builtin_amdgcn_s_setprio(2);
     auto phase2 = [&](auto split) {
+      if constexpr (!decltype(split)::value) {
+        mma_fold_pinned(n2, n3, 2, 3, n0, n1, 0, 1, info);
+        return;
+      }
       n2 = Acc{};
       n3 = Acc{};
 #pragma unroll

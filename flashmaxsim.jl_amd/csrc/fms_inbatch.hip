@@ -296,8 +296,16 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
   __shared__ int lst_count;
   __shared__ int any_nf;  // some document's first valid row is not finite
   __shared__ int16_t res_tape[kIbWaves][kIbQpw][kIbMaxDocs][kTile];  // Td <= 2048
-  __shared__ float res_score[kIbWaves][kIbQpw][kIbMaxDocs];
-  __shared__ float score_sink[kHalf ? 64 : 1];  // branch-free close: the other lanes' stores
+  // Scores per (wave, query tile, document), then (units) 64 sink floats
+  // for the branch-free close: lane 0 stores the score, the other lanes
+  // store to the sink.  One array, so the compiler can tell the store from
+  // the chunk buffers the loads to LDS write (a store through a pointer
+  // that may point into either of two arrays made it wait for every load
+  // in flight at each close).
+  constexpr int kScoreWords = kIbWaves * kIbQpw * kIbMaxDocs;
+  __shared__ float score_buf[kScoreWords + (kHalf ? 64 : 0)];
+  float (&res_score)[kIbWaves][kIbQpw][kIbMaxDocs] =
+      *reinterpret_cast<float(*)[kIbWaves][kIbQpw][kIbMaxDocs]>(score_buf);
 
   const int tid = threadIdx.x, lane = tid & 63, wave = uniform(tid >> 6);
   const int r32 = lane & 31, h = lane >> 5;
@@ -678,7 +686,7 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
       // without branches: both halves hold the merged token and store it to
       // the same place; lanes other than 0 store the score to a sink
       res_tape[wave][q][jj][r32] = (int16_t)(tv ? tok : 0);
-      *(lane == 0 ? &res_score[wave][q][jj] : &score_sink[lane]) = score;
+      score_buf[lane == 0 ? (wave * kIbQpw + q) * kIbMaxDocs + jj : kScoreWords + lane] = score;
     } else {
       if (h == 0) res_tape[wave][q][jj][r32] = (int16_t)(tv ? tok : 0);
       if (lane == 0) res_score[wave][q][jj] = score;
@@ -741,6 +749,33 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
     }
   };
 
+  // Tiles (qa, qb) x a chunk (fragments `a`) as two MFMA chains, and after
+  // each MFMA one eighth of the fold of tiles fa and fb (scores x0, x1 of
+  // an entry whose first slot is slot0), fenced so that every MFMA has its
+  // share of VALU work beside it and the fold's compares need no wait-state
+  // padding (fold_piece).
+  auto mma_fold_pinned = [&](const Frag (&a)[kIbNkb], Acc& na, Acc& nb, int qa, int qb,
+                             const Acc& x0, const Acc& x1, int fa, int fb, int slot0) {
+    float s0[16], s1[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) { s0[r] = x0[r]; s1[r] = x1[r]; }
+    na = Acc{};
+    nb = Acc{};
+    FoldPieces pa, pb;
+    constexpr int kM = 2 * kIbNkb;  // MFMAs of the phase
+    static_for<0, kM>([&](auto kc) {
+      constexpr int k = decltype(kc)::value;
+      if constexpr (k % 2 == 0) na = Op::mma(a[k / 2], qf[qa][k / 2], na);
+      else nb = Op::mma(a[k / 2], qf[qb][k / 2], nb);
+      static_for<(16 * k + kM - 1) / kM, (16 * (k + 1) + kM - 1) / kM>([&](auto pc) {
+        constexpr int p = decltype(pc)::value;
+        if constexpr (p < 8) fold_piece<p>(pa, s0, slot0, mx[fa], slot[fa]);
+        else fold_piece<p - 8>(pb, s1, slot0, mx[fb], slot[fb]);
+      });
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  };
+
   // One step: entry i+1 register -> LDS, refill that register stage with
   // entry i+3, read the list info for the next step, then two phases of 16
   // MFMAs (two independent accumulation chains each):
@@ -774,24 +809,11 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
     Frag a[kIbNkb];
 #pragma unroll
     for (int kb = 0; kb < kIbNkb; ++kb) a[kb] = cur[kb * 64 + lane];
-    Acc n0 = Acc{}, n1 = Acc{};
-#pragma unroll
-    for (int kb = 0; kb < kIbNkb; ++kb) {
-      n0 = Op::mma(a[kb], qf[0][kb], n0);
-      n1 = Op::mma(a[kb], qf[1][kb], n1);
-    }
-    fold_close(2, lag2, pinfo);
-    fold_close(3, lag3, pinfo);
+    Acc n0, n1, n2, n3;
+    mma_fold_pinned(a, n0, n1, 0, 1, lag2, lag3, 2, 3, (int)(pinfo & 63u) * 16);
     close_if_last(2, 3, pinfo);
     __builtin_amdgcn_s_setprio(2);
-    Acc n2 = Acc{}, n3 = Acc{};
-#pragma unroll
-    for (int kb = 0; kb < kIbNkb; ++kb) {
-      n2 = Op::mma(a[kb], qf[2][kb], n2);
-      n3 = Op::mma(a[kb], qf[3][kb], n3);
-    }
-    fold_close(0, n0, info);
-    fold_close(1, n1, info);
+    mma_fold_pinned(a, n2, n3, 2, 3, n0, n1, 0, 1, (int)(info & 63u) * 16);
     close_if_last(0, 1, info);
     __builtin_amdgcn_s_setprio(1);
     lag2 = n2;
@@ -867,36 +889,9 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
 #pragma unroll
     for (int kb = 0; kb < kIbNkb; ++kb) a[kb] = cur[kb * 64 + lane];
     Acc n0, n1, n2, n3;
-    // A phase whose folded entry is not split: tiles (qa, qb) x this chunk
-    // as two MFMA chains, and after each MFMA one eighth of the fold of tile
-    // fa or fb (scores x0, x1 of entry `inf`), fenced so that every MFMA
-    // has its share of VALU work beside it and the fold's compares need no
-    // wait-state padding.
-    auto mma_fold_pinned = [&](Acc& na, Acc& nb, int qa, int qb, const Acc& x0, const Acc& x1,
-                               int fa, int fb, uint32_t inf) {
-      float s0[16], s1[16];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) { s0[r] = x0[r]; s1[r] = x1[r]; }
-      const int slot0 = ((int)(inf & kHUMask) + 1) * 16;
-      na = Acc{};
-      nb = Acc{};
-      FoldPieces pa, pb;
-      constexpr int kM = 2 * kIbNkb;  // MFMAs of the phase
-      static_for<0, kM>([&](auto kc) {
-        constexpr int k = decltype(kc)::value;
-        if constexpr (k % 2 == 0) na = Op::mma(a[k / 2], qf[qa][k / 2], na);
-        else nb = Op::mma(a[k / 2], qf[qb][k / 2], nb);
-        static_for<(16 * k + kM - 1) / kM, (16 * (k + 1) + kM - 1) / kM>([&](auto pc) {
-          constexpr int p = decltype(pc)::value;
-          if constexpr (p < 8) fold_piece<p>(pa, s0, slot0, mx[fa], slot[fa]);
-          else fold_piece<p - 8>(pb, s1, slot0, mx[fb], slot[fb]);
-        });
-        __builtin_amdgcn_sched_barrier(0);
-      });
-    };
     auto phase1 = [&](auto split) {
       if constexpr (!decltype(split)::value) {
-        mma_fold_pinned(n0, n1, 0, 1, lag2, lag3, 2, 3, pinfo);
+        mma_fold_pinned(a, n0, n1, 0, 1, lag2, lag3, 2, 3, ((int)(pinfo & kHUMask) + 1) * 16);
         return;
       }
       n0 = Acc{};
@@ -915,7 +910,7 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
     __builtin_amdgcn_s_setprio(2);
     auto phase2 = [&](auto split) {
       if constexpr (!decltype(split)::value) {
-        mma_fold_pinned(n2, n3, 2, 3, n0, n1, 0, 1, info);
+        mma_fold_pinned(a, n2, n3, 2, 3, n0, n1, 0, 1, ((int)(info & kHUMask) + 1) * 16);
         return;
       }
       n2 = Acc{};

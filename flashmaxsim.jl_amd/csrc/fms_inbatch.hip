@@ -673,14 +673,14 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
     int tok = kHalf ? slot_to_token16(slot[q], h) : slot_to_token(slot[q], h);
     float m = mx[q];
     merge_halves(m, tok, h);
-    // Branch-free: the mask word is read for every lane (t0 is always a
-    // valid token index of the document).
-    const int t0 = tok > 0 ? tok - 1 : 0;
-    const uint32_t mw = chunk_mask[jj * nch + (t0 >> 5)];
-    const bool real = (tok > 0) & (((mw >> (t0 & 31)) & 1u) != 0u);
-    tok = real ? tok : f + 1;
+    // Map a winning copy back to f.  The winner is the lowest row that
+    // reaches the maximum, and every copy scores exactly what f scores, so
+    // a copy after f never wins (f reaches the same maximum first): only a
+    // masked row before f can, or none (tok 0, all scores -Inf or NaN).
+    // Both are the tokens below f + 1.  After the mapping tok >= 1.
+    tok = tok > f + 1 ? tok : f + 1;
     const bool tv = token_valid(q);
-    const float part = (tv & (tok != 0)) ? m : 0.0f;
+    const float part = tv ? m : 0.0f;
     const float score = half_sum(part);
     if constexpr (kHalf) {
       // without branches: both halves hold the merged token and store it to
@@ -727,12 +727,9 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
         int tok = slot_to_token(slot[t], h);
         float m = mx[t];
         merge_halves(m, tok, h);
-        const int t0 = tok > 0 ? tok - 1 : 0;
-        const uint32_t mw = chunk_mask[jj * nch + (t0 >> 5)];
-        const bool real = (tok > 0) & (((mw >> (t0 & 31)) & 1u) != 0u);
-        tok = real ? tok : f + 1;
+        tok = tok > f + 1 ? tok : f + 1;  // a winning copy maps back to f, as in `close`
         const bool tv = t24_valid(t);
-        part[t] = (tv & (tok != 0)) ? m : 0.0f;
+        part[t] = tv ? m : 0.0f;
         if (h == 0) res_tape[wave][t24_query(t)][jj][t24_token(t)] = (int16_t)(tv ? tok : 0);
         mx[t] = -INFINITY;
         slot[t] = -1;

@@ -9,10 +9,11 @@
 // same fused scores and argmax tape as the other in-batch kernel.
 //
 // Work item = one document j x kRows query rows (a query row is a 32-token
-// tile of a query: query v / ntq, tokens 32 (v % ntq) ..).  One block of 4
-// waves per CU walks its items in turn (a persistent grid).  An item's
-// document chunks are taken kCg at a time (a chunk group); per group the
-// block runs the whole K loop:
+// tile of a query: query v / ntq, tokens 32 (v % ntq) ..).  Blocks of 4
+// waves, one per CU for 16-bit features and two for fp32, each walk their
+// items in turn (a persistent grid).  An item's document chunks are taken
+// kCg at a time (a chunk group: 6 chunks for 16-bit features, 3 for fp32);
+// per group the block runs the whole K loop:
 //   * K advances by a slice of 128 bytes of every row (64 features of a
 //     16-bit type, 32 of fp32).  The document's slice (shared by the four
 //     waves) goes HBM/L2 -> LDS with direct buffer-to-LDS loads (no
@@ -67,20 +68,34 @@ namespace {
 
 constexpr int kSpWaves = 4;
 constexpr int kRows = 2 * kSpWaves;     // query rows per block (two per wave)
-constexpr int kCg = 6;                  // document chunks per group
 constexpr int kSliceBytes = 128;        // bytes of every row per K step
 constexpr int kPairs = kSliceBytes / 32;  // unit pairs per slice (4)
-constexpr int kDFrags = kCg * kPairs;   // 1 KB blocks of a document slice
 constexpr int kStages = 3;              // document slice stages in LDS (2 slices ahead)
 static_assert(kTile == 8 * kSpWaves, "every wave copies 8 whole rows of each chunk");
-// Vector memory operations per slice and wave: kCg document copies into LDS,
-// then 2 x kPairs query fragment loads into registers.
-constexpr int kQLoads = 2 * kPairs;
-constexpr int kOpsPerSlice = kCg + kQLoads;
-// Issued after a slice's document copies by the time that slice is read: its
-// own query loads and the two slices requested since.
-constexpr int kAfterCopies = kQLoads + (kStages - 2) * kOpsPerSlice;
-static_assert(kAfterCopies < 64, "vmcnt field");
+constexpr int kQLoads = 2 * kPairs;     // query fragment loads per slice and wave
+
+// The chunk group per element size.  kCg document chunks per group, kBlocks
+// blocks per CU.  16-bit: six chunks, one block (a wave holds 12 accumulator
+// tiles and its query fragments in about 424 registers).  fp32: three
+// chunks, two blocks (256 registers): its MFMAs take 8 times as long per
+// byte, so a second wave per SIMD covers the first one's per-slice work
+// (measured at the C3 shape: 3.55 -> 3.39 ms), while for 16-bit features the
+// halved reuse of each query fragment costs more than that (2.85 -> 3.71 ms).
+template <int kEsz>
+struct SplitShape {
+  static constexpr int kCg = kEsz == 4 ? 3 : 6;
+  static constexpr int kBlocks = kEsz == 4 ? 2 : 1;
+  static constexpr int kDFrags = kCg * kPairs;  // 1 KB blocks of a document slice
+  // Vector memory operations per slice and wave: kCg document copies into
+  // LDS, then the query fragment loads into registers.
+  static constexpr int kOpsPerSlice = kCg + kQLoads;
+  // Issued after a slice's document copies by the time that slice is read:
+  // its own query loads and the two slices requested since.
+  static constexpr int kAfterCopies = kQLoads + (kStages - 2) * kOpsPerSlice;
+  static_assert(kAfterCopies < 64, "vmcnt field");
+};
+constexpr int kMaxCg = SplitShape<2>::kCg;  // the largest group (range checks)
+static_assert(SplitShape<4>::kCg <= kMaxCg, "range checks cover every shape");
 constexpr int kSpXcds = 8;
 constexpr int kBand = 8;  // documents an XCD keeps in flight together
 
@@ -158,8 +173,11 @@ __device__ __forceinline__ int split_slot_doc(int x, int nqg, int ndx, int& qg) 
 // d = 768 in 16 bits or d = 128 in fp32), so no unit lies past a row's end
 // and the slice's byte offset goes to the loads' scalar offset.
 template <class Op, bool kWhole>
-__global__ void __launch_bounds__(64 * kSpWaves, 1) inbatch_split(const InBatchSplitArgs A) {
+__global__ void __launch_bounds__(64 * kSpWaves, SplitShape<Op::kEsz>::kBlocks)
+    inbatch_split(const InBatchSplitArgs A) {
   typedef typename Op::Acc Acc;
+  typedef SplitShape<Op::kEsz> Shape;
+  constexpr int kCg = Shape::kCg, kDFrags = Shape::kDFrags, kAfterCopies = Shape::kAfterCopies;
   constexpr int kMmaPerPair = Op::kEsz == 4 ? 4 : 1;
   typedef __attribute__((address_space(3))) void* lds_void_t;
   __shared__ u32x4 dbuf[kStages][kDFrags * 64];
@@ -498,7 +516,7 @@ bool inbatch_split_supported(int esz, int64_t dim, int64_t Tq, int64_t Td, int64
   const int64_t lim = ((int64_t)1 << 31) - 4096;
   return (esz == 2 || esz == 4) && dim > 0 && rowbytes % 16 == 0 && al && Tq >= 1 && Td >= 0 &&
          Bq >= 1 && Bd >= 1 && Bq * ntq <= ((int64_t)1 << 30) && Bd <= ((int64_t)1 << 26) &&
-         (Td + kTile * kCg) * rowbytes < lim && kTile * rowbytes < lim &&
+         (Td + kTile * kMaxCg) * rowbytes < lim && kTile * rowbytes < lim &&
          nqg <= lim / kSpXcds / ndx;
 }
 
@@ -544,10 +562,11 @@ hipError_t launch_inbatch_split(int32_t dtype, const InBatchSplitArgs& args_in,
                      dim3(256), 0, stream, A.dm, A.qm, A.Bd, A.Td, nch, A.Bq, A.Tq, A.ntq,
                      static_cast<uint32_t*>(ws));
   e = hipGetLastError();
-  // One block per CU (a multiple of 8, so slot x stays on XCD x % 8), each
-  // walking its slots.
+  // kBlocks blocks per CU (CUs a multiple of 8, so slot x stays on XCD
+  // x % 8), each walking its slots.
   const int cus = std::max(kSpXcds, device_cus() / kSpXcds * kSpXcds);
-  const dim3 grid((unsigned)std::min(A.nslots, cus)), block(64 * kSpWaves);
+  const int per_cu = dtype == 0 ? SplitShape<4>::kBlocks : SplitShape<2>::kBlocks;
+  const dim3 grid((unsigned)std::min(A.nslots, cus * per_cu)), block(64 * kSpWaves);
   if (e == hipSuccess) {
     const bool whole = A.rowbytes % kSliceBytes == 0;
     switch (dtype) {

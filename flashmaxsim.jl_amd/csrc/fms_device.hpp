@@ -395,15 +395,22 @@ __device__ __forceinline__ bool is_nan_bits(float x) {
 
 // Merge the (max, token) of lanes l and l^32, which hold disjoint document
 // rows of the same query token.  Equal maxima keep the lower token, matching
-// a sequential ascending scan.  h = lane / 32.
+// a sequential ascending scan.  h = lane / 32.  kNoNaN: neither maximum can
+// be NaN (a fold that never takes a NaN score), so the NaN tests drop out.
+template <bool kNoNaN = false>
 __device__ __forceinline__ void merge_halves(float& mx, int& tok, int h) {
   const float omx = __builtin_bit_cast(float, lane_xor32(__builtin_bit_cast(uint32_t, mx), h));
   const int otok = (int)lane_xor32((uint32_t)tok, h);
   // Bitwise, not short-circuit: no exec-mask branches.  A NaN maximum can
   // only be the first valid token's (take_first_row) and it stands.
-  const bool nan_here = is_nan_bits(mx), nan_there = is_nan_bits(omx);
-  const bool take = (otok != 0) & !nan_here &
-                    ((tok == 0) | nan_there | (omx > mx) | ((omx == mx) & (otok < tok)));
+  bool take;
+  if constexpr (kNoNaN) {
+    take = (otok != 0) & ((tok == 0) | (omx > mx) | ((omx == mx) & (otok < tok)));
+  } else {
+    const bool nan_here = is_nan_bits(mx), nan_there = is_nan_bits(omx);
+    take = (otok != 0) & !nan_here &
+           ((tok == 0) | nan_there | (omx > mx) | ((omx == mx) & (otok < tok)));
+  }
   mx = take ? omx : mx;
   tok = take ? otok : tok;
 }

@@ -636,13 +636,17 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
       // Every per-lane term is recomputed here from the lane id (an asm the
       // compiler cannot hoist) and selects between uniform values, so no
       // lane constant stays live across the step loop.
+      // The half of the entry is picked by per-lane shift amounts and the
+      // row by a multiply, not by selects: selects between uniform values
+      // on a lane condition became exec-masked branches.
       const int ln = lane_id_here();
-      const bool hi = (ln & 16) != 0;
-      const uint32_t ux = hi ? info >> kHU1Shift : info;
-      const uint32_t jx = hi ? info >> kHDoc1Shift : info >> kHDoc0Shift;
-      const uint32_t fx = hi ? (uint32_t)row0 >> 16 : (uint32_t)row0 & 0xffffu;
-      const int src = ((m >> (ln & 31)) & 1u) ? 16 * (int)(ux & kHUMask) + (ln & 15) : (int)fx;
-      voff = ((int)(jx & kInfoDocMask) * Td + src) * kIbRowBytes + ((ln >> 5) << 4);
+      const uint32_t hi = ((uint32_t)ln >> 4) & 1u;  // chunk rows 16..31: the second half
+      const int ux = (int)((info >> (hi * kHU1Shift)) & kHUMask);
+      const int jx = (int)((info >> (kHDoc0Shift + hi * (kHDoc1Shift - kHDoc0Shift))) & kInfoDocMask);
+      const int fx = (int)(((uint32_t)row0 >> (hi << 4)) & 0xffffu);
+      const int real = (int)((m >> (ln & 31)) & 1u);
+      const int src = fx + real * (16 * ux + (ln & 15) - fx);
+      voff = (jx * Td + src) * kIbRowBytes + ((ln >> 5) << 4);
     } else {
       const int ch = info & 63u, jj = (info >> kInfoDocShift) & kInfoDocMask;
       const int f = (int)((info >> kInfoFirstShift) & kInfoFirstMask) - 1;
@@ -672,7 +676,7 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
   auto close = [&](int q, int jj, int f) {
     int tok = kHalf ? slot_to_token16(slot[q], h) : slot_to_token(slot[q], h);
     float m = mx[q];
-    merge_halves(m, tok, h);
+    merge_halves<true>(m, tok, h);  // the folds here never take a NaN
     // Map a winning copy back to f.  The winner is the lowest row that
     // reaches the maximum, and every copy scores exactly what f scores, so
     // a copy after f never wins (f reaches the same maximum first): only a
@@ -726,7 +730,7 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
       for (int t = 0; t < 3; ++t) {
         int tok = slot_to_token(slot[t], h);
         float m = mx[t];
-        merge_halves(m, tok, h);
+        merge_halves<true>(m, tok, h);
         tok = tok > f + 1 ? tok : f + 1;  // a winning copy maps back to f, as in `close`
         const bool tv = t24_valid(t);
         part[t] = tv ? m : 0.0f;

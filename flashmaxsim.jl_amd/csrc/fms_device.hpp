@@ -236,7 +236,23 @@ __device__ __forceinline__ void first_equal3(int& ci, float x0, float x1, float 
 // spread a tile's fold between the MFMAs of the next tiles as it does with
 // the compiler's own compares; the in-batch kernel, whose throughput rests
 // on that interleave, keeps the compiler's form.
-template <bool kPadFree>
+// kRowSlots: the slot records the register's row offset acc_row(r, 0)
+// instead of r (slot0 + acc_row(r, 0) + 4 h is then the chunk row), so a
+// close turns a slot into a token with one add.  Both are compile-time
+// constants of the scan.
+template <bool kRowSlots>
+__device__ __forceinline__ constexpr int reg_slot(int r) {
+  return kRowSlots ? acc_row(r, 0) : r;
+}
+
+// first_equal3 over registers r0, r0 - 1, r0 - 2 of a chunk's scores.
+template <bool kRowSlots, int kR0>
+__device__ __forceinline__ void first_equal_regs(int& ci, const float (&s)[16], float cm) {
+  first_equal3<reg_slot<kRowSlots>(kR0), reg_slot<kRowSlots>(kR0 - 1), reg_slot<kRowSlots>(kR0 - 2)>(
+      ci, s[kR0], s[kR0 - 1], s[kR0 - 2], cm);
+}
+
+template <bool kPadFree, bool kRowSlots = false>
 __device__ __forceinline__ void fold_tree(const float (&s)[16], int slot0, float& mx, int& slot) {
   const float m0 = max3_ieee(s[0], s[1], s[2]);
   const float m1 = max3_ieee(s[3], s[4], s[5]);
@@ -246,16 +262,16 @@ __device__ __forceinline__ void fold_tree(const float (&s)[16], int slot0, float
   const float m5 = max3_ieee(s[15], m0, m1);
   const float m6 = max3_ieee(m2, m3, m4);
   const float cm = max3_ieee(m5, m6, -INFINITY);
-  int ci = 15;
+  int ci = reg_slot<kRowSlots>(15);
   if constexpr (kPadFree) {
-    first_equal3<14, 13, 12>(ci, s[14], s[13], s[12], cm);
-    first_equal3<11, 10, 9>(ci, s[11], s[10], s[9], cm);
-    first_equal3<8, 7, 6>(ci, s[8], s[7], s[6], cm);
-    first_equal3<5, 4, 3>(ci, s[5], s[4], s[3], cm);
-    first_equal3<2, 1, 0>(ci, s[2], s[1], s[0], cm);
+    first_equal_regs<kRowSlots, 14>(ci, s, cm);
+    first_equal_regs<kRowSlots, 11>(ci, s, cm);
+    first_equal_regs<kRowSlots, 8>(ci, s, cm);
+    first_equal_regs<kRowSlots, 5>(ci, s, cm);
+    first_equal_regs<kRowSlots, 2>(ci, s, cm);
   } else {
 #pragma unroll
-    for (int r = 14; r >= 0; --r) ci = (s[r] == cm) ? r : ci;
+    for (int r = 14; r >= 0; --r) ci = (s[r] == cm) ? reg_slot<kRowSlots>(r) : ci;
   }
   const bool take = cm > mx;
   mx = take ? cm : mx;
@@ -283,7 +299,7 @@ struct FoldPieces {
   int ci;
 };
 
-template <int kP>
+template <int kP, bool kRowSlots = false>
 __device__ __forceinline__ void fold_piece(FoldPieces& f, const float (&s)[16], int slot0,
                                            float& mx, int& slot) {
   static_assert(kP >= 0 && kP < 8, "eight pieces");
@@ -297,17 +313,17 @@ __device__ __forceinline__ void fold_piece(FoldPieces& f, const float (&s)[16], 
     const float m5 = max3_ieee(s[15], f.m0, f.m1);
     const float m6 = max3_ieee(f.m2, f.m3, m4);
     f.cm = max3_ieee(m5, m6, -INFINITY);
-    f.ci = 15;
+    f.ci = reg_slot<kRowSlots>(15);
   } else if constexpr (kP == 2) {
-    first_equal3<14, 13, 12>(f.ci, s[14], s[13], s[12], f.cm);
+    first_equal_regs<kRowSlots, 14>(f.ci, s, f.cm);
   } else if constexpr (kP == 3) {
-    first_equal3<11, 10, 9>(f.ci, s[11], s[10], s[9], f.cm);
+    first_equal_regs<kRowSlots, 11>(f.ci, s, f.cm);
   } else if constexpr (kP == 4) {
-    first_equal3<8, 7, 6>(f.ci, s[8], s[7], s[6], f.cm);
+    first_equal_regs<kRowSlots, 8>(f.ci, s, f.cm);
   } else if constexpr (kP == 5) {
-    first_equal3<5, 4, 3>(f.ci, s[5], s[4], s[3], f.cm);
+    first_equal_regs<kRowSlots, 5>(f.ci, s, f.cm);
   } else if constexpr (kP == 6) {
-    first_equal3<2, 1, 0>(f.ci, s[2], s[1], s[0], f.cm);
+    first_equal_regs<kRowSlots, 2>(f.ci, s, f.cm);
   } else {
     const bool take = f.cm > mx;
     mx = take ? f.cm : mx;
@@ -318,17 +334,18 @@ __device__ __forceinline__ void fold_piece(FoldPieces& f, const float (&s)[16], 
 // fold_tree8: the same update over one half of the registers, 0..7 (rows
 // 0..15 of the chunk) or 8..15 (rows 16..31), when the two halves of a chunk
 // belong to different documents.  slot = slot0 + register index within the
-// half.
-template <bool kUpper>
+// half (kRowSlots: its row offset, acc_row(8 + r, 0) = 16 + acc_row(r, 0)).
+template <bool kUpper, bool kRowSlots = false>
 __device__ __forceinline__ void fold_tree8(const float (&s)[16], int slot0, float& mx, int& slot) {
   constexpr int o = kUpper ? 8 : 0;
+  // (reg_slot of the half's own index: slot0 carries the rest)
   const float m0 = max3_ieee(s[o + 0], s[o + 1], s[o + 2]);
   const float m1 = max3_ieee(s[o + 3], s[o + 4], s[o + 5]);
   const float m2 = max3_ieee(s[o + 6], s[o + 7], m0);
   const float cm = max3_ieee(m1, m2, -INFINITY);
-  int ci = 7;
+  int ci = reg_slot<kRowSlots>(7);
 #pragma unroll
-  for (int r = 6; r >= 0; --r) ci = (s[o + r] == cm) ? r : ci;
+  for (int r = 6; r >= 0; --r) ci = (s[o + r] == cm) ? reg_slot<kRowSlots>(r) : ci;
   const bool take = cm > mx;
   mx = take ? cm : mx;
   slot = take ? slot0 + ci : slot;
@@ -405,7 +422,8 @@ __device__ __forceinline__ void merge_halves(float& mx, int& tok, int h) {
   // only be the first valid token's (take_first_row) and it stands.
   bool take;
   if constexpr (kNoNaN) {
-    take = (otok != 0) & ((tok == 0) | (omx > mx) | ((omx == mx) & (otok < tok)));
+    // (tokens <= 0 mean none: the row-slot encoding leaves no slot negative)
+    take = (otok > 0) & ((tok <= 0) | (omx > mx) | ((omx == mx) & (otok < tok)));
   } else {
     const bool nan_here = is_nan_bits(mx), nan_there = is_nan_bits(omx);
     take = (otok != 0) & !nan_here &

@@ -663,10 +663,18 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
     if (ld_i + 1 < nsteps_pad) ++ld_i;
   };
 
+  // Running maxima and their slots.  Slots hold the chunk row base plus the
+  // register's row offset (kRowSlots of the folds): unit stream, 16 (v + 1)
+  // where chunk row 0 is document row 16 v; 32-row chunks, 32 x chunk.  The
+  // 1-based token is then slot + tok_off(), and kNoSlot (nothing taken)
+  // gives a token below 1.  (tok_off is recomputed from the lane id where it
+  // is used: one more register live across the step loop made it spill.)
+  constexpr int kNoSlot = -(1 << 24);
+  auto tok_off = [&]() { return ((lane_id_here() >> 3) & 4) + (kHalf ? -15 : 1); };
   float mx[kIbQpw];
   int slot[kIbQpw];
 #pragma unroll
-  for (int q = 0; q < kIbQpw; ++q) { mx[q] = -INFINITY; slot[q] = -1; }
+  for (int q = 0; q < kIbQpw; ++q) { mx[q] = -INFINITY; slot[q] = kNoSlot; }
 
   // Close query q's document jj: merge the wave halves, map a winning
   // substituted row back to the first valid token f, reduce the score,
@@ -674,7 +682,7 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
   // scores are all -Inf closes on f with -Inf, as the reference's first-token
   // rule gives; the NaN case of that rule is settled after the loop.)
   auto close = [&](int q, int jj, int f) {
-    int tok = kHalf ? slot_to_token16(slot[q], h) : slot_to_token(slot[q], h);
+    int tok = slot[q] + tok_off();
     float m = mx[q];
     merge_halves<true>(m, tok, h);  // the folds here never take a NaN
     // Map a winning copy back to f.  The winner is the lowest row that
@@ -696,7 +704,7 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
       if (lane == 0) res_score[wave][q][jj] = score;
     }
     mx[q] = -INFINITY;
-    slot[q] = -1;
+    slot[q] = kNoSlot;
   };
 
   // Fold one query tile's chunk scores into its running max/argmax, and
@@ -705,7 +713,7 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
     float sc[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) sc[r] = ac[r];
-    fold_tree<false>(sc, (int)(inf & 63u) * 16, mx[q], slot[q]);
+    fold_tree<false, true>(sc, (int)(inf & 63u) * kTile, mx[q], slot[q]);
   };
   auto close_if_last = [&](int q0, int q1, uint32_t inf) {
     if (inf & (1u << kInfoLastBit)) {
@@ -728,7 +736,7 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
       float part[3];
 #pragma unroll
       for (int t = 0; t < 3; ++t) {
-        int tok = slot_to_token(slot[t], h);
+        int tok = slot[t] + tok_off();
         float m = mx[t];
         merge_halves<true>(m, tok, h);
         tok = tok > f + 1 ? tok : f + 1;  // a winning copy maps back to f, as in `close`
@@ -736,7 +744,7 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
         part[t] = tv ? m : 0.0f;
         if (h == 0) res_tape[wave][t24_query(t)][jj][t24_token(t)] = (int16_t)(tv ? tok : 0);
         mx[t] = -INFINITY;
-        slot[t] = -1;
+        slot[t] = kNoSlot;
       }
       const float l0 = half_sum(r32 < 24 ? part[0] : 0.0f), u0 = half_sum(r32 < 24 ? 0.0f : part[0]);
       const float l1 = half_sum(r32 < 16 ? part[1] : 0.0f), u1 = half_sum(r32 < 16 ? 0.0f : part[1]);
@@ -770,8 +778,8 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
       else nb = Op::mma(a[k / 2], qf[qb][k / 2], nb);
       static_for<(16 * k + kM - 1) / kM, (16 * (k + 1) + kM - 1) / kM>([&](auto pc) {
         constexpr int p = decltype(pc)::value;
-        if constexpr (p < 8) fold_piece<p>(pa, s0, slot0, mx[fa], slot[fa]);
-        else fold_piece<p - 8>(pb, s1, slot0, mx[fb], slot[fb]);
+        if constexpr (p < 8) fold_piece<p, true>(pa, s0, slot0, mx[fa], slot[fa]);
+        else fold_piece<p - 8, true>(pb, s1, slot0, mx[fb], slot[fb]);
       });
       __builtin_amdgcn_sched_barrier(0);
     });
@@ -811,10 +819,10 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
 #pragma unroll
     for (int kb = 0; kb < kIbNkb; ++kb) a[kb] = cur[kb * 64 + lane];
     Acc n0, n1, n2, n3;
-    mma_fold_pinned(a, n0, n1, 0, 1, lag2, lag3, 2, 3, (int)(pinfo & 63u) * 16);
+    mma_fold_pinned(a, n0, n1, 0, 1, lag2, lag3, 2, 3, (int)(pinfo & 63u) * kTile);
     close_if_last(2, 3, pinfo);
     __builtin_amdgcn_s_setprio(2);
-    mma_fold_pinned(a, n2, n3, 2, 3, n0, n1, 0, 1, (int)(info & 63u) * 16);
+    mma_fold_pinned(a, n2, n3, 2, 3, n0, n1, 0, 1, (int)(info & 63u) * kTile);
     close_if_last(0, 1, info);
     __builtin_amdgcn_s_setprio(1);
     lag2 = n2;
@@ -831,8 +839,8 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
   // the first document, closes it, and starts the second document with
   // registers 8..15 (the close is branch-free, so the whole phase stays one
   // block for the scheduler to interleave with its MFMAs).  Slots are
-  // (v + 1) * 16 + register, where chunk row 0 is document row 16 v
-  // (slot_to_token16).
+  // (v + 1) * 16 + the register's row offset, where chunk row 0 is document
+  // row 16 v (the upper half's registers 8..15 start at row offset 16).
   auto fold_units = [&](int q0, int q1, const Acc& x0, const Acc& x1, uint32_t inf, auto split) {
     float s0[16], s1[16];
 #pragma unroll
@@ -842,15 +850,15 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
       const int v1 = (int)((inf >> kHU1Shift) & kHUMask) - 1;
       const int jj = (int)((inf >> kHDoc0Shift) & kInfoDocMask);
       const int f = uniform(doc_first[jj]) & 0xffff;
-      fold_tree8<false>(s0, (v0 + 1) * 16, mx[q0], slot[q0]);
-      fold_tree8<false>(s1, (v0 + 1) * 16, mx[q1], slot[q1]);
+      fold_tree8<false, true>(s0, (v0 + 1) * 16, mx[q0], slot[q0]);
+      fold_tree8<false, true>(s1, (v0 + 1) * 16, mx[q1], slot[q1]);
       close(q0, jj, f);
       close(q1, jj, f);
-      fold_tree8<true>(s0, (v1 + 1) * 16 + 8, mx[q0], slot[q0]);
-      fold_tree8<true>(s1, (v1 + 1) * 16 + 8, mx[q1], slot[q1]);
+      fold_tree8<true, true>(s0, (v1 + 1) * 16 + 16, mx[q0], slot[q0]);
+      fold_tree8<true, true>(s1, (v1 + 1) * 16 + 16, mx[q1], slot[q1]);
     } else {
-      fold_tree<false>(s0, (v0 + 1) * 16, mx[q0], slot[q0]);
-      fold_tree<false>(s1, (v0 + 1) * 16, mx[q1], slot[q1]);
+      fold_tree<false, true>(s0, (v0 + 1) * 16, mx[q0], slot[q0]);
+      fold_tree<false, true>(s1, (v0 + 1) * 16, mx[q1], slot[q1]);
     }
   };
   // After a phase: the entry's last bit closes its second half's document.

@@ -412,23 +412,34 @@ __device__ __forceinline__ bool is_nan_bits(float x) {
 
 // Merge the (max, token) of lanes l and l^32, which hold disjoint document
 // rows of the same query token.  Equal maxima keep the lower token, matching
-// a sequential ascending scan.  h = lane / 32.  kNoNaN: neither maximum can
-// be NaN (a fold that never takes a NaN score), so the NaN tests drop out.
-template <bool kNoNaN = false>
+// a sequential ascending scan.  h = lane / 32.
 __device__ __forceinline__ void merge_halves(float& mx, int& tok, int h) {
   const float omx = __builtin_bit_cast(float, lane_xor32(__builtin_bit_cast(uint32_t, mx), h));
   const int otok = (int)lane_xor32((uint32_t)tok, h);
   // Bitwise, not short-circuit: no exec-mask branches.  A NaN maximum can
   // only be the first valid token's (take_first_row) and it stands.
-  bool take;
-  if constexpr (kNoNaN) {
-    // (tokens <= 0 mean none: the row-slot encoding leaves no slot negative)
-    take = (otok > 0) & ((tok <= 0) | (omx > mx) | ((omx == mx) & (otok < tok)));
-  } else {
-    const bool nan_here = is_nan_bits(mx), nan_there = is_nan_bits(omx);
-    take = (otok != 0) & !nan_here &
-           ((tok == 0) | nan_there | (omx > mx) | ((omx == mx) & (otok < tok)));
-  }
+  const bool nan_here = is_nan_bits(mx), nan_there = is_nan_bits(omx);
+  const bool take = (otok != 0) & !nan_here &
+                    ((tok == 0) | nan_there | (omx > mx) | ((omx == mx) & (otok < tok)));
+  mx = take ? omx : mx;
+  tok = take ? otok : tok;
+}
+
+// The (max, token) of the two wave halves merged in every lane, for folds
+// that never take a NaN (merge_halves<true>'s rule): one v_permlane32_swap
+// of each value gives every lane the low half's value in its first result
+// and the high half's in its second, so every lane merges (low, high) in the
+// same order and no lane needs its own half picked out.
+__device__ __forceinline__ void merge_halves_all(float& mx, int& tok) {
+  const auto ms = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, mx),
+                                                   __builtin_bit_cast(uint32_t, mx), false, false);
+  const auto ts = __builtin_amdgcn_permlane32_swap((uint32_t)tok, (uint32_t)tok, false, false);
+  mx = __builtin_bit_cast(float, (uint32_t)ms[0]);
+  tok = (int)ts[0];
+  const float omx = __builtin_bit_cast(float, (uint32_t)ms[1]);
+  const int otok = (int)ts[1];
+  // (tokens <= 0 mean none)
+  const bool take = (otok > 0) & ((tok <= 0) | (omx > mx) | ((omx == mx) & (otok < tok)));
   mx = take ? omx : mx;
   tok = take ? otok : tok;
 }
@@ -465,14 +476,26 @@ __device__ __forceinline__ void take_first_row(const float (&s)[16], uint32_t m3
 // of 16 lanes holding its sum; rows 0 and 1 are then read with v_readlane.
 // (v_permlane16_swap would do the last step in vector registers, but this
 // compiler folds `r[0] + r[1]` of its two results into `r[0] + r[0]`.)
-__device__ __forceinline__ float half_sum(float v) {
+__device__ __forceinline__ float row_sums(float v) {
   v = dpp_add<0xB1>(v);   // quad_perm [1,0,3,2]: lane ^ 1
   v = dpp_add<0x4E>(v);   // quad_perm [2,3,0,1]: lane ^ 2
   v = dpp_add<0x124>(v);  // row_ror:4
   v = dpp_add<0x128>(v);  // row_ror:8 -> each row of 16 holds its sum
-  const int bits = __builtin_bit_cast(int, v);
+  return v;
+}
+__device__ __forceinline__ float half_sum(float v) {
+  const int bits = __builtin_bit_cast(int, row_sums(v));
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(bits, 0)) +
          __builtin_bit_cast(float, __builtin_amdgcn_readlane(bits, 16));
+}
+
+// half_sum left in lanes 16-31 (and 48-63) instead of read out: a
+// row_bcast:15 DPP add puts row 0's sum into row 1 (row 2's into row 3),
+// the same two row sums half_sum adds (row 1's + row 0's).
+__device__ __forceinline__ float half_sum_in_lanes(float v) {
+  v = row_sums(v);
+  return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                           0, __builtin_bit_cast(int, v), 0x142, 0xa, 0xf, false));
 }
 
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }

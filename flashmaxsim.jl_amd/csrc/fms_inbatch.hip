@@ -297,7 +297,7 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
   __shared__ int any_nf;  // some document's first valid row is not finite
   __shared__ int16_t res_tape[kIbWaves][kIbQpw][kIbMaxDocs][kTile];  // Td <= 2048
   // Scores per (wave, query tile, document), then (units) 64 sink floats
-  // for the branch-free close: lane 0 stores the score, the other lanes
+  // for the branch-free close: lane 31 stores the score, the other lanes
   // store to the sink.  One array, so the compiler can tell the store from
   // the chunk buffers the loads to LDS write (a store through a pointer
   // that may point into either of two arrays made it wait for every load
@@ -684,7 +684,7 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
   auto close = [&](int q, int jj, int f) {
     int tok = slot[q] + tok_off();
     float m = mx[q];
-    merge_halves<true>(m, tok, h);  // the folds here never take a NaN
+    merge_halves_all(m, tok);  // the folds here never take a NaN
     // Map a winning copy back to f.  The winner is the lowest row that
     // reaches the maximum, and every copy scores exactly what f scores, so
     // a copy after f never wins (f reaches the same maximum first): only a
@@ -692,16 +692,16 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
     // Both are the tokens below f + 1.  After the mapping tok >= 1.
     tok = tok > f + 1 ? tok : f + 1;
     const bool tv = token_valid(q);
-    const float part = tv ? m : 0.0f;
-    const float score = half_sum(part);
+    // the score, left in lanes 16-31 (and 48-63): lane 31 stores it
+    const float score = half_sum_in_lanes(tv ? m : 0.0f);
     if constexpr (kHalf) {
       // without branches: both halves hold the merged token and store it to
-      // the same place; lanes other than 0 store the score to a sink
+      // the same place; lanes other than 31 store the score to a sink
       res_tape[wave][q][jj][r32] = (int16_t)(tv ? tok : 0);
-      score_buf[lane == 0 ? (wave * kIbQpw + q) * kIbMaxDocs + jj : kScoreWords + lane] = score;
+      score_buf[lane == 31 ? (wave * kIbQpw + q) * kIbMaxDocs + jj : kScoreWords + lane] = score;
     } else {
       if (h == 0) res_tape[wave][q][jj][r32] = (int16_t)(tv ? tok : 0);
-      if (lane == 0) res_score[wave][q][jj] = score;
+      if (lane == 31) res_score[wave][q][jj] = score;
     }
     mx[q] = -INFINITY;
     slot[q] = kNoSlot;
@@ -738,7 +738,7 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
       for (int t = 0; t < 3; ++t) {
         int tok = slot[t] + tok_off();
         float m = mx[t];
-        merge_halves<true>(m, tok, h);
+        merge_halves_all(m, tok);
         tok = tok > f + 1 ? tok : f + 1;  // a winning copy maps back to f, as in `close`
         const bool tv = t24_valid(t);
         part[t] = tv ? m : 0.0f;

@@ -944,8 +944,9 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
   };
 
   // kT24 step: entry i's chunk times the three tiles (three independent MFMA
-  // chains) while the three tiles of entry i-1 fold; one phase, closes after
-  // the fold.  Loads, list reads and the barrier as in `step`.
+  // chains) while the three tiles of entry i-1 fold (pinned, one fold piece
+  // per MFMA); one phase, closes after the fold.  Loads, list reads and the
+  // barrier as in `step`.
   Acc lagt[3];
 #pragma unroll
   for (int t = 0; t < 3; ++t)
@@ -962,20 +963,34 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
     Frag a[kIbNkb];
 #pragma unroll
     for (int kb = 0; kb < kIbNkb; ++kb) a[kb] = cur[kb * 64 + lane];
-    Acc n0 = Acc{}, n1 = Acc{}, n2 = Acc{};
+    // The three MFMA chains, each MFMA followed by one eighth of the fold of
+    // a tile of entry i-1 (24 pieces over the 3 x kIbNkb MFMAs), fenced as
+    // in mma_fold_pinned.
+    Acc n[3];
+    {
+      const int slot0 = (int)(pinfo & 63u) * kTile;
+      float s[3][16];
 #pragma unroll
-    for (int kb = 0; kb < kIbNkb; ++kb) {
-      n0 = Op::mma(a[kb], qf[0][kb], n0);
-      n1 = Op::mma(a[kb], qf[1][kb], n1);
-      n2 = Op::mma(a[kb], qf[2][kb], n2);
+      for (int t = 0; t < 3; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[t][r] = lagt[t][r];
+      n[0] = n[1] = n[2] = Acc{};
+      FoldPieces pc[3];
+      constexpr int kM = 3 * kIbNkb;
+      static_for<0, kM>([&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        n[k % 3] = Op::mma(a[k / 3], qf[k % 3][k / 3], n[k % 3]);
+        static_for<(24 * k + kM - 1) / kM, (24 * (k + 1) + kM - 1) / kM>([&](auto pcc) {
+          constexpr int p = decltype(pcc)::value;
+          fold_piece<p % 8, true>(pc[p / 8], s[p / 8], slot0, mx[p / 8], slot[p / 8]);
+        });
+        __builtin_amdgcn_sched_barrier(0);
+      });
     }
-    fold_close(0, lagt[0], pinfo);
-    fold_close(1, lagt[1], pinfo);
-    fold_close(2, lagt[2], pinfo);
     close24_if_last(pinfo);
-    lagt[0] = n0;
-    lagt[1] = n1;
-    lagt[2] = n2;
+    lagt[0] = n[0];
+    lagt[1] = n[1];
+    lagt[2] = n[2];
     prev_info = info;
     cur_info = next_info;
     dma_barrier<(kIbBufs - 2) * kIbKbPerWave>();

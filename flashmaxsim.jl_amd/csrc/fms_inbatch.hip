@@ -651,7 +651,8 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
       const int ch = info & 63u, jj = (info >> kInfoDocShift) & kInfoDocMask;
       const int f = (int)((info >> kInfoFirstShift) & kInfoFirstMask) - 1;
       const int fsrc = f < 0 ? 0 : f;  // (never: listed chunks have a valid row)
-      const int src = ((m >> r32) & 1u) ? ch * kTile + r32 : fsrc;
+      const int real = (int)((m >> r32) & 1u);  // (a multiply, not a select: see above)
+      const int src = fsrc + real * (ch * kTile + r32 - fsrc);
       voff = ((kPacked ? row0 : jj * Td) + src) * kIbRowBytes + h * 16;
     }
 #pragma unroll

@@ -351,6 +351,42 @@ __device__ __forceinline__ void fold_tree8(const float (&s)[16], int slot0, floa
   slot = take ? slot0 + ci : slot;
 }
 
+// fold_tree8 (row slots) cut into four pieces for a kernel that pins them
+// beside its MFMAs: 0 the max3 tree, 1 and 2 the scan of registers 6..1,
+// 3 registers 2..0 and the update.  Piece 3 repeats registers 2 and 1 to
+// keep three compares per block (no wait-state padding); a descending
+// re-scan ends on the same lowest register, so the result is fold_tree8's.
+struct FoldPieces8 {
+  float cm;
+  int ci;
+};
+
+template <int kP, bool kUpper>
+__device__ __forceinline__ void fold_piece8(FoldPieces8& f, const float (&s)[16], int slot0,
+                                            float& mx, int& slot) {
+  static_assert(kP >= 0 && kP < 4, "four pieces");
+  constexpr int o = kUpper ? 8 : 0;
+  if constexpr (kP == 0) {
+    const float m0 = max3_ieee(s[o + 0], s[o + 1], s[o + 2]);
+    const float m1 = max3_ieee(s[o + 3], s[o + 4], s[o + 5]);
+    const float m2 = max3_ieee(s[o + 6], s[o + 7], m0);
+    f.cm = max3_ieee(m1, m2, -INFINITY);
+    f.ci = reg_slot<true>(7);
+  } else if constexpr (kP == 1) {
+    first_equal3<reg_slot<true>(6), reg_slot<true>(5), reg_slot<true>(4)>(f.ci, s[o + 6], s[o + 5],
+                                                                            s[o + 4], f.cm);
+  } else if constexpr (kP == 2) {
+    first_equal3<reg_slot<true>(3), reg_slot<true>(2), reg_slot<true>(1)>(f.ci, s[o + 3], s[o + 2],
+                                                                            s[o + 1], f.cm);
+  } else {
+    first_equal3<reg_slot<true>(2), reg_slot<true>(1), reg_slot<true>(0)>(f.ci, s[o + 2], s[o + 1],
+                                                                            s[o + 0], f.cm);
+    const bool take = f.cm > mx;
+    mx = take ? f.cm : mx;
+    slot = take ? slot0 + f.ci : slot;
+  }
+}
+
 // running_max_seq: the sequential scan itself, with row masking, for the
 // HBM-bound scans (fewest live registers).  `rowbits` is the
 // chunk validity shifted to this lane half (bit 8*(r/4) + r%4 = register r);

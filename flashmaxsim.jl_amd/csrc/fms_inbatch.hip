@@ -871,17 +871,40 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
       close(q1, jj, f);
     }
   };
-  // A split phase's fold holds two closes; left to itself the scheduler
-  // issues all 16 MFMAs first and the VALU work after them.  This pins the
-  // interleave: each MFMA followed by 10 VALU instructions.
-  auto interleave_split = [&](auto split) {
-    if constexpr (decltype(split)::value) {
+  // A phase whose folded entry is split: tiles (qa, qb) x the chunk as two
+  // MFMA chains and beside them, fenced, 18 units in fold_units' order: the
+  // lower halves of tiles fa and fb (four pieces each), the closes of their
+  // first document, the upper halves (four pieces each).  Without the fences
+  // the scheduler issued all MFMAs first and the fold after them.
+  auto mma_fold_split_pinned = [&](const Frag (&a)[kIbNkb], Acc& na, Acc& nb, int qa, int qb,
+                                   const Acc& x0, const Acc& x1, int fa, int fb, uint32_t inf) {
+    float s0[16], s1[16];
 #pragma unroll
-      for (int k = 0; k < 2 * kIbNkb; ++k) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-        __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);  // ten VALU
-      }
-    }
+    for (int r = 0; r < 16; ++r) { s0[r] = x0[r]; s1[r] = x1[r]; }
+    const int v0 = (int)(inf & kHUMask);
+    const int v1 = (int)((inf >> kHU1Shift) & kHUMask) - 1;
+    const int jj = (int)((inf >> kHDoc0Shift) & kInfoDocMask);
+    const int f = uniform(doc_first[jj]) & 0xffff;
+    const int lo0 = (v0 + 1) * 16, hi0 = (v1 + 1) * 16 + 16;
+    na = Acc{};
+    nb = Acc{};
+    FoldPieces8 la, lb, ua, ub;
+    constexpr int kM = 2 * kIbNkb, kU = 18;
+    static_for<0, kM>([&](auto kc) {
+      constexpr int k = decltype(kc)::value;
+      if constexpr (k % 2 == 0) na = Op::mma(a[k / 2], qf[qa][k / 2], na);
+      else nb = Op::mma(a[k / 2], qf[qb][k / 2], nb);
+      static_for<(kU * k + kM - 1) / kM, (kU * (k + 1) + kM - 1) / kM>([&](auto uc) {
+        constexpr int u = decltype(uc)::value;
+        if constexpr (u < 4) fold_piece8<u, false>(la, s0, lo0, mx[fa], slot[fa]);
+        else if constexpr (u < 8) fold_piece8<u - 4, false>(lb, s1, lo0, mx[fb], slot[fb]);
+        else if constexpr (u == 8) close(fa, jj, f);
+        else if constexpr (u == 9) close(fb, jj, f);
+        else if constexpr (u < 14) fold_piece8<u - 10, true>(ua, s0, hi0, mx[fa], slot[fa]);
+        else fold_piece8<u - 14, true>(ub, s1, hi0, mx[fb], slot[fb]);
+      });
+      __builtin_amdgcn_sched_barrier(0);
+    });
   };
   // The step of `step` over the unit stream: each phase is written out for
   // both kinds of entry it folds (split or not), with its MFMAs, so the
@@ -904,15 +927,7 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
         mma_fold_pinned(a, n0, n1, 0, 1, lag2, lag3, 2, 3, ((int)(pinfo & kHUMask) + 1) * 16);
         return;
       }
-      n0 = Acc{};
-      n1 = Acc{};
-#pragma unroll
-      for (int kb = 0; kb < kIbNkb; ++kb) {
-        n0 = Op::mma(a[kb], qf[0][kb], n0);
-        n1 = Op::mma(a[kb], qf[1][kb], n1);
-      }
-      fold_units(2, 3, lag2, lag3, pinfo, split);
-      interleave_split(split);
+      mma_fold_split_pinned(a, n0, n1, 0, 1, lag2, lag3, 2, 3, pinfo);
     };
     if (pinfo & (1u << kHSplitBit)) phase1(std::true_type());
     else phase1(std::false_type());
@@ -923,15 +938,7 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
         mma_fold_pinned(a, n2, n3, 2, 3, n0, n1, 0, 1, ((int)(info & kHUMask) + 1) * 16);
         return;
       }
-      n2 = Acc{};
-      n3 = Acc{};
-#pragma unroll
-      for (int kb = 0; kb < kIbNkb; ++kb) {
-        n2 = Op::mma(a[kb], qf[2][kb], n2);
-        n3 = Op::mma(a[kb], qf[3][kb], n3);
-      }
-      fold_units(0, 1, n0, n1, info, split);
-      interleave_split(split);
+      mma_fold_split_pinned(a, n2, n3, 2, 3, n0, n1, 0, 1, info);
     };
     if (info & (1u << kHSplitBit)) phase2(std::true_type());
     else phase2(std::false_type());

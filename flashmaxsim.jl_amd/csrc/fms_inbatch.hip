@@ -45,10 +45,12 @@
 //   * per chunk and wave: 8 LDS fragment reads feed 4 x 8 MFMA 32x32x16 in
 //     two phases of two independent accumulation chains (a dependent
 //     32x32x16 MFMA issues at about half the rate of an independent one).
-//     Each phase's MFMAs overlap the running max/argmax update (fold_tree)
-//     of the two tiles multiplied before them: phase 1 multiplies tiles 0,1
-//     while tiles 2,3 of the previous chunk fold, phase 2 multiplies tiles
-//     2,3 while tiles 0,1 fold;
+//     Each phase's MFMAs overlap the running max/argmax update of the two
+//     tiles multiplied before them: phase 1 multiplies tiles 0,1 while tiles
+//     2,3 of the previous chunk fold, phase 2 multiplies tiles 2,3 while
+//     tiles 0,1 fold.  The fold is cut into pieces (fold_piece, fold_piece8,
+//     the closes of a split entry) and each MFMA is followed by its share,
+//     fenced by sched_barrier, with the pad-free reverse scan (first_equal3);
 //   * the document close (merge of the wave halves, score) uses v_permlane32
 //     and DPP, not LDS shuffles, and no branches;
 //   * per-document tape (int16, Td <= 2048) / score go to LDS and leave in

@@ -12,6 +12,9 @@ Other workloads (--workload c3 | c4 | c4d1024 | c5) measure the in-batch,
 packed and INT8 scans the same way (each prints its own JSON line); c3bwd
 measures the pullback of the c3 scores on their argmax tape (dQ and dD);
 c4mq scores the c4 workload with the multi-query packed scan (one launch).
+--scores-only runs c3, c3d768, c3f32 and c4mq with a null args: S alone, as the
+reference's maxsim returns it (dispatch.jl:124 drops the in-batch tape), which
+the in-batch kernel computes with a running maximum alone.
 """
 from __future__ import annotations
 
@@ -50,6 +53,8 @@ def parse():
                     help="target duration of the bounded CPU baseline sample")
     ap.add_argument("--grouping", default="auto", choices=["auto", "always", "never"],
                     help="candidate pair order (document-grouped or output order)")
+    ap.add_argument("--scores-only", action="store_true",
+                    help="c3*/c4mq: no argmax tape (args null), S alone")
     ap.add_argument("--check", type=int, default=256,
                     help="pairs re-scored by the CPU oracle as a full-size parity spot check")
     return ap.parse_args()
@@ -336,7 +341,7 @@ def run_c3(args, torch, fm, boundary, dev, dim=128, dtype=None):
     dmask = torch.arange(Ld, device=dev)[None, :] < lens[:, None]
     qmask = torch.ones(Bq, Lq, dtype=torch.bool, device=dev)
     S = torch.empty(Bq, Bd, dtype=torch.float32, device=dev)
-    args_t = torch.empty(Bq, Bd, Lq, dtype=torch.int32, device=dev)
+    args_t = None if args.scores_only else torch.empty(Bq, Bd, Lq, dtype=torch.int32, device=dev)
 
     def step():
         boundary.inbatch_device_scan(S, args_t, Q, D, qmask, dmask)
@@ -344,11 +349,13 @@ def run_c3(args, torch, fm, boundary, dev, dim=128, dtype=None):
     wall, launch_ms = timed_steps(torch, step, args.steps, args.warmup)
     valid_flops = 2 * dim * Lq * Bq * int(lens.sum().item())
     name = "c3_inbatch_fp16" if (dim, dtype) == (128, torch.float16) else f"c3_inbatch_{dname}_d{dim}"
+    name += "_scores_only" if args.scores_only else ""
     res = dict(pairs_per_step=Bq * Bd, flops_per_launch=valid_flops, wall=wall,
                launch_ms=launch_ms, dtype=dname, bound="mfma",
                padded_flops=2 * dim * Lq * Ld * Bq * Bd,
                config={"workload": name, "dim": dim, "Lq": Lq, "Ld": Ld, "Bq": Bq,
-                       "Bd": Bd, "doc_len": "U[64,180], tail masked"})
+                       "Bd": Bd, "doc_len": "U[64,180], tail masked",
+                       "output": "S" if args.scores_only else "S and the argmax tape"})
     if dtype == torch.float32:
         res["peak_tflops"] = FP32_PEAK_TFLOPS
     if (dim, dtype) != (128, torch.float16):
@@ -538,7 +545,7 @@ def run_c4mq(args, torch, fm, boundary, dev):
     tok = normalized_randn(torch, (ntok, dim), gen, torch.bfloat16, dev, chunk_rows=1 << 20)
     Qs = normalized_randn(torch, (nq, Lq, dim), gen, torch.bfloat16, dev)
     S = torch.empty(nq, nd, dtype=torch.float32, device=dev)
-    args_t = torch.empty(nq, nd, Lq, dtype=torch.int32, device=dev)
+    args_t = None if args.scores_only else torch.empty(nq, nd, Lq, dtype=torch.int32, device=dev)
 
     def step():
         boundary.launch_packed_multi_scan(args_t, S, Qs, tok, cu, None, max_len)
@@ -548,7 +555,8 @@ def run_c4mq(args, torch, fm, boundary, dev):
     res = dict(pairs_per_step=nq * nd, flops_per_launch=2 * dim * Lq * nq * ntok, wall=wall,
                launch_ms=launch_ms, dtype="bf16", bound="mfma",
                padded_flops=2 * dim * 32 * nq * chunks * 32,
-               config={"workload": "c4mq_packed_multi_bf16_d128", "dim": dim, "Lq": Lq,
+               config={"workload": "c4mq_packed_multi_bf16_d128" + ("_scores_only" if args.scores_only else ""),
+                       "dim": dim, "Lq": Lq,
                        "docs": nd, "doc_len": "U[700,1100]", "tokens": ntok, "queries": nq,
                        "call": "one multi-query packed scan for all queries"})
     # spot check: 3 queries x 64 documents against the single-query scan
@@ -647,6 +655,8 @@ def main():
               "c4d1024": lambda *a: run_c4(*a, dim=1024),
               "c3d768": lambda *a: run_c3(*a, dim=768),
               "c3f32": lambda *a: run_c3(*a, dim=128, dtype=torch.float32)}[args.workload]
+    if args.scores_only and args.workload not in ("c3", "c3d768", "c3f32", "c4mq"):
+        sys.exit("--scores-only applies to c3, c3d768, c3f32 and c4mq")
     r = runner(args, torch, fm, boundary, dev)
     steps = args.steps
     wall = r["wall"]
@@ -679,7 +689,8 @@ def main():
         roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak,
                 "unit": "TFLOP/s", "frac": round(achieved / peak, 4)}
     roof["traffic"] = None
-    prof = os.path.join(ROOT, "profiles", f"traffic_{args.workload}.json")
+    prof = os.path.join(ROOT, "profiles",
+                        f"traffic_{args.workload}{'_scores_only' if args.scores_only else ''}.json")
     if os.path.exists(prof):
         # HBM bytes per launch from two rocprofv3 --pmc passes (FETCH_SIZE,
         # WRITE_SIZE, calibrated on a copy of known size), committed beside the

@@ -387,6 +387,65 @@ __device__ __forceinline__ void fold_piece8(FoldPieces8& f, const float (&s)[16]
   }
 }
 
+// The running maximum alone, for scans that write no argmax tape: fold_tree's
+// max3 tree with the running max as its root's third input, so mx ends on
+// the value fold_tree's strictly-greater update gives (the two can differ
+// only in the sign of a zero maximum: the tree orders -0 below +0, the
+// update keeps the earlier of equal values).  Cut into eight pieces of one
+// v_max3 (one node of the tree each, piece 7 the root) for kernels that pin
+// them beside their MFMAs; fold_max runs all eight.
+struct MaxPieces {
+  float n0, n1, n2, n3, n4, n5, n6;
+};
+
+template <int kP>
+__device__ __forceinline__ void fold_max_piece(MaxPieces& f, const float (&s)[16], float& mx) {
+  static_assert(kP >= 0 && kP < 8, "eight pieces");
+  if constexpr (kP == 0) f.n0 = max3_ieee(s[0], s[1], s[2]);
+  else if constexpr (kP == 1) f.n1 = max3_ieee(s[3], s[4], s[5]);
+  else if constexpr (kP == 2) f.n2 = max3_ieee(s[6], s[7], s[8]);
+  else if constexpr (kP == 3) f.n3 = max3_ieee(s[9], s[10], s[11]);
+  else if constexpr (kP == 4) f.n4 = max3_ieee(s[12], s[13], s[14]);
+  else if constexpr (kP == 5) f.n5 = max3_ieee(s[15], f.n0, f.n1);
+  else if constexpr (kP == 6) f.n6 = max3_ieee(f.n2, f.n3, f.n4);
+  else mx = max3_ieee(f.n5, f.n6, mx);
+}
+
+__device__ __forceinline__ void fold_max(const float (&s)[16], float& mx) {
+  MaxPieces f;
+  static_for<0, 8>([&](auto p) { fold_max_piece<decltype(p)::value>(f, s, mx); });
+}
+
+// The same over one half of the registers (fold_tree8's rows), four pieces.
+struct MaxPieces8 {
+  float n0, n1, n2;
+};
+
+template <int kP, bool kUpper>
+__device__ __forceinline__ void fold_max_piece8(MaxPieces8& f, const float (&s)[16], float& mx) {
+  static_assert(kP >= 0 && kP < 4, "four pieces");
+  constexpr int o = kUpper ? 8 : 0;
+  if constexpr (kP == 0) f.n0 = max3_ieee(s[o + 0], s[o + 1], s[o + 2]);
+  else if constexpr (kP == 1) f.n1 = max3_ieee(s[o + 3], s[o + 4], s[o + 5]);
+  else if constexpr (kP == 2) f.n2 = max3_ieee(s[o + 6], s[o + 7], f.n0);
+  else mx = max3_ieee(f.n1, f.n2, mx);
+}
+
+template <bool kUpper>
+__device__ __forceinline__ void fold_max8(const float (&s)[16], float& mx) {
+  MaxPieces8 f;
+  static_for<0, 4>([&](auto p) { fold_max_piece8<decltype(p)::value, kUpper>(f, s, mx); });
+}
+
+// The maxima of the two wave halves merged in every lane (for folds that
+// never take a NaN): both halves' values from one v_permlane32_swap.
+__device__ __forceinline__ float merge_halves_max(float mx) {
+  const auto ms = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, mx),
+                                                   __builtin_bit_cast(uint32_t, mx), false, false);
+  return __builtin_fmaximum_numf(__builtin_bit_cast(float, (uint32_t)ms[0]),
+                                 __builtin_bit_cast(float, (uint32_t)ms[1]));
+}
+
 // running_max_seq: the sequential scan itself, with row masking, for the
 // HBM-bound scans (fewest live registers).  `rowbits` is the
 // chunk validity shifted to this lane half (bit 8*(r/4) + r%4 = register r);

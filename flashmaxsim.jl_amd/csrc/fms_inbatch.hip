@@ -269,7 +269,9 @@ __device__ int block_exclusive_scan_i32(int v, int* total) {
 // is kNkb k-blocks of 1 KB; wave w copies k-block w mod kNkb of every chunk
 // (with fewer k-blocks than waves, two waves copy the same bytes to the same
 // place, so every wave issues the same loads per step).
-template <class Op, bool kPacked, bool kT24, int kNkb>
+// kTape = false: args is null (scores only, as the reference's maxsim keeps
+// them, dispatch.jl:124): the fold keeps the running maximum alone.
+template <class Op, bool kPacked, bool kT24, int kNkb, bool kTape>
 __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(const InBatchArgs A) {
   typedef typename Op::Acc Acc;
   typedef typename Op::Frag Frag;
@@ -476,9 +478,11 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
   // ---- defaults of the results --------------------------------------------------
   // A document without a valid token never closes: score 0, tape 0.
   static_assert(sizeof(res_tape) % (16 * 64 * kIbWaves) == 0, "whole 16-byte stores");
+  if constexpr (kTape) {
 #pragma unroll
-  for (int k = 0; k < (int)(sizeof(res_tape) / (16 * 64 * kIbWaves)); ++k)
-    reinterpret_cast<u32x4*>(&res_tape[0][0][0][0])[tid + k * 64 * kIbWaves] = u32x4{0u, 0u, 0u, 0u};
+    for (int k = 0; k < (int)(sizeof(res_tape) / (16 * 64 * kIbWaves)); ++k)
+      reinterpret_cast<u32x4*>(&res_tape[0][0][0][0])[tid + k * 64 * kIbWaves] = u32x4{0u, 0u, 0u, 0u};
+  }
   for (int e = tid; e < kIbWaves * kIbQpw * kIbMaxDocs; e += 64 * kIbWaves)
     (&res_score[0][0][0])[e] = 0.0f;
   __syncthreads();  // chunk_mask, doc_first complete
@@ -685,6 +689,15 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
   // scores are all -Inf closes on f with -Inf, as the reference's first-token
   // rule gives; the NaN case of that rule is settled after the loop.)
   auto close = [&](int q, int jj, int f) {
+    if constexpr (!kTape) {
+      // scores only: the maximum of both halves, summed as below
+      const float m = merge_halves_max(mx[q]);
+      const float score = half_sum_in_lanes(token_valid(q) ? m : 0.0f);
+      if constexpr (kHalf) score_buf[lane == 31 ? (wave * kIbQpw + q) * kIbMaxDocs + jj : kScoreWords + lane] = score;
+      else if (lane == 31) res_score[wave][q][jj] = score;
+      mx[q] = -INFINITY;
+      return;
+    }
     int tok = slot[q] + tok_off();
     float m = mx[q];
     merge_halves_all(m, tok);  // the folds here never take a NaN
@@ -716,7 +729,8 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
     float sc[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) sc[r] = ac[r];
-    fold_tree<false, true>(sc, (int)(inf & 63u) * kTile, mx[q], slot[q]);
+    if constexpr (kTape) fold_tree<false, true>(sc, (int)(inf & 63u) * kTile, mx[q], slot[q]);
+    else fold_max(sc, mx[q]);
   };
   auto close_if_last = [&](int q0, int q1, uint32_t inf) {
     if (inf & (1u << kInfoLastBit)) {
@@ -739,13 +753,17 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
       float part[3];
 #pragma unroll
       for (int t = 0; t < 3; ++t) {
-        int tok = slot[t] + tok_off();
-        float m = mx[t];
-        merge_halves_all(m, tok);
-        tok = tok > f + 1 ? tok : f + 1;  // a winning copy maps back to f, as in `close`
-        const bool tv = t24_valid(t);
-        part[t] = tv ? m : 0.0f;
-        if (h == 0) res_tape[wave][t24_query(t)][jj][t24_token(t)] = (int16_t)(tv ? tok : 0);
+        if constexpr (kTape) {
+          int tok = slot[t] + tok_off();
+          float m = mx[t];
+          merge_halves_all(m, tok);
+          tok = tok > f + 1 ? tok : f + 1;  // a winning copy maps back to f, as in `close`
+          const bool tv = t24_valid(t);
+          part[t] = tv ? m : 0.0f;
+          if (h == 0) res_tape[wave][t24_query(t)][jj][t24_token(t)] = (int16_t)(tv ? tok : 0);
+        } else {
+          part[t] = t24_valid(t) ? merge_halves_max(mx[t]) : 0.0f;
+        }
         mx[t] = -INFINITY;
         slot[t] = kNoSlot;
       }
@@ -774,6 +792,7 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
     na = Acc{};
     nb = Acc{};
     FoldPieces pa, pb;
+    MaxPieces xa, xb;  // (scores only)
     constexpr int kM = 2 * kIbNkb;  // MFMAs of the phase
     static_for<0, kM>([&](auto kc) {
       constexpr int k = decltype(kc)::value;
@@ -781,8 +800,14 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
       else nb = Op::mma(a[k / 2], qf[qb][k / 2], nb);
       static_for<(16 * k + kM - 1) / kM, (16 * (k + 1) + kM - 1) / kM>([&](auto pc) {
         constexpr int p = decltype(pc)::value;
-        if constexpr (p < 8) fold_piece<p, true>(pa, s0, slot0, mx[fa], slot[fa]);
-        else fold_piece<p - 8, true>(pb, s1, slot0, mx[fb], slot[fb]);
+        if constexpr (!kTape) {
+          if constexpr (p < 8) fold_max_piece<p>(xa, s0, mx[fa]);
+          else fold_max_piece<p - 8>(xb, s1, mx[fb]);
+        } else if constexpr (p < 8) {
+          fold_piece<p, true>(pa, s0, slot0, mx[fa], slot[fa]);
+        } else {
+          fold_piece<p - 8, true>(pb, s1, slot0, mx[fb], slot[fb]);
+        }
       });
       __builtin_amdgcn_sched_barrier(0);
     });
@@ -849,7 +874,20 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
 #pragma unroll
     for (int r = 0; r < 16; ++r) { s0[r] = x0[r]; s1[r] = x1[r]; }
     const int v0 = (int)(inf & kHUMask);
-    if constexpr (decltype(split)::value) {
+    if constexpr (!kTape) {
+      if constexpr (decltype(split)::value) {
+        const int jj = (int)((inf >> kHDoc0Shift) & kInfoDocMask);
+        fold_max8<false>(s0, mx[q0]);
+        fold_max8<false>(s1, mx[q1]);
+        close(q0, jj, 0);
+        close(q1, jj, 0);
+        fold_max8<true>(s0, mx[q0]);
+        fold_max8<true>(s1, mx[q1]);
+      } else {
+        fold_max(s0, mx[q0]);
+        fold_max(s1, mx[q1]);
+      }
+    } else if constexpr (decltype(split)::value) {
       const int v1 = (int)((inf >> kHU1Shift) & kHUMask) - 1;
       const int jj = (int)((inf >> kHDoc0Shift) & kInfoDocMask);
       const int f = uniform(doc_first[jj]) & 0xffff;
@@ -891,6 +929,7 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
     na = Acc{};
     nb = Acc{};
     FoldPieces8 la, lb, ua, ub;
+    MaxPieces8 xla, xlb, xua, xub;  // (scores only)
     constexpr int kM = 2 * kIbNkb, kU = 18;
     static_for<0, kM>([&](auto kc) {
       constexpr int k = decltype(kc)::value;
@@ -898,12 +937,22 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
       else nb = Op::mma(a[k / 2], qf[qb][k / 2], nb);
       static_for<(kU * k + kM - 1) / kM, (kU * (k + 1) + kM - 1) / kM>([&](auto uc) {
         constexpr int u = decltype(uc)::value;
-        if constexpr (u < 4) fold_piece8<u, false>(la, s0, lo0, mx[fa], slot[fa]);
-        else if constexpr (u < 8) fold_piece8<u - 4, false>(lb, s1, lo0, mx[fb], slot[fb]);
-        else if constexpr (u == 8) close(fa, jj, f);
+        if constexpr (u == 8) close(fa, jj, f);
         else if constexpr (u == 9) close(fb, jj, f);
-        else if constexpr (u < 14) fold_piece8<u - 10, true>(ua, s0, hi0, mx[fa], slot[fa]);
-        else fold_piece8<u - 14, true>(ub, s1, hi0, mx[fb], slot[fb]);
+        else if constexpr (!kTape) {
+          if constexpr (u < 4) fold_max_piece8<u, false>(xla, s0, mx[fa]);
+          else if constexpr (u < 8) fold_max_piece8<u - 4, false>(xlb, s1, mx[fb]);
+          else if constexpr (u < 14) fold_max_piece8<u - 10, true>(xua, s0, mx[fa]);
+          else fold_max_piece8<u - 14, true>(xub, s1, mx[fb]);
+        } else if constexpr (u < 4) {
+          fold_piece8<u, false>(la, s0, lo0, mx[fa], slot[fa]);
+        } else if constexpr (u < 8) {
+          fold_piece8<u - 4, false>(lb, s1, lo0, mx[fb], slot[fb]);
+        } else if constexpr (u < 14) {
+          fold_piece8<u - 10, true>(ua, s0, hi0, mx[fa], slot[fa]);
+        } else {
+          fold_piece8<u - 14, true>(ub, s1, hi0, mx[fb], slot[fb]);
+        }
       });
       __builtin_amdgcn_sched_barrier(0);
     });
@@ -986,13 +1035,15 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
         for (int r = 0; r < 16; ++r) s[t][r] = lagt[t][r];
       n[0] = n[1] = n[2] = Acc{};
       FoldPieces pc[3];
+      MaxPieces xc[3];  // (scores only)
       constexpr int kM = 3 * kIbNkb;
       static_for<0, kM>([&](auto kc) {
         constexpr int k = decltype(kc)::value;
         n[k % 3] = Op::mma(a[k / 3], qf[k % 3][k / 3], n[k % 3]);
         static_for<(24 * k + kM - 1) / kM, (24 * (k + 1) + kM - 1) / kM>([&](auto pcc) {
           constexpr int p = decltype(pcc)::value;
-          fold_piece<p % 8, true>(pc[p / 8], s[p / 8], slot0, mx[p / 8], slot[p / 8]);
+          if constexpr (kTape) fold_piece<p % 8, true>(pc[p / 8], s[p / 8], slot0, mx[p / 8], slot[p / 8]);
+          else fold_max_piece<p % 8>(xc[p / 8], s[p / 8], mx[p / 8]);
         });
         __builtin_amdgcn_sched_barrier(0);
       });
@@ -1103,7 +1154,7 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
           const float s0 = acc[0];  // every row is f: <f, this lane's query token>
           const bool fix = t24_valid(t) && is_nan_bits(s0);
           if (__ballot(fix) == 0ull) continue;
-          if (fix & (h == 0)) res_tape[wave][t24_query(t)][jj][t24_token(t)] = (int16_t)(f + 1);
+          if (kTape && (fix & (h == 0))) res_tape[wave][t24_query(t)][jj][t24_token(t)] = (int16_t)(f + 1);
           const int qa = (32 * t) / 24;  // the tile's first query; the other is qa + 1
           const bool fa = __ballot(fix && t24_query(t) == qa) != 0ull;
           const bool fb = __ballot(fix && t24_query(t) == qa + 1) != 0ull;
@@ -1141,7 +1192,7 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
           const float s0 = acc[0];  // every row is f: <f, q token lane%32>
           const bool fix = token_valid(q) && is_nan_bits(s0);
           if (__ballot(fix) == 0ull) continue;
-          if (fix & (h == 0)) res_tape[wave][q][jj][r32] = (int16_t)(f + 1);
+          if (kTape && (fix & (h == 0))) res_tape[wave][q][jj][r32] = (int16_t)(f + 1);
           if (lane == 0) res_score[wave][q][jj] = __builtin_bit_cast(float, 0x7fc00000u);
         }
       }
@@ -1157,7 +1208,7 @@ __global__ void __launch_bounds__(64 * kIbWaves, kIbBlocksPerCu) inbatch_mfma(co
   for (int q = 0; q < kIbQpw; ++q) {
     if (!qlive[q]) continue;
     const int64_t p0 = (int64_t)qrow[q] * A.Bd + j0;
-    if (A.args) {
+    if (kTape && A.args) {
       int32_t* const out = A.args + p0 * Tq + qt0[q];
       const int tn = qtn[q], n = ndoc * tn;
       const int16_t* const src = &res_tape[wave][q][0][0];
@@ -1305,19 +1356,25 @@ hipError_t launch_inbatch_mfma(int dtype_bf16, const InBatchArgs& args_in, hipSt
     const dim3 grid((unsigned)(A.nqb * ((A.ndb + kXcds - 1) / kXcds) * kXcds)), block(64 * kIbWaves);
     // Tq == 24: four queries fill three tiles (kT24)
     auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, block, 0, stream, A); };
-    auto by_nkb = [&](auto op, auto packed, auto t24) {
+    // args null: the scores-only kernels (running maximum, no argmax)
+    auto by_nkb = [&](auto op, auto packed, auto t24, auto tape) {
       typedef decltype(op) O;
       constexpr bool P = decltype(packed)::value, T = decltype(t24)::value;
+      constexpr bool K = decltype(tape)::value;
       switch (A.dim / 16) {
-        case 2: go(inbatch_mfma<O, P, T, 2>); break;
-        case 4: go(inbatch_mfma<O, P, T, 4>); break;
-        case 6: go(inbatch_mfma<O, P, T, 6>); break;
-        default: go(inbatch_mfma<O, P, T, 8>); break;
+        case 2: go(inbatch_mfma<O, P, T, 2, K>); break;
+        case 4: go(inbatch_mfma<O, P, T, 4, K>); break;
+        case 6: go(inbatch_mfma<O, P, T, 6, K>); break;
+        default: go(inbatch_mfma<O, P, T, 8, K>); break;
       }
     };
+    auto by_tape = [&](auto op, auto packed, auto t24) {
+      if (A.args) by_nkb(op, packed, t24, std::true_type());
+      else by_nkb(op, packed, t24, std::false_type());
+    };
     auto by_t24 = [&](auto op, auto packed) {
-      if (A.Tq == 24) by_nkb(op, packed, std::true_type());
-      else by_nkb(op, packed, std::false_type());
+      if (A.Tq == 24) by_tape(op, packed, std::true_type());
+      else by_tape(op, packed, std::false_type());
     };
     auto by_packed = [&](auto op) {
       if (A.cu) by_t24(op, std::true_type());

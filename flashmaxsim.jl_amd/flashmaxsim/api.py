@@ -135,7 +135,7 @@ def maxsim(*args, neg=None, normalize=None, backward=None):
     if isinstance(b, PackedSeq):
         qmask = rest[0] if rest else None
         if a.dim() == 3:  # several queries in one pass (extension): (nq, B) scores
-            S, _ = F.packed_multi_forward(a, b, qmask, cfg.neg, cfg.normalize)
+            S, _ = F.packed_multi_forward(a, b, qmask, cfg.neg, cfg.normalize, tape=False)
             return S
         scores, _ = F.packed_forward(a, b, qmask, cfg.neg, cfg.normalize)
         return scores
@@ -162,7 +162,7 @@ def maxsim(*args, neg=None, normalize=None, backward=None):
         return S
     qmask, dmask = (rest + [None, None])[:2]
     if inbatch:
-        S, _ = F.inbatch_forward(a, b, qmask, dmask, cfg.neg, cfg.normalize)
+        S, _ = F.inbatch_forward(a, b, qmask, dmask, cfg.neg, cfg.normalize, tape=False)
         return S
     if a.dim() == 2:
         score, _ = F.pair_forward(a, b, qmask, dmask, cfg.neg, cfg.normalize)

@@ -122,12 +122,16 @@ def paired_forward(Q, D, qmask=None, dmask=None, neg=None, normalize=False):
     return scores, args
 
 
-def inbatch_forward(Q, D, qmask=None, dmask=None, neg=None, normalize=False):
-    """inbatch_forward_ka (forward_layouts.jl:188-200): (S (Bq,Bd), args (Bq,Bd,Tq))."""
+def inbatch_forward(Q, D, qmask=None, dmask=None, neg=None, normalize=False, tape=True):
+    """inbatch_forward_ka (forward_layouts.jl:188-200): (S (Bq,Bd), args (Bq,Bd,Tq)).
+
+    tape=False returns (S, None) and makes no tape: the reference's ``maxsim``
+    discards it (``S, _ = inbatch_forward(...)``, dispatch.jl:124), and without
+    it the kernel keeps a running maximum alone (the same S)."""
     boundary.require_device(Q, D, qmask, dmask)
     _, Tq, Bq, Td, Bd = require_inbatch_shapes(Q, D, qmask, dmask)
     S = _zeros(Q, SCORE_DTYPE, Bq, Bd)
-    args = _zeros(Q, torch.int32, Bq, Bd, Tq)
+    args = _zeros(Q, torch.int32, Bq, Bd, Tq) if tape else None
     if Bd == 0 or Bq == 0 or Tq == 0 or Td == 0:
         return S, args
     boundary.inbatch_device_scan(S, args, Q, D, qmask, dmask, normalize)
@@ -162,13 +166,14 @@ def packed_forward(q, P: PackedSeq, qmask=None, neg=None, normalize=False):
     return scores, args
 
 
-def packed_multi_forward(Q, P: PackedSeq, qmask=None, neg=None, normalize=False):
+def packed_multi_forward(Q, P: PackedSeq, qmask=None, neg=None, normalize=False, tape=True):
     """nq queries against one PackedSeq in one pass: (S (nq,B), args (nq,B,Tq)).
 
     No reference counterpart (the reference's packed_forward takes one query,
     packed.jl:191-202); row i equals packed_forward(Q[i], P, qmask[i]) within
     the score tolerance.  Each document is read once per block of 32 queries
-    (the in-batch MFMA kernel over CSR documents)."""
+    (the in-batch MFMA kernel over CSR documents).  tape=False returns
+    (S, None): no tape, the kernel keeps a running maximum alone (the same S)."""
     boundary.require_device(Q, P.tokens, P.cu, qmask)
     if Q.dim() != 3:
         raise DimensionMismatch("multi-query packed scan takes Q (nq, Tq, dim)")
@@ -179,7 +184,7 @@ def packed_multi_forward(Q, P: PackedSeq, qmask=None, neg=None, normalize=False)
         raise DimensionMismatch("qmask")
     B = P.nseq()
     S = _zeros(Q, SCORE_DTYPE, nq, B)
-    args = _zeros(Q, torch.int32, nq, B, Tq)
+    args = _zeros(Q, torch.int32, nq, B, Tq) if tape else None
     if nq == 0 or B == 0:
         return S, args
     boundary.launch_packed_multi_scan(args, S, Q, P.tokens, P.cu, qmask, P.max_len, normalize)

@@ -54,7 +54,10 @@
 //   * the document close (merge of the wave halves, score) uses v_permlane32
 //     and DPP, not LDS shuffles, and no branches;
 //   * per-document tape (int16, Td <= 2048) / score go to LDS and leave in
-//     one coalesced pass at the end of the block.
+//     one coalesced pass at the end of the block;
+//   * with args null (scores only, kTape = false) the fold is the v_max3
+//     tree alone, with the running maximum as its root's third input, and
+//     the close merges the halves by a max: no argmax, no tape.
 // Block -> (query block, document range) is XCD-aware: the query blocks of
 // one document range run together on one XCD, so its L2 serves the range's
 // chunks to all of them.

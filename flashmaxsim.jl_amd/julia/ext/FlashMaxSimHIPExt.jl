@@ -166,12 +166,16 @@ function c_candidates_scan(dtype, args, partial, Q, gallery, idx, qmask, dmask,
           "candidate scan")
 end
 
-function c_inbatch_scan(dtype, S, args, Q, D, qmask, dmask, dim, Tq, Bq, Td, Bd)
+# args = nothing: S alone (no tape made; the kernel keeps a running maximum
+# without the argmax).  normalize: S .* inv_token_counts(qmask) fused into the
+# score write (normalize.jl:18-25).
+function c_inbatch_scan(dtype, S, args, Q, D, qmask, dmask, dim, Tq, Bq, Td, Bd;
+                        normalize::Bool = false)
     check(ccall((:fms_inbatch_device_scan, libfms), Int32,
                 (Int32, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid},
                  Int64, Int64, Int64, Int64, Int64, Int32, Ptr{Cvoid}),
                 dtype, dptr(S), dptr(args), dptr(Q), dptr(D), dptr(qmask), dptr(dmask),
-                dim, Tq, Bq, Td, Bd, Int32(0), stream_ptr()),
+                dim, Tq, Bq, Td, Bd, Int32(normalize), stream_ptr()),
           "in-batch scan")
 end
 
@@ -307,6 +311,27 @@ function FlashMaxSim.inbatch_forward_ka(backend::ROCBackend, Q::ROCArray{T,3}, D
     (Bd == 0 || Bq == 0 || Tq == 0 || Td == 0) && return S, args
     c_inbatch_scan(dtype_code(T), S, args, Q, D, qmask, dmask, dim, Tq, Bq, Td, Bd)
     S, args
+end
+
+# ---- the InBatch verb: S without a tape ---------------------------------------
+# The reference's maxsim(cfg, Q, D, qmask, dmask, InBatch()) keeps S and drops
+# the tape (src/dispatch.jl:121-125, `S, _ = inbatch_forward(...)`); here no tape
+# is made.  Same S (Float32, as inbatch_forward_ka above), and with
+# cfg.normalize the length normalisation fused into the score write.
+# Differentiation is unaffected: the reference's rrule for this call
+# (src/rrule.jl:84-99) runs inbatch_forward, which keeps the tape.
+
+function FlashMaxSim.maxsim(cfg::FlashMaxSim.MaxSim{T}, Q::ROCArray{T,3}, D::ROCArray{T,3},
+                            qmask::DenseMask{2}, dmask::DenseMask{2},
+                            layout::FlashMaxSim.InBatch) where {T<:AnyFeature}
+    gfx950() || return @invoke FlashMaxSim.maxsim(cfg, Q::AbstractArray{T,3}, D::AbstractArray{T,3}, qmask::AbstractMatrix{Bool}, dmask::AbstractMatrix{Bool}, layout)
+    FlashMaxSim.require_colocated(Q, D, qmask, dmask)
+    dim, Tq, Bq, Td, Bd = FlashMaxSim.require_inbatch_shapes(Q, D, qmask, dmask)
+    S = AMDGPU.zeros(Float32, Bd, Bq)
+    (Bd == 0 || Bq == 0 || Tq == 0 || Td == 0) && return S
+    c_inbatch_scan(dtype_code(T), S, nothing, Q, D, qmask, dmask, dim, Tq, Bq, Td, Bd;
+                   normalize = cfg.normalize)
+    S
 end
 
 function FlashMaxSim.candidates_forward_ka(backend::ROCBackend, Q::ROCArray{T,3},

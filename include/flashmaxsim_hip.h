@@ -183,6 +183,9 @@ fms_status fms_launch_candidates_scan_noalloc(int32_t dtype, int32_t* args, floa
  * a 128-byte slice at a time (both with 16-byte aligned Q and D); any other
  * shape scores each pair on its own.  Results agree to the float
  * tolerances either way (the same products, summed in another order).
+ * With args NULL (S alone, as the reference's maxsim(..., InBatch()) keeps
+ * it, src/dispatch.jl:121-125) the register-resident kernel keeps a running
+ * maximum without the argmax: the same S, bit for bit.
  */
 fms_status fms_inbatch_device_scan(int32_t dtype, float* S, int32_t* args,
                                    const void* Q, const void* D,
@@ -230,7 +233,8 @@ fms_status fms_topk(const float* scores, int64_t nrows, int64_t ncols, int64_t k
  * Q (dim,Tq,nq), tokens (dim,ntokens), cu (B+1,) 1-based, qmask (Tq,nq)
  * nullable; scores (B,nq) receives S[b, i] = Sigma_t of query i against
  * document b (required); args (Tq,B,nq) nullable, tapes as in
- * fms_launch_packed_scan.  max_len >= every document's length (PackedSeq's
+ * fms_launch_packed_scan (NULL: the MFMA kernel keeps a running maximum
+ * without the argmax, the same scores).  max_len >= every document's length (PackedSeq's
  * max_len).  f16/bf16 with dim = 128, Tq <= 32 and max_len <= 2048 run on
  * MFMA; other shapes make one packed scan per query.  Row i of the result
  * equals fms_launch_packed_scan of query i within the score tolerance (tapes

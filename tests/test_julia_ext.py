@@ -246,7 +246,7 @@ def test_every_override_falls_back_to_the_reference_off_gfx950():
     text = open(EXT).read()
     bodies = override_bodies(text)
     names = {b[0] for b in bodies}
-    assert set(REFERENCE_BACKEND) | {"quantize_int8_symmetric"} == names, names
+    assert set(REFERENCE_BACKEND) | {"quantize_int8_symmetric", "maxsim"} == names, names
     for name, sig, first in bodies:
         m = re.fullmatch(r"gfx950\(\) \|\| return @invoke FlashMaxSim\.(\w+!?)\((.*)\)", first)
         assert m, f"{name}: first statement {first!r}"
@@ -256,6 +256,12 @@ def test_every_override_falls_back_to_the_reference_off_gfx950():
         assert [n for n, _ in invoked] == declared, f"{name}: {invoked} vs {declared}"
         if name == "quantize_int8_symmetric":
             assert invoked == [("X", "AbstractArray{T}")], invoked
+            continue
+        if name == "maxsim":
+            # src/dispatch.jl:121-125: the arrays as the reference declares them
+            assert invoked == [("cfg", None), ("Q", "AbstractArray{T,3}"),
+                               ("D", "AbstractArray{T,3}"), ("qmask", "AbstractMatrix{Bool}"),
+                               ("dmask", "AbstractMatrix{Bool}"), ("layout", None)], invoked
             continue
         bi = declared.index("backend")
         assert arg_list(sig)[bi][1] == "ROCBackend", name
@@ -306,13 +312,28 @@ def test_pointer_arguments_are_dense_device_arrays():
             if mk:
                 args.append((mk.group(1), mk.group(2)))
         for arg, typ in args:
-            if arg in ("backend", "mode") or arg in SCALAR_ARGS or name == "topk":
+            if arg in ("backend", "mode", "cfg", "layout") or arg in SCALAR_ARGS or name == "topk":
                 continue
             assert typ is not None, f"{name}: argument {arg} is untyped"
             if arg in POINTER_ARG_TYPES:
                 assert re.fullmatch(POINTER_ARG_TYPES[arg], typ), f"{name}: {arg}::{typ}"
             else:
                 assert re.match(r"ROC(Array|Vector|Matrix)\{|Int8Index$", typ), f"{name}: {arg}::{typ}"
+
+
+def test_inbatch_verb_makes_no_tape():
+    """maxsim(cfg, Q, D, qmask, dmask, InBatch()) drops the tape in the reference
+    (src/dispatch.jl:121-125): the override passes no args buffer (the scores-only
+    kernel) and the config's normalize flag, and returns S alone."""
+    text = open(EXT).read()
+    m = re.search(r"function FlashMaxSim\.maxsim\((.*?)\nend\n", text, flags=re.S)
+    assert m, "no maxsim override"
+    body = m.group(1)
+    assert "layout::FlashMaxSim.InBatch" in body and "cfg::FlashMaxSim.MaxSim{T}" in body
+    assert re.search(r"c_inbatch_scan\(dtype_code\(T\), S, nothing, Q, D, qmask, dmask, dim, Tq, "
+                     r"Bq, Td, Bd;\s*normalize = cfg\.normalize\)", body), body
+    assert "AMDGPU.zeros(Float32, Bd, Bq)" in body and body.rstrip().endswith("S")
+    assert "args" not in body
 
 
 def test_project_fragment_wires_the_extension():

@@ -12,9 +12,10 @@ Other workloads (--workload c3 | c4 | c4d1024 | c5) measure the in-batch,
 packed and INT8 scans the same way (each prints its own JSON line); c3bwd
 measures the pullback of the c3 scores on their argmax tape (dQ and dD);
 c4mq scores the c4 workload with the multi-query packed scan (one launch).
---scores-only runs c3, c3d768, c3f32 and c4mq with a null args: S alone, as the
-reference's maxsim returns it (dispatch.jl:124 drops the in-batch tape), which
-the in-batch kernel computes with a running maximum alone.
+--scores-only runs c2, c5, c3, c3d768, c3f32 and c4mq with a null args: scores
+alone, as the reference's maxsim returns them (dispatch.jl:44-287 drop the tape);
+the in-batch kernel then keeps a running maximum alone, the scans skip the tape
+writes.
 """
 from __future__ import annotations
 
@@ -53,8 +54,10 @@ def parse():
                     help="target duration of the bounded CPU baseline sample")
     ap.add_argument("--grouping", default="auto", choices=["auto", "always", "never"],
                     help="candidate pair order (document-grouped or output order)")
+    ap.add_argument("--settle-ms", type=float, default=150.0,
+                    help="untimed run of the step before its warmup steps (0: none)")
     ap.add_argument("--scores-only", action="store_true",
-                    help="c3*/c4mq: no argmax tape (args null), S alone")
+                    help="c2, c5, c3*, c4mq: no argmax tape (args null), scores alone")
     ap.add_argument("--check", type=int, default=256,
                     help="pairs re-scored by the CPU oracle as a full-size parity spot check")
     return ap.parse_args()
@@ -78,12 +81,38 @@ def normalized_randn(torch, shape, gen, dtype, device, chunk_rows=4096):
     return out
 
 
+SETTLE = {"ms": 0.0, "calls": 0}
+ARGS_SETTLE_MS = [150.0]
+
+
+def settle(torch, fn, ms):
+    """Run the step untimed for at least `ms` milliseconds before its warmup: a scan
+    on a fresh process runs slower for its first few dozen calls (at C2: 1.28 ms per
+    call over the first 20, 0.96 over the next 20, 0.953 from then on; unrelated
+    memory-bound work beforehand does not shorten that), so W warmup steps alone
+    leave part of it in the timed steps.  Reported in the line as `settle`."""
+    if ms <= 0:
+        return
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    n = 0
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        for _ in range(8):
+            fn()
+        n += 8
+        torch.cuda.synchronize()
+    SETTLE["ms"] += (time.perf_counter() - t0) * 1e3
+    SETTLE["calls"] += n
+
+
 def timed_steps(torch, fn, steps, warmup):
     """W untimed steps, then exactly K steps bracketed by synchronize, with one pair of
     HIP events on the current stream (the stream every scan is enqueued on) around the
     K steps: the per-launch figure is their elapsed time / K.  (An event pair around
     every step would add ~10 us of GPU idle time per step: a timestamp packet is a
-    barrier for the command processor.)"""
+    barrier for the command processor.)  A settle phase (`settle`, --settle-ms) runs
+    the step before the W warmup steps."""
+    settle(torch, fn, ARGS_SETTLE_MS[0])
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -124,24 +153,37 @@ def run_c2(args, torch, fm, boundary, dev):
     S = torch.empty(B, C, dtype=torch.float32, device=dev)
     neg = -1.0e4
 
+    tape_t = None if args.scores_only else args_t
+
     def step():
-        boundary.launch_candidates_scan(args_t, None, Q, G, idx, qmask, dmask, N, S, neg)
+        boundary.launch_candidates_scan(tape_t, None, Q, G, idx, qmask, dmask, N, S, neg)
 
     wall, launch_ms = timed_steps(torch, step, args.steps, args.warmup)
+    so_ms = None
+    if not args.scores_only:  # the same call without the tape, as maxsim makes it
+        _, so_ms = timed_steps(
+            torch, lambda: boundary.launch_candidates_scan(None, None, Q, G, idx, qmask, dmask, N, S,
+                                                           neg), args.steps, args.warmup)
     n_valid = C * B - n_invalid
-    bytes_per_launch = (n_valid * (Ld * dim * 2 + Ld) + C * B * (4 * Lq + 4)
+    out_b = 4 if args.scores_only else 4 * Lq + 4  # per pair: score (+ tape row)
+    bytes_per_launch = (n_valid * (Ld * dim * 2 + Ld) + C * B * out_b
                         + B * (Lq * dim * 2 + Lq) + C * B * 8)
     # compulsory bytes: every distinct referenced document once, plus the rest
     n_docs = int(torch.unique(idx[idx > 0]).numel())
-    compulsory = (n_docs * (Ld * dim * 2 + Ld) + C * B * (4 * Lq + 4)
+    compulsory = (n_docs * (Ld * dim * 2 + Ld) + C * B * out_b
                   + B * (Lq * dim * 2 + Lq) + C * B * 8)
     res = dict(pairs_per_step=C * B, bytes_per_launch=bytes_per_launch, wall=wall,
                launch_ms=launch_ms, dtype="f16", compulsory_bytes=compulsory,
                distinct_docs=n_docs,
-               config={"workload": "c2_candidates_fp16", "dim": dim, "Lq": Lq, "Ld": Ld,
+               config={"workload": "c2_candidates_fp16" + ("_scores_only" if args.scores_only else ""),
+                       "dim": dim, "Lq": Lq, "Ld": Ld,
                        "C": C, "B": B, "N": N, "invalid_slots": n_invalid, "idx": "int64",
-                       "masks": "all true (device Bool)", "outputs": "scores (C,B) + tape (Lq,C,B)"})
+                       "masks": "all true (device Bool)",
+                       "outputs": "scores (C,B)" if args.scores_only else "scores (C,B) + tape (Lq,C,B)"})
     res["bound"] = "hbm"
+    if so_ms is not None:
+        res["side_scores_only"] = {"launch_ms": so_ms,
+                                   "compulsory_bytes": compulsory - C * B * 4 * Lq}
     if not args.no_cpu or args.check:
         res.update(cpu_candidates(args, torch, Q, G, idx, qmask, dmask, S, args_t, neg,
                                   fp16=True))
@@ -237,12 +279,13 @@ def cpu_candidates(args, torch, Q, G, idx, qmask, dmask, S, args_t, neg, fp16=Fa
         pairs = rng.choice(B * C, size=min(args.check, B * C), replace=False)
         Sc, ac, _ = run_oracle(pairs, nthreads)
         Sg = S.reshape(-1)[torch.from_numpy(pairs).to(S.device)].cpu().numpy()
-        ag = args_t.reshape(B * C, -1)[torch.from_numpy(pairs).to(S.device)].cpu().numpy()
+        ag = (args_t.reshape(B * C, -1)[torch.from_numpy(pairs).to(S.device)].cpu().numpy()
+              if not args.scores_only else None)
         tol = 2e-3 if (fp16 and int8 is None) else 1e-6
         ok = np.abs(Sg - Sc) <= tol * np.maximum(1.0, np.abs(Sc))
         out["check"] = {"pairs": int(len(pairs)), "scores_within_tol": bool(ok.all()),
                         "max_abs_err": float(np.abs(Sg - Sc).max()),
-                        "tape_agreement": float((ag == ac).mean())}
+                        "tape_agreement": None if ag is None else float((ag == ac).mean())}
         log(f"parity spot check: {out['check']}")
     if not args.no_cpu:
         calib = rng.choice(B * C, size=64, replace=False)
@@ -303,21 +346,35 @@ def run_c5(args, torch, fm, boundary, dev):
     Qc = torch.empty(B, Lq, dim, dtype=torch.int8, device=dev)
     Qs = torch.empty(B, Lq, dtype=torch.float32, device=dev)
 
+    tape_t = None if args.scores_only else args_t
+
     def step():  # on-the-fly query quantisation + INT8 candidate scan
         boundary.int8_quantize(Qf, Qc, Qs)
-        boundary.launch_int8_candidates_scan(args_t, None, Qc, Qs, Gc, Gs, idx, qmask, dmask, N,
+        boundary.launch_int8_candidates_scan(tape_t, None, Qc, Qs, Gc, Gs, idx, qmask, dmask, N,
                                              S, -1.0e4)
 
     wall, launch_ms = timed_steps(torch, step, args.steps, args.warmup)
-    bytes_per_launch = C * B * (Ld * dim + Ld * 4 + Ld + 4 * Lq + 4) + C * B * 8 + B * Lq * (dim * 5 + 4)
+    so_ms = None
+    if not args.scores_only:  # the same call without the tape, as maxsim makes it
+        def step_so():
+            boundary.int8_quantize(Qf, Qc, Qs)
+            boundary.launch_int8_candidates_scan(None, None, Qc, Qs, Gc, Gs, idx, qmask, dmask, N,
+                                                 S, -1.0e4)
+        _, so_ms = timed_steps(torch, step_so, args.steps, args.warmup)
+    out_b = 4 if args.scores_only else 4 * Lq + 4  # per pair: score (+ tape row)
+    bytes_per_launch = C * B * (Ld * dim + Ld * 4 + Ld + out_b) + C * B * 8 + B * Lq * (dim * 5 + 4)
     n_docs = int(torch.unique(idx).numel())
-    compulsory = (n_docs * (Ld * dim + Ld * 4 + Ld) + C * B * (4 * Lq + 4) + C * B * 8
+    compulsory = (n_docs * (Ld * dim + Ld * 4 + Ld) + C * B * out_b + C * B * 8
                   + B * Lq * (dim * 5 + 4))
     res = dict(pairs_per_step=C * B, bytes_per_launch=bytes_per_launch, wall=wall,
                launch_ms=launch_ms, dtype="int8", bound="hbm", compulsory_bytes=compulsory,
                distinct_docs=n_docs,
-               config={"workload": "c5_int8_candidates", "dim": dim, "Lq": Lq, "Ld": Ld, "C": C,
+               config={"workload": "c5_int8_candidates" + ("_scores_only" if args.scores_only else ""),
+                       "dim": dim, "Lq": Lq, "Ld": Ld, "C": C,
                        "B": B, "N": N, "idx": "int64", "query": "fp32, quantised per step"})
+    if so_ms is not None:
+        res["side_scores_only"] = {"launch_ms": so_ms,
+                                   "compulsory_bytes": compulsory - C * B * 4 * Lq}
     if not args.no_cpu or args.check:
         res.update(cpu_candidates(args, torch, Qf, None, idx, qmask, dmask, S, args_t, -1.0e4,
                                   int8=(Gc, Gs, Qf)))
@@ -638,6 +695,7 @@ def run_gather(args, torch, fm, boundary, dev, cfg):
 
 def main():
     args = parse()
+    ARGS_SETTLE_MS[0] = args.settle_ms
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only (single-GPU box); "
                                    "run with --gpus 1", "n_gpus": args.gpus}))
@@ -655,8 +713,8 @@ def main():
               "c4d1024": lambda *a: run_c4(*a, dim=1024),
               "c3d768": lambda *a: run_c3(*a, dim=768),
               "c3f32": lambda *a: run_c3(*a, dim=128, dtype=torch.float32)}[args.workload]
-    if args.scores_only and args.workload not in ("c3", "c3d768", "c3f32", "c4mq"):
-        sys.exit("--scores-only applies to c3, c3d768, c3f32 and c4mq")
+    if args.scores_only and args.workload not in ("c2", "c5", "c3", "c3d768", "c3f32", "c4mq"):
+        sys.exit("--scores-only applies to c2, c5, c3, c3d768, c3f32 and c4mq")
     r = runner(args, torch, fm, boundary, dev)
     steps = args.steps
     wall = r["wall"]
@@ -716,6 +774,8 @@ def main():
         "config": r["config"],
         "roofline": roof,
         "cpu_baseline": r.get("cpu"),
+        "settle": {"ms": round(SETTLE["ms"], 1), "calls": SETTLE["calls"],
+                   "note": "untimed runs of the step before its warmup steps (--settle-ms)"},
     }
     if "check" in r:
         out["parity_check"] = r["check"]
@@ -728,6 +788,16 @@ def main():
         out["roofline"]["gather_GBps"] = round(r["gather_bytes"] / avg_launch_s / 1e9, 1)
     if r["bound"] == "mfma":
         out["roofline"]["padded_tflops"] = round(r["padded_flops"] / avg_launch_s / 1e12, 2)
+    if "side_scores_only" in r:
+        # The config's output alone (scores, no tape): what maxsim's call makes
+        # (the reference's maxsim drops the tape, dispatch.jl:164), timed the same way.
+        so = r["side_scores_only"]
+        so_s = (sum(so["launch_ms"]) / len(so["launch_ms"])) / 1e3
+        out["scores_only"] = {
+            "ms_per_step": round(so_s * 1e3, 4), "value": round(r["pairs_per_step"] / so_s, 1),
+            "unit": "pairs/s", "frac": round(so["compulsory_bytes"] / so_s / 1e9 / HBM_PEAK_GBS, 4),
+            "basis": "compulsory bytes without the tape rows",
+            "call": "the same scan with a null args (no tape)"}
     if args.workload == "read":
         out["metric"] = "HBM streaming read GB/s"
         out["value"] = out["roofline"]["achieved"]

@@ -128,7 +128,7 @@ def maxsim(*args, neg=None, normalize=None, backward=None):
     if isinstance(a, PackedSeq):
         if not isinstance(b, PackedSeq) or rest:
             raise ArgumentError("varlen maxsim takes two PackedSeq")
-        scores, _ = F.varlen_forward(a, b, cfg.neg, cfg.normalize)
+        scores, _ = F.varlen_forward(a, b, cfg.neg, cfg.normalize, tape=False)
         return scores
 
     # ---- packed ----
@@ -137,7 +137,7 @@ def maxsim(*args, neg=None, normalize=None, backward=None):
         if a.dim() == 3:  # several queries in one pass (extension): (nq, B) scores
             S, _ = F.packed_multi_forward(a, b, qmask, cfg.neg, cfg.normalize, tape=False)
             return S
-        scores, _ = F.packed_forward(a, b, qmask, cfg.neg, cfg.normalize)
+        scores, _ = F.packed_forward(a, b, qmask, cfg.neg, cfg.normalize, tape=False)
         return scores
 
     # ---- INT8 index ----
@@ -145,27 +145,28 @@ def maxsim(*args, neg=None, normalize=None, backward=None):
         if rest and _is_index(rest[0]):
             idxs, masks = rest[0], rest[1:]
             qmask, dmask = (masks + [None, None])[:2]
-            S, _ = F.int8_candidates_forward(a, b, idxs, qmask, dmask, cfg.neg, cfg.normalize)
+            S, _ = F.int8_candidates_forward(a, b, idxs, qmask, dmask, cfg.neg, cfg.normalize,
+                                             tape=False)
             return S
         qmask, dmask = (rest + [None, None])[:2]
         if a.dim() == 2:
-            score, _ = F.int8_pair_forward(a, b, qmask, dmask, cfg.normalize)
+            score, _ = F.int8_pair_forward(a, b, qmask, dmask, cfg.normalize, tape=False)
             return score
-        scores, _ = F.int8_paired_forward(a, b, qmask, dmask, cfg.normalize)
+        scores, _ = F.int8_paired_forward(a, b, qmask, dmask, cfg.normalize, tape=False)
         return scores
 
     # ---- dense features ----
     if rest and _is_index(rest[0]) and not inbatch:
         idxs, masks = rest[0], rest[1:]
         qmask, dmask = (masks + [None, None])[:2]
-        S, _ = F.candidates_forward(a, b, idxs, qmask, dmask, cfg.neg, cfg.normalize)
+        S, _ = F.candidates_forward(a, b, idxs, qmask, dmask, cfg.neg, cfg.normalize, tape=False)
         return S
     qmask, dmask = (rest + [None, None])[:2]
     if inbatch:
         S, _ = F.inbatch_forward(a, b, qmask, dmask, cfg.neg, cfg.normalize, tape=False)
         return S
     if a.dim() == 2:
-        score, _ = F.pair_forward(a, b, qmask, dmask, cfg.neg, cfg.normalize)
+        score, _ = F.pair_forward(a, b, qmask, dmask, cfg.neg, cfg.normalize, tape=False)
         return score
-    scores, _ = F.paired_forward(a, b, qmask, dmask, cfg.neg, cfg.normalize)
+    scores, _ = F.paired_forward(a, b, qmask, dmask, cfg.neg, cfg.normalize, tape=False)
     return scores

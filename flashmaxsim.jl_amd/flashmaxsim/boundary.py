@@ -305,10 +305,18 @@ def topk_rows(vals, idx, scores, k):
     _lib.check(st, "topk")
 
 
-def launch_varlen_scan(args, partial, Qp, Dp, cu_q, cu_d, scores=None, normalize=False):
-    if args is None or args.dim() != 2:
+def launch_varlen_scan(args, partial, Qp, Dp, cu_q, cu_d, scores=None, normalize=False,
+                       max_q=None):
+    """The shapes come from args (N, max_q), as in the reference method; without a
+    tape (args None) max_q is given and N is the pair count of cu_q."""
+    if args is None:
+        if max_q is None or scores is None:
+            raise ArgumentError("launch_varlen_scan without args needs max_q and scores")
+        N = cu_q.numel() - 1
+    elif args.dim() != 2:
         raise DimensionMismatch("varlen args must be (N, max_q)")
-    N, max_q = args.shape
+    else:
+        N, max_q = args.shape
     _feat(Qp, "Q tokens", 2)
     _feat(Dp, "D tokens", 2, Qp)
     dim = Qp.shape[1]

@@ -101,22 +101,25 @@ def indices_on(prototype: torch.Tensor, idxs: torch.Tensor) -> torch.Tensor:
 
 # ---- forward drivers ---------------------------------------------------------------------
 
-def pair_forward(q, d, qmask=None, dmask=None, neg=None, normalize=False):
-    """pair_forward_ka (forward_pair.jl:104-116): (score (1,), argmax_u (Tq,))."""
+def pair_forward(q, d, qmask=None, dmask=None, neg=None, normalize=False, tape=True):
+    """pair_forward_ka (forward_pair.jl:104-116): (score (1,), argmax_u (Tq,)).
+    tape=False: (score, None), no tape made (every driver below takes the same
+    keyword; ``maxsim`` passes it, as the reference's drops the tape,
+    dispatch.jl:44-287)."""
     boundary.require_device(q, d, qmask, dmask)
     _, Tq, _ = require_pair_shapes(q, d, qmask, dmask)
-    argmax_u = _zeros(q, torch.int32, Tq)
-    partial = _zeros(q, SCORE_DTYPE, Tq)
+    argmax_u = _zeros(q, torch.int32, Tq) if tape else None
+    partial = _zeros(q, SCORE_DTYPE, Tq) if tape else None
     score = _zeros(q, SCORE_DTYPE, 1)
     boundary.launch_pair_scan(argmax_u, partial, q, d, qmask, dmask, score, normalize)
     return score, argmax_u
 
 
-def paired_forward(Q, D, qmask=None, dmask=None, neg=None, normalize=False):
+def paired_forward(Q, D, qmask=None, dmask=None, neg=None, normalize=False, tape=True):
     """paired_forward_ka (forward_layouts.jl:112-124): (scores (B,), args (B,Tq))."""
     boundary.require_device(Q, D, qmask, dmask)
     _, Tq, _, B = require_paired_shapes(Q, D, qmask, dmask)
-    args = _zeros(Q, torch.int32, B, Tq)
+    args = _zeros(Q, torch.int32, B, Tq) if tape else None
     scores = _zeros(Q, SCORE_DTYPE, B)
     boundary.launch_paired_scan(args, None, Q, D, qmask, dmask, scores, normalize)
     return scores, args
@@ -138,20 +141,21 @@ def inbatch_forward(Q, D, qmask=None, dmask=None, neg=None, normalize=False, tap
     return S, args
 
 
-def candidates_forward(Q, gallery, idxs, qmask=None, dmask=None, neg=-1.0e4, normalize=False):
+def candidates_forward(Q, gallery, idxs, qmask=None, dmask=None, neg=-1.0e4, normalize=False,
+                       tape=True):
     """candidates_forward_ka (forward_layouts.jl:272-290): (S (B,C), args (B,C,Tq))."""
     boundary.require_device(Q, gallery, qmask, dmask)
     _, Tq, B, _, N = require_candidates_shapes(Q, gallery, idxs, qmask, dmask)
     idx = indices_on(Q, idxs)
     C = idx.shape[1]
-    args = _zeros(Q, torch.int32, B, C, Tq)
+    args = _zeros(Q, torch.int32, B, C, Tq) if tape else None
     S = _zeros(Q, SCORE_DTYPE, B, C)
     boundary.launch_candidates_scan(args, None, Q, gallery, idx, qmask, dmask, N, S, neg,
                                     normalize)
     return S, args
 
 
-def packed_forward(q, P: PackedSeq, qmask=None, neg=None, normalize=False):
+def packed_forward(q, P: PackedSeq, qmask=None, neg=None, normalize=False, tape=True):
     """packed_forward_ka (packed.jl:191-202): (scores (B,), args (B,Tq))."""
     boundary.require_device(q, P.tokens, P.cu, qmask)
     Tq = q.shape[0]
@@ -160,7 +164,7 @@ def packed_forward(q, P: PackedSeq, qmask=None, neg=None, normalize=False):
     if qmask is not None and qmask.numel() != Tq:
         raise DimensionMismatch("qmask")
     B = P.nseq()
-    args = _zeros(q, torch.int32, B, Tq)
+    args = _zeros(q, torch.int32, B, Tq) if tape else None
     scores = _zeros(q, SCORE_DTYPE, B)
     boundary.launch_packed_scan(args, None, q, P.tokens, P.cu, qmask, scores, normalize)
     return scores, args
@@ -221,7 +225,7 @@ def topk(scores: torch.Tensor, k: int):
     return vals, idx
 
 
-def varlen_forward(Qp: PackedSeq, Dp: PackedSeq, neg=None, normalize=False):
+def varlen_forward(Qp: PackedSeq, Dp: PackedSeq, neg=None, normalize=False, tape=True):
     """varlen_forward_ka (packed.jl:274-284): (scores (N,), args (N,max_q))."""
     boundary.require_device(Qp.tokens, Dp.tokens, Qp.cu, Dp.cu)
     N = Qp.nseq()
@@ -230,13 +234,14 @@ def varlen_forward(Qp: PackedSeq, Dp: PackedSeq, neg=None, normalize=False):
     if Qp.tokens.shape[1] != Dp.tokens.shape[1]:
         raise DimensionMismatch("feature dim")
     max_q = Qp.max_len
-    args = _zeros(Qp.tokens, torch.int32, N, max_q)
+    args = _zeros(Qp.tokens, torch.int32, N, max_q) if tape else None
     scores = _zeros(Qp.tokens, SCORE_DTYPE, N)
-    boundary.launch_varlen_scan(args, None, Qp.tokens, Dp.tokens, Qp.cu, Dp.cu, scores, normalize)
+    boundary.launch_varlen_scan(args, None, Qp.tokens, Dp.tokens, Qp.cu, Dp.cu, scores, normalize,
+                                max_q=max_q)
     return scores, args
 
 
-def int8_pair_forward(q, d: Int8Index, qmask=None, dmask=None, normalize=False):
+def int8_pair_forward(q, d: Int8Index, qmask=None, dmask=None, normalize=False, tape=True):
     """int8_pair_forward (quant.jl:156-170): quantise q on device, then the INT8 scan."""
     qq = quantize_int8_symmetric(q)
     require_int8_index(d)
@@ -251,14 +256,14 @@ def int8_pair_forward(q, d: Int8Index, qmask=None, dmask=None, normalize=False):
         raise DimensionMismatch("qmask")
     if dmask is not None and dmask.numel() != Td:
         raise DimensionMismatch("dmask")
-    args = _zeros(q, torch.int32, Tq)
+    args = _zeros(q, torch.int32, Tq) if tape else None
     score = _zeros(q, SCORE_DTYPE, 1)
     boundary.launch_int8_pair_scan(args, None, qq.codes, qq.scales, d.codes, d.scales, qmask,
                                    dmask, score, normalize)
     return score, args
 
 
-def int8_paired_forward(Q, D: Int8Index, qmask=None, dmask=None, normalize=False):
+def int8_paired_forward(Q, D: Int8Index, qmask=None, dmask=None, normalize=False, tape=True):
     """int8_paired_forward (quant.jl:219-226)."""
     QQ = quantize_int8_symmetric(Q)
     require_int8_index(D)
@@ -275,7 +280,7 @@ def int8_paired_forward(Q, D: Int8Index, qmask=None, dmask=None, normalize=False
         raise DimensionMismatch("qmask")
     if dmask is not None and tuple(dmask.shape) != (B, Td):
         raise DimensionMismatch("dmask")
-    args = _zeros(Q, torch.int32, B, Tq)
+    args = _zeros(Q, torch.int32, B, Tq) if tape else None
     scores = _zeros(Q, SCORE_DTYPE, B)
     boundary.launch_int8_paired_scan(args, None, QQ.codes, QQ.scales, D.codes, D.scales, qmask,
                                      dmask, scores, normalize)
@@ -283,7 +288,7 @@ def int8_paired_forward(Q, D: Int8Index, qmask=None, dmask=None, normalize=False
 
 
 def int8_candidates_forward(Q, G: Int8Index, idxs, qmask=None, dmask=None, neg=-1.0e4,
-                            normalize=False):
+                            normalize=False, tape=True):
     """INT8 candidate layout (no reference method): quantised Q_b vs gallery[idxs[c,b]]."""
     QQ = quantize_int8_symmetric(Q)
     boundary.require_device(Q, QQ.codes, QQ.scales, G.codes, G.scales, qmask, dmask)
@@ -301,7 +306,7 @@ def int8_candidates_forward(Q, G: Int8Index, idxs, qmask=None, dmask=None, neg=-
         raise DimensionMismatch("dmask")
     idx = indices_on(Q, idxs)
     C = idx.shape[1]
-    args = _zeros(Q, torch.int32, B, C, Tq)
+    args = _zeros(Q, torch.int32, B, C, Tq) if tape else None
     S = _zeros(Q, SCORE_DTYPE, B, C)
     boundary.launch_int8_candidates_scan(args, None, QQ.codes, QQ.scales, G.codes, G.scales, idx,
                                          qmask, dmask, N, S, neg, normalize)

@@ -1,4 +1,4 @@
-"""GPU: scores without the argmax tape (args null).
+"""GPU: scores without the argmax tape (args null), and every maxsim verb without one.
 
 The reference's ``maxsim(Q, D, qmask, dmask, InBatch())`` keeps S and drops the
 tape (``S, _ = inbatch_forward(...)``, dispatch.jl:124).  Called with args null,
@@ -170,3 +170,106 @@ def test_inbatch_scores_only_nonfinite(device, dtype):
     S_o, _ = oracle.inbatch_forward(Qo, Do, qm.astype(np.uint8), dm.astype(np.uint8), bf16=bf)
     assert np.array_equal(np.isnan(ss), np.isnan(S_o))
     assert np.isnan(ss[:, 3]).all() and np.isfinite(ss[0, 12]) and ss[0, 20] == 0.0
+
+
+# ---- every maxsim verb: S without a tape ----------------------------------------------
+
+def _mask(rng, n, T, p, device):
+    m = rng.random((n, T)) < p
+    m[:, 0] = True
+    return torch.from_numpy(m).to(device)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32],
+                         ids=lambda d: DT_ID[d])
+@pytest.mark.parametrize("layout", ["pair", "paired", "candidates_grouped", "candidates_ordered",
+                                    "packed", "varlen"])
+@pytest.mark.parametrize("normalize", [False, True], ids=["raw", "norm"])
+def test_maxsim_makes_no_tape(device, dtype, layout, normalize):
+    """The reference's maxsim drops the tape for every layout (src/dispatch.jl:44, 83,
+    164, 201, 229): maxsim here makes none (tape=False, null args), and its scores are
+    bit-identical to the drivers' with the tape."""
+    rng = np.random.default_rng(sum(map(ord, layout + DT_ID[dtype])) + int(normalize))
+    dim, Tq, Td = 128, 32, 96
+    dev = lambda x: as_feature(x, dtype)[0].to(device)  # noqa: E731
+    if layout == "pair":
+        q, d = dev(tokens(rng, (Tq, dim))), dev(tokens(rng, (Td, dim)))
+        qm, dm = _mask(rng, 1, Tq, 0.9, device)[0], _mask(rng, 1, Td, 0.8, device)[0]
+        want, _ = fm.pair_forward(q, d, qm, dm, normalize=normalize)
+        got, none = fm.pair_forward(q, d, qm, dm, normalize=normalize, tape=False)
+        verb = fm.maxsim(q, d, qm, dm, normalize=normalize)
+    elif layout == "paired":
+        B = 37
+        Q, D = dev(tokens(rng, (B, Tq, dim))), dev(tokens(rng, (B, Td, dim)))
+        qm, dm = _mask(rng, B, Tq, 0.9, device), _mask(rng, B, Td, 0.8, device)
+        want, _ = fm.paired_forward(Q, D, qm, dm, normalize=normalize)
+        got, none = fm.paired_forward(Q, D, qm, dm, normalize=normalize, tape=False)
+        verb = fm.maxsim(Q, D, qm, dm, normalize=normalize)
+    elif layout.startswith("candidates"):
+        B, C, N = 24, 40, 300
+        Q, G = dev(tokens(rng, (B, Tq, dim))), dev(tokens(rng, (N, Td, dim)))
+        idx = torch.from_numpy(rng.integers(0, N + 2, size=(B, C))).to(device)
+        qm, dm = _mask(rng, B, Tq, 0.9, device), _mask(rng, N, Td, 0.8, device)
+        prev = boundary.candidates_grouping("always" if layout.endswith("grouped") else "never")
+        try:
+            want, _ = fm.candidates_forward(Q, G, idx, qm, dm, -7.0, normalize=normalize)
+            got, none = fm.candidates_forward(Q, G, idx, qm, dm, -7.0, normalize=normalize,
+                                              tape=False)
+            verb = fm.maxsim(Q, G, idx, qm, dm, neg=-7.0, normalize=normalize)
+        finally:
+            boundary.candidates_grouping(prev)
+    elif layout == "packed":
+        lens = [5, 0, 33, 64, 200, 1]
+        q = dev(tokens(rng, (Tq, dim)))
+        tt = as_feature(np.concatenate([tokens(rng, (n, dim)) for n in lens], 0), dtype)[0]
+        cu = torch.from_numpy(np.concatenate([[1], 1 + np.cumsum(lens)]).astype(np.int32))
+        P = fm.PackedSeq(tt, cu).to(device)
+        qm = _mask(rng, 1, Tq, 0.9, device)[0]
+        want, _ = fm.packed_forward(q, P, qm, normalize=normalize)
+        got, none = fm.packed_forward(q, P, qm, normalize=normalize, tape=False)
+        verb = fm.maxsim(q, P, qm, normalize=normalize)
+    else:  # varlen
+        ql, dl = [7, 32, 1, 40], [50, 3, 90, 0]
+        qt = as_feature(np.concatenate([tokens(rng, (n, dim)) for n in ql], 0), dtype)[0]
+        dt = as_feature(np.concatenate([tokens(rng, (n, dim)) for n in dl], 0), dtype)[0]
+        cq = torch.from_numpy(np.concatenate([[1], 1 + np.cumsum(ql)]).astype(np.int32))
+        cd = torch.from_numpy(np.concatenate([[1], 1 + np.cumsum(dl)]).astype(np.int32))
+        Qp, Dp = fm.PackedSeq(qt, cq).to(device), fm.PackedSeq(dt, cd).to(device)
+        want, _ = fm.varlen_forward(Qp, Dp, normalize=normalize)
+        got, none = fm.varlen_forward(Qp, Dp, normalize=normalize, tape=False)
+        verb = fm.maxsim(Qp, Dp, normalize=normalize)
+    torch.cuda.synchronize()
+    assert none is None
+    assert torch.equal(got, want) and torch.equal(verb, want)
+
+
+@pytest.mark.parametrize("layout", ["pair", "paired", "candidates"])
+def test_int8_maxsim_makes_no_tape(device, layout):
+    """The INT8 verbs (src/dispatch.jl:261, 287; candidates: no reference method) without
+    the tape: scores bit-identical to the drivers' with it."""
+    rng = np.random.default_rng({"pair": 81, "paired": 82, "candidates": 83}[layout])
+    dim, Tq, Td = 128, 32, 96
+    if layout == "pair":
+        q = torch.from_numpy(tokens(rng, (Tq, dim))).to(device)
+        d = fm.quantize_int8_symmetric(torch.from_numpy(tokens(rng, (Td, dim))).to(device))
+        want, _ = fm.int8_pair_forward(q, d)
+        got, none = fm.int8_pair_forward(q, d, tape=False)
+        verb = fm.maxsim(q, d)
+    elif layout == "paired":
+        B = 21
+        Q = torch.from_numpy(tokens(rng, (B, Tq, dim))).to(device)
+        D = fm.quantize_int8_symmetric(torch.from_numpy(tokens(rng, (B, Td, dim))).to(device))
+        want, _ = fm.int8_paired_forward(Q, D)
+        got, none = fm.int8_paired_forward(Q, D, tape=False)
+        verb = fm.maxsim(Q, D)
+    else:
+        B, C, N = 16, 30, 200
+        Q = torch.from_numpy(tokens(rng, (B, Tq, dim))).to(device)
+        G = fm.quantize_int8_symmetric(torch.from_numpy(tokens(rng, (N, Td, dim))).to(device))
+        idx = torch.from_numpy(rng.integers(0, N + 2, size=(B, C))).to(device)
+        want, _ = fm.int8_candidates_forward(Q, G, idx, neg=-3.0)
+        got, none = fm.int8_candidates_forward(Q, G, idx, neg=-3.0, tape=False)
+        verb = fm.maxsim(Q, G, idx, neg=-3.0)
+    torch.cuda.synchronize()
+    assert none is None
+    assert torch.equal(got, want) and torch.equal(verb, want)

@@ -145,24 +145,25 @@ function c_pair_scan(dtype, argmax_u, partial, q, d, qmask, dmask, dim, Tq, Td, 
           "pair scan")
 end
 
-function c_paired_scan(dtype, args, partial, Q, D, qmask, dmask, dim, Tq, Td, B, scores)
+function c_paired_scan(dtype, args, partial, Q, D, qmask, dmask, dim, Tq, Td, B, scores;
+                       normalize::Bool = false)
     check(ccall((:fms_launch_paired_scan, libfms), Int32,
                 (Int32, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid},
                  Int64, Int64, Int64, Int64, Ptr{Cvoid}, Int32, Ptr{Cvoid}),
                 dtype, dptr(args), dptr(partial), dptr(Q), dptr(D), dptr(qmask), dptr(dmask),
-                dim, Tq, Td, B, dptr(scores), Int32(0), stream_ptr()),
+                dim, Tq, Td, B, dptr(scores), Int32(normalize), stream_ptr()),
           "paired scan")
 end
 
 function c_candidates_scan(dtype, args, partial, Q, gallery, idx, qmask, dmask,
-                           dim, Tq, B, Td, N, C, scores, neg)
+                           dim, Tq, B, Td, N, C, scores, neg; normalize::Bool = false)
     check(ccall((:fms_launch_candidates_scan, libfms), Int32,
                 (Int32, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Int32,
                  Ptr{Cvoid}, Ptr{Cvoid}, Int64, Int64, Int64, Int64, Int64, Int64,
                  Ptr{Cvoid}, Float32, Int32, Ptr{Cvoid}),
                 dtype, dptr(args), dptr(partial), dptr(Q), dptr(gallery), dptr(idx),
                 Int32(sizeof(eltype(idx))), dptr(qmask), dptr(dmask), dim, Tq, B, Td, N, C,
-                dptr(scores), Float32(neg), Int32(0), stream_ptr()),
+                dptr(scores), Float32(neg), Int32(normalize), stream_ptr()),
           "candidate scan")
 end
 
@@ -332,6 +333,36 @@ function FlashMaxSim.maxsim(cfg::FlashMaxSim.MaxSim{T}, Q::ROCArray{T,3}, D::ROC
     c_inbatch_scan(dtype_code(T), S, nothing, Q, D, qmask, dmask, dim, Tq, Bq, Td, Bd;
                    normalize = cfg.normalize)
     S
+end
+
+# The paired and candidate verbs drop the tape in the reference too
+# (src/dispatch.jl:80-85, 160-167): the same scans with no tape buffer, scores
+# in Float32, cfg.normalize fused into the score write (invalid candidates keep
+# neg, as length_normalize_candidates does).
+
+function FlashMaxSim.maxsim(cfg::FlashMaxSim.MaxSim{T}, Q::ROCArray{T,3}, D::ROCArray{T,3},
+                            qmask::DenseMask{2}, dmask::DenseMask{2}) where {T<:AnyFeature}
+    gfx950() || return @invoke FlashMaxSim.maxsim(cfg, Q::AbstractArray{T,3}, D::AbstractArray{T,3}, qmask::AbstractMatrix{Bool}, dmask::AbstractMatrix{Bool})
+    FlashMaxSim.require_colocated(Q, D, qmask, dmask)
+    dim, Tq, Td, B = FlashMaxSim.require_paired_shapes(Q, D, qmask, dmask)
+    scores = AMDGPU.zeros(Float32, B)
+    c_paired_scan(dtype_code(T), nothing, nothing, Q, D, qmask, dmask, dim, Tq, Td, B, scores;
+                  normalize = cfg.normalize)
+    scores
+end
+
+function FlashMaxSim.maxsim(cfg::FlashMaxSim.MaxSim{T}, Q::ROCArray{T,3}, gallery::ROCArray{T,3},
+                            idxs::DenseIndex, qmask::DenseMask{2},
+                            dmask::DenseMask{2}) where {T<:AnyFeature}
+    gfx950() || return @invoke FlashMaxSim.maxsim(cfg, Q::AbstractArray{T,3}, gallery::AbstractArray{T,3}, idxs::AbstractMatrix{<:Integer}, qmask::AbstractMatrix{Bool}, dmask::AbstractMatrix{Bool})
+    FlashMaxSim.require_colocated(Q, gallery, qmask, dmask)
+    dim, Tq, B, Td, N = FlashMaxSim.require_candidates_shapes(Q, gallery, idxs, qmask, dmask)
+    idx = FlashMaxSim.indices_on(Q, idxs)
+    C = size(idx, 1)
+    scores = AMDGPU.zeros(Float32, C, B)
+    c_candidates_scan(dtype_code(T), nothing, nothing, Q, gallery, idx, qmask, dmask,
+                      dim, Tq, B, Td, N, C, scores, cfg.neg; normalize = cfg.normalize)
+    scores
 end
 
 function FlashMaxSim.candidates_forward_ka(backend::ROCBackend, Q::ROCArray{T,3},

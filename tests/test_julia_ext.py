@@ -237,6 +237,12 @@ def override_bodies(text, prefix=r"FlashMaxSim\."):
     return out
 
 
+MAXSIM_REFERENCE_TYPES = {
+    "cfg": None, "layout": None, "Q": "AbstractArray{T,3}", "D": "AbstractArray{T,3}",
+    "gallery": "AbstractArray{T,3}", "idxs": "AbstractMatrix{<:Integer}",
+    "qmask": "AbstractMatrix{Bool}", "dmask": "AbstractMatrix{Bool}"}
+
+
 def test_every_override_falls_back_to_the_reference_off_gfx950():
     """On an AMD GPU that is not gfx950 every override keeps the reference's own
     method, as the CUDA extension does when its tensor cores are off
@@ -258,10 +264,9 @@ def test_every_override_falls_back_to_the_reference_off_gfx950():
             assert invoked == [("X", "AbstractArray{T}")], invoked
             continue
         if name == "maxsim":
-            # src/dispatch.jl:121-125: the arrays as the reference declares them
-            assert invoked == [("cfg", None), ("Q", "AbstractArray{T,3}"),
-                               ("D", "AbstractArray{T,3}"), ("qmask", "AbstractMatrix{Bool}"),
-                               ("dmask", "AbstractMatrix{Bool}"), ("layout", None)], invoked
+            # src/dispatch.jl:80-85, 121-125, 160-167: the arrays as the reference
+            # declares them, the config and layout marker as they are
+            assert invoked == [(n, MAXSIM_REFERENCE_TYPES[n]) for n in declared], invoked
             continue
         bi = declared.index("backend")
         assert arg_list(sig)[bi][1] == "ROCBackend", name
@@ -334,6 +339,27 @@ def test_inbatch_verb_makes_no_tape():
                      r"Bq, Td, Bd;\s*normalize = cfg\.normalize\)", body), body
     assert "AMDGPU.zeros(Float32, Bd, Bq)" in body and body.rstrip().endswith("S")
     assert "args" not in body
+
+
+def test_paired_and_candidate_verbs_make_no_tape():
+    """maxsim's paired and candidate methods (src/dispatch.jl:80-85, 160-167) drop the
+    tape in the reference: the overrides pass no tape or partial buffer and the
+    config's normalize flag, and return the Float32 scores alone."""
+    text = open(EXT).read()
+    bodies = re.findall(r"function FlashMaxSim\.maxsim\((.*?)\nend\n", text, flags=re.S)
+    assert len(bodies) == 3
+    paired = [b for b in bodies if "c_paired_scan" in b]
+    cand = [b for b in bodies if "c_candidates_scan" in b]
+    assert len(paired) == 1 and len(cand) == 1
+    assert re.search(r"c_paired_scan\(dtype_code\(T\), nothing, nothing, Q, D, qmask, dmask, dim, "
+                     r"Tq, Td, B, scores;\s*normalize = cfg\.normalize\)", paired[0])
+    assert re.search(r"c_candidates_scan\(dtype_code\(T\), nothing, nothing, Q, gallery, idx, "
+                     r"qmask, dmask,\s*dim, Tq, B, Td, N, C, scores, cfg\.neg; "
+                     r"normalize = cfg\.normalize\)", cand[0])
+    assert "idxs::DenseIndex" in cand[0]
+    for b in paired + cand:
+        assert "AMDGPU.zeros(Float32" in b and b.rstrip().endswith("scores")
+        assert "args" not in b
 
 
 def test_project_fragment_wires_the_extension():

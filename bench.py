@@ -56,6 +56,8 @@ def parse():
                     help="candidate pair order (document-grouped or output order)")
     ap.add_argument("--settle-ms", type=float, default=150.0,
                     help="untimed run of the step before its warmup steps (0: none)")
+    ap.add_argument("--no-side", action="store_true",
+                    help="c2, c5: skip the no-tape side measurement (scores_only)")
     ap.add_argument("--scores-only", action="store_true",
                     help="c2, c5, c3*, c4mq: no argmax tape (args null), scores alone")
     ap.add_argument("--check", type=int, default=256,
@@ -160,7 +162,7 @@ def run_c2(args, torch, fm, boundary, dev):
 
     wall, launch_ms = timed_steps(torch, step, args.steps, args.warmup)
     so_ms = None
-    if not args.scores_only:  # the same call without the tape, as maxsim makes it
+    if not args.scores_only and not args.no_side:  # the same call without the tape, as maxsim makes it
         _, so_ms = timed_steps(
             torch, lambda: boundary.launch_candidates_scan(None, None, Q, G, idx, qmask, dmask, N, S,
                                                            neg), args.steps, args.warmup)
@@ -355,7 +357,7 @@ def run_c5(args, torch, fm, boundary, dev):
 
     wall, launch_ms = timed_steps(torch, step, args.steps, args.warmup)
     so_ms = None
-    if not args.scores_only:  # the same call without the tape, as maxsim makes it
+    if not args.scores_only and not args.no_side:  # the same call without the tape, as maxsim makes it
         def step_so():
             boundary.int8_quantize(Qf, Qc, Qs)
             boundary.launch_int8_candidates_scan(None, None, Qc, Qs, Gc, Gs, idx, qmask, dmask, N,

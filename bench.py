@@ -777,7 +777,8 @@ def main():
         "roofline": roof,
         "cpu_baseline": r.get("cpu"),
         "settle": {"ms": round(SETTLE["ms"], 1), "calls": SETTLE["calls"],
-                   "note": "untimed runs of the step before its warmup steps (--settle-ms)"},
+                   "note": ("untimed runs of the step before its warmup steps (--settle-ms), "
+                            "summed over the line's measurements (main and side)")},
     }
     if "check" in r:
         out["parity_check"] = r["check"]
